@@ -1,0 +1,206 @@
+#!/usr/bin/env python3
+"""Decode throughput (tok/s, HBM GB/s and fraction of peak) and prefill throughput of the 8B-class
+fp16 Llama-style decoder at batch 1 on one MI355X, through the engine's C ABI.
+
+Workload: 32 layers, d_model 4096, 32 query / 8 KV heads (head_dim 128), SwiGLU FFN 14336, vocab
+32000, RMSNorm eps 1e-5, RoPE theta 500000, fp16 weights N(0, 0.02) generated on the device, KV
+cache fp16 with capacity 4096; prompt of 512 uniform-random token ids (prefill timed on its own),
+then greedy decode.  A step is one decode token; K steps are timed between two synchronisations.
+
+Prints one JSON line.  --gpus N with N > 1 exits: this build targets one GPU.
+"""
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PEAK_HBM = 8.0e12       # MI355X HBM3E, bytes/s
+PEAK_F16 = 2.5e15       # MI355X dense fp16 MFMA, flop/s
+
+CFG = dict(hidden_size=4096, num_layers=32, num_heads=32, num_kv_heads=8, intermediate_size=14336, vocab_size=32000,
+           max_position_embeddings=32768, rope_theta=500000.0, rms_eps=1e-5, dtype=1)
+KV_CAPACITY = 4096
+
+
+def load_package():
+    name = "vulkan_symbiote_loader_amd"
+    spec = importlib.util.spec_from_file_location(name, os.path.join(ROOT, "vulkan-symbiote-loader_amd", "__init__.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def model_bytes(c):
+    d, L, nq, nkv, F, V = (c["hidden_size"], c["num_layers"], c["num_heads"], c["num_kv_heads"],
+                           c["intermediate_size"], c["vocab_size"])
+    hd = d // nq
+    p_lin = L * (d * nq * hd + 2 * d * nkv * hd + nq * hd * d + 3 * d * F) + V * d
+    p_norm = L * 2 * d + d
+    kvb = 2 * L * nkv * hd * 2  # K and V, fp16, per position
+    return p_lin, p_norm, kvb
+
+
+def decode_bytes(c, attended):
+    """Algorithmic HBM bytes of one decode token that attends `attended` positions: every weight
+    once, the embedding row, K/V of the attended positions and the new position's K/V write."""
+    p_lin, p_norm, kvb = model_bytes(c)
+    return 2 * p_lin + 2 * p_norm + 2 * c["hidden_size"] + kvb * attended + kvb
+
+
+def prefill_flops(c, S):
+    d, L, nq, V = c["hidden_size"], c["num_layers"], c["num_heads"], c["vocab_size"]
+    hd = d // nq
+    p_lin, _, _ = model_bytes(c)
+    p_layers = p_lin - V * d
+    return 2 * S * p_layers + 2 * V * d + 4 * L * nq * hd * S * (S + 1) / 2
+
+
+def cpu_baseline(eng, cfg, prompt, seconds):
+    """The oracle (CPU restatement of the reference's token loop) on this host, timed on a bounded
+    sample: the engine's resident weights copied to host memory, a short prompt, then greedy decode
+    steps for about `seconds`."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    d, L, nq, nkv, F, V = (cfg["hidden_size"], cfg["num_layers"], cfg["num_heads"], cfg["num_kv_heads"],
+                           cfg["intermediate_size"], cfg["vocab_size"])
+    hd = d // nq
+    m = orc.Model(config=dict(hidden_size=d, num_layers=L, num_heads=nq, num_kv_heads=nkv, intermediate_size=F,
+                              vocab_size=V, head_dim=hd, max_position_embeddings=cfg["max_position_embeddings"],
+                              rope_theta=cfg["rope_theta"], rms_eps=cfg["rms_eps"]))
+    sizes = {"token_embd.weight": V * d, "output.weight": V * d}
+    for l in range(L):
+        sizes.update({f"blk.{l}.attn_q.weight": nq * hd * d, f"blk.{l}.attn_k.weight": nkv * hd * d,
+                      f"blk.{l}.attn_v.weight": nkv * hd * d, f"blk.{l}.attn_o.weight": d * nq * hd,
+                      f"blk.{l}.ffn_gate.weight": F * d, f"blk.{l}.ffn_up.weight": F * d,
+                      f"blk.{l}.ffn_down.weight": d * F})
+    for n, cnt in sizes.items():
+        m.set_tensor(n, eng.read_tensor(n, cnt * 2))
+    for n in ["output_norm.weight"] + [f"blk.{l}.{s}.weight" for l in range(L) for s in ("attn_norm", "ffn_norm")]:
+        m.set_tensor(n, eng.read_tensor(n, d * 4))
+    threads = orc.num_threads()
+    n, secs = m.decode_rate(prompt, max_seconds=seconds, max_tokens=4096)
+    m.close()
+    return {"value": n / secs, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle greedy decode of {n} tokens after a {len(prompt)}-token prompt on the same 8B "
+                      f"weights ({secs:.1f} s, {threads} threads, fp16 weights / fp32 math)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512, help="timed decode steps (tokens)")
+    ap.add_argument("--warmup", type=int, default=32, help="untimed decode steps before the timed run")
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-kernel-timing", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (use --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+    if a.prompt + a.steps > KV_CAPACITY:
+        print("bench.py: prompt + steps exceed the KV capacity", file=sys.stderr)
+        sys.exit(2)
+
+    vsl = load_package()
+    t_init = time.perf_counter()
+    eng = vsl.Engine(spec=CFG, seed=0, kv_capacity=KV_CAPACITY)
+    init_s = time.perf_counter() - t_init
+    prompt = np.random.default_rng(1).integers(0, CFG["vocab_size"], a.prompt).astype(np.uint32)
+
+    # warmup: one full generation (graph capture, caches, clocks)
+    eng.begin(prompt, a.warmup + 1)
+    eng.decode(a.warmup)
+    eng.finish()
+
+    # timed: prefill (events) + exactly K decode steps between two synchronisations
+    eng.begin(prompt, a.steps + 1)
+    eng.sync()
+    t0 = time.perf_counter()
+    issued = eng.decode(a.steps)
+    eng.sync()
+    t1 = time.perf_counter()
+    toks = eng.finish()
+    st = eng.last_stats()
+    assert issued == a.steps and len(toks) == a.steps + 1, (issued, len(toks))
+    dec_s = t1 - t0
+    tok_s = a.steps / dec_s
+    # step i (1..K) processes position prompt+i-1 and attends prompt+i positions
+    total_bytes = sum(decode_bytes(CFG, a.prompt + i) for i in range(1, a.steps + 1))
+    hbm = total_bytes / dec_s
+    pre_s = st["prefill_ms"] / 1e3
+    pre_flops = prefill_flops(CFG, a.prompt)
+
+    out = {
+        "metric": "decode tok/s + HBM GB/s (% peak), 8B fp16 bs=1; prefill tok/s",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(dec_s * 1e3 / a.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: random-init N(0,0.02) fp16 weights (Philox on device), uniform-random prompt ids",
+        "config": {"workload": f"8B-class Llama decoder fp16 bs=1 (32L, d4096, 32/8 heads, FFN 14336, V32000): "
+                               f"prompt {a.prompt}, greedy decode {a.steps}, KV cap {KV_CAPACITY}",
+                   "global_batch": 1, "seq_len": a.prompt + a.steps, "parallelism": "single-gpu"},
+        "decode_hbm_gbps": round(hbm / 1e9, 1),
+        "decode_hbm_frac": round(hbm / PEAK_HBM, 4),
+        "decode_bytes_per_token": int(total_bytes / a.steps),
+        "decode_ms_events": round(st["decode_ms"], 3),
+        "prefill_tok_s": round(a.prompt / pre_s, 1),
+        "prefill_ms": round(st["prefill_ms"], 3),
+        "prefill_tflops": round(pre_flops / pre_s / 1e12, 1),
+        "prefill_mfma_frac": round(pre_flops / pre_s / PEAK_F16, 4),
+        "engine_init_s": round(init_s, 2),
+    }
+
+    if not a.no_kernel_timing:
+        d, F, V = CFG["hidden_size"], CFG["intermediate_size"], CFG["vocab_size"]
+        nq, nkv = CFG["num_heads"], CFG["num_kv_heads"]
+        hd = d // nq
+        names = ["qkv_rope_append", "attn_decode", "o_proj_resid", "norm_gateup_swiglu", "down_proj_resid",
+                 "lm_head_argmax"]
+        p_att = a.prompt + a.steps
+        bytes_per_launch = [
+            2 * (nq + 2 * nkv) * hd * d + 8 * d + 4 * nq * hd + 2 * 2 * nkv * hd,
+            2 * 2 * nkv * hd * p_att + 8 * nq * hd,
+            2 * d * nq * hd + 4 * nq * hd + 8 * d,
+            2 * 2 * F * d + 8 * d + 4 * F,
+            2 * d * F + 4 * F + 8 * d,
+            2 * V * d + 8 * d + 4 * V,
+        ]
+        ops = {}
+        for op, nm in enumerate(names):
+            ms = eng.time_op(op, 3)
+            ops[nm] = {"avg_us": round(ms * 1e3, 2), "bytes": bytes_per_launch[op],
+                       "gbps": round(bytes_per_launch[op] / (ms * 1e-3) / 1e9, 1)}
+        dom = ops["norm_gateup_swiglu"]
+        achieved = dom["bytes"] / (dom["avg_us"] * 1e-6)
+        out["roofline"] = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                           "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+                           "kernel": "k_gemv_dec<EPI_SWIGLU> (ffn norm + [Wgate;Wup] GEMV + SwiGLU)"}
+        out["decode_ops"] = ops
+
+    if not a.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_baseline(eng, CFG, prompt[:8], a.cpu_seconds)
+        except Exception as ex:  # reported, never fatal to the GPU measurement
+            out["cpu_baseline"] = {"value": None, "unit": "tok/s", "cores": None, "kind": "port",
+                                   "sample": f"failed: {ex}"}
+    eng.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,134 @@
+/*
+ * vsl_engine.h -- C ABI of the MI355X engine (the token loop behind
+ * VulkanSymbioteEngine::generate(), vk_symbiote/src/VulkanSymbioteEngine.cpp:678-765).
+ *
+ * The reference exposes only a C++ class (vk_symbiote/include/vk_symbiote/VulkanSymbioteEngine.h:72-118)
+ * and has no FFI.  These entry points are what a foreign binding of that class needs: open a model
+ * (constructor, :74), generate from token ids (the additive token-id form of generate, :86),
+ * generate from text (:86), config() (:90), run_benchmark (:98), get_vram_stats (:112),
+ * clear_kv_cache / get_kv_cache_memory_usage (:116-117), and GGUFLoader's model-file format
+ * (write_synthetic_gguf produces files the reference's loader layout reads).
+ * All functions return 0 on success and a negative code on failure; vsl_engine_last_error()
+ * gives the message of the calling thread's last failure.
+ */
+#ifndef VSL_ENGINE_H
+#define VSL_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "vsl_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct vsl_engine vsl_engine;
+
+/* ModelConfig (Common.h:56-76) subset that defines a Llama-style decoder */
+typedef struct vsl_model_spec {
+    uint32_t hidden_size, num_layers, num_heads, num_kv_heads, intermediate_size, vocab_size;
+    uint32_t max_position_embeddings;
+    float rope_theta, rms_eps;
+    float init_std;    /* synthetic weights only: N(0, init_std) */
+    uint32_t dtype;    /* VSL_DT_F32 / VSL_DT_F16 for the linear weights */
+    uint32_t head_dim; /* filled by vsl_engine_get_config; ignored on input */
+} vsl_model_spec;
+
+typedef struct vsl_engine_options {
+    int32_t device;
+    uint32_t kv_capacity;    /* 0 = min(context length, 4096) */
+    uint32_t use_graph;      /* 1 = capture each decode step as a hipGraph (default) */
+    uint32_t prefill_chunk;  /* 0 = 2048 */
+    uint32_t attn_splits;    /* 0 = automatic */
+    uint32_t batched_prefill;/* 1 = MFMA prefill for fp16 models (default) */
+} vsl_engine_options;
+
+typedef struct vsl_gen_params {
+    int32_t mode;          /* VSL_SAMPLE_* */
+    float temperature;     /* <= 0 means greedy */
+    uint32_t top_k;        /* VSL_SAMPLE_TOPK_SEEDED: 40 at the reference call site */
+    uint32_t stop_on_eos;  /* stop after sampling 0 or 2 (VulkanSymbioteEngine.cpp:747-749) */
+    uint64_t seed;
+} vsl_gen_params;
+
+typedef struct vsl_gen_stats {
+    uint32_t prompt_tokens, generated_tokens, kv_positions, pad;
+    double prefill_ms, decode_ms;
+} vsl_gen_stats;
+
+void vsl_engine_default_options(vsl_engine_options* o);
+const char* vsl_engine_last_error(void);
+
+int vsl_engine_open(const char* gguf_path, const vsl_engine_options* opt, vsl_engine** out);
+int vsl_engine_open_synthetic(const vsl_model_spec* spec, uint64_t seed, const vsl_engine_options* opt,
+                              vsl_engine** out);
+int vsl_engine_close(vsl_engine* e);
+
+/* Token-id generation.  out_tokens holds max_new entries; out_logits (nullable) holds
+ * max_new * vocab floats: the logits each generated token was sampled from.  *n_out receives the
+ * number of generated tokens. */
+int vsl_engine_generate_ids(vsl_engine* e, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                            const vsl_gen_params* params, uint32_t* out_tokens, float* out_logits, uint32_t* n_out);
+/* generate(prompt, max_tokens, temperature): text in, prompt + decoded tokens out (NUL-terminated) */
+int vsl_engine_generate_text(vsl_engine* e, const char* prompt, uint32_t max_tokens, float temperature, char* out,
+                             uint64_t out_cap, uint64_t* out_len);
+
+/* Split form of generate_ids (prefill timed apart from decode): begin runs the prompt and samples
+ * the first token; decode enqueues up to n decode steps without waiting (*issued receives how many);
+ * finish waits, then copies the generated tokens (max_new entries) and sets *n_out. */
+int vsl_engine_begin(vsl_engine* e, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
+                     const vsl_gen_params* params);
+int vsl_engine_decode(vsl_engine* e, uint32_t n, uint32_t* issued);
+int vsl_engine_sync(vsl_engine* e);
+int vsl_engine_finish(vsl_engine* e, uint32_t* out_tokens, uint32_t* n_out);
+/* Average device time (ms) of one launch of a decode op, HIP events on the engine's stream, every
+ * layer visited per round: 0 qkv+rope+kv-append, 1 attention, 2 o-proj+residual,
+ * 3 ffn-norm+gate/up+swiglu, 4 down-proj+residual, 5 final-norm+lm_head+argmax. */
+int vsl_engine_time_op(vsl_engine* e, int op, uint32_t iterations, double* avg_ms);
+
+int vsl_engine_get_config(vsl_engine* e, vsl_model_spec* out);
+int vsl_engine_last_stats(vsl_engine* e, vsl_gen_stats* out);
+int vsl_engine_vram_stats(vsl_engine* e, vsl_pool_stats* out);
+int vsl_engine_kv_bytes(vsl_engine* e, uint64_t* out);
+int vsl_engine_weight_bytes(vsl_engine* e, uint64_t* out);
+int vsl_engine_clear_kv(vsl_engine* e);
+/* run_benchmark(warmup, tokens, iterations) -> average / min / max decode tok/s */
+int vsl_engine_benchmark(vsl_engine* e, uint32_t warmup, uint32_t tokens, uint32_t iterations, double* avg_tps,
+                         double* min_tps, double* max_tps);
+/* device -> host copy of one resident pack (GGUF tensor name); *dtype_out = VSL_DT_* */
+int vsl_engine_read_tensor(vsl_engine* e, const char* name, void* dst, uint64_t bytes, int* dtype_out);
+
+/* GGUF writer: synthetic Llama-style model with the reference's tensor names.
+ * convention 0 = the reference's tensor-type ids (F32 6, F16 48), 1 = ggml ids (F32 0, F16 1). */
+int vsl_write_synthetic_gguf(const char* path, const vsl_model_spec* spec, uint64_t seed, int convention);
+/* the host synthetic generator (same stream as vsl_fill_normal) */
+int vsl_synthetic_fill_host(void* out, int dtype, uint64_t n, uint64_t seed, const char* name, float mean,
+                            float stddev);
+
+/* GGUFLoader (GGUFLoader.h:265-333): load / get_model_config / get_tensor / read_tensor_data.
+ * vsl_gguf_open returns the reference's codes: -1 open, -2 magic, -3 metadata, -4 tensor info. */
+typedef struct vsl_gguf vsl_gguf;
+int vsl_gguf_open(const char* path, vsl_gguf** out);
+int vsl_gguf_close(vsl_gguf* g);
+int vsl_gguf_info(vsl_gguf* g, uint64_t* tensor_count, uint64_t* metadata_count, uint32_t* version, int* convention,
+                  uint64_t* data_start);
+int vsl_gguf_model_config(vsl_gguf* g, vsl_model_spec* out);
+/* -30 when the tensor does not exist */
+int vsl_gguf_tensor(vsl_gguf* g, const char* name, uint64_t* data_offset, uint64_t* data_size, uint32_t* raw_type,
+                    uint32_t* n_dims, uint64_t dims[4]);
+/* returns the element count, or the reference's read codes (-11 read, -12 type, -20 quantized, -30 missing) */
+int64_t vsl_gguf_read_f32(vsl_gguf* g, const char* name, float* out, uint64_t cap);
+
+/* ConfigManager (ConfigManager.h:133-270): parse CLI args / a TOML file into the singleton and read
+ * the fields the engine uses.  enable_gpu is 0 after --disable-gpu; opening an engine then fails. */
+int vsl_config_load_args(int argc, const char* const* argv);
+int vsl_config_load_file(const char* path);
+int vsl_config_save_file(const char* path);
+int vsl_config_reset(void);
+int vsl_config_get(int* enable_gpu, int* device, uint32_t* kv_capacity, uint64_t* seed, float* vram_budget_gb);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

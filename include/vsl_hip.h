@@ -1,0 +1,228 @@
+/*
+ * vsl_hip.h -- C ABI of the MI355X (gfx950) compute layer for Vulkan-Symbiote-Loader's token loop.
+ *
+ * This library replaces the reference's Vulkan compute column: ShaderRuntime
+ * (vk_symbiote/src/ShaderRuntime.cpp, get_*_pipeline / allocate_descriptor_set /
+ * dispatch_compute :1484-1541), the GLSL shaders under vk_symbiote/shaders/, the per-op VMA
+ * buffers and staging round trips of VulkanSymbioteEngine.cpp (:1637-1745, :2396-2423), and the
+ * GPU mirror of KVCacheManager (:64-194).  Kernels are precompiled gfx950 code objects; there is no
+ * runtime shader compilation.
+ *
+ * Conventions
+ *  - Every function returns int: 0 = OK, negative = error (VSL_E_*).  vsl_last_error() gives text.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the default stream).  Every launch is
+ *    asynchronous on that stream.
+ *  - Device pointers are owned by the caller (normally suballocated from a vsl_arena); kernels do
+ *    not allocate.  Workspaces are explicit arguments.
+ *  - dtype codes: VSL_DT_F32 = 0, VSL_DT_F16 = 1 (IEEE binary16).
+ *  - Linear weights are row-major [out][in] ("GGUF ne0 = input dim"): y[o] = sum_i W[o*K+i] x[i]
+ *    (final_linear.comp:63, feed_forward.comp:45).
+ *  - Decode kernels take a device control block (vsl_ctrl) holding the current position, the
+ *    sampling step and a done flag, so one captured hipGraph serves every decode step.
+ */
+#ifndef VSL_HIP_H
+#define VSL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    VSL_OK = 0,
+    VSL_E_INVALID = -100,     /* bad argument / shape not supported by the kernel */
+    VSL_E_HIP = -101,         /* HIP runtime error */
+    VSL_E_OOM = -102,         /* arena or device allocation failed */
+    VSL_E_UNSUPPORTED = -103, /* dtype / layout not implemented */
+    VSL_E_CAPACITY = -104     /* KV capacity or workspace too small */
+};
+
+enum { VSL_DT_F32 = 0, VSL_DT_F16 = 1 };
+
+/* Sampling modes (VulkanSymbioteEngine::sample_token, VulkanSymbioteEngine.cpp:1540-1553) */
+enum {
+    VSL_SAMPLE_GREEDY = 0,     /* greedy_sampling (:1794-1804): first index of the max            */
+    VSL_SAMPLE_REFERENCE = 1,  /* T>0 through member top_k_sampling (:1806-1855) == argmax          */
+    VSL_SAMPLE_TOPK_SEEDED = 2 /* Utils.cpp:140-172 top-k with a Philox4x32-10 uniform             */
+};
+
+const char* vsl_last_error(void);
+int vsl_device_count(int* n);
+int vsl_set_device(int device);
+int vsl_device_sync(void);
+
+/* ------------------------------------------------------------------------------------------
+ * HBM arena (the FractalMemoryAllocator role, vk_symbiote/include/vk_symbiote/NomadPack.h:59-104)
+ * One hipMalloc; first-fit suballocation with coalescing free list; 256-byte minimum alignment.
+ * ------------------------------------------------------------------------------------------ */
+typedef struct vsl_pool_stats { /* MemoryPoolStats, NomadPack.h:53-57 */
+    uint64_t total_size, used_size, free_size;
+    uint32_t allocation_count;
+    float fragmentation_ratio;
+} vsl_pool_stats;
+
+typedef struct vsl_arena vsl_arena;
+int vsl_arena_create(int device, uint64_t bytes, vsl_arena** out);
+int vsl_arena_destroy(vsl_arena* a);
+int vsl_arena_alloc(vsl_arena* a, uint64_t bytes, uint64_t align, void** dptr);
+int vsl_arena_free(vsl_arena* a, void* dptr);
+int vsl_arena_reset(vsl_arena* a);
+int vsl_arena_stats(const vsl_arena* a, vsl_pool_stats* out);
+void* vsl_arena_base(const vsl_arena* a);
+
+/* ------------------------------------------------------------------------------------------
+ * Packs: pinned-host staging and async upload on a side stream (NomadPack / PackManager role,
+ * NomadPack.h:33-44; the reference uploads per tensor with a blocking staging copy,
+ * VulkanSymbioteEngine.cpp:2051-2107).
+ * ------------------------------------------------------------------------------------------ */
+int vsl_host_pinned_alloc(uint64_t bytes, void** out);
+int vsl_host_pinned_free(void* p);
+int vsl_stream_create(void** stream);
+int vsl_stream_destroy(void* stream);
+int vsl_stream_sync(void* stream);
+int vsl_event_create(void** ev);
+int vsl_event_destroy(void* ev);
+int vsl_event_record(void* ev, void* stream);
+int vsl_event_sync(void* ev);
+int vsl_stream_wait_event(void* stream, void* ev);
+int vsl_event_elapsed_ms(void* start, void* stop, float* ms);
+/* copy `bytes` from host memory (pinned for full speed) to device memory; records `done_event`
+ * (may be NULL) on `stream` after the copy */
+int vsl_pack_upload(void* dst_dev, const void* src_host, uint64_t bytes, void* stream, void* done_event);
+int vsl_copy_d2h(void* dst_host, const void* src_dev, uint64_t bytes, void* stream);
+int vsl_copy_h2d(void* dst_dev, const void* src_host, uint64_t bytes, void* stream);
+int vsl_copy_d2d(void* dst_dev, const void* src_dev, uint64_t bytes, void* stream);
+int vsl_memset_d(void* dst_dev, int value, uint64_t bytes, void* stream);
+
+/* Synthetic weights on the device: Philox4x32-10 keyed by (seed, hash_string(name)) (Utils.cpp:9-16),
+ * Box-Muller in fp64, rounded to the output dtype.  Same stream as the host generator. */
+int vsl_fill_normal(void* dst, int dtype, uint64_t n, uint64_t seed, const char* name, float mean,
+                    float stddev, void* stream);
+int vsl_fill_const(void* dst, int dtype, uint64_t n, float value, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Decode control block (device memory).  One per engine; read by every decode kernel.
+ * ------------------------------------------------------------------------------------------ */
+typedef struct vsl_ctrl {
+    uint32_t pos;         /* position of the token being processed == cached positions before it */
+    uint32_t step;        /* tokens sampled so far in this generation                            */
+    uint32_t done;        /* 1 once max_steps tokens were sampled or EOS was hit (stop_on_eos)    */
+    uint32_t stop_on_eos; /* stop after sampling 0 or 2 (VulkanSymbioteEngine.cpp:747-749)         */
+    uint32_t max_steps;   /* number of tokens to sample                                          */
+    uint32_t token;       /* last sampled token                                                  */
+    uint32_t capacity;    /* KV capacity; decode kernels stop (done=1) rather than overflow      */
+    uint32_t error;       /* nonzero when a kernel refused to run (capacity)                     */
+} vsl_ctrl;
+
+/* sampler parameters (by value) */
+typedef struct vsl_sampler {
+    int32_t mode;        /* VSL_SAMPLE_* ; temperature <= 0 always means greedy (sample_token :1541) */
+    float temperature;
+    uint32_t top_k;      /* 40 at the reference call site (VulkanSymbioteEngine.cpp:1546)         */
+    uint32_t pad;
+    uint64_t seed;
+} vsl_sampler;
+
+/* ------------------------------------------------------------------------------------------
+ * Ops.  Each replaces one reference dispatch (shader) or a fused group of them.
+ * ------------------------------------------------------------------------------------------ */
+
+/* embedding_lookup.comp:29-40: out[t][h] = table[min(ids[t], vocab-1)][h]; out fp32 [n][d] */
+int vsl_embed(const void* table, int dtype, uint32_t vocab, uint32_t d, const uint32_t* ids_dev,
+              uint32_t n, float* out, void* stream);
+
+/* rms_norm.comp:24-34 over `rows` rows: y = x / sqrt(mean(x^2)+eps) * gamma; out fp32 or fp16 */
+int vsl_rmsnorm(const float* x, const float* gamma, uint32_t rows, uint32_t d, float eps, void* out,
+                int out_dtype, void* stream);
+
+/* GEMV / skinny GEMM (the GEMV sweep): Y[N][B] = W[N][K] * X[K][B] (X, Y row-major), fp32
+ * accumulation.  W f16/f32; X, Y f16 or f32; 1 <= B <= 16; K % 8 == 0. */
+int vsl_gemv(const void* W, int wdtype, uint32_t N, uint32_t K, const void* X, int xdtype, uint32_t B,
+             void* Y, int ydtype, void* stream);
+
+/* Fused attention input stage (rms_norm.comp + attention.comp:63-108 QKV/KV-write + RoPE,
+ * fused_matmul_rope.comp:48-81):
+ *   n = RMSNorm(x, gamma); [q;k;v] = Wqkv n with Wqkv = [Wq; Wk; Wv] contiguous rows;
+ *   RoPE (adjacent pairs, cos/sin tables [cap][hd/2]) on q and k at position ctrl->pos;
+ *   q -> q_out (fp32 [n_q*hd]); k, v -> caches [n_kv][cap][hd] (kv_dtype) at ctrl->pos. */
+int vsl_qkv_rope_append(const float* x, const float* gamma, float eps, const void* Wqkv, int wdtype,
+                        uint32_t d, uint32_t n_q, uint32_t n_kv, uint32_t hd, const float* rope_cos,
+                        const float* rope_sin, void* kcache, void* vcache, int kv_dtype, uint32_t cap,
+                        float* q_out, vsl_ctrl* ctrl, void* stream);
+
+/* Flash-decode attention (attention.comp:116-189 semantics: softmax(q.k*scale) over positions
+ * 0..ctrl->pos, GQA kv_head = head*n_kv/n_q): split-KV over `nsplit` chunks with online softmax,
+ * combined in-kernel by the last chunk to finish.  Workspace: part_o [n_q][nsplit][hd] f32,
+ * part_ml [n_q][nsplit][2] f32, counters [n_kv] u32 (zero before first use; left zero). */
+int vsl_attn_decode(const float* q, const void* kcache, const void* vcache, int kv_dtype, uint32_t n_q,
+                    uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* part_o,
+                    float* part_ml, uint32_t* counters, float* out, vsl_ctrl* ctrl, void* stream);
+
+/* y[N] += W[N][K] x[K]  (O projection / FFN down projection with the residual add fused) */
+int vsl_gemv_residual(const void* W, int wdtype, uint32_t N, uint32_t K, const float* x, float* resid,
+                      vsl_ctrl* ctrl, void* stream);
+
+/* feed_forward.comp:21,38-51 fused with the FFN RMSNorm:
+ *   m = RMSNorm(x, gamma); h = silu(Wgate m) * (Wup m), with Wgu = [Wgate; Wup] contiguous rows;
+ *   h fp32 [F] */
+int vsl_norm_swiglu(const float* x, const float* gamma, float eps, const void* Wgu, int wdtype,
+                    uint32_t d, uint32_t F, float* h_out, vsl_ctrl* ctrl, void* stream);
+
+/* Output stage (final norm + final_linear.comp + sample_token) for one position:
+ *   f = RMSNorm(x, gamma) (gamma may be NULL: no final norm); logits = W f (fp32 [V]);
+ *   greedy / reference mode: the argmax is fused into the GEMV; top-k mode runs a second kernel.
+ *   The sampled token is written to tokens[ctrl->step]; then x <- embed[token] (the next step's
+ *   embedding_lookup), ctrl->pos += 1, ctrl->step += 1, and done is set on max_steps / EOS.
+ *   Workspace: ws_val/ws_idx >= vsl_lm_head_ws_blocks() entries, counter (1 u32, zero). */
+int vsl_lm_head_sample(const float* gamma, float eps, const void* W, int wdtype, uint32_t V, uint32_t d,
+                       float* x, const void* embed, int embed_dtype, float* logits, vsl_sampler sampler,
+                       float* ws_val, uint32_t* ws_idx, uint32_t* counter, uint32_t* tokens,
+                       vsl_ctrl* ctrl, void* stream);
+uint32_t vsl_lm_head_ws_blocks(void);
+
+/* Sample one token from fp32 logits already in memory (no bookkeeping): the samplers alone,
+ * exposed for the sampler parity tests.  out: one u32. */
+int vsl_sample_logits(const float* logits, uint32_t V, vsl_sampler sampler, uint64_t step,
+                      uint32_t* out, void* stream);
+
+/* Host-side reset of the control block (device memory) for a new generation. */
+int vsl_ctrl_reset(vsl_ctrl* ctrl, uint32_t pos, uint32_t max_steps, uint32_t stop_on_eos,
+                   uint32_t capacity, void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Prefill (S positions at once): fp16 MFMA GEMMs and flash attention.
+ * ------------------------------------------------------------------------------------------ */
+/* C[M][N] (+)= A[M][K] * B[N][K]^T, fp16 inputs, fp32 accumulate.  epilogue:
+ *   VSL_EPI_STORE_F32 (C f32), VSL_EPI_STORE_F16 (C f16), VSL_EPI_RESID (C f32 +=),
+ *   VSL_EPI_SWIGLU (B = [Wgate; Wup], N = F: C f16 = silu(A Wg^T) * (A Wu^T)). */
+enum { VSL_EPI_STORE_F32 = 0, VSL_EPI_STORE_F16 = 1, VSL_EPI_RESID = 2, VSL_EPI_SWIGLU = 3 };
+int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
+                 void* stream);
+
+/* Q/K/V split of a prefill QKV GEMM output (f32 [S][(n_q+2 n_kv) hd]) with RoPE at positions
+ * pos0..pos0+S-1: q -> q_out f16 [S][n_q][hd], k/v -> caches at pos0+s. */
+int vsl_rope_split_append(const float* qkv, uint32_t S, uint32_t n_q, uint32_t n_kv, uint32_t hd,
+                          uint32_t pos0, const float* rope_cos, const float* rope_sin, void* q_out,
+                          void* kcache, void* vcache, int kv_dtype, uint32_t cap, void* stream);
+
+/* Causal prefill attention for S queries at positions pos0..pos0+S-1 against cache positions
+ * 0..pos0+s: q f16 [S][n_q][hd], caches f16 [n_kv][cap][hd], out f16 [S][n_q*hd]. */
+int vsl_attn_prefill(const void* q, const void* kcache, const void* vcache, uint32_t S, uint32_t pos0,
+                     uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, void* out,
+                     void* stream);
+
+/* ------------------------------------------------------------------------------------------
+ * hipGraph helpers (each decode step is captured once and replayed).
+ * ------------------------------------------------------------------------------------------ */
+typedef struct vsl_graph vsl_graph;
+int vsl_graph_begin(void* stream);
+int vsl_graph_end(void* stream, vsl_graph** out);
+int vsl_graph_launch(vsl_graph* g, void* stream);
+int vsl_graph_destroy(vsl_graph* g);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

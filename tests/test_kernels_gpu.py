@@ -1,0 +1,364 @@
+"""Kernel-level parity on the GPU: every op of include/vsl_hip.h against the oracle on the same
+seeded inputs, called through the C ABI.  Device memory comes from torch (plumbing only)."""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+import vsl_testlib
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    return vsl_testlib.Dev()
+
+
+@pytest.fixture(scope="module")
+def H(vsl):
+    return vsl.hip()
+
+
+def ok(vsl, rc):
+    vsl.check(rc)
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(1e-30, np.max(np.abs(b))))
+
+
+# ------------------------------------------------------------------------------------------
+# GEMV sweep (y = W X, fp16 W, fp32 accumulate)
+# ------------------------------------------------------------------------------------------
+SWEEP = [(4096, 4096), (14336, 4096), (4096, 14336), (32000, 4096)]
+
+
+@pytest.mark.parametrize("N,K", SWEEP)
+@pytest.mark.parametrize("B", [1, 4, 16])
+def test_gemv_sweep(vsl, orc, dev, H, N, K, B):
+    rng = np.random.default_rng(N * 131 + K * 7 + B)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    X = rng.normal(0, 1, (K, B)).astype(np.float16)
+    ref = orc.gemm_nt(W, X.astype(np.float32))
+    dW = dev.put(W)
+    if B == 1:
+        dX = dev.put(X.astype(np.float32))
+        dY = dev.empty((N, 1), np.float32)
+        ok(vsl, H.vsl_gemv(dev.p(dW), vsl.VSL_DT_F16, N, K, dev.p(dX), vsl.VSL_DT_F32, 1, dev.p(dY),
+                           vsl.VSL_DT_F32, None))
+        y = dev.get(dY)
+        assert rel_err(y, ref) < 1e-5
+    else:
+        dX = dev.put(X)
+        dY = dev.empty((N, B), np.float16)
+        ok(vsl, H.vsl_gemv(dev.p(dW), vsl.VSL_DT_F16, N, K, dev.p(dX), vsl.VSL_DT_F16, B, dev.p(dY),
+                           vsl.VSL_DT_F16, None))
+        y = dev.get(dY).astype(np.float32)
+        # fp16 output: within half an fp16 ulp of the fp32-accumulated value, plus accumulation noise
+        assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -11 + 1e-4 * np.max(np.abs(ref)))
+
+
+def test_gemv_rejects_bad_shapes(vsl, dev, H):
+    d = dev.empty((16,), np.float32)
+    assert H.vsl_gemv(dev.p(d), 1, 4, 12, dev.p(d), 0, 1, dev.p(d), 0, None) == -100  # K % 8
+    assert H.vsl_gemv(dev.p(d), 1, 4, 16, dev.p(d), 0, 17, dev.p(d), 0, None) == -100  # B > 16
+    assert H.vsl_gemv(None, 1, 4, 16, dev.p(d), 0, 1, dev.p(d), 0, None) == -100
+
+
+# ------------------------------------------------------------------------------------------
+# decode-step ops
+# ------------------------------------------------------------------------------------------
+def ctrl_buf(vsl, dev, H, pos, max_steps=4, cap=64, stop=0):
+    c = dev.empty((8,), np.int32)
+    ok(vsl, H.vsl_ctrl_reset(dev.p(c), pos, max_steps, stop, cap, None))
+    return c
+
+
+def rope_tables(cap, hd, theta):
+    j = np.arange(hd // 2, dtype=np.float64)
+    f = theta ** (-(2 * j) / hd)
+    a = np.arange(cap, dtype=np.float64)[:, None] * f[None, :]
+    return np.cos(a).astype(np.float32), np.sin(a).astype(np.float32)
+
+
+@pytest.mark.parametrize("wdt,kvdt,d,nq,nkv,hd", [(1, 1, 4096, 32, 8, 128), (1, 1, 2048, 32, 8, 64),
+                                                  (0, 0, 256, 4, 4, 64)])
+def test_qkv_rope_append(vsl, orc, dev, H, wdt, kvdt, d, nq, nkv, hd):
+    rng = np.random.default_rng(d + nq)
+    cap, pos, theta, eps = 64, 37, 500000.0, 1e-5
+    wnp = np.float16 if wdt == 1 else np.float32
+    kvnp = np.float16 if kvdt == 1 else np.float32
+    N = (nq + 2 * nkv) * hd
+    W = rng.normal(0, 0.02, (N, d)).astype(wnp)
+    x = rng.normal(0, 1, d).astype(np.float32)
+    g = rng.normal(1, 0.1, d).astype(np.float32)
+    cs, sn = rope_tables(cap, hd, theta)
+    kc = dev.empty((nkv, cap, hd), kvnp)
+    vc = dev.empty((nkv, cap, hd), kvnp)
+    q = dev.empty((nq * hd,), np.float32)
+    c = ctrl_buf(vsl, dev, H, pos, cap=cap)
+    dcs, dsn = dev.put(cs), dev.put(sn)
+    ok(vsl, H.vsl_qkv_rope_append(dev.p(dev.put(x)), dev.p(dev.put(g)), eps, dev.p(dev.put(W)), wdt, d, nq, nkv, hd,
+                                  dev.p(dcs), dev.p(dsn), dev.p(kc), dev.p(vc), kvdt, cap, dev.p(q), dev.p(c), None))
+    n = orc.rmsnorm(x, g, eps)
+    y = orc.gemm_nt(W, n)[:, 0]
+    qr = orc.rope(y[:nq * hd], nq, hd, pos, theta)
+    kr = orc.rope(y[nq * hd:(nq + nkv) * hd], nkv, hd, pos, theta)
+    vr = y[(nq + nkv) * hd:]
+    tol = 1e-5 if wdt == 0 else 1e-4
+    assert rel_err(dev.get(q), qr) < tol
+    K = dev.get(kc).astype(np.float32)
+    V = dev.get(vc).astype(np.float32)
+    kt = 2.0 ** -10 if kvdt == 1 else tol
+    assert rel_err(K[:, pos].reshape(-1), kr) < kt
+    assert rel_err(V[:, pos].reshape(-1), vr) < kt
+    assert np.all(K[:, :pos] == 0) and np.all(K[:, pos + 1:] == 0)  # only position `pos` is written
+
+
+def test_qkv_capacity_guard(vsl, dev, H):
+    """A position at or beyond the capacity makes the kernels refuse (error flag, done) instead of
+    writing past the cache."""
+    d, nq, nkv, hd, cap = 256, 4, 4, 64, 8
+    c = ctrl_buf(vsl, dev, H, cap, cap=cap)
+    W = dev.empty(((nq + 2 * nkv) * hd, d), np.float32)
+    kc = dev.empty((nkv, cap, hd), np.float32)
+    x = dev.empty((d,), np.float32)
+    t = dev.empty((cap, hd // 2), np.float32)
+    q = dev.empty((nq * hd,), np.float32)
+    ok(vsl, H.vsl_qkv_rope_append(dev.p(x), None, 1e-5, dev.p(W), 0, d, nq, nkv, hd, dev.p(t), dev.p(t), dev.p(kc),
+                                  dev.p(kc), 0, cap, dev.p(q), dev.p(c), None))
+    ctrl = dev.get(c)
+    assert ctrl[2] == 1 and ctrl[7] == 1
+
+
+@pytest.mark.parametrize("kvdt,hd,nq,nkv", [(1, 128, 32, 8), (1, 64, 32, 8), (0, 64, 4, 4), (1, 128, 8, 8)])
+@pytest.mark.parametrize("length", [1, 5, 300, 1025])
+def test_attn_decode(vsl, orc, dev, H, kvdt, hd, nq, nkv, length):
+    rng = np.random.default_rng(length * 3 + hd)
+    cap, nsplit = 2048, 32
+    kvnp = np.float16 if kvdt == 1 else np.float32
+    K = rng.normal(0, 1, (nkv, cap, hd)).astype(kvnp)
+    V = rng.normal(0, 1, (nkv, cap, hd)).astype(kvnp)
+    q = rng.normal(0, 1, nq * hd).astype(np.float32)
+    scale = 1.0 / math.sqrt(hd)
+    po = dev.empty((nq * nsplit * hd,), np.float32)
+    pml = dev.empty((nq * nsplit * 2,), np.float32)
+    cnt = dev.empty((nkv,), np.int32)
+    out = dev.empty((nq * hd,), np.float32)
+    c = ctrl_buf(vsl, dev, H, length - 1, cap=cap)
+    ok(vsl, H.vsl_attn_decode(dev.p(dev.put(q)), dev.p(dev.put(K)), dev.p(dev.put(V)), kvdt, nq, nkv, hd, cap, scale,
+                              nsplit, dev.p(po), dev.p(pml), dev.p(cnt), dev.p(out), dev.p(c), None))
+    ref = orc.attention_decode(q, K.astype(np.float32), V.astype(np.float32), nq, nkv, hd, cap, length, scale)
+    assert rel_err(dev.get(out), ref) < 2e-5
+    assert np.all(dev.get(cnt) == 0)  # the combining block leaves the counters at zero
+
+
+def test_gemv_residual_and_swiglu(vsl, orc, dev, H):
+    rng = np.random.default_rng(9)
+    d, F = 4096, 14336
+    Wd = rng.normal(0, 0.02, (d, F)).astype(np.float16)
+    h = rng.normal(0, 1, F).astype(np.float32)
+    r = rng.normal(0, 1, d).astype(np.float32)
+    dr = dev.put(r)
+    ok(vsl, H.vsl_gemv_residual(dev.p(dev.put(Wd)), 1, d, F, dev.p(dev.put(h)), dev.p(dr), None, None))
+    assert rel_err(dev.get(dr), r + orc.gemm_nt(Wd, h)[:, 0]) < 1e-5
+    Wgu = rng.normal(0, 0.02, (2 * F, d)).astype(np.float16)
+    x = rng.normal(0, 1, d).astype(np.float32)
+    gm = rng.normal(1, 0.1, d).astype(np.float32)
+    dh = dev.empty((F,), np.float32)
+    ok(vsl, H.vsl_norm_swiglu(dev.p(dev.put(x)), dev.p(dev.put(gm)), 1e-5, dev.p(dev.put(Wgu)), 1, d, F, dev.p(dh),
+                              None, None))
+    m = orc.rmsnorm(x, gm, 1e-5)
+    gu = orc.gemm_nt(Wgu, m)[:, 0]
+    assert rel_err(dev.get(dh), orc.swiglu(gu[:F], gu[F:])) < 1e-4
+
+
+def test_lm_head_greedy_and_bookkeeping(vsl, orc, dev, H):
+    rng = np.random.default_rng(12)
+    V, d = 32000, 4096
+    W = rng.normal(0, 0.02, (V, d)).astype(np.float16)
+    E = rng.normal(0, 0.02, (V, d)).astype(np.float16)
+    x = rng.normal(0, 1, d).astype(np.float32)
+    g = np.ones(d, np.float32)
+    nb = H.vsl_lm_head_ws_blocks()
+    ws_v, ws_i, cnt = dev.empty((nb,), np.float32), dev.empty((nb,), np.int32), dev.empty((1,), np.int32)
+    toks = dev.empty((8,), np.int32)
+    logits = dev.empty((V,), np.float32)
+    dx = dev.put(x)
+    c = ctrl_buf(vsl, dev, H, 10, max_steps=2, cap=64)
+    s = vsl.Sampler(0, 0.0, 40, 0, 0)
+    ok(vsl, H.vsl_lm_head_sample(dev.p(dev.put(g)), 1e-5, dev.p(dev.put(W)), 1, V, d, dev.p(dx), dev.p(dev.put(E)), 1,
+                                 dev.p(logits), s, dev.p(ws_v), dev.p(ws_i), dev.p(cnt), dev.p(toks), dev.p(c), None))
+    ref = orc.gemm_nt(W, orc.rmsnorm(x, g, 1e-5))[:, 0]
+    lg = dev.get(logits)
+    assert rel_err(lg, ref) < 1e-5
+    t = int(dev.get(toks)[0])
+    assert t == int(np.argmax(lg))
+    srt = np.sort(ref)
+    if srt[-1] - srt[-2] > 1e-3:
+        assert t == int(np.argmax(ref))
+    ctrl = dev.get(c)
+    assert (ctrl[0], ctrl[1], ctrl[2], ctrl[5]) == (11, 1, 0, t)
+    assert np.array_equal(dev.get(dx), E[t].astype(np.float32))  # next step's embedding row
+    assert dev.get(cnt)[0] == 0
+
+
+def test_sample_logits_greedy_ties_and_topk(vsl, orc, dev, H):
+    out = dev.empty((1,), np.int32)
+    lg = np.zeros(32000, np.float32)
+    lg[[77, 5000, 31999]] = 3.0
+    ok(vsl, H.vsl_sample_logits(dev.p(dev.put(lg)), 32000, vsl.Sampler(0, 0.0, 40, 0, 0), 0, dev.p(out), None))
+    assert dev.get(out)[0] == 77
+    rng = np.random.default_rng(13)
+    l = rng.normal(0, 1.3, 32000).astype(np.float32)
+    dl = dev.put(l)
+    for step in range(64):
+        ok(vsl, H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 0.7, 40, 0, 99), step, dev.p(out), None))
+        assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_TOPK_SEEDED, 0.7, 40, 99, step)
+
+
+# ------------------------------------------------------------------------------------------
+# prefill ops
+# ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K", [(1, 128, 32), (77, 256, 4096), (512, 6144, 4096), (200, 4096, 14336)])
+@pytest.mark.parametrize("epi", [0, 1, 2])
+def test_gemm_f16(vsl, dev, H, M, N, K, epi):
+    rng = np.random.default_rng(M + N + K + epi)
+    A = rng.normal(0, 1, (M, K)).astype(np.float16)
+    B = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    if epi == 1:
+        C = dev.empty((M, N), np.float16)
+    else:
+        C0 = rng.normal(0, 1, (M, N)).astype(np.float32) if epi == 2 else np.zeros((M, N), np.float32)
+        C = dev.put(C0)
+        ref = ref + C0
+    ok(vsl, H.vsl_gemm_f16(dev.p(dev.put(A)), dev.p(dev.put(B)), M, N, K, dev.p(C), epi, None))
+    y = dev.get(C).astype(np.float64)
+    tol = 2.0 ** -10 if epi == 1 else 1e-5
+    assert rel_err(y, ref) < tol
+
+
+def test_gemm_f16_swiglu(vsl, orc, dev, H):
+    rng = np.random.default_rng(21)
+    M, F, K = 130, 512, 2048
+    A = rng.normal(0, 1, (M, K)).astype(np.float16)
+    B = rng.normal(0, 0.02, (2 * F, K)).astype(np.float16)
+    C = dev.empty((M, F), np.float16)
+    ok(vsl, H.vsl_gemm_f16(dev.p(dev.put(A)), dev.p(dev.put(B)), M, F, K, dev.p(C), 3, None))
+    gu = A.astype(np.float64) @ B.astype(np.float64).T
+    ref = orc.swiglu(gu[:, :F].astype(np.float32).ravel(), gu[:, F:].astype(np.float32).ravel()).reshape(M, F)
+    assert rel_err(dev.get(C).astype(np.float32), ref) < 2.0 ** -9
+
+
+@pytest.mark.parametrize("hd,nq,nkv,S,pos0", [(128, 32, 8, 77, 0), (128, 32, 8, 64, 100), (64, 32, 8, 200, 0),
+                                              (64, 8, 8, 33, 5)])
+def test_rope_split_and_attn_prefill(vsl, orc, dev, H, hd, nq, nkv, S, pos0):
+    rng = np.random.default_rng(hd + S + pos0)
+    cap, theta = 512, 10000.0
+    W = (nq + 2 * nkv) * hd
+    qkv = rng.normal(0, 1, (S, W)).astype(np.float32)
+    cs, sn = rope_tables(cap, hd, theta)
+    K0 = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16)
+    V0 = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16)
+    kc, vc = dev.put(K0), dev.put(V0)
+    q = dev.empty((S, nq * hd), np.float16)
+    ok(vsl, H.vsl_rope_split_append(dev.p(dev.put(qkv)), S, nq, nkv, hd, pos0, dev.p(dev.put(cs)), dev.p(dev.put(sn)),
+                                    dev.p(q), dev.p(kc), dev.p(vc), 1, cap, None))
+    K = dev.get(kc).astype(np.float32)
+    V = dev.get(vc).astype(np.float32)
+    Q = dev.get(q).astype(np.float32)
+    for s in (0, S // 2, S - 1):
+        pos = pos0 + s
+        qr = orc.rope(qkv[s, :nq * hd], nq, hd, pos, theta)
+        kr = orc.rope(qkv[s, nq * hd:(nq + nkv) * hd], nkv, hd, pos, theta)
+        assert rel_err(Q[s], qr) < 2.0 ** -10
+        assert rel_err(K[:, pos].reshape(-1), kr) < 2.0 ** -10
+        assert rel_err(V[:, pos].reshape(-1), qkv[s, (nq + nkv) * hd:]) < 2.0 ** -10
+    assert np.array_equal(K[:, :pos0], K0[:, :pos0].astype(np.float32))
+    out = dev.empty((S, nq * hd), np.float16)
+    scale = 1.0 / math.sqrt(hd)
+    ok(vsl, H.vsl_attn_prefill(dev.p(q), dev.p(kc), dev.p(vc), S, pos0, nq, nkv, hd, cap, scale, dev.p(out), None))
+    O = dev.get(out).astype(np.float32)
+    for s in range(0, S, max(1, S // 9)):
+        ref = orc.attention_decode(Q[s], K, V, nq, nkv, hd, cap, pos0 + s + 1, scale)
+        # P is rounded to fp16 before the PV product and the output is fp16
+        assert rel_err(O[s], ref) < 4e-3
+
+
+# ------------------------------------------------------------------------------------------
+# runtime: synthetic fill, arena, graphs
+# ------------------------------------------------------------------------------------------
+def test_fill_normal_matches_host_generator(vsl, orc, dev, H):
+    n = 1000003
+    d16 = dev.empty((n,), np.float16)
+    ok(vsl, H.vsl_fill_normal(dev.p(d16), 1, n, 3, b"blk.0.attn_q.weight", 0.0, 0.02, None))
+    ref16 = orc.fill_normal(n, orc.F16, 3, "blk.0.attn_q.weight")
+    assert np.array_equal(dev.get(d16).view(np.uint16), ref16.view(np.uint16))
+    d32 = dev.empty((n,), np.float32)
+    ok(vsl, H.vsl_fill_normal(dev.p(d32), 0, n, 3, b"x", 0.0, 1.0, None))
+    ref32 = orc.fill_normal(n, orc.F32, 3, "x", 0.0, 1.0)
+    g = dev.get(d32)
+    # fp64 log/sin/cos may differ in the last bit between libraries; after rounding to fp32 that
+    # shows up in at most a few elements, by one fp32 ulp
+    diff = g.view(np.uint32).astype(np.int64) - ref32.view(np.uint32).astype(np.int64)
+    assert np.count_nonzero(diff) <= 8 and np.max(np.abs(diff)) <= 1
+
+
+def test_arena_suballocation(vsl, H):
+    a = ctypes.c_void_p()
+    ok(vsl, H.vsl_arena_create(0, 1 << 24, ctypes.byref(a)))
+    try:
+        ptrs = []
+        for sz in (1000, 1 << 20, 256, 5 << 20):
+            p = ctypes.c_void_p()
+            ok(vsl, H.vsl_arena_alloc(a, sz, 256, ctypes.byref(p)))
+            assert p.value % 256 == 0
+            ptrs.append(p)
+        st = vsl.PoolStats()
+        ok(vsl, H.vsl_arena_stats(a, ctypes.byref(st)))
+        assert st.allocation_count == 4 and st.used_size == 1024 + (1 << 20) + 256 + (5 << 20)
+        ok(vsl, H.vsl_arena_free(a, ptrs[1]))
+        ok(vsl, H.vsl_arena_free(a, ptrs[2]))
+        p = ctypes.c_void_p()
+        ok(vsl, H.vsl_arena_alloc(a, (1 << 20) + 256, 256, ctypes.byref(p)))
+        assert p.value == ptrs[1].value  # coalesced hole reused first-fit
+        big = ctypes.c_void_p()
+        assert H.vsl_arena_alloc(a, 1 << 25, 256, ctypes.byref(big)) == -102
+        ok(vsl, H.vsl_arena_reset(a))
+        ok(vsl, H.vsl_arena_stats(a, ctypes.byref(st)))
+        assert st.used_size == 0 and st.allocation_count == 0
+    finally:
+        H.vsl_arena_destroy(a)
+
+
+def test_graph_replay_matches_eager(vsl, orc, dev, H):
+    """A captured residual GEMV replayed several times, with eager work and syncs in between."""
+    rng = np.random.default_rng(30)
+    d, K = 1024, 2048
+    W = dev.put(rng.normal(0, 0.02, (d, K)).astype(np.float16))
+    x = dev.put(rng.normal(0, 1, K).astype(np.float32))
+    r0 = rng.normal(0, 1, d).astype(np.float32)
+    r = dev.put(r0)
+    st = ctypes.c_void_p()
+    ok(vsl, H.vsl_stream_create(ctypes.byref(st)))
+    g = ctypes.c_void_p()
+    ok(vsl, H.vsl_graph_begin(st))
+    ok(vsl, H.vsl_gemv_residual(dev.p(W), 1, d, K, dev.p(x), dev.p(r), None, st))
+    ok(vsl, H.vsl_graph_end(st, ctypes.byref(g)))
+    dev.sync()
+    assert np.array_equal(dev.get(r), r0)  # capture does not execute
+    eager = dev.empty((d,), np.float32)
+    inc = orc.gemm_nt(dev.get(W), dev.get(x))[:, 0]
+    for i in range(1, 4):
+        ok(vsl, H.vsl_graph_launch(g, st))
+        ok(vsl, H.vsl_stream_sync(st))
+        ok(vsl, H.vsl_gemv_residual(dev.p(W), 1, d, K, dev.p(x), dev.p(eager), None, None))
+        dev.sync()
+        assert rel_err(dev.get(r), r0 + i * inc) < 1e-5
+    ok(vsl, H.vsl_graph_destroy(g))
+    ok(vsl, H.vsl_stream_destroy(st))

@@ -1,0 +1,102 @@
+// vsl_device.h -- device-side helpers shared by the gfx950 kernels (wave64, CDNA4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define VSL_WAVE 64
+
+typedef _Float16 vsl_half;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+// Weight / cache element types used as template parameters.
+struct WF16 { typedef vsl_half T; static constexpr int kVec = 8; };   // 16-byte vector = 8 halfs
+struct WF32 { typedef float T; static constexpr int kVec = 4; };      // 16-byte vector = 4 floats
+
+__device__ __forceinline__ float to_f32(vsl_half h) { return (float)h; }
+__device__ __forceinline__ float to_f32(float f) { return f; }
+__device__ __forceinline__ void store_elem(vsl_half* p, float v) { *p = (vsl_half)v; }
+__device__ __forceinline__ void store_elem(float* p, float v) { *p = v; }
+
+// 16-byte global load, returned as 4 dwords.  nt=true marks the access streaming (non-temporal),
+// used for weights that are read exactly once per token.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ uint4 load16(const void* p) {
+    u32x4 v;
+    if constexpr (NT)
+        v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    else
+        v = *reinterpret_cast<const u32x4*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Unpack a 16-byte vector of weights into fp32 values.
+__device__ __forceinline__ void unpack(const uint4& v, WF16, float* out) {
+    const half8 h = __builtin_bit_cast(half8, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = (float)h[i];
+}
+__device__ __forceinline__ void unpack(const uint4& v, WF32, float* out) {
+    out[0] = __builtin_bit_cast(float, v.x);
+    out[1] = __builtin_bit_cast(float, v.y);
+    out[2] = __builtin_bit_cast(float, v.z);
+    out[3] = __builtin_bit_cast(float, v.w);
+}
+
+// Butterfly sum across the full wave (every lane ends with the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, VSL_WAVE);
+    return v;
+}
+
+// Sum across aligned groups of `W` lanes (W a power of two <= 64).
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int o = W / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, VSL_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, VSL_WAVE));
+    return v;
+}
+
+// (value, index) argmax with the reference's tie rule: larger value wins, equal values keep the
+// lower index (greedy_sampling scans upward with a strict '>').
+__device__ __forceinline__ void argmax_merge(float& v, uint32_t& i, float ov, uint32_t oi) {
+    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+
+__device__ __forceinline__ void wave_argmax(float& v, uint32_t& i) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        float ov = __shfl_xor(v, o, VSL_WAVE);
+        uint32_t oi = __shfl_xor(i, o, VSL_WAVE);
+        argmax_merge(v, i, ov, oi);
+    }
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// Philox4x32-10 (Salmon et al., SC'11), identical to the host implementation.
+__device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        uint64_t p0 = (uint64_t)0xD2511F53u * c[0];
+        uint64_t p1 = (uint64_t)0xCD9E8D57u * c[2];
+        uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+        uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+        uint32_t n0 = hi1 ^ c[1] ^ k0;
+        uint32_t n2 = hi0 ^ c[3] ^ k1;
+        c[0] = n0; c[1] = lo1; c[2] = n2; c[3] = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+}

@@ -1,0 +1,506 @@
+// GGUFLoader.cpp -- memory-mapped GGUF reader and a v3 writer.
+// Layout and metadata semantics follow the reference's GGUFLoaderImpl
+// (vk_symbiote/src/GGUFLoader.cpp:625-663 load, :847-980 metadata / tensor infos / read_value,
+// :673-728 get_model_config, :730-751 generate_packs, :1085-1119 sizes, :1225-1262 fp16).
+#include "GGUFLoader.h"
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <future>
+#include <thread>
+
+#include "vsl_hip.h"
+
+namespace vk_symbiote {
+
+// ------------------------------------------------------------------------------------------
+// metadata accessors (GGUFLoader.cpp:32-66): a value of another type reads as 0 / "" / false
+// ------------------------------------------------------------------------------------------
+std::string GGUFMetadataKV::get_string() const {
+    if (value_type != GGUFValueType::STRING || raw_value.size() < 8) return "";
+    uint64_t len;
+    std::memcpy(&len, raw_value.data(), 8);
+    if (len > raw_value.size() - 8) return "";
+    return std::string(reinterpret_cast<const char*>(raw_value.data() + 8), len);
+}
+uint32_t GGUFMetadataKV::get_uint32() const {
+    if (value_type != GGUFValueType::UINT32 || raw_value.size() < 4) return 0;
+    uint32_t v;
+    std::memcpy(&v, raw_value.data(), 4);
+    return v;
+}
+int32_t GGUFMetadataKV::get_int32() const {
+    if (value_type != GGUFValueType::INT32 || raw_value.size() < 4) return 0;
+    int32_t v;
+    std::memcpy(&v, raw_value.data(), 4);
+    return v;
+}
+float GGUFMetadataKV::get_float32() const {
+    if (value_type != GGUFValueType::FLOAT32 || raw_value.size() < 4) return 0.0f;
+    float v;
+    std::memcpy(&v, raw_value.data(), 4);
+    return v;
+}
+bool GGUFMetadataKV::get_bool() const {
+    if (value_type != GGUFValueType::BOOL || raw_value.empty()) return false;
+    return raw_value[0] != 0;
+}
+std::vector<uint8_t> GGUFMetadataKV::get_array_data() const {
+    if (value_type != GGUFValueType::ARRAY || raw_value.size() < 12) return {};
+    return raw_value;
+}
+
+// ------------------------------------------------------------------------------------------
+// parsing
+// ------------------------------------------------------------------------------------------
+namespace {
+
+struct Cursor {
+    const uint8_t* p;
+    const uint8_t* end;
+    bool take(void* dst, size_t n) {
+        if (static_cast<size_t>(end - p) < n) return false;
+        if (dst) std::memcpy(dst, p, n);
+        p += n;
+        return true;
+    }
+};
+
+// read_value (GGUFLoader.cpp:913-980): raw_value holds scalars as bytes, strings as
+// (u64 len, bytes), arrays as (u32 elem type, u64 count, elements...)
+bool read_value(Cursor& c, uint32_t type, std::vector<uint8_t>& out, int depth) {
+    if (depth > 4) return false;
+    auto take_n = [&](size_t n) {
+        size_t o = out.size();
+        out.resize(o + n);
+        return c.take(out.data() + o, n);
+    };
+    switch (type) {
+        case 0: case 1: case 7: return take_n(1);
+        case 2: case 3: return take_n(2);
+        case 4: case 5: case 6: return take_n(4);
+        case 10: case 11: case 12: return take_n(8);
+        case 8: {
+            uint64_t len;
+            if (!c.take(&len, 8) || len > static_cast<uint64_t>(c.end - c.p)) return false;
+            size_t o = out.size();
+            out.resize(o + 8);
+            std::memcpy(out.data() + o, &len, 8);
+            return take_n(len);
+        }
+        case 9: {
+            uint32_t et;
+            uint64_t cnt;
+            if (!c.take(&et, 4) || !c.take(&cnt, 8)) return false;
+            size_t o = out.size();
+            out.resize(o + 12);
+            std::memcpy(out.data() + o, &et, 4);
+            std::memcpy(out.data() + o + 4, &cnt, 8);
+            for (uint64_t i = 0; i < cnt; ++i)
+                if (!read_value(c, et, out, depth + 1)) return false;
+            return true;
+        }
+        default: return false;
+    }
+}
+
+uint64_t reference_type_size(uint32_t t, uint64_t n) {  // calculate_tensor_data_size :1085-1119
+    switch (t) {
+        case 0: case 1: return n;
+        case 2: case 3: case 47: case 48: return n * 2;
+        case 4: case 5: case 6: return n * 4;
+        case 10: case 11: case 12: return n * 8;
+        case 13: return (n / 32) * 18 + ((n % 32) ? 18 : 0);
+        case 14: return (n / 32) * 20 + ((n % 32) ? 20 : 0);
+        case 15: return (n / 32) * 22 + ((n % 32) ? 22 : 0);
+        case 16: return (n / 32) * 24 + ((n % 32) ? 24 : 0);
+        case 17: return (n / 32) * 34 + ((n % 32) ? 34 : 0);
+        default: return n * 4;
+    }
+}
+
+uint64_t ggml_type_size(uint32_t t, uint64_t n) {
+    switch (t) {
+        case 0: return n * 4;
+        case 1: return n * 2;
+        case 2: return (n / 32) * 18;
+        case 3: return (n / 32) * 20;
+        case 8: return (n / 32) * 34;
+        case 30: return n * 2;
+        default: return 0;
+    }
+}
+
+float half_to_float(uint16_t h) {
+    uint32_t sign = static_cast<uint32_t>(h >> 15) << 31, e = (h >> 10) & 0x1F, m = h & 0x3FF, bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            float v = static_cast<float>(m) * 5.9604644775390625e-08f;
+            std::memcpy(&bits, &v, 4);
+            bits |= sign;
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+}  // namespace
+
+GGUFLoader::GGUFLoader(const Path& file_path) : file_path_(file_path) {}
+GGUFLoader::~GGUFLoader() { close(); }
+
+uint64 GGUFLoader::align_offset(uint64 offset, uint64 alignment) {
+    if (alignment == 0) return offset;
+    return (offset + alignment - 1) / alignment * alignment;
+}
+
+ExpectedVoid GGUFLoader::close() {
+    if (map_) munmap(const_cast<uint8_t*>(map_), size_);
+    if (fd_ >= 0) ::close(fd_);
+    map_ = nullptr;
+    fd_ = -1;
+    size_ = 0;
+    loaded_ = false;
+    metadata_.clear();
+    metadata_order_.clear();
+    tensors_.clear();
+    tensor_order_.clear();
+    {
+        std::lock_guard<std::mutex> lk(cache_mu_);
+        cache_.clear();
+    }
+    return ExpectedVoid();
+}
+
+ExpectedVoid GGUFLoader::load() {
+    close();
+    fd_ = ::open(file_path_.c_str(), O_RDONLY);
+    if (fd_ < 0) return kErrOpen;
+    struct stat st;
+    if (fstat(fd_, &st) != 0) { close(); return kErrOpen; }
+    size_ = static_cast<size_t>(st.st_size);
+    if (size_ < sizeof(GGUFHeader)) { close(); return kErrMagic; }
+    void* m = mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd_, 0);
+    if (m == MAP_FAILED) { close(); return kErrOpen; }
+    map_ = static_cast<const uint8_t*>(m);
+    Cursor c{map_, map_ + size_};
+    c.take(&header_.magic, 4);
+    if (header_.magic != 0x46554747u) { close(); return kErrMagic; }
+    c.take(&header_.version, 4);
+    c.take(&header_.tensor_count, 8);
+    c.take(&header_.metadata_kv_count, 8);
+    if (header_.metadata_kv_count > size_ / 12 || header_.tensor_count > size_ / 24) { close(); return kErrMetadata; }
+    for (uint64_t i = 0; i < header_.metadata_kv_count; ++i) {  // parse_metadata :847-874
+        uint64_t klen;
+        if (!c.take(&klen, 8) || klen > static_cast<uint64_t>(c.end - c.p)) { close(); return kErrMetadata; }
+        GGUFMetadataKV kv;
+        kv.key.assign(reinterpret_cast<const char*>(c.p), klen);
+        c.p += klen;
+        uint32_t vt;
+        if (!c.take(&vt, 4)) { close(); return kErrMetadata; }
+        kv.value_type = static_cast<GGUFValueType>(vt);
+        if (!read_value(c, vt, kv.raw_value, 0)) { close(); return kErrMetadata; }
+        if (!metadata_.count(kv.key)) metadata_order_.push_back(kv.key);
+        metadata_[kv.key] = std::move(kv);
+    }
+    for (uint64_t i = 0; i < header_.tensor_count; ++i) {  // parse_tensor_info :876-911
+        GGUFTensorInfo info;
+        uint64_t nlen;
+        if (!c.take(&nlen, 8) || nlen > static_cast<uint64_t>(c.end - c.p)) { close(); return kErrTensorInfo; }
+        info.name.assign(reinterpret_cast<const char*>(c.p), nlen);
+        c.p += nlen;
+        if (!c.take(&info.n_dimensions, 4) || info.n_dimensions > 8) { close(); return kErrTensorInfo; }
+        info.dimensions.resize(info.n_dimensions);
+        for (uint32_t d = 0; d < info.n_dimensions; ++d)
+            if (!c.take(&info.dimensions[d], 8)) { close(); return kErrTensorInfo; }
+        uint32_t dt;
+        if (!c.take(&dt, 4) || !c.take(&info.offset, 8)) { close(); return kErrTensorInfo; }
+        info.data_type = static_cast<GGUFValueType>(dt);
+        if (!tensors_.count(info.name)) tensor_order_.push_back(info.name);
+        tensors_[info.name] = std::move(info);
+    }
+    const uint64_t after_infos = static_cast<uint64_t>(c.p - map_);
+
+    convention_ = GGUFConvention::REFERENCE;
+    if (auto* kv = get_metadata("vsl.tensor_type_convention")) {
+        convention_ = kv->get_string() == "ggml" ? GGUFConvention::GGML : GGUFConvention::REFERENCE;
+    } else if (get_metadata("general.alignment")) {
+        convention_ = GGUFConvention::GGML;
+    } else {
+        bool has_ggml = false, has_ref = false;
+        for (auto& kv : tensors_) {
+            uint32_t t = static_cast<uint32_t>(kv.second.data_type);
+            if (t == 0 || t == 1 || t == 2 || t == 3 || t == 8) has_ggml = true;
+            if (t == 48) has_ref = true;
+        }
+        convention_ = (has_ggml && !has_ref) ? GGUFConvention::GGML : GGUFConvention::REFERENCE;
+    }
+    if (convention_ == GGUFConvention::REFERENCE) {
+        data_start_ = after_infos;  // GGUFLoader.cpp:653
+    } else {
+        uint64_t align = 32;
+        if (auto* kv = get_metadata("general.alignment"))
+            if (kv->get_uint32()) align = kv->get_uint32();
+        data_start_ = align_offset(after_infos, align);
+    }
+    for (auto& kv : tensors_) {
+        GGUFTensorInfo& t = kv.second;
+        uint64_t n = 1;
+        for (auto d : t.dimensions) n *= d;
+        t.data_offset = data_start_ + t.offset;
+        t.data_size = convention_ == GGUFConvention::REFERENCE ? reference_type_size(static_cast<uint32_t>(t.data_type), n)
+                                                               : ggml_type_size(static_cast<uint32_t>(t.data_type), n);
+    }
+    loaded_ = true;
+    return ExpectedVoid();
+}
+
+ModelConfig GGUFLoader::get_model_config() const {  // GGUFLoader.cpp:673-728
+    ModelConfig c;
+    if (auto* kv = get_metadata("llama.embedding_length")) c.hidden_size = kv->get_uint32();
+    else if (auto* kv2 = get_metadata("general.embedding_length")) c.hidden_size = kv2->get_uint32();
+    if (auto* kv = get_metadata("llama.block_count")) c.num_layers = kv->get_uint32();
+    else if (auto* kv2 = get_metadata("general.block_count")) c.num_layers = kv2->get_uint32();
+    if (auto* kv = get_metadata("llama.attention.head_count")) c.num_attention_heads = kv->get_uint32();
+    if (auto* kv = get_metadata("llama.attention.head_count_kv")) c.num_key_value_heads = kv->get_uint32();
+    else c.num_key_value_heads = c.num_attention_heads;
+    if (auto* kv = get_metadata("llama.feed_forward_length")) c.intermediate_size = kv->get_uint32();
+    if (auto* kv = get_metadata("llama.vocab_size")) {
+        c.vocab_size = kv->get_uint32();
+    } else if (auto* kv2 = get_metadata("tokenizer.ggml.tokens")) {
+        auto arr = kv2->get_array_data();
+        if (arr.size() >= 12) {
+            uint64_t cnt;
+            std::memcpy(&cnt, arr.data() + 4, 8);
+            c.vocab_size = static_cast<uint32_t>(cnt);
+        }
+    }
+    if (auto* kv = get_metadata("llama.rope.freq_base")) c.rope_theta = kv->get_float32();
+    if (auto* kv = get_metadata("llama.context_length")) c.max_position_embeddings = kv->get_uint32();
+    if (auto* kv = get_metadata("general.architecture")) c.model_type = kv->get_string();
+    if (auto* kv = get_metadata("llama.attention.layer_norm_rms_epsilon"))
+        if (kv->value_type == GGUFValueType::FLOAT32) c.rms_epsilon = kv->get_float32();
+    c.head_dim = c.num_attention_heads ? c.hidden_size / c.num_attention_heads : 0;
+    if (const GGUFTensorInfo* q = get_tensor("blk.0.attn_q.weight")) c.use_fp16 = storage_dtype(*q) == VSL_DT_F16;
+    return c;
+}
+
+std::vector<PackMetadata> GGUFLoader::generate_packs(const ModelConfig&) {  // GGUFLoader.cpp:730-751
+    std::vector<PackMetadata> packs;
+    packs.reserve(tensors_.size());
+    for (const auto& name : tensor_order_) {
+        const GGUFTensorInfo& info = tensors_.at(name);
+        PackMetadata p;
+        p.pack_id = std::hash<std::string>{}(name);
+        p.tensor_name = name;
+        p.layer_idx = extract_layer_index(name);
+        p.head_idx = 0;
+        p.compressed_size = info.data_size;
+        p.decompressed_size = info.data_size;
+        p.file_offset = info.data_offset;
+        p.base_priority = calculate_pack_priority(name);
+        p.type = classify_tensor_type(name);
+        p.alignment = 256;
+        p.n_dimensions = info.n_dimensions;
+        p.dimensions = info.dimensions;
+        packs.push_back(std::move(p));
+    }
+    return packs;
+}
+
+uint64 GGUFLoader::tensor_count() const { return header_.tensor_count; }
+uint64 GGUFLoader::metadata_count() const { return header_.metadata_kv_count; }
+
+const GGUFTensorInfo* GGUFLoader::get_tensor(const std::string& name) const {
+    auto it = tensors_.find(name);
+    return it == tensors_.end() ? nullptr : &it->second;
+}
+
+int GGUFLoader::storage_dtype(const GGUFTensorInfo& t) const {
+    const uint32_t id = static_cast<uint32_t>(t.data_type);
+    if (convention_ == GGUFConvention::REFERENCE) {
+        if (id == 6) return VSL_DT_F32;
+        if (id == 48) return VSL_DT_F16;
+        return -1;
+    }
+    if (id == 0) return VSL_DT_F32;
+    if (id == 1) return VSL_DT_F16;
+    return -1;
+}
+
+const uint8_t* GGUFLoader::tensor_bytes(const GGUFTensorInfo& t) const {
+    if (!map_ || t.data_offset + t.data_size > size_ || t.data_offset < data_start_) return nullptr;
+    return map_ + t.data_offset;
+}
+
+Expected<std::vector<float>> GGUFLoader::read_tensor_data(const GGUFTensorInfo& t, bool fp16_to_fp32) {
+    if (!loaded_) return -10;
+    const uint8_t* p = tensor_bytes(t);
+    if (!p) return kErrRead;
+    const int dt = storage_dtype(t);
+    if (dt == VSL_DT_F32) {
+        std::vector<float> r(t.data_size / 4);
+        std::memcpy(r.data(), p, r.size() * 4);
+        return r;
+    }
+    if (dt == VSL_DT_F16 && fp16_to_fp32) {
+        std::vector<float> r(t.data_size / 2);
+        for (size_t i = 0; i < r.size(); ++i) {
+            uint16_t h;
+            std::memcpy(&h, p + 2 * i, 2);
+            r[i] = half_to_float(h);
+        }
+        return r;
+    }
+    const uint32_t id = static_cast<uint32_t>(t.data_type);
+    if (convention_ == GGUFConvention::REFERENCE ? (id >= 13 && id <= 53) : (id >= 2 && id != 30))
+        return kErrUnsupportedQuant;
+    return kErrUnsupportedType;
+}
+
+Expected<std::vector<float>> GGUFLoader::read_tensor_cached(const std::string& name, bool fp16_to_fp32) {
+    {
+        std::lock_guard<std::mutex> lk(cache_mu_);
+        auto it = cache_.find(name);
+        if (it != cache_.end()) return it->second;
+    }
+    const GGUFTensorInfo* t = get_tensor(name);
+    if (!t) return kErrNotFound;
+    auto r = read_tensor_data(*t, fp16_to_fp32);
+    if (r.has_value()) {
+        std::lock_guard<std::mutex> lk(cache_mu_);
+        cache_[name] = r.value();
+    }
+    return r;
+}
+
+std::vector<Expected<std::vector<float>>> GGUFLoader::read_tensors_parallel(const std::vector<std::string>& names,
+                                                                            bool fp16_to_fp32) {
+    std::vector<std::future<Expected<std::vector<float>>>> fs;
+    fs.reserve(names.size());
+    for (const auto& n : names)
+        fs.push_back(std::async(std::launch::async, [this, n, fp16_to_fp32]() -> Expected<std::vector<float>> {
+            const GGUFTensorInfo* t = get_tensor(n);
+            if (!t) return kErrNotFound;
+            return read_tensor_data(*t, fp16_to_fp32);
+        }));
+    std::vector<Expected<std::vector<float>>> out;
+    out.reserve(names.size());
+    for (auto& f : fs) out.push_back(f.get());
+    return out;
+}
+
+std::vector<std::string> GGUFLoader::get_tensor_names() const { return tensor_order_; }
+std::vector<std::string> GGUFLoader::get_metadata_keys() const { return metadata_order_; }
+const GGUFMetadataKV* GGUFLoader::get_metadata(const std::string& key) const {
+    auto it = metadata_.find(key);
+    return it == metadata_.end() ? nullptr : &it->second;
+}
+
+// ------------------------------------------------------------------------------------------
+// writer
+// ------------------------------------------------------------------------------------------
+void GGUFWriter::add_u32(const std::string& key, uint32_t v) {
+    KV kv{key, 4, std::vector<uint8_t>(4)};
+    std::memcpy(kv.bytes.data(), &v, 4);
+    kvs_.push_back(std::move(kv));
+}
+void GGUFWriter::add_f32(const std::string& key, float v) {
+    KV kv{key, 6, std::vector<uint8_t>(4)};
+    std::memcpy(kv.bytes.data(), &v, 4);
+    kvs_.push_back(std::move(kv));
+}
+void GGUFWriter::add_string(const std::string& key, const std::string& v) {
+    KV kv{key, 8, std::vector<uint8_t>(8 + v.size())};
+    uint64_t l = v.size();
+    std::memcpy(kv.bytes.data(), &l, 8);
+    std::memcpy(kv.bytes.data() + 8, v.data(), v.size());
+    kvs_.push_back(std::move(kv));
+}
+void GGUFWriter::add_tensor(const std::string& name, const std::vector<uint64_t>& dims, bool is_f16, const void* data,
+                            uint64_t bytes) {
+    tensors_.push_back(T{name, dims, is_f16, data, bytes});
+}
+
+ExpectedVoid GGUFWriter::write(const Path& path) const {
+    const uint64_t kAlign = 32;
+    std::vector<KV> kvs = kvs_;
+    kvs.push_back(KV{"vsl.tensor_type_convention", 8, {}});
+    {
+        std::string c = conv_ == GGUFConvention::GGML ? "ggml" : "reference";
+        uint64_t l = c.size();
+        kvs.back().bytes.resize(8 + c.size());
+        std::memcpy(kvs.back().bytes.data(), &l, 8);
+        std::memcpy(kvs.back().bytes.data() + 8, c.data(), c.size());
+    }
+    if (conv_ == GGUFConvention::GGML) {
+        KV a{"general.alignment", 4, std::vector<uint8_t>(4)};
+        uint32_t v = static_cast<uint32_t>(kAlign);
+        std::memcpy(a.bytes.data(), &v, 4);
+        kvs.push_back(std::move(a));
+    }
+    // "vsl.pad": a string sized so that the tensor infos end on a 32-byte boundary, making the
+    // reference's data-start rule (no padding) and ggml's (align up) agree.
+    kvs.push_back(KV{"vsl.pad", 8, std::vector<uint8_t>(8)});
+    auto header_bytes = [&]() {
+        uint64_t n = 24;
+        for (auto& kv : kvs) n += 8 + kv.key.size() + 4 + kv.bytes.size();
+        for (auto& t : tensors_) n += 8 + t.name.size() + 4 + 8 * t.dims.size() + 4 + 8;
+        return n;
+    };
+    const uint64_t pad = (kAlign - header_bytes() % kAlign) % kAlign;
+    {
+        KV& p = kvs.back();
+        p.bytes.assign(8 + pad, static_cast<uint8_t>(' '));
+        std::memcpy(p.bytes.data(), &pad, 8);
+    }
+    std::ofstream f(path.string(), std::ios::binary);
+    if (!f) return kErrOpen;
+    auto put = [&](const void* p, size_t n) { f.write(static_cast<const char*>(p), static_cast<std::streamsize>(n)); };
+    uint32_t magic = 0x46554747u, version = 3;
+    uint64_t nt = tensors_.size(), nkv = kvs.size();
+    put(&magic, 4); put(&version, 4); put(&nt, 8); put(&nkv, 8);
+    for (auto& kv : kvs) {
+        uint64_t l = kv.key.size();
+        put(&l, 8); put(kv.key.data(), kv.key.size()); put(&kv.type, 4); put(kv.bytes.data(), kv.bytes.size());
+    }
+    uint64_t off = 0;
+    std::vector<uint64_t> offs;
+    for (auto& t : tensors_) {
+        uint64_t l = t.name.size();
+        put(&l, 8); put(t.name.data(), t.name.size());
+        uint32_t nd = static_cast<uint32_t>(t.dims.size());
+        put(&nd, 4);
+        for (auto d : t.dims) put(&d, 8);
+        uint32_t ty = conv_ == GGUFConvention::GGML ? (t.is_f16 ? 1u : 0u) : (t.is_f16 ? 48u : 6u);
+        put(&ty, 4);
+        put(&off, 8);
+        offs.push_back(off);
+        off = GGUFLoader::align_offset(off + t.bytes, kAlign);
+    }
+    static const char zeros[64] = {0};
+    uint64_t written = 0;
+    for (size_t i = 0; i < tensors_.size(); ++i) {
+        if (offs[i] > written) put(zeros, offs[i] - written);
+        put(tensors_[i].data, tensors_[i].bytes);
+        written = offs[i] + tensors_[i].bytes;
+    }
+    if (!f) return kErrRead;
+    return ExpectedVoid();
+}
+
+}  // namespace vk_symbiote

@@ -1,0 +1,238 @@
+// VulkanSymbioteEngine.h -- the reference's engine API (vk_symbiote/include/vk_symbiote/
+// VulkanSymbioteEngine.h:72-118) on an MI355X HIP backend.
+//
+// Kept: the path constructor, generate / encode / decode, config(), run_benchmark(_detailed),
+// generate_text_batch, get_vram_stats / get_peak_vram_usage, clear_kv_cache /
+// get_kv_cache_memory_usage, get_performance_metrics / reset_performance_metrics.
+// Dropped (Vulkan-typed): the GUI constructor taking Vk handles and device() /
+// physical_device() / compute_queue().
+// Added: a token-id entry point (generate_ids) with explicit sampling parameters and optional
+// logits, engine options, a synthetic-weights constructor, per-generation timings, and
+// read_tensor (device -> host copy of one pack).
+#pragma once
+
+#include <map>
+#include <memory>
+#include <string>
+#include <tuple>
+#include <unordered_map>
+#include <vector>
+
+#include "Common.h"
+#include "GGUFLoader.h"
+#include "NomadPack.h"
+
+struct vsl_arena;
+struct vsl_graph;
+struct vsl_ctrl;
+
+namespace vk_symbiote {
+
+struct BenchmarkResult {
+    uint32_t warmup_tokens = 0;
+    uint32_t benchmark_tokens = 0;
+    uint32_t iterations = 0;
+    double avg_tokens_per_sec = 0.0;
+    double min_tokens_per_sec = 0.0;
+    double max_tokens_per_sec = 0.0;
+    double std_dev_tokens_per_sec = 0.0;
+    double avg_latency_ms = 0.0;
+    double peak_vram_gb = 0.0;
+    double cache_hit_rate = 0.0;
+    double cache_size_mb = 0.0;
+    std::unordered_map<std::string, double> power_mode_results;
+    double memory_pressure_result = 0.0;
+};
+
+struct BenchmarkStats {
+    double avg_tokens_per_sec = 0.0;
+    double min_tokens_per_sec = 0.0;
+    double max_tokens_per_sec = 0.0;
+    double std_dev_tokens_per_sec = 0.0;
+    double avg_latency_ms = 0.0;
+    double peak_vram_gb = 0.0;
+    double avg_vram_usage_gb = 0.0;
+    double fragmentation_ratio = 0.0;
+    double cache_hit_rate = 0.0;
+    uint64_t total_evictions = 0;
+    double eviction_rate = 0.0;
+    void print() const;
+};
+
+struct EngineOptions {
+    int device = 0;
+    uint32_t kv_capacity = 0;     // 0 = min(max_position_embeddings, 4096)
+    bool use_graph = true;        // capture each decode step once, replay it
+    uint32_t prefill_chunk = 2048;
+    uint32_t attn_splits = 0;     // 0 = chosen from the capacity
+    bool batched_prefill = true;  // fp16 models: MFMA prefill (else token by token)
+    bool verbose = false;
+};
+
+// Synthetic Llama-style model: every linear weight ~ N(0, init_std) from the Philox stream keyed by
+// (seed, tensor name), norm gains 1.0.
+struct SyntheticSpec {
+    ModelConfig config;
+    bool fp16 = true;
+    float init_std = 0.02f;
+    uint64_t seed = 0;
+};
+
+struct SamplingParams {
+    int mode = 0;  // VSL_SAMPLE_*
+    float temperature = 0.0f;
+    uint32_t top_k = 40;
+    uint64_t seed = 0;
+    bool stop_on_eos = true;
+};
+
+struct GenerationTimings {
+    uint32_t prompt_tokens = 0;
+    uint32_t generated_tokens = 0;
+    double prefill_ms = 0.0;  // prompt processing up to and including the first sampled token
+    double decode_ms = 0.0;   // the remaining generated_tokens - 1 decode steps
+    uint32_t kv_positions = 0;
+};
+
+class VulkanSymbioteEngine {
+   public:
+    explicit VulkanSymbioteEngine(const Path& model_path);
+    VulkanSymbioteEngine(const Path& model_path, const EngineOptions& options);
+    VulkanSymbioteEngine(const SyntheticSpec& spec, const EngineOptions& options);
+    ~VulkanSymbioteEngine();
+    VulkanSymbioteEngine(const VulkanSymbioteEngine&) = delete;
+    VulkanSymbioteEngine& operator=(const VulkanSymbioteEngine&) = delete;
+
+    std::string generate(const std::string& prompt, uint32_t max_tokens = 256, float temperature = 0.7f);
+    std::vector<uint32_t> encode(const std::string& text);
+    std::string decode(const std::vector<uint32_t>& tokens);
+
+    // Token-id entry point.  Returns the number of generated tokens (<0 on error).
+    // logits_out (optional) receives one vocab-sized row per generated token: the logits that
+    // token was sampled from.
+    int generate_ids(const std::vector<uint32_t>& prompt, uint32_t max_new, const SamplingParams& params,
+                     std::vector<uint32_t>& out_tokens, std::vector<float>* logits_out = nullptr);
+
+    const ModelConfig& config() const noexcept { return config_; }
+    ModelConfig& config() noexcept { return config_; }
+
+    BenchmarkResult run_benchmark(uint32_t warmup_tokens = 10, uint32_t benchmark_tokens = 100, uint32_t iterations = 3);
+    BenchmarkStats run_benchmark_detailed(uint32_t warmup_tokens, uint32_t benchmark_tokens, uint32_t iterations);
+    std::vector<std::string> generate_text_batch(const std::vector<std::string>& prompts,
+                                                 uint32_t max_tokens_per_prompt = 256, float temperature = 0.7f);
+
+    MemoryPoolStats get_vram_stats();
+    double get_peak_vram_usage();
+    void clear_kv_cache();
+    size_t get_kv_cache_memory_usage() const;
+
+    const PerformanceMetrics& get_performance_metrics() const { return performance_metrics_; }
+    void reset_performance_metrics() { performance_metrics_.reset(); }
+
+    // Split form of generate_ids: begin_generation runs the prompt and samples the first token;
+    // decode_steps enqueues n decode steps (asynchronous); finish_generation waits and collects.
+    int begin_generation(const std::vector<uint32_t>& prompt, uint32_t max_new, const SamplingParams& params);
+    int decode_steps(uint32_t n);
+    int finish_generation(std::vector<uint32_t>& out_tokens);
+    void synchronize();
+    // Average duration (ms) of one launch of a decode-step op, timed with HIP events on the engine's
+    // stream over `iterations` rounds that visit every layer (so no weight is re-read from cache).
+    // op: 0 qkv+rope+kv, 1 attention, 2 o-proj, 3 norm+gate/up+swiglu, 4 down-proj, 5 lm_head+sample.
+    double time_op(int op, uint32_t iterations);
+
+    // additive
+    const GenerationTimings& last_timings() const { return timings_; }
+    const EngineOptions& options() const { return options_; }
+    const std::vector<ResidentPack>& packs() const { return pack_manager_.packs(); }
+    ExpectedVoid read_tensor(const std::string& name, void* host_dst, size_t bytes, int* dtype_out = nullptr);
+    uint32_t kv_capacity() const { return cap_; }
+    bool weights_fp16() const { return wdt_ == 1; }
+    uint64_t weight_bytes() const { return weight_bytes_; }
+
+   private:
+    struct Layer {
+        float* attn_norm = nullptr;
+        float* ffn_norm = nullptr;
+        void* wqkv = nullptr;
+        void* wo = nullptr;
+        void* wgu = nullptr;
+        void* wdown = nullptr;
+        void* kc = nullptr;
+        void* vc = nullptr;
+    };
+
+    ModelConfig config_;
+    EngineOptions options_;
+    PerformanceMetrics performance_metrics_;
+    GenerationTimings timings_;
+    PackManager pack_manager_;
+    std::unique_ptr<GGUFLoader> loader_;
+
+    int wdt_ = 1, kvdt_ = 1, edt_ = 1;  // VSL_DT_* of linear weights, KV cache, embedding
+    uint32_t cap_ = 0, nsplit_ = 32;
+    uint64_t weight_bytes_ = 0, kv_bytes_ = 0;
+    double peak_vram_gb_ = 0.0;
+
+    vsl_arena* arena_ = nullptr;
+    void* stream_ = nullptr;
+    void* upload_stream_ = nullptr;
+    void* ev_[4] = {nullptr, nullptr, nullptr, nullptr};
+
+    // device buffers
+    void* embed_ = nullptr;
+    void* out_w_ = nullptr;
+    float* out_norm_ = nullptr;
+    std::vector<Layer> layers_;
+    float* rope_cos_ = nullptr;
+    float* rope_sin_ = nullptr;
+    float *x_ = nullptr, *q_ = nullptr, *attn_ = nullptr, *h_ = nullptr, *logits_ = nullptr;
+    float *part_o_ = nullptr, *part_ml_ = nullptr;
+    uint32_t* attn_cnt_ = nullptr;
+    float* lm_val_ = nullptr;
+    uint32_t* lm_idx_ = nullptr;
+    uint32_t* lm_cnt_ = nullptr;
+    uint32_t* tokens_ = nullptr;
+    uint32_t* prompt_dev_ = nullptr;
+    vsl_ctrl* ctrl_ = nullptr;
+    // prefill (fp16 MFMA path)
+    uint32_t chunk_ = 0;
+    float *px_ = nullptr, *pqkv_ = nullptr;
+    void *pxn_ = nullptr, *pq_ = nullptr, *pattn_ = nullptr, *ph_ = nullptr;
+    // pinned host mirrors
+    uint32_t* host_tokens_ = nullptr;
+    vsl_ctrl* host_ctrl_ = nullptr;
+
+    std::map<std::tuple<int, uint32_t, uint32_t, uint64_t>, vsl_graph*> graphs_;
+    // state of the generation in flight
+    SamplingParams gen_params_;
+    uint32_t gen_prompt_ = 0, gen_max_new_ = 0, gen_issued_ = 0;
+    bool gen_active_ = false;
+
+    void init_device(const ModelConfig& cfg, bool fp16_weights, int embed_dtype);
+    void plan_and_allocate();
+    void upload_rope_tables();
+    void load_weights_from_gguf();
+    void init_synthetic_weights(const SyntheticSpec& spec);
+    void enqueue_layers(uint32_t l0, uint32_t l1);
+    void enqueue_step(const SamplingParams& p);
+    void prefill_tokenwise(uint32_t n_prompt, const SamplingParams& p);
+    void prefill_batched(uint32_t n_prompt, const SamplingParams& p);
+    vsl_graph* step_graph(const SamplingParams& p);
+    void release();
+    void check(int rc, const char* what) const;
+};
+
+// Writes a synthetic Llama-style GGUF (tensor names as the reference reads them,
+// VulkanSymbioteEngine.cpp:2145-2213; linear weights N(0, init_std), norm gains 1.0).
+ExpectedVoid write_synthetic_gguf(const Path& path, const SyntheticSpec& spec, GGUFConvention conv);
+
+// Host generator shared by the GGUF writer: Philox4x32-10 keyed by (seed, hash_string(name)),
+// Box-Muller in fp64; out is binary16 when fp16 else binary32.
+void synthetic_fill_host(void* out, bool fp16, uint64_t n, uint64_t seed, const std::string& name, float mean,
+                         float stddev);
+
+// The reference's fallback byte tokenizer (Tokenizer.cpp:113-198).
+std::vector<uint32_t> simple_encode(const std::string& text);
+std::string simple_decode(const std::vector<uint32_t>& tokens);
+
+}  // namespace vk_symbiote
