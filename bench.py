@@ -100,6 +100,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-kernel-timing", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch each decode step's kernels directly instead of replaying the captured hipGraph "
+                         "(same kernels; used under rocprofv3, whose graph-launch interception crashes here)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (use --gpus 1)",
@@ -111,7 +114,7 @@ def main():
 
     vsl = load_package()
     t_init = time.perf_counter()
-    eng = vsl.Engine(spec=CFG, seed=0, kv_capacity=KV_CAPACITY)
+    eng = vsl.Engine(spec=CFG, seed=0, kv_capacity=KV_CAPACITY, use_graph=not a.eager)
     init_s = time.perf_counter() - t_init
     prompt = np.random.default_rng(1).integers(0, CFG["vocab_size"], a.prompt).astype(np.uint32)
 
@@ -163,6 +166,7 @@ def main():
         "prefill_tflops": round(pre_flops / pre_s / 1e12, 1),
         "prefill_mfma_frac": round(pre_flops / pre_s / PEAK_F16, 4),
         "engine_init_s": round(init_s, 2),
+        "decode_launch": "eager" if a.eager else "hipGraph replay",
     }
 
     if not a.no_kernel_timing:

@@ -42,6 +42,9 @@ typedef struct vsl_engine_options {
     uint32_t prefill_chunk;  /* 0 = 2048 */
     uint32_t attn_splits;    /* 0 = automatic */
     uint32_t batched_prefill;/* 1 = MFMA prefill for fp16 models (default) */
+    uint32_t prefill_split;  /* prefill activations carried as hi/lo fp16 pairs: bit 0 QKV input, bit 1
+                                attention q/probabilities, bit 2 O input, bit 3 gate/up input, bit 4
+                                down input; vsl_engine_default_options sets all five */
 } vsl_engine_options;
 
 typedef struct vsl_gen_params {

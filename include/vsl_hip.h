@@ -39,7 +39,10 @@ enum {
     VSL_E_CAPACITY = -104     /* KV capacity or workspace too small */
 };
 
-enum { VSL_DT_F32 = 0, VSL_DT_F16 = 1 };
+/* VSL_DT_F16X2 -- split activations for the prefill MFMA path: an fp32 value v is held as two
+ * binary16 planes, hi = fp16(v) and lo = fp16(v - hi) (hi plane first, then the lo plane of the
+ * same shape), so that hi + lo carries ~22 significant bits through fp16 MFMA. */
+enum { VSL_DT_F32 = 0, VSL_DT_F16 = 1, VSL_DT_F16X2 = 2 };
 
 /* Sampling modes (VulkanSymbioteEngine::sample_token, VulkanSymbioteEngine.cpp:1540-1553) */
 enum {
@@ -133,7 +136,8 @@ typedef struct vsl_sampler {
 int vsl_embed(const void* table, int dtype, uint32_t vocab, uint32_t d, const uint32_t* ids_dev,
               uint32_t n, float* out, void* stream);
 
-/* rms_norm.comp:24-34 over `rows` rows: y = x / sqrt(mean(x^2)+eps) * gamma; out fp32 or fp16 */
+/* rms_norm.comp:24-34 over `rows` rows: y = x / sqrt(mean(x^2)+eps) * gamma; out fp32, fp16 or
+ * VSL_DT_F16X2 (two planes of rows*d halfs) */
 int vsl_rmsnorm(const float* x, const float* gamma, uint32_t rows, uint32_t d, float eps, void* out,
                 int out_dtype, void* stream);
 
@@ -154,11 +158,10 @@ int vsl_qkv_rope_append(const float* x, const float* gamma, float eps, const voi
 
 /* Flash-decode attention (attention.comp:116-189 semantics: softmax(q.k*scale) over positions
  * 0..ctrl->pos, GQA kv_head = head*n_kv/n_q): split-KV over `nsplit` chunks with online softmax,
- * combined in-kernel by the last chunk to finish.  Workspace: part_o [n_q][nsplit][hd] f32,
- * part_ml [n_q][nsplit][2] f32, counters [n_kv] u32 (zero before first use; left zero). */
+ * then a combine launch.  Workspace: part_o [n_q][nsplit][hd] f32, part_ml [n_q][nsplit][2] f32. */
 int vsl_attn_decode(const float* q, const void* kcache, const void* vcache, int kv_dtype, uint32_t n_q,
                     uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* part_o,
-                    float* part_ml, uint32_t* counters, float* out, vsl_ctrl* ctrl, void* stream);
+                    float* part_ml, float* out, vsl_ctrl* ctrl, void* stream);
 
 /* y[N] += W[N][K] x[K]  (O projection / FFN down projection with the residual add fused) */
 int vsl_gemv_residual(const void* W, int wdtype, uint32_t N, uint32_t K, const float* x, float* resid,
@@ -172,14 +175,14 @@ int vsl_norm_swiglu(const float* x, const float* gamma, float eps, const void* W
 
 /* Output stage (final norm + final_linear.comp + sample_token) for one position:
  *   f = RMSNorm(x, gamma) (gamma may be NULL: no final norm); logits = W f (fp32 [V]);
- *   greedy / reference mode: the argmax is fused into the GEMV; top-k mode runs a second kernel.
+ *   greedy / reference mode: per-block argmax fused into the GEMV, reduced by a second launch;
+ *   top-k mode: the GEMV writes logits and a sampling launch follows.
  *   The sampled token is written to tokens[ctrl->step]; then x <- embed[token] (the next step's
  *   embedding_lookup), ctrl->pos += 1, ctrl->step += 1, and done is set on max_steps / EOS.
- *   Workspace: ws_val/ws_idx >= vsl_lm_head_ws_blocks() entries, counter (1 u32, zero). */
+ *   Workspace: ws_val/ws_idx >= vsl_lm_head_ws_blocks() entries. */
 int vsl_lm_head_sample(const float* gamma, float eps, const void* W, int wdtype, uint32_t V, uint32_t d,
                        float* x, const void* embed, int embed_dtype, float* logits, vsl_sampler sampler,
-                       float* ws_val, uint32_t* ws_idx, uint32_t* counter, uint32_t* tokens,
-                       vsl_ctrl* ctrl, void* stream);
+                       float* ws_val, uint32_t* ws_idx, uint32_t* tokens, vsl_ctrl* ctrl, void* stream);
 uint32_t vsl_lm_head_ws_blocks(void);
 
 /* Sample one token from fp32 logits already in memory (no bookkeeping): the samplers alone,
@@ -196,22 +199,27 @@ int vsl_ctrl_reset(vsl_ctrl* ctrl, uint32_t pos, uint32_t max_steps, uint32_t st
  * ------------------------------------------------------------------------------------------ */
 /* C[M][N] (+)= A[M][K] * B[N][K]^T, fp16 inputs, fp32 accumulate.  epilogue:
  *   VSL_EPI_STORE_F32 (C f32), VSL_EPI_STORE_F16 (C f16), VSL_EPI_RESID (C f32 +=),
- *   VSL_EPI_SWIGLU (B = [Wgate; Wup], N = F: C f16 = silu(A Wg^T) * (A Wu^T)). */
+ *   VSL_EPI_SWIGLU (B = [Wgate; Wup], N = F: C f16 = silu(A Wg^T) * (A Wu^T)).
+ * Flags or'ed into `epilogue`: VSL_GEMM_A_X2 (A is VSL_DT_F16X2: two MFMAs per tile, hi and lo),
+ * VSL_GEMM_C_X2 (SwiGLU output written as VSL_DT_F16X2). */
 enum { VSL_EPI_STORE_F32 = 0, VSL_EPI_STORE_F16 = 1, VSL_EPI_RESID = 2, VSL_EPI_SWIGLU = 3 };
+enum { VSL_GEMM_A_X2 = 0x100, VSL_GEMM_C_X2 = 0x200 };
 int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
                  void* stream);
 
 /* Q/K/V split of a prefill QKV GEMM output (f32 [S][(n_q+2 n_kv) hd]) with RoPE at positions
- * pos0..pos0+S-1: q -> q_out f16 [S][n_q][hd], k/v -> caches at pos0+s. */
+ * pos0..pos0+S-1: q -> q_out [S][n_q][hd] (q_dtype VSL_DT_F16 or VSL_DT_F16X2), k/v -> caches at
+ * pos0+s. */
 int vsl_rope_split_append(const float* qkv, uint32_t S, uint32_t n_q, uint32_t n_kv, uint32_t hd,
-                          uint32_t pos0, const float* rope_cos, const float* rope_sin, void* q_out,
+                          uint32_t pos0, const float* rope_cos, const float* rope_sin, void* q_out, int q_dtype,
                           void* kcache, void* vcache, int kv_dtype, uint32_t cap, void* stream);
 
 /* Causal prefill attention for S queries at positions pos0..pos0+S-1 against cache positions
- * 0..pos0+s: q f16 [S][n_q][hd], caches f16 [n_kv][cap][hd], out f16 [S][n_q*hd]. */
-int vsl_attn_prefill(const void* q, const void* kcache, const void* vcache, uint32_t S, uint32_t pos0,
-                     uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, void* out,
-                     void* stream);
+ * 0..pos0+s: q [S][n_q][hd] (q_dtype F16 or F16X2), caches f16 [n_kv][cap][hd],
+ * out [S][n_q*hd] (out_dtype F16 or F16X2).  With F16X2 q the probabilities are split as well. */
+int vsl_attn_prefill(const void* q, int q_dtype, const void* kcache, const void* vcache, uint32_t S,
+                     uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale,
+                     void* out, int out_dtype, void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * hipGraph helpers (each decode step is captured once and replayed).

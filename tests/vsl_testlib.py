@@ -48,15 +48,25 @@ class Dev:
         self.torch = torch
         assert torch.cuda.is_available(), "GPU tests need a HIP device"
         self.dev = torch.device("cuda:0")
+        # every buffer stays referenced until release(): a pointer handed to the C ABI must not
+        # outlive its tensor (torch's caching allocator reuses freed blocks at once)
+        self._live = []
+
+    def release(self):
+        self.torch.cuda.synchronize()
+        self._live = []
 
     def put(self, a):
         t = self.torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)
+        self._live.append(t)
         return t
 
     def empty(self, shape, dtype):
         tdt = {np.float32: self.torch.float32, np.float16: self.torch.float16, np.uint32: self.torch.int32,
                np.int32: self.torch.int32, np.uint8: self.torch.uint8}[np.dtype(dtype).type]
-        return self.torch.zeros(shape, dtype=tdt, device=self.dev)
+        t = self.torch.zeros(shape, dtype=tdt, device=self.dev)
+        self._live.append(t)
+        return t
 
     @staticmethod
     def p(t):

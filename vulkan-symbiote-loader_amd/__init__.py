@@ -20,7 +20,8 @@ LIB_DIR = os.path.join(_HERE, "lib")
 HIP_LIB = os.path.join(LIB_DIR, "libvsl_hip.so")
 ENGINE_LIB = os.path.join(LIB_DIR, "libvsl_engine.so")
 
-VSL_DT_F32, VSL_DT_F16 = 0, 1
+VSL_DT_F32, VSL_DT_F16, VSL_DT_F16X2 = 0, 1, 2
+GEMM_A_X2, GEMM_C_X2 = 0x100, 0x200
 SAMPLE_GREEDY, SAMPLE_REFERENCE, SAMPLE_TOPK_SEEDED = 0, 1, 2
 EPI_STORE_F32, EPI_STORE_F16, EPI_RESID, EPI_SWIGLU = 0, 1, 2, 3
 _MODES = {"greedy": SAMPLE_GREEDY, "reference": SAMPLE_REFERENCE, "topk": SAMPLE_TOPK_SEEDED}
@@ -43,7 +44,7 @@ class ModelSpec(ctypes.Structure):
 class EngineOptions(ctypes.Structure):
     _fields_ = [("device", ctypes.c_int32), ("kv_capacity", ctypes.c_uint32), ("use_graph", ctypes.c_uint32),
                 ("prefill_chunk", ctypes.c_uint32), ("attn_splits", ctypes.c_uint32),
-                ("batched_prefill", ctypes.c_uint32)]
+                ("batched_prefill", ctypes.c_uint32), ("prefill_split", ctypes.c_uint32)]
 
 
 class GenParams(ctypes.Structure):
@@ -117,17 +118,16 @@ _HIP_SIGS = {
     "vsl_gemv": (_I32, [_P, _I32, _U32, _U32, _P, _I32, _U32, _P, _I32, _P]),
     "vsl_qkv_rope_append": (_I32, [_P, _P, _F32, _P, _I32, _U32, _U32, _U32, _U32, _P, _P, _P, _P, _I32, _U32, _P,
                                    _P, _P]),
-    "vsl_attn_decode": (_I32, [_P, _P, _P, _I32, _U32, _U32, _U32, _U32, _F32, _U32, _P, _P, _P, _P, _P, _P]),
+    "vsl_attn_decode": (_I32, [_P, _P, _P, _I32, _U32, _U32, _U32, _U32, _F32, _U32, _P, _P, _P, _P, _P]),
     "vsl_gemv_residual": (_I32, [_P, _I32, _U32, _U32, _P, _P, _P, _P]),
     "vsl_norm_swiglu": (_I32, [_P, _P, _F32, _P, _I32, _U32, _U32, _P, _P, _P]),
-    "vsl_lm_head_sample": (_I32, [_P, _F32, _P, _I32, _U32, _U32, _P, _P, _I32, _P, Sampler, _P, _P, _P, _P, _P,
-                                  _P]),
+    "vsl_lm_head_sample": (_I32, [_P, _F32, _P, _I32, _U32, _U32, _P, _P, _I32, _P, Sampler, _P, _P, _P, _P, _P]),
     "vsl_lm_head_ws_blocks": (_U32, []),
     "vsl_sample_logits": (_I32, [_P, _U32, Sampler, _U64, _P, _P]),
     "vsl_ctrl_reset": (_I32, [_P, _U32, _U32, _U32, _U32, _P]),
     "vsl_gemm_f16": (_I32, [_P, _P, _U32, _U32, _U32, _P, _I32, _P]),
-    "vsl_rope_split_append": (_I32, [_P, _U32, _U32, _U32, _U32, _U32, _P, _P, _P, _P, _P, _I32, _U32, _P]),
-    "vsl_attn_prefill": (_I32, [_P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F32, _P, _P]),
+    "vsl_rope_split_append": (_I32, [_P, _U32, _U32, _U32, _U32, _U32, _P, _P, _P, _I32, _P, _P, _I32, _U32, _P]),
+    "vsl_attn_prefill": (_I32, [_P, _I32, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F32, _P, _I32, _P]),
     "vsl_graph_begin": (_I32, [_P]),
     "vsl_graph_end": (_I32, [_P, ctypes.POINTER(_P)]),
     "vsl_graph_launch": (_I32, [_P, _P]),
@@ -243,12 +243,14 @@ class Engine:
     """VulkanSymbioteEngine on one MI355X."""
 
     def __init__(self, gguf_path=None, spec=None, seed=0, device=0, kv_capacity=0, use_graph=True,
-                 prefill_chunk=0, attn_splits=0, batched_prefill=True, init_std=0.02):
+                 prefill_chunk=0, attn_splits=0, batched_prefill=True, init_std=0.02, prefill_split=None):
         self._lib = engine_lib()
         opt = EngineOptions()
         self._lib.vsl_engine_default_options(ctypes.byref(opt))
         opt.device, opt.kv_capacity, opt.use_graph = device, kv_capacity, int(bool(use_graph))
         opt.prefill_chunk, opt.attn_splits, opt.batched_prefill = prefill_chunk, attn_splits, int(bool(batched_prefill))
+        if prefill_split is not None:
+            opt.prefill_split = prefill_split
         h = ctypes.c_void_p()
         if gguf_path is not None:
             rc = self._lib.vsl_engine_open(str(gguf_path).encode(), ctypes.byref(opt), ctypes.byref(h))

@@ -43,7 +43,6 @@ struct GemvArgs {
     // EPI_ARGMAX
     float* ws_val;
     uint32_t* ws_idx;
-    uint32_t* counter;
     uint32_t* tokens;
     const void* embed;
     float* x_next;
@@ -103,8 +102,15 @@ __device__ void finish_token(uint32_t tok, uint32_t V, uint32_t d, const void* e
                              uint32_t* tokens, vsl_ctrl* ctrl) {
     const uint32_t tid = threadIdx.x;
     const uint32_t row = tok < V ? tok : V - 1;  // embedding_lookup.comp:32
+    constexpr int VEC = ET::kVec;              // d % 8 == 0: whole 16-byte vectors
     const typename ET::T* e = static_cast<const typename ET::T*>(embed) + (size_t)row * d;
-    for (uint32_t i = tid; i < d; i += blockDim.x) x_next[i] = to_f32(e[i]);
+    for (uint32_t i = tid * VEC; i < d; i += blockDim.x * VEC) {
+        float f[VEC];
+        unpack(load16<false>(e + i), ET(), f);
+#pragma unroll
+        for (int j = 0; j < VEC; j += 4)
+            *reinterpret_cast<float4*>(x_next + i + j) = make_float4(f[j], f[j + 1], f[j + 2], f[j + 3]);
+    }
     if (tid == 0) {
         const uint32_t step = ctrl->step;
         tokens[step] = tok;
@@ -123,7 +129,6 @@ __global__ __launch_bounds__(kBlock) void k_gemv_dec(GemvArgs a) {
     __shared__ float red[kWaves];
     __shared__ float bval[kWaves];
     __shared__ uint32_t bidx[kWaves];
-    __shared__ uint32_t s_last;
     extern __shared__ float xs[];
 
     uint32_t pos = 0;
@@ -269,6 +274,8 @@ __global__ __launch_bounds__(kBlock) void k_gemv_dec(GemvArgs a) {
     }
 
     if constexpr (EPI == EPI_ARGMAX) {
+        // per-block partial argmax; k_argmax_finish reduces the partials in the next launch (a
+        // kernel boundary is the cheapest cross-block visibility point on this chip)
         if (lane == 0) {
             bval[wave] = best_v;
             bidx[wave] = best_i;
@@ -281,47 +288,53 @@ __global__ __launch_bounds__(kBlock) void k_gemv_dec(GemvArgs a) {
             for (int w = 1; w < kWaves; ++w) argmax_merge(v, i, bval[w], bidx[w]);
             a.ws_val[blockIdx.x] = v;
             a.ws_idx[blockIdx.x] = i;
-            __threadfence();
-            const uint32_t ticket = atomicAdd(a.counter, 1u);
-            s_last = (ticket == gridDim.x - 1) ? 1u : 0u;
-        }
-        __syncthreads();
-        if (s_last) {
-            __threadfence();
-            float v = -INFINITY;
-            uint32_t i = 0xFFFFFFFFu;
-            for (uint32_t b = threadIdx.x; b < gridDim.x; b += kBlock) {
-                float ov = __builtin_nontemporal_load(a.ws_val + b);
-                uint32_t oi = __builtin_nontemporal_load(a.ws_idx + b);
-                argmax_merge(v, i, ov, oi);
-            }
-            wave_argmax(v, i);
-            if (lane == 0) {
-                bval[wave] = v;
-                bidx[wave] = i;
-            }
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                float bv = bval[0];
-                uint32_t bi = bidx[0];
-                for (int w = 1; w < kWaves; ++w) argmax_merge(bv, bi, bval[w], bidx[w]);
-                // every logit NaN: greedy_sampling returns 0 (its first element is never beaten)
-                bidx[0] = bi == 0xFFFFFFFFu ? 0u : bi;
-                *a.counter = 0u;
-            }
-            __syncthreads();
-            finish_token<ET>(bidx[0], a.N, a.K, a.embed, a.x_next, a.tokens, a.ctrl);
         }
     }
 }
 
-template <class WT, int R, int U, int EPI, class ET = WF32>
-int launch_gemv(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
+// Final greedy reduction over the lm_head blocks' partials, then the token bookkeeping.
+constexpr int kFinishThreads = 1024;
+template <class ET>
+__global__ __launch_bounds__(kFinishThreads) void k_argmax_finish(const float* __restrict__ ws_val,
+                                                                  const uint32_t* __restrict__ ws_idx, uint32_t nblocks,
+                                                                  uint32_t V, uint32_t d, const void* embed,
+                                                                  float* x_next, uint32_t* tokens, vsl_ctrl* ctrl) {
+    __shared__ float bval[kFinishThreads / 64];
+    __shared__ uint32_t bidx[kFinishThreads / 64];
+    if (ctrl->done) return;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float v = -INFINITY;
+    uint32_t i = 0xFFFFFFFFu;
+    for (uint32_t b = threadIdx.x; b < nblocks; b += kFinishThreads) argmax_merge(v, i, ws_val[b], ws_idx[b]);
+    wave_argmax(v, i);
+    if (lane == 0) {
+        bval[wave] = v;
+        bidx[wave] = i;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        v = threadIdx.x < kFinishThreads / 64 ? bval[threadIdx.x] : -INFINITY;
+        i = threadIdx.x < kFinishThreads / 64 ? bidx[threadIdx.x] : 0xFFFFFFFFu;
+        wave_argmax(v, i);
+        // every logit NaN: greedy_sampling returns 0 (its first element is never beaten)
+        if (threadIdx.x == 0) bidx[0] = i == 0xFFFFFFFFu ? 0u : i;
+    }
+    __syncthreads();
+    finish_token<ET>(bidx[0], V, d, embed, x_next, tokens, ctrl);
+}
+
+template <int R, int EPI>
+uint32_t gemv_blocks(uint32_t N, uint32_t max_blocks) {
     constexpr int RG = (EPI == EPI_SWIGLU) ? R / 2 : R;
-    const uint32_t groups = (a.N + RG - 1) / RG;
+    const uint32_t groups = (N + RG - 1) / RG;
     uint32_t blocks = (groups + kWaves - 1) / kWaves;
     if (blocks > max_blocks) blocks = max_blocks;
-    if (blocks == 0) blocks = 1;
+    return blocks == 0 ? 1 : blocks;
+}
+
+template <class WT, int R, int U, int EPI, class ET = WF32>
+int launch_gemv(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
+    const uint32_t blocks = gemv_blocks<R, EPI>(a.N, max_blocks);
     const size_t lds = (size_t)a.K * sizeof(float);
     k_gemv_dec<WT, R, U, EPI, ET><<<blocks, kBlock, lds, s>>>(a);
     HIP_TRY(hipGetLastError());
@@ -347,7 +360,6 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
                                                         const void* __restrict__ vcache, uint32_t n_q, uint32_t n_kv,
                                                         uint32_t cap, float scale, uint32_t nsplit,
                                                         float* __restrict__ part_o, float* __restrict__ part_ml,
-                                                        uint32_t* __restrict__ counters, float* __restrict__ out,
                                                         vsl_ctrl* ctrl) {
     typedef typename KT::T T;
     constexpr int LPP = HD / 8;            // lanes per position (8 elements of 16 bytes... per lane)
@@ -355,7 +367,6 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
     constexpr int NSLOT = kWaves * SLOTS;  // positions per block per step
     __shared__ float s_ml[NSLOT][G][2];
     __shared__ float s_acc[NSLOT][G][HD];
-    __shared__ uint32_t s_last;
 
     if (ctrl->done) return;
     const uint32_t pos = ctrl->pos;
@@ -453,44 +464,84 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
             part_ml[pidx * 2 + 1] = L;
         }
     }
+}
+
+// Combines the nsplit partials of every query head: out = sum_s A_s 2^(m_s-M) / sum_s l_s 2^(m_s-M).
+// One block per head; the split weights are computed once (one thread per split) and the output
+// dimensions accumulate over splits with independent loads.
+constexpr int kCombineThreads = 128;
+constexpr uint32_t kMaxSplits = 1024;
+template <int HD>
+__global__ __launch_bounds__(kCombineThreads) void k_attn_combine(const float* __restrict__ part_o,
+                                                                  const float* __restrict__ part_ml, uint32_t nsplit,
+                                                                  float* __restrict__ out, const vsl_ctrl* ctrl) {
+    __shared__ float wts[kMaxSplits];
+    __shared__ float red[kCombineThreads / 64];
+    __shared__ float s_M, s_L;
+    if (ctrl->done) return;
+    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t base = (size_t)h * nsplit;
+    float mx = -INFINITY;
+    for (uint32_t s = tid; s < nsplit; s += kCombineThreads) {
+        const float m = part_ml[(base + s) * 2];
+        wts[s] = m;
+        mx = fmaxf(mx, m);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        const uint32_t ticket = atomicAdd(counters + kvh, 1u);
-        s_last = (ticket == nsplit - 1) ? 1u : 0u;
+    if (tid == 0) {
+        float M = red[0];
+        for (int w = 1; w < kCombineThreads / 64; ++w) M = fmaxf(M, red[w]);
+        s_M = M;
     }
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (uint32_t e = threadIdx.x; e < (uint32_t)(G * HD); e += kBlock) {
-        const uint32_t g = e / HD, dd = e % HD;
-        const size_t base = (size_t)(h0 + g) * nsplit;
-        float M = -INFINITY;
-        for (uint32_t s = 0; s < nsplit; ++s) M = fmaxf(M, __builtin_nontemporal_load(part_ml + (base + s) * 2));
-        float L = 0.f, A = 0.f;
-        for (uint32_t s = 0; s < nsplit; ++s) {
-            const float ms = __builtin_nontemporal_load(part_ml + (base + s) * 2);
-            if (ms == -INFINITY) continue;
-            const float f = exp2f(ms - M);
-            L += __builtin_nontemporal_load(part_ml + (base + s) * 2 + 1) * f;
-            A += __builtin_nontemporal_load(part_o + (base + s) * HD + dd) * f;
+    const float M = s_M;
+    float lsum = 0.f;
+    for (uint32_t s = tid; s < nsplit; s += kCombineThreads) {
+        const float m = wts[s];
+        const float f = m == -INFINITY ? 0.f : exp2f(m - M);
+        wts[s] = f;
+        lsum += part_ml[(base + s) * 2 + 1] * f;
+    }
+    lsum = wave_sum(lsum);
+    __syncthreads();
+    if (lane == 0) red[wave] = lsum;
+    __syncthreads();
+    if (tid == 0) {
+        float L = 0.f;
+        for (int w = 0; w < kCombineThreads / 64; ++w) L += red[w];
+        s_L = L;
+    }
+    __syncthreads();
+    const float inv = 1.0f / s_L;
+    for (uint32_t dd = tid; dd < (uint32_t)HD; dd += kCombineThreads) {
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        uint32_t s = 0;
+        for (; s + 4 <= nsplit; s += 4) {
+            a0 = fmaf(part_o[(base + s) * HD + dd], wts[s], a0);
+            a1 = fmaf(part_o[(base + s + 1) * HD + dd], wts[s + 1], a1);
+            a2 = fmaf(part_o[(base + s + 2) * HD + dd], wts[s + 2], a2);
+            a3 = fmaf(part_o[(base + s + 3) * HD + dd], wts[s + 3], a3);
         }
-        out[(size_t)(h0 + g) * HD + dd] = A / L;
+        for (; s < nsplit; ++s) a0 = fmaf(part_o[(base + s) * HD + dd], wts[s], a0);
+        out[(size_t)h * HD + dd] = ((a0 + a1) + (a2 + a3)) * inv;
     }
-    if (threadIdx.x == 0) counters[kvh] = 0u;
 }
 
 template <class KT, int HD>
 int launch_attn_g(uint32_t G, dim3 grid, hipStream_t s, const float* q, const void* kc, const void* vc, uint32_t n_q,
-                  uint32_t n_kv, uint32_t cap, float scale, uint32_t nsplit, float* po, float* pml, uint32_t* cnt,
-                  float* out, vsl_ctrl* ctrl) {
+                  uint32_t n_kv, uint32_t cap, float scale, uint32_t nsplit, float* po, float* pml, float* out,
+                  vsl_ctrl* ctrl) {
     switch (G) {
-        case 1: k_attn_decode<KT, HD, 1><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, cnt, out, ctrl); break;
-        case 2: k_attn_decode<KT, HD, 2><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, cnt, out, ctrl); break;
-        case 4: k_attn_decode<KT, HD, 4><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, cnt, out, ctrl); break;
-        case 8: k_attn_decode<KT, HD, 8><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, cnt, out, ctrl); break;
+        case 1: k_attn_decode<KT, HD, 1><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl); break;
+        case 2: k_attn_decode<KT, HD, 2><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl); break;
+        case 4: k_attn_decode<KT, HD, 4><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl); break;
+        case 8: k_attn_decode<KT, HD, 8><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl); break;
         default: return vsl_unsupported("vsl_attn_decode: GQA ratio %u (supported 1,2,4,8)", G);
     }
+    HIP_TRY(hipGetLastError());
+    k_attn_combine<HD><<<n_q, kCombineThreads, 0, s>>>(po, pml, nsplit, out, ctrl);
     HIP_TRY(hipGetLastError());
     return VSL_OK;
 }
@@ -604,9 +655,9 @@ __global__ void k_embed(const void* table, uint32_t vocab, uint32_t d, const uin
     for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) out[(size_t)t * d + i] = to_f32(e[i]);
 }
 
-template <typename OT>
-__global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float* x, const float* gamma, uint32_t d, float eps,
-                                                         OT* out) {
+template <typename OT, bool X2>
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float* x, const float* gamma, uint32_t rows, uint32_t d,
+                                                         float eps, OT* out) {
     __shared__ float red[kWaves];
     const float* xr = x + (size_t)blockIdx.x * d;
     float ss = 0.f;
@@ -617,8 +668,16 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float* x, const f
     float tot = 0.f;
     for (int w = 0; w < kWaves; ++w) tot += red[w];
     const float inv = 1.0f / sqrtf(tot / (float)d + eps);
-    for (uint32_t i = threadIdx.x; i < d; i += kBlock)
-        store_elem(out + (size_t)blockIdx.x * d + i, xr[i] * inv * (gamma ? gamma[i] : 1.0f));
+    for (uint32_t i = threadIdx.x; i < d; i += kBlock) {
+        const float v = xr[i] * inv * (gamma ? gamma[i] : 1.0f);
+        if constexpr (X2) {
+            const vsl_half hi = (vsl_half)v;
+            out[(size_t)blockIdx.x * d + i] = hi;
+            out[(size_t)rows * d + (size_t)blockIdx.x * d + i] = (vsl_half)(v - (float)hi);
+        } else {
+            store_elem(out + (size_t)blockIdx.x * d + i, v);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -719,9 +778,11 @@ extern "C" int vsl_rmsnorm(const float* x, const float* gamma, uint32_t rows, ui
     if (rows == 0) return VSL_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (out_dtype == VSL_DT_F16)
-        k_rmsnorm_rows<vsl_half><<<rows, kBlock, 0, s>>>(x, gamma, d, eps, static_cast<vsl_half*>(out));
+        k_rmsnorm_rows<vsl_half, false><<<rows, kBlock, 0, s>>>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out));
+    else if (out_dtype == VSL_DT_F16X2)
+        k_rmsnorm_rows<vsl_half, true><<<rows, kBlock, 0, s>>>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out));
     else if (out_dtype == VSL_DT_F32)
-        k_rmsnorm_rows<float><<<rows, kBlock, 0, s>>>(x, gamma, d, eps, static_cast<float*>(out));
+        k_rmsnorm_rows<float, false><<<rows, kBlock, 0, s>>>(x, gamma, rows, d, eps, static_cast<float*>(out));
     else
         return vsl_unsupported("vsl_rmsnorm: dtype %d", out_dtype);
     HIP_TRY(hipGetLastError());
@@ -790,20 +851,20 @@ extern "C" int vsl_qkv_rope_append(const float* x, const float* gamma, float eps
 
 extern "C" int vsl_attn_decode(const float* q, const void* kcache, const void* vcache, int kv_dtype, uint32_t n_q,
                                uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* part_o,
-                               float* part_ml, uint32_t* counters, float* out, vsl_ctrl* ctrl, void* stream) {
-    if (!q || !kcache || !vcache || !part_o || !part_ml || !counters || !out || !ctrl)
+                               float* part_ml, float* out, vsl_ctrl* ctrl, void* stream) {
+    if (!q || !kcache || !vcache || !part_o || !part_ml || !out || !ctrl)
         return vsl_invalid("vsl_attn_decode: null pointer");
     if (n_kv == 0 || n_q % n_kv) return vsl_invalid("vsl_attn_decode: n_q=%u not a multiple of n_kv=%u", n_q, n_kv);
-    if (nsplit == 0 || nsplit > 65535) return vsl_invalid("vsl_attn_decode: nsplit=%u", nsplit);
+    if (nsplit == 0 || nsplit > kMaxSplits) return vsl_invalid("vsl_attn_decode: nsplit=%u (1..%u)", nsplit, kMaxSplits);
     const uint32_t G = n_q / n_kv;
     dim3 grid(nsplit, n_kv);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (kv_dtype == VSL_DT_F16) {
-        if (hd == 128) return launch_attn_g<WF16, 128>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, counters, out, ctrl);
-        if (hd == 64) return launch_attn_g<WF16, 64>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, counters, out, ctrl);
+        if (hd == 128) return launch_attn_g<WF16, 128>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl);
+        if (hd == 64) return launch_attn_g<WF16, 64>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl);
     } else if (kv_dtype == VSL_DT_F32) {
-        if (hd == 128) return launch_attn_g<WF32, 128>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, counters, out, ctrl);
-        if (hd == 64) return launch_attn_g<WF32, 64>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, counters, out, ctrl);
+        if (hd == 128) return launch_attn_g<WF32, 128>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl);
+        if (hd == 64) return launch_attn_g<WF32, 64>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl);
     }
     return vsl_unsupported("vsl_attn_decode: head_dim %u / kv dtype %d (supported 64,128 / f16,f32)", hd, kv_dtype);
 }
@@ -836,27 +897,30 @@ extern "C" uint32_t vsl_lm_head_ws_blocks(void) { return kMaxLmBlocks; }
 
 extern "C" int vsl_lm_head_sample(const float* gamma, float eps, const void* W, int wdtype, uint32_t V, uint32_t d,
                                   float* x, const void* embed, int embed_dtype, float* logits, vsl_sampler sampler,
-                                  float* ws_val, uint32_t* ws_idx, uint32_t* counter, uint32_t* tokens, vsl_ctrl* ctrl,
-                                  void* stream) {
-    if (!W || !x || !embed || !logits || !ws_val || !ws_idx || !counter || !tokens || !ctrl)
+                                  float* ws_val, uint32_t* ws_idx, uint32_t* tokens, vsl_ctrl* ctrl, void* stream) {
+    if (!W || !x || !embed || !logits || !ws_val || !ws_idx || !tokens || !ctrl)
         return vsl_invalid("vsl_lm_head_sample: null pointer");
     if (int rc = check_gemv_shape(V, d, "vsl_lm_head_sample")) return rc;
     if (embed_dtype != VSL_DT_F16 && embed_dtype != VSL_DT_F32) return vsl_unsupported("embed dtype %d", embed_dtype);
+    if (wdtype != VSL_DT_F16 && wdtype != VSL_DT_F32) return vsl_unsupported("vsl_lm_head_sample: dtype %d", wdtype);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool fused = sampler.mode == VSL_SAMPLE_GREEDY || sampler.mode == VSL_SAMPLE_REFERENCE ||
                        sampler.temperature <= 0.f;
     GemvArgs a{};
     a.W = W; a.N = V; a.K = d; a.x = x; a.gamma = gamma; a.eps = eps; a.y = logits;
-    a.ws_val = ws_val; a.ws_idx = ws_idx; a.counter = counter; a.tokens = tokens; a.embed = embed; a.x_next = x;
+    a.ws_val = ws_val; a.ws_idx = ws_idx; a.tokens = tokens; a.embed = embed; a.x_next = x;
     a.ctrl = ctrl;
     if (fused) {
-        if (wdtype == VSL_DT_F16)
-            return embed_dtype == VSL_DT_F16 ? launch_gemv<WF16, 2, 8, EPI_ARGMAX, WF16>(a, kMaxLmBlocks, s)
-                                             : launch_gemv<WF16, 2, 8, EPI_ARGMAX, WF32>(a, kMaxLmBlocks, s);
-        if (wdtype == VSL_DT_F32)
-            return embed_dtype == VSL_DT_F16 ? launch_gemv<WF32, 2, 8, EPI_ARGMAX, WF16>(a, kMaxLmBlocks, s)
-                                             : launch_gemv<WF32, 2, 8, EPI_ARGMAX, WF32>(a, kMaxLmBlocks, s);
-        return vsl_unsupported("vsl_lm_head_sample: dtype %d", wdtype);
+        int rc = wdtype == VSL_DT_F16 ? launch_gemv<WF16, 2, 8, EPI_ARGMAX>(a, kMaxLmBlocks, s)
+                                      : launch_gemv<WF32, 2, 8, EPI_ARGMAX>(a, kMaxLmBlocks, s);
+        if (rc) return rc;
+        const uint32_t nb = gemv_blocks<2, EPI_ARGMAX>(V, kMaxLmBlocks);
+        if (embed_dtype == VSL_DT_F16)
+            k_argmax_finish<WF16><<<1, kFinishThreads, 0, s>>>(ws_val, ws_idx, nb, V, d, embed, x, tokens, ctrl);
+        else
+            k_argmax_finish<WF32><<<1, kFinishThreads, 0, s>>>(ws_val, ws_idx, nb, V, d, embed, x, tokens, ctrl);
+        HIP_TRY(hipGetLastError());
+        return VSL_OK;
     }
     if (sampler.mode != VSL_SAMPLE_TOPK_SEEDED) return vsl_invalid("vsl_lm_head_sample: sampler mode %d", sampler.mode);
     if (V > (uint32_t)(kSampBlock * kSampPer)) return vsl_unsupported("top-k sampling supports V <= %d", kSampBlock * kSampPer);

@@ -276,6 +276,9 @@ __global__ void k_fill_normal(T* out, uint64_t n, uint32_t k0, uint32_t k1, floa
             uint64_t e = b * 4 + j;
             if (e < n) {
                 float v = (float)((double)mean + (double)stddev * z[j]);
+                // The value is defined as double -> float -> output type (two roundings, as the host
+                // generator does); the empty asm keeps the compiler from fusing them into one.
+                asm volatile("" : "+v"(v));
                 store_elem(out + e, v);
             }
         }

@@ -346,29 +346,26 @@ void VulkanSymbioteEngine::plan_and_allocate() {
     add(V * 4, reinterpret_cast<void**>(&logits_));
     add(nq * nsplit_ * hd * 4, reinterpret_cast<void**>(&part_o_));
     add(nq * nsplit_ * 2 * 4, reinterpret_cast<void**>(&part_ml_));
-    add(nkv * 4, reinterpret_cast<void**>(&attn_cnt_));
     add(vsl_lm_head_ws_blocks() * 4, reinterpret_cast<void**>(&lm_val_));
     add(vsl_lm_head_ws_blocks() * 4, reinterpret_cast<void**>(&lm_idx_));
-    add(4, reinterpret_cast<void**>(&lm_cnt_));
     add((cap + 1) * 4, reinterpret_cast<void**>(&tokens_));
     add((cap + 1) * 4, reinterpret_cast<void**>(&prompt_dev_));
     add(sizeof(vsl_ctrl), reinterpret_cast<void**>(&ctrl_));
     if (ch) {
         const uint64_t wide = std::max<uint64_t>(std::max<uint64_t>(d, nq * hd), F);
         add(ch * d * 4, reinterpret_cast<void**>(&px_));
-        add(ch * wide * 2, &pxn_);
+        // activations carried as hi/lo fp16 planes take twice the space
+        add(2 * ch * wide * 2, &pxn_);
         add(ch * (nq + 2 * nkv) * hd * 4, reinterpret_cast<void**>(&pqkv_));
-        add(ch * nq * hd * 2, &pq_);
-        add(ch * nq * hd * 2, &pattn_);
-        add(ch * F * 2, &ph_);
+        add(2 * ch * nq * hd * 2, &pq_);
+        add(2 * ch * nq * hd * 2, &pattn_);
+        add(2 * ch * F * 2, &ph_);
     }
     uint64_t total = (1ull << 20);
     for (auto& r : reqs) total += r.bytes;
     check(vsl_arena_create(options_.device, total, &arena_), "vsl_arena_create");
     for (auto& r : reqs) check(vsl_arena_alloc(arena_, r.bytes, 256, r.out), "vsl_arena_alloc");
     // counters and workspaces that kernels expect zeroed
-    check(vsl_memset_d(attn_cnt_, 0, nkv * 4, stream_), "memset");
-    check(vsl_memset_d(lm_cnt_, 0, 4, stream_), "memset");
     check(vsl_memset_d(x_, 0, d * 4, stream_), "memset");
     check(vsl_stream_sync(stream_), "sync");
     MemoryPoolStats st = get_vram_stats();
@@ -550,8 +547,8 @@ void VulkanSymbioteEngine::enqueue_layers(uint32_t l0, uint32_t l1) {
         const Layer& y = layers_[l];
         check(vsl_qkv_rope_append(x_, y.attn_norm, eps, y.wqkv, wdt_, d, nq, nkv, hd, rope_cos_, rope_sin_, y.kc, y.vc,
                                   kvdt_, cap_, q_, ctrl_, stream_), "vsl_qkv_rope_append");
-        check(vsl_attn_decode(q_, y.kc, y.vc, kvdt_, nq, nkv, hd, cap_, scale, nsplit_, part_o_, part_ml_, attn_cnt_,
-                              attn_, ctrl_, stream_), "vsl_attn_decode");
+        check(vsl_attn_decode(q_, y.kc, y.vc, kvdt_, nq, nkv, hd, cap_, scale, nsplit_, part_o_, part_ml_, attn_,
+                              ctrl_, stream_), "vsl_attn_decode");
         check(vsl_gemv_residual(y.wo, wdt_, d, nq * hd, attn_, x_, ctrl_, stream_), "vsl_gemv_residual(o)");
         check(vsl_norm_swiglu(x_, y.ffn_norm, eps, y.wgu, wdt_, d, F, h_, ctrl_, stream_), "vsl_norm_swiglu");
         check(vsl_gemv_residual(y.wdown, wdt_, d, F, h_, x_, ctrl_, stream_), "vsl_gemv_residual(down)");
@@ -570,7 +567,7 @@ static vsl_sampler to_vsl_sampler(const SamplingParams& p) {
 void VulkanSymbioteEngine::enqueue_step(const SamplingParams& p) {
     enqueue_layers(0, config_.num_layers);
     check(vsl_lm_head_sample(out_norm_, config_.rms_epsilon, out_w_, wdt_, config_.vocab_size, config_.hidden_size, x_,
-                             embed_, edt_, logits_, to_vsl_sampler(p), lm_val_, lm_idx_, lm_cnt_, tokens_, ctrl_, stream_),
+                             embed_, edt_, logits_, to_vsl_sampler(p), lm_val_, lm_idx_, tokens_, ctrl_, stream_),
           "vsl_lm_head_sample");
 }
 
@@ -605,7 +602,7 @@ void VulkanSymbioteEngine::prefill_tokenwise(uint32_t n_prompt, const SamplingPa
         enqueue_layers(0, c.num_layers);
     }
     check(vsl_lm_head_sample(out_norm_, c.rms_epsilon, out_w_, wdt_, c.vocab_size, c.hidden_size, x_, embed_, edt_,
-                             logits_, to_vsl_sampler(p), lm_val_, lm_idx_, lm_cnt_, tokens_, ctrl_, stream_),
+                             logits_, to_vsl_sampler(p), lm_val_, lm_idx_, tokens_, ctrl_, stream_),
           "vsl_lm_head_sample");
 }
 
@@ -616,6 +613,13 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
     const uint32_t d = c.hidden_size, hd = c.head_dim, nq = c.num_attention_heads, nkv = c.num_key_value_heads,
                    F = c.intermediate_size, V = c.vocab_size;
     const float eps = c.rms_epsilon, scale = 1.0f / std::sqrt((float)hd);
+    const uint32_t sp = options_.prefill_split;
+    const int n1 = (sp & 1) ? VSL_DT_F16X2 : VSL_DT_F16, qdt = (sp & 2) ? VSL_DT_F16X2 : VSL_DT_F16;
+    const int odt = (sp & 4) ? VSL_DT_F16X2 : VSL_DT_F16, n2 = (sp & 8) ? VSL_DT_F16X2 : VSL_DT_F16;
+    const int g_qkv = VSL_EPI_STORE_F32 | ((sp & 1) ? VSL_GEMM_A_X2 : 0);
+    const int g_o = VSL_EPI_RESID | ((sp & 4) ? VSL_GEMM_A_X2 : 0);
+    const int g_gu = VSL_EPI_SWIGLU | ((sp & 8) ? VSL_GEMM_A_X2 : 0) | ((sp & 16) ? VSL_GEMM_C_X2 : 0);
+    const int g_dn = VSL_EPI_RESID | ((sp & 16) ? VSL_GEMM_A_X2 : 0);
     uint32_t last_rows = 0;
     for (uint32_t c0 = 0; c0 < n_prompt; c0 += chunk_) {
         const uint32_t S = std::min(chunk_, n_prompt - c0);
@@ -623,22 +627,23 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
         check(vsl_embed(embed_, edt_, V, d, prompt_dev_ + c0, S, px_, stream_), "vsl_embed");
         for (uint32_t l = 0; l < c.num_layers; ++l) {
             const Layer& y = layers_[l];
-            check(vsl_rmsnorm(px_, y.attn_norm, S, d, eps, pxn_, VSL_DT_F16, stream_), "vsl_rmsnorm");
-            check(vsl_gemm_f16(pxn_, y.wqkv, S, (nq + 2 * nkv) * hd, d, pqkv_, VSL_EPI_STORE_F32, stream_), "gemm qkv");
-            check(vsl_rope_split_append(pqkv_, S, nq, nkv, hd, c0, rope_cos_, rope_sin_, pq_, y.kc, y.vc, kvdt_, cap_,
-                                        stream_), "vsl_rope_split_append");
-            check(vsl_attn_prefill(pq_, y.kc, y.vc, S, c0, nq, nkv, hd, cap_, scale, pattn_, stream_), "vsl_attn_prefill");
-            check(vsl_gemm_f16(pattn_, y.wo, S, d, nq * hd, px_, VSL_EPI_RESID, stream_), "gemm o");
-            check(vsl_rmsnorm(px_, y.ffn_norm, S, d, eps, pxn_, VSL_DT_F16, stream_), "vsl_rmsnorm");
-            check(vsl_gemm_f16(pxn_, y.wgu, S, F, d, ph_, VSL_EPI_SWIGLU, stream_), "gemm gate/up");
-            check(vsl_gemm_f16(ph_, y.wdown, S, d, F, px_, VSL_EPI_RESID, stream_), "gemm down");
+            check(vsl_rmsnorm(px_, y.attn_norm, S, d, eps, pxn_, n1, stream_), "vsl_rmsnorm");
+            check(vsl_gemm_f16(pxn_, y.wqkv, S, (nq + 2 * nkv) * hd, d, pqkv_, g_qkv, stream_), "gemm qkv");
+            check(vsl_rope_split_append(pqkv_, S, nq, nkv, hd, c0, rope_cos_, rope_sin_, pq_, qdt, y.kc, y.vc, kvdt_,
+                                        cap_, stream_), "vsl_rope_split_append");
+            check(vsl_attn_prefill(pq_, qdt, y.kc, y.vc, S, c0, nq, nkv, hd, cap_, scale, pattn_, odt, stream_),
+                  "vsl_attn_prefill");
+            check(vsl_gemm_f16(pattn_, y.wo, S, d, nq * hd, px_, g_o, stream_), "gemm o");
+            check(vsl_rmsnorm(px_, y.ffn_norm, S, d, eps, pxn_, n2, stream_), "vsl_rmsnorm");
+            check(vsl_gemm_f16(pxn_, y.wgu, S, F, d, ph_, g_gu, stream_), "gemm gate/up");
+            check(vsl_gemm_f16(ph_, y.wdown, S, d, F, px_, g_dn, stream_), "gemm down");
         }
     }
     check(vsl_copy_d2d(x_, px_ + (size_t)(last_rows - 1) * d, (size_t)d * 4, stream_), "last row");
     check(vsl_ctrl_reset(ctrl_, n_prompt - 1, host_ctrl_->max_steps, host_ctrl_->stop_on_eos, cap_, stream_),
           "vsl_ctrl_reset");
     check(vsl_lm_head_sample(out_norm_, eps, out_w_, wdt_, V, d, x_, embed_, edt_, logits_, to_vsl_sampler(p), lm_val_,
-                             lm_idx_, lm_cnt_, tokens_, ctrl_, stream_),
+                             lm_idx_, tokens_, ctrl_, stream_),
           "vsl_lm_head_sample");
 }
 
@@ -754,7 +759,7 @@ double VulkanSymbioteEngine::time_op(int op, uint32_t iterations) {
                 break;
             case 1:
                 check(vsl_attn_decode(q_, y.kc, y.vc, kvdt_, nq, nkv, hd, cap_, scale, nsplit_, part_o_, part_ml_,
-                                      attn_cnt_, attn_, ctrl_, stream_), "attn");
+                                      attn_, ctrl_, stream_), "attn");
                 break;
             case 2: check(vsl_gemv_residual(y.wo, wdt_, d, nq * hd, attn_, x_, ctrl_, stream_), "o"); break;
             case 3: check(vsl_norm_swiglu(x_, y.ffn_norm, eps, y.wgu, wdt_, d, F, h_, ctrl_, stream_), "gate/up"); break;
@@ -763,7 +768,7 @@ double VulkanSymbioteEngine::time_op(int op, uint32_t iterations) {
                 SamplingParams p;
                 check(vsl_ctrl_reset(ctrl_, pos, 0xFFFFFFFFu, 0, cap_, stream_), "vsl_ctrl_reset");
                 check(vsl_lm_head_sample(out_norm_, eps, out_w_, wdt_, c.vocab_size, d, x_, embed_, edt_, logits_,
-                                         to_vsl_sampler(p), lm_val_, lm_idx_, lm_cnt_, tokens_, ctrl_, stream_), "lm_head");
+                                         to_vsl_sampler(p), lm_val_, lm_idx_, tokens_, ctrl_, stream_), "lm_head");
             }
         }
     };

@@ -28,6 +28,7 @@ extern "C" void vsl_engine_default_options(vsl_engine_options* o) {
     std::memset(o, 0, sizeof(*o));
     o->use_graph = 1;
     o->batched_prefill = 1;
+    o->prefill_split = EngineOptions::kPrefillSplitAll;
 }
 
 static EngineOptions to_options(const vsl_engine_options* o) {
@@ -39,6 +40,7 @@ static EngineOptions to_options(const vsl_engine_options* o) {
     e.prefill_chunk = o->prefill_chunk ? o->prefill_chunk : 2048;
     e.attn_splits = o->attn_splits;
     e.batched_prefill = o->batched_prefill != 0;
+    e.prefill_split = o->prefill_split & EngineOptions::kPrefillSplitAll;
     return e;
 }
 

@@ -66,7 +66,12 @@ struct EngineOptions {
     uint32_t prefill_chunk = 2048;
     uint32_t attn_splits = 0;     // 0 = chosen from the capacity
     bool batched_prefill = true;  // fp16 models: MFMA prefill (else token by token)
+    // Which prefill activations are carried as hi/lo fp16 pairs (two MFMAs per tile, ~22-bit
+    // inputs) instead of one rounded fp16 value: bit 0 QKV GEMM input, bit 1 attention (q and the
+    // probabilities), bit 2 O-projection input, bit 3 gate/up GEMM input, bit 4 down-projection input.
+    uint32_t prefill_split = kPrefillSplitAll;
     bool verbose = false;
+    static constexpr uint32_t kPrefillSplitAll = 0x1F;
 };
 
 // Synthetic Llama-style model: every linear weight ~ N(0, init_std) from the Philox stream keyed by
@@ -187,10 +192,8 @@ class VulkanSymbioteEngine {
     float* rope_sin_ = nullptr;
     float *x_ = nullptr, *q_ = nullptr, *attn_ = nullptr, *h_ = nullptr, *logits_ = nullptr;
     float *part_o_ = nullptr, *part_ml_ = nullptr;
-    uint32_t* attn_cnt_ = nullptr;
     float* lm_val_ = nullptr;
     uint32_t* lm_idx_ = nullptr;
-    uint32_t* lm_cnt_ = nullptr;
     uint32_t* tokens_ = nullptr;
     uint32_t* prompt_dev_ = nullptr;
     vsl_ctrl* ctrl_ = nullptr;
