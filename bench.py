@@ -26,6 +26,11 @@ CFG = dict(hidden_size=4096, num_layers=32, num_heads=32, num_kv_heads=8, interm
            max_position_embeddings=32768, rope_theta=500000.0, rms_eps=1e-5, dtype=1)
 KV_CAPACITY = 4096
 
+# HBM bytes per launch of the dominant decode kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+# passes summarised in profiles/decode_8b_rocprof.md (FETCH_SIZE scaled x1.9999 by a 1 GiB copy).
+# Re-measure with the commands listed there whenever the kernel changes.
+DOMINANT_TRAFFIC_BYTES = 235_220_000 + 57_000
+
 
 def load_package():
     name = "vulkan_symbiote_loader_amd"
@@ -100,6 +105,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-kernel-timing", action="store_true")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="after the run, copy this many MB device-to-device once (a kernel of known traffic "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--eager", action="store_true",
                     help="launch each decode step's kernels directly instead of replaying the captured hipGraph "
                          "(same kernels; used under rocprofv3, whose graph-launch interception crashes here)")
@@ -192,8 +200,10 @@ def main():
         dom = ops["norm_gateup_swiglu"]
         achieved = dom["bytes"] / (dom["avg_us"] * 1e-6)
         out["roofline"] = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
-                           "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
-                           "kernel": "k_gemv_dec<EPI_SWIGLU> (ffn norm + [Wgate;Wup] GEMV + SwiGLU)"}
+                           "frac": round(achieved / PEAK_HBM, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
+                           "algorithmic_bytes": dom["bytes"],
+                           "kernel": "k_gemv_dec<EPI_SWIGLU> (ffn norm + [Wgate;Wup] GEMV + SwiGLU)",
+                           "traffic_source": "profiles/decode_8b_rocprof.md"}
         out["decode_ops"] = ops
 
     if not a.no_cpu_baseline:
@@ -203,6 +213,19 @@ def main():
             out["cpu_baseline"] = {"value": None, "unit": "tok/s", "cores": None, "kind": "port",
                                    "sample": f"failed: {ex}"}
     eng.close()
+    if a.copy_calibration_mb:
+        import ctypes
+        H = vsl.hip()
+        nbytes = a.copy_calibration_mb << 20
+        arena = ctypes.c_void_p()
+        vsl.check(H.vsl_arena_create(0, 2 * nbytes + (1 << 20), ctypes.byref(arena)))
+        src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+        vsl.check(H.vsl_arena_alloc(arena, nbytes, 256, ctypes.byref(src)))
+        vsl.check(H.vsl_arena_alloc(arena, nbytes, 256, ctypes.byref(dst)))
+        vsl.check(H.vsl_copy_d2d(dst, src, nbytes, None))
+        vsl.check(H.vsl_device_sync())
+        vsl.check(H.vsl_arena_destroy(arena))
+        out["copy_calibration_bytes"] = nbytes
     print(json.dumps(out), flush=True)
 
 

@@ -1,7 +1,7 @@
 """ctypes wrapper of the oracle (oracle/libvsl_oracle.so).
 
-TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the cpu_baseline leg of
-bench.py, as the checker.  The product never imports it.
+TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke() entry point and the cpu_baseline leg of
+bench.py, as the oracle.  The product never imports it.
 """
 import ctypes
 import os

@@ -1,7 +1,7 @@
 /*
  * vsl_oracle.c -- CPU restatement of Vulkan-Symbiote-Loader's per-token forward pass.
  *
- * TEST INFRASTRUCTURE ONLY (the checker).  Loaded by tests/, __graft_entry__.smoke() and the
+ * TEST INFRASTRUCTURE ONLY (the oracle).  Loaded by tests/, the smoke() entry point and the
  * cpu_baseline leg of bench.py; never by the product.
  *
  * Parity pins (what checks each function; see tests/test_oracle.py):

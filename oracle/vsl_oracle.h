@@ -1,7 +1,7 @@
 /*
  * vsl_oracle.h -- CPU restatement of Vulkan-Symbiote-Loader's per-token forward pass.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/, the smoke() entry of
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle: only tests/, the smoke() entry point of
  * __graft_entry__.py and the cpu_baseline leg of bench.py may load it.  The product (the HIP
  * backend and its host engine) never links, loads or calls it, and has no CPU fallback.
  *
