@@ -7,11 +7,12 @@
 //   k_gemv_dec<EPI_RESID>  W_o / W_down -> residual add
 //   k_gemv_dec<EPI_SWIGLU> RMSNorm -> [Wgate;Wup] -> silu(g)*u
 //   k_gemv_dec<EPI_ARGMAX> final RMSNorm -> W_out -> logits + fused greedy argmax + next embedding
-// and k_attn_decode is a split-KV flash-decode kernel with an in-kernel combine.
+// k_attn_decode is a split-KV flash-decode kernel whose partials k_attn_combine merges.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 
 #include "vsl_device.h"
 #include "vsl_hip.h"
@@ -52,35 +53,85 @@ struct GemvArgs {
 // ---------------------------------------------------------------------------------------------
 // activation staging (optionally RMS-normalised, rms_norm.comp:24-34)
 // ---------------------------------------------------------------------------------------------
-__device__ __forceinline__ void stage_x(const float* __restrict__ x, const float* __restrict__ gamma, float eps,
-                                        uint32_t K, float* __restrict__ xs, float* red) {
-    const uint32_t tid = threadIdx.x;
-    float ss = 0.f;
-    for (uint32_t i = tid * 4; i < K; i += kBlock * 4) {
-        float4 v = *reinterpret_cast<const float4*>(x + i);
-        *reinterpret_cast<float4*>(xs + i) = v;
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
-    if (gamma) {
-        ss = wave_sum(ss);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-        __syncthreads();
-        float tot = 0.f;
+// Barrier for LDS traffic only: waits for this wave's LDS operations, not for its outstanding
+// global loads (the weight stream keeps flowing across it).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The block's activation slice lives in registers between its loads and the LDS store, so that
+// the loads can be issued ahead of the first weight tile (vector loads complete in issue order:
+// waiting for the activations then never waits for the weights behind them).
+template <int WAVES>
+struct XStage {
+    static constexpr uint32_t NT = WAVES * 64;
+    static constexpr int XPT = 8;  // float4 per thread: K <= 8192 at 4 waves, K <= 16384 at 8 waves
+    float4 xr[XPT];
+    float4 gr[XPT];
+
+    // Branch-free, with indexes past K clamped to 0: the waits that later consume these registers
+    // then count exactly the loads issued after them.
+    __device__ __forceinline__ void load(const float* __restrict__ x, const float* __restrict__ gamma, uint32_t K) {
+        const uint32_t tid = threadIdx.x;
+        const float* g = gamma ? gamma : x;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) tot += red[w];
-        const float inv = 1.0f / sqrtf(tot / (float)K + eps);
-        for (uint32_t i = tid * 4; i < K; i += kBlock * 4) {
-            float4 v = *reinterpret_cast<float4*>(xs + i);
-            float4 g = *reinterpret_cast<const float4*>(gamma + i);
-            v.x = v.x * inv * g.x;
-            v.y = v.y * inv * g.y;
-            v.z = v.z * inv * g.z;
-            v.w = v.w * inv * g.w;
-            *reinterpret_cast<float4*>(xs + i) = v;
+        for (int j = 0; j < XPT; ++j) {
+            const uint32_t i = (j * NT + tid) * 4;
+            const uint32_t ic = i < K ? i : 0;
+            xr[j] = *reinterpret_cast<const float4*>(x + ic);
+            gr[j] = *reinterpret_cast<const float4*>(g + ic);
         }
     }
-    __syncthreads();
-}
+    // RMS-normalise (rms_norm.comp:24-34) when gamma is given, and store to LDS as fp32
+    __device__ __forceinline__ void store(const float* __restrict__ gamma, float eps, uint32_t K, float* __restrict__ xs,
+                                          float* red) {
+        const uint32_t tid = threadIdx.x;
+        // Read every staged register here, on every path: the branches below would otherwise leave
+        // some loads pending, and the loop's first weight issue would wait on them.
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            asm volatile("" ::"v"(xr[j].x), "v"(xr[j].y), "v"(xr[j].z), "v"(xr[j].w));
+            asm volatile("" ::"v"(gr[j].x), "v"(gr[j].y), "v"(gr[j].z), "v"(gr[j].w));
+        }
+        float inv = 1.f;
+        if (gamma) {
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < XPT; ++j) {
+                const uint32_t i = (j * NT + tid) * 4;
+                if (j * NT * 4 < K && i < K) {
+                    const float4 v = xr[j];
+                    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                }
+            }
+            ss = wave_sum_dpp(ss);
+            if ((tid & 63) == 0) red[tid >> 6] = ss;
+            lds_barrier();
+            float tot = 0.f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) tot += red[w];
+            inv = 1.0f / sqrtf(tot / (float)K + eps);
+        }
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const uint32_t i = (j * NT + tid) * 4;
+            if (j * NT * 4 < K && i < K) {
+                float4 v = xr[j];
+                if (gamma) {
+                    const float4 g = gr[j];
+                    v.x = v.x * inv * g.x;
+                    v.y = v.y * inv * g.y;
+                    v.z = v.z * inv * g.z;
+                    v.w = v.w * inv * g.w;
+                }
+                *reinterpret_cast<float4*>(xs + i) = v;
+            }
+        }
+        lds_barrier();
+    }
+};
 
 template <class WT>
 __device__ __forceinline__ void load_x(const float* xs, uint32_t kk, float* xv) {
@@ -124,40 +175,37 @@ __device__ void finish_token(uint32_t tok, uint32_t V, uint32_t d, const void* e
 // ---------------------------------------------------------------------------------------------
 // decode GEMV
 // ---------------------------------------------------------------------------------------------
-template <class WT, int R, int U, int EPI, class ET>
-__global__ __launch_bounds__(kBlock) void k_gemv_dec(GemvArgs a) {
-    __shared__ float red[kWaves];
-    __shared__ float bval[kWaves];
-    __shared__ uint32_t bidx[kWaves];
+// Work unit: a row group (R weight rows; EPI_SWIGLU: R/2 gate rows + the matching up rows) split
+// into K-chunks of U x 64 lanes x 16 bytes. A wave walks its tiles (group, chunk) with two register
+// buffers: tile t+1 is requested before tile t is consumed, so every wave keeps one tile in
+// flight at all times, including across its row-group boundaries. Operands the epilogue reads
+// from memory (residual rows, RoPE angles) are requested together with each tile.
+template <class WT, int R, int U, int EPI, class ET, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
+    __shared__ float red[WAVES];
+    __shared__ float bval[WAVES];
+    __shared__ uint32_t bidx[WAVES];
     extern __shared__ float xs[];
-
-    uint32_t pos = 0;
-    if (a.ctrl) {
-        if (a.ctrl->done) return;
-        pos = a.ctrl->pos;
-        if constexpr (EPI == EPI_QKV) {
-            if (pos >= a.cap) {
-                if (blockIdx.x == 0 && threadIdx.x == 0) { a.ctrl->error = 1u; a.ctrl->done = 1u; }
-                return;
-            }
-        }
-    }
-    stage_x(a.x, a.gamma, a.eps, a.K, xs, red);
 
     typedef typename WT::T T;
     constexpr int VEC = WT::kVec;
     constexpr uint32_t SPAN = 64 * VEC;
-    const T* __restrict__ W = static_cast<const T*>(a.W);
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr uint32_t CHUNK = SPAN * U;
     constexpr int RG = (EPI == EPI_SWIGLU) ? R / 2 : R;  // logical rows per group
+    static_assert(EPI != EPI_SWIGLU || R % 2 == 0, "SwiGLU groups pair gate and up rows");
+    static_assert(EPI != EPI_QKV || R % 2 == 0, "QKV groups hold whole RoPE pairs");
+    const T* __restrict__ W = static_cast<const T*>(a.W);
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const uint32_t n_groups = (a.N + RG - 1) / RG;
+    const uint32_t stride = gridDim.x * WAVES;
+    const uint32_t g0 = blockIdx.x * WAVES + wave;
+    const uint32_t cpg = (a.K + CHUNK - 1) / CHUNK;  // chunks per group
+    const uint32_t n_tiles = g0 < n_groups ? ((n_groups - 1 - g0) / stride + 1) * cpg : 0;
 
-    float best_v = -INFINITY;
-    uint32_t best_i = 0xFFFFFFFFu;
+    uint32_t pos = 0;
 
-    for (uint32_t g = blockIdx.x * kWaves + wave; g < n_groups; g += gridDim.x * kWaves) {
-        uint32_t rows[R];
-        bool ok[R];
+    auto group_rows = [&](uint32_t g, uint32_t* rows, bool* ok) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if constexpr (EPI == EPI_SWIGLU) {
@@ -169,42 +217,65 @@ __global__ __launch_bounds__(kBlock) void k_gemv_dec(GemvArgs a) {
                 ok[r] = rows[r] < a.N;
             }
         }
-        float acc[R];
+    };
+    // weights of tile t
+    auto issue_w = [&](uint4 (&w)[R][U], uint32_t t) {
+        const uint32_t gi = t / cpg, c = t - gi * cpg;
+        const uint32_t k0 = c * CHUNK;
+        uint32_t rows[R];
+        bool ok[R];
+        group_rows(g0 + gi * stride, rows, ok);
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = 0.f;
-
-        for (uint32_t k0 = 0; k0 < a.K; k0 += SPAN * U) {
-            uint4 w[R][U];
+        for (int u = 0; u < U; ++u) {
+            const uint32_t kk = k0 + u * SPAN + lane * VEC;
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t kk = k0 + u * SPAN + lane * VEC;
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    if (ok[r] && kk < a.K)
-                        w[r][u] = load16<true>(W + (size_t)rows[r] * a.K + kk);
-                    else
-                        w[r][u] = make_uint4(0u, 0u, 0u, 0u);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const uint32_t kk = k0 + u * SPAN + lane * VEC;
-                if (kk < a.K) {
-                    float xv[VEC];
-                    load_x<WT>(xs, kk, xv);
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float wf[VEC];
-                        unpack(w[r][u], WT(), wf);
-#pragma unroll
-                        for (int i = 0; i < VEC; ++i) acc[r] = fmaf(wf[i], xv[i], acc[r]);
-                    }
-                }
+            for (int r = 0; r < R; ++r) {
+                // Out-of-range rows and columns load element 0 of the matrix instead: no branch
+                // or select touches a tile between its loads and its use (columns past K are
+                // skipped in consume, rows past N never reach an output).
+                const bool in = ok[r] && kk < a.K;
+                w[r][u] = load16<true>(W + (in ? (size_t)rows[r] * a.K + kk : 0));
             }
         }
+    };
+    // operands the epilogue reads from memory
+    // (requested with every tile, so that no branch separates a tile's loads from their waits)
+    auto issue_pf = [&](float (&pf)[R], uint32_t t) {
+        const uint32_t gi = t / cpg;
+        uint32_t rows[R];
+        bool ok[R];
+        group_rows(g0 + gi * stride, rows, ok);
+        // addresses are clamped in range; rows past N are never stored
+        if constexpr (EPI == EPI_RESID) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+            for (int r = 0; r < R; ++r) pf[r] = a.y[ok[r] ? rows[r] : 0];
+        } else if constexpr (EPI == EPI_QKV) {
+            const uint32_t half = a.hd >> 1;
+#pragma unroll
+            for (int r = 0; r < R; r += 2) {
+                const size_t ti = (size_t)pos * half + ((rows[r] % a.hd) >> 1);  // pos < cap here
+                pf[r] = a.rope_cos[ti];
+                pf[r + 1] = a.rope_sin[ti];
+            }
+        }
+    };
+    auto issue = [&](uint4 (&w)[R][U], float (&pf)[R], uint32_t t) {
+        issue_w(w, t);
+        issue_pf(pf, t);
+    };
 
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    float best_v = -INFINITY;
+    uint32_t best_i = 0xFFFFFFFFu;
+
+    auto epilogue = [&](uint32_t g, const float (&pf)[R]) {
+        uint32_t rows[R];
+        bool ok[R];
+        group_rows(g, rows, ok);
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = wave_sum_dpp(acc[r]);
         if constexpr (EPI == EPI_STORE) {
             if (lane == 0) {
 #pragma unroll
@@ -221,7 +292,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv_dec(GemvArgs a) {
             if (lane == 0) {
 #pragma unroll
                 for (int r = 0; r < R; ++r)
-                    if (ok[r]) a.y[rows[r]] += acc[r];
+                    if (ok[r]) a.y[rows[r]] = pf[r] + acc[r];
             }
         } else if constexpr (EPI == EPI_SWIGLU) {
             if (lane == 0) {
@@ -230,23 +301,17 @@ __global__ __launch_bounds__(kBlock) void k_gemv_dec(GemvArgs a) {
                     if (ok[r]) a.y[rows[r]] = silu(acc[r]) * acc[r + RG];
             }
         } else if constexpr (EPI == EPI_QKV) {
-            static_assert(R % 2 == 0, "QKV groups hold whole RoPE pairs");
             if (lane == 0) {
                 const uint32_t qrows = a.n_q * a.hd, krows = a.n_kv * a.hd;
 #pragma unroll
                 for (int r = 0; r < R; r += 2) {
                     if (!ok[r]) continue;
                     const uint32_t row = rows[r];
-                    float v0 = acc[r], v1 = acc[r + 1];
-                    if (row < qrows + krows) {  // RoPE on q and k (adjacent pair row, row+1)
-                        const uint32_t j = (row % a.hd) >> 1;
-                        const float c = a.rope_cos[(size_t)pos * (a.hd >> 1) + j];
-                        const float s = a.rope_sin[(size_t)pos * (a.hd >> 1) + j];
-                        const float r0 = v0 * c - v1 * s;
-                        const float r1 = v0 * s + v1 * c;
-                        v0 = r0;
-                        v1 = r1;
-                    }
+                    // RoPE on q and k rows (adjacent pair row, row+1); v rows pass through
+                    const bool rot = row < qrows + krows;
+                    const float c = rot ? pf[r] : 1.f, sn = rot ? pf[r + 1] : 0.f;
+                    const float v0 = acc[r] * c - acc[r + 1] * sn;
+                    const float v1 = acc[r] * sn + acc[r + 1] * c;
                     if (row < qrows) {
                         a.q_out[row] = v0;
                         a.q_out[row + 1] = v1;
@@ -271,6 +336,74 @@ __global__ __launch_bounds__(kBlock) void k_gemv_dec(GemvArgs a) {
                 }
             }
         }
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    };
+    // Every register of a tile is read on every path (columns past K are zeroed by selects, not
+    // skipped by branches), so no path leaves a load pending into the next issue of its buffer.
+    auto consume = [&](const uint4 (&w)[R][U], const float (&pf)[R], uint32_t t) {
+        const uint32_t gi = t / cpg, c = t - gi * cpg;
+        const uint32_t k0 = c * CHUNK;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t kk = k0 + u * SPAN + lane * VEC;
+            const bool in = kk < a.K;
+            float xv[VEC];
+            load_x<WT>(xs, in ? kk : 0, xv);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint4 wr = in ? w[r][u] : make_uint4(0u, 0u, 0u, 0u);
+                float wf[VEC];
+                unpack(wr, WT(), wf);
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) acc[r] = fmaf(wf[i], xv[i], acc[r]);
+            }
+        }
+        if constexpr (EPI == EPI_RESID || EPI == EPI_QKV) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) asm volatile("" ::"v"(pf[r]));
+        }
+        if (c == cpg - 1) epilogue(g0 + gi * stride, pf);
+    };
+
+    // Prologue: activation and gain loads, then the first weight tile, then the control block; the
+    // staging, the norm and the control-block latency all complete under the weight fetch.
+    XStage<WAVES> st;
+    st.load(a.x, a.gamma, a.K);
+    uint4 wa[R][U], wb[R][U];
+    float pa[R], pb[R];
+    issue_w(wa, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (a.ctrl) {
+        if (a.ctrl->done) return;
+        pos = a.ctrl->pos;
+    }
+    if constexpr (EPI == EPI_QKV) {
+        if (pos >= a.cap) {
+            if (blockIdx.x == 0 && threadIdx.x == 0) {
+                a.ctrl->error = 1u;
+                a.ctrl->done = 1u;
+            }
+            return;
+        }
+    }
+    issue_pf(pa, 0);  // the RoPE angles depend on pos
+    st.store(a.gamma, a.eps, a.K, xs, red);
+
+    // Straight-line pairs with a single loop exit: the compiler's memory-counter waits merge over
+    // every control-flow edge, so a conditional issue, a skipped consume or a mid-loop exit would
+    // leave a buffer's loads pending on some edge and serialise the pipeline. An odd tile count is
+    // padded with one tile past the wave's last group (clamped addresses, no output rows), and the
+    // tile issued by the last pair is never consumed.
+    const uint32_t n_pairs = (n_tiles + 1) / 2;
+    // (sched_barrier: keep each issue ahead of the previous tile's arithmetic in the schedule)
+    for (uint32_t p = 0; p < n_pairs; ++p) {
+        issue(wb, pb, 2 * p + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(wa, pa, 2 * p);
+        issue(wa, pa, 2 * p + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(wb, pb, 2 * p + 1);
     }
 
     if constexpr (EPI == EPI_ARGMAX) {
@@ -285,7 +418,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv_dec(GemvArgs a) {
             float v = bval[0];
             uint32_t i = bidx[0];
 #pragma unroll
-            for (int w = 1; w < kWaves; ++w) argmax_merge(v, i, bval[w], bidx[w]);
+            for (int w = 1; w < WAVES; ++w) argmax_merge(v, i, bval[w], bidx[w]);
             a.ws_val[blockIdx.x] = v;
             a.ws_idx[blockIdx.x] = i;
         }
@@ -323,22 +456,62 @@ __global__ __launch_bounds__(kFinishThreads) void k_argmax_finish(const float* _
     finish_token<ET>(bidx[0], V, d, embed, x_next, tokens, ctrl);
 }
 
-template <int R, int EPI>
+// Upper bound on a decode GEMV's grid: blocks-per-CU x the current device's CU count, 4 by default
+// (16 waves per CU at 4-wave blocks: one resident round), VSL_GEMV_BLOCKS_PER_CU overrides it and
+// 0 removes the bound. A bounded grid strides over the row groups, staging the activation vector
+// once per block instead of once per few groups.
+uint32_t gemv_grid_cap() {
+    static int per_cu = -1;
+    if (per_cu < 0) {
+        const char* e = getenv("VSL_GEMV_BLOCKS_PER_CU");
+        per_cu = e ? atoi(e) : 4;
+        if (per_cu < 0) per_cu = 0;
+    }
+    if (per_cu == 0) return 0xFFFFFFFFu;
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0xFFFFFFFFu;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return (uint32_t)per_cu * (uint32_t)cus[dev];
+}
+
+template <int R, int EPI, int WAVES>
 uint32_t gemv_blocks(uint32_t N, uint32_t max_blocks) {
     constexpr int RG = (EPI == EPI_SWIGLU) ? R / 2 : R;
     const uint32_t groups = (N + RG - 1) / RG;
-    uint32_t blocks = (groups + kWaves - 1) / kWaves;
+    uint32_t blocks = (groups + WAVES - 1) / WAVES;
     if (blocks > max_blocks) blocks = max_blocks;
+    const uint32_t cap = gemv_grid_cap();
+    if (blocks > cap) blocks = cap;
     return blocks == 0 ? 1 : blocks;
 }
 
-template <class WT, int R, int U, int EPI, class ET = WF32>
+template <class WT, int R, int U, int EPI, int WAVES, class ET = WF32>
 int launch_gemv(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
-    const uint32_t blocks = gemv_blocks<R, EPI>(a.N, max_blocks);
+    const uint32_t blocks = gemv_blocks<R, EPI, WAVES>(a.N, max_blocks);
     const size_t lds = (size_t)a.K * sizeof(float);
-    k_gemv_dec<WT, R, U, EPI, ET><<<blocks, kBlock, lds, s>>>(a);
+    k_gemv_dec<WT, R, U, EPI, ET, WAVES><<<blocks, WAVES * 64, lds, s>>>(a);
     HIP_TRY(hipGetLastError());
     return VSL_OK;
+}
+
+// Block size by K: the fp32 activation vector takes K*4 bytes of LDS per block; past 8192
+// columns, 8-wave blocks keep 16 waves resident per CU within the 160 KB of LDS.
+constexpr uint32_t kWideK = 8192;
+
+template <class WT, int R, int U, int EPI, class ET = WF32>
+int launch_gemv_k(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
+    return a.K > kWideK ? launch_gemv<WT, R, U, EPI, 8, ET>(a, max_blocks, s)
+                        : launch_gemv<WT, R, U, EPI, 4, ET>(a, max_blocks, s);
+}
+
+template <int R, int EPI>
+uint32_t gemv_blocks_k(uint32_t N, uint32_t K, uint32_t max_blocks) {
+    return K > kWideK ? gemv_blocks<R, EPI, 8>(N, max_blocks) : gemv_blocks<R, EPI, 4>(N, max_blocks);
 }
 
 constexpr uint32_t kMaxK = 16384;  // activation vector held in LDS as fp32 (64 KB)
@@ -351,10 +524,15 @@ int check_gemv_shape(uint32_t N, uint32_t K, const char* who) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// flash-decode attention (split-KV, online softmax, in-kernel combine)
+// flash-decode attention (split-KV, online softmax) + split combine
 // ---------------------------------------------------------------------------------------------
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Block (split s, KV head h). Positions are taken in tiles of NSLOT (one position per LPP-lane
+// group); block s owns tiles s, s + nsplit, s + 2 nsplit, ... A block's tile addresses do not
+// depend on the sequence length, so its first tile is requested before the control block is read,
+// and every next tile before the current one is consumed (two register buffers, as in the GEMV).
+// Positions at or past the length are masked by selects; tiles past the cache read position 0.
 template <class KT, int HD, int G>
 __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict__ q, const void* __restrict__ kcache,
                                                         const void* __restrict__ vcache, uint32_t n_q, uint32_t n_kv,
@@ -362,32 +540,60 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
                                                         float* __restrict__ part_o, float* __restrict__ part_ml,
                                                         vsl_ctrl* ctrl) {
     typedef typename KT::T T;
-    constexpr int LPP = HD / 8;            // lanes per position (8 elements of 16 bytes... per lane)
-    constexpr int SLOTS = 64 / LPP;        // positions per wave per step
-    constexpr int NSLOT = kWaves * SLOTS;  // positions per block per step
+    constexpr int LPP = HD / 8;            // lanes per position, 8 elements per lane
+    constexpr int SLOTS = 64 / LPP;        // positions per wave per tile
+    constexpr int NSLOT = kWaves * SLOTS;  // positions per tile
+    constexpr int KW = sizeof(T) * 8 / 16; // 16-byte loads per lane per row (1 fp16, 2 fp32)
     __shared__ float s_ml[NSLOT][G][2];
     __shared__ float s_acc[NSLOT][G][HD];
 
-    if (ctrl->done) return;
-    const uint32_t pos = ctrl->pos;
-    if (pos >= cap) return;
-    const uint32_t len = pos + 1;
     const uint32_t kvh = blockIdx.y, split = blockIdx.x;
-    uint32_t chunk = (len + nsplit - 1) / nsplit;
-    chunk = (chunk + NSLOT - 1) / NSLOT * NSLOT;
-    const uint32_t s0 = split * chunk;
-    const uint32_t s1 = min(len, s0 + chunk);
-
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t slot = lane / LPP, sub = lane % LPP;
     const uint32_t h0 = kvh * G;  // first query head of this KV head (kv_head = head*n_kv/n_q)
+    const T* Kb = static_cast<const T*>(kcache) + (size_t)kvh * cap * HD;
+    const T* Vb = static_cast<const T*>(vcache) + (size_t)kvh * cap * HD;
+
+    struct Tile {
+        uint4 k[KW], v[KW];
+    };
+    auto position = [&](uint32_t j) { return (j * nsplit + split) * NSLOT + wave * SLOTS + slot; };
+    // positions at or past `limit` read position 0 instead (in bounds, and the same cache lines
+    // for every such lane)
+    auto issue = [&](Tile& b, uint32_t j, uint32_t limit) {
+        uint32_t t = position(j);
+        t = t < limit ? t : 0;
+        const T* kp = Kb + (size_t)t * HD + sub * 8;
+        const T* vp = Vb + (size_t)t * HD + sub * 8;
+#pragma unroll
+        for (int w = 0; w < KW; ++w) {
+            b.k[w] = load16<false>(kp + w * (8 / KW));
+            b.v[w] = load16<false>(vp + w * (8 / KW));
+        }
+    };
+
+    // q and the first two tiles are requested before the control block is read. Both tiles are
+    // consumed on every path and no branch depends on `done` (it only gates the stores), so the
+    // compiler has no path to sink these loads into behind the control-block wait.
+    float4 qr[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float* qp = q + (size_t)(h0 + g) * HD + sub * 8;
+        qr[g][0] = *reinterpret_cast<const float4*>(qp);
+        qr[g][1] = *reinterpret_cast<const float4*>(qp + 4);
+    }
+    Tile ta, tb;
+    issue(ta, 0, cap);
+    issue(tb, 1, cap);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t done = ctrl->done;
+    const uint32_t pos = ctrl->pos;
+    const uint32_t len = pos < cap ? pos + 1 : cap;  // pos >= cap only with done set
 
     float qv[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const float* qp = q + (size_t)(h0 + g) * HD + sub * 8;
-        float4 a = *reinterpret_cast<const float4*>(qp);
-        float4 b = *reinterpret_cast<const float4*>(qp + 4);
+        const float4 a = qr[g][0], b = qr[g][1];
         const float f = scale * kLog2e;
         qv[g][0] = a.x * f; qv[g][1] = a.y * f; qv[g][2] = a.z * f; qv[g][3] = a.w * f;
         qv[g][4] = b.x * f; qv[g][5] = b.y * f; qv[g][6] = b.z * f; qv[g][7] = b.w * f;
@@ -401,38 +607,54 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
         for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
     }
 
-    const T* Kb = static_cast<const T*>(kcache) + (size_t)kvh * cap * HD;
-    const T* Vb = static_cast<const T*>(vcache) + (size_t)kvh * cap * HD;
-    for (uint32_t t = s0 + wave * SLOTS + slot; t < s1; t += NSLOT) {
+    auto consume = [&](const Tile& b, uint32_t j) {
+        const bool valid = position(j) < len;
         float kf[8], vf[8];
-        if constexpr (sizeof(T) == 2) {
-            uint4 kr = *reinterpret_cast<const uint4*>(Kb + (size_t)t * HD + sub * 8);
-            uint4 vr = *reinterpret_cast<const uint4*>(Vb + (size_t)t * HD + sub * 8);
-            unpack(kr, WF16(), kf);
-            unpack(vr, WF16(), vf);
+        if constexpr (KW == 1) {
+            unpack(b.k[0], KT(), kf);
+            unpack(b.v[0], KT(), vf);
         } else {
-            const float* kp = reinterpret_cast<const float*>(Kb) + (size_t)t * HD + sub * 8;
-            const float* vp = reinterpret_cast<const float*>(Vb) + (size_t)t * HD + sub * 8;
-            float4 k0 = *reinterpret_cast<const float4*>(kp), k1 = *reinterpret_cast<const float4*>(kp + 4);
-            float4 v0 = *reinterpret_cast<const float4*>(vp), v1 = *reinterpret_cast<const float4*>(vp + 4);
-            kf[0] = k0.x; kf[1] = k0.y; kf[2] = k0.z; kf[3] = k0.w; kf[4] = k1.x; kf[5] = k1.y; kf[6] = k1.z; kf[7] = k1.w;
-            vf[0] = v0.x; vf[1] = v0.y; vf[2] = v0.z; vf[3] = v0.w; vf[4] = v1.x; vf[5] = v1.y; vf[6] = v1.z; vf[7] = v1.w;
+            unpack(b.k[0], KT(), kf);
+            unpack(b.k[1], KT(), kf + 4);
+            unpack(b.v[0], KT(), vf);
+            unpack(b.v[1], KT(), vf + 4);
         }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vf[i] = valid ? vf[i] : 0.f;  // cache memory past len is arbitrary
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float sc = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) sc = fmaf(qv[g][i], kf[i], sc);
             sc = group_sum<LPP>(sc);
-            const float mn = fmaxf(m[g], sc);
-            const float corr = exp2f(m[g] - mn);
-            const float p = exp2f(sc - mn);
+            const float mn = valid ? fmaxf(m[g], sc) : m[g];
+            const float corr = valid ? exp2f(m[g] - mn) : 1.f;
+            const float p = valid ? exp2f(sc - mn) : 0.f;
             l[g] = l[g] * corr + p;
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[i], acc[g][i] * corr);
             m[g] = mn;
         }
+    };
+
+    consume(ta, 0);
+    issue(ta, 2, len);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(tb, 1);
+    const uint32_t total = (len + NSLOT - 1) / NSLOT;  // tiles holding positions < len
+    const uint32_t mine = total > split ? (total - 1 - split) / nsplit + 1 : 0;
+    // tiles 2 .. mine-1 in pairs with a single loop exit (an odd remainder is padded with one
+    // masked tile); the tile issued by the last pair is never consumed
+    const uint32_t n_pairs = mine > 2 ? (mine - 1) / 2 : 0;
+    for (uint32_t pp = 0; pp < n_pairs; ++pp) {
+        issue(tb, 2 * pp + 3, len);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(ta, 2 * pp + 2);
+        issue(ta, 2 * pp + 4, len);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(tb, 2 * pp + 3);
     }
+
     // per-slot partials -> LDS -> block combine
     const uint32_t sl = wave * SLOTS + slot;
 #pragma unroll
@@ -444,7 +666,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
 #pragma unroll
         for (int i = 0; i < 8; ++i) s_acc[sl][g][sub * 8 + i] = acc[g][i];
     }
-    __syncthreads();
+    lds_barrier();  // (no wait on the unconsumed tile's loads)
     for (uint32_t e = threadIdx.x; e < (uint32_t)(G * HD); e += kBlock) {
         const uint32_t g = e / HD, dd = e % HD;
         float M = -INFINITY;
@@ -458,34 +680,60 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
             }
         }
         const size_t pidx = (size_t)(h0 + g) * nsplit + split;
-        part_o[pidx * HD + dd] = A;
-        if (dd == 0) {
-            part_ml[pidx * 2 + 0] = M;
-            part_ml[pidx * 2 + 1] = L;
+        if (!done) {
+            part_o[pidx * HD + dd] = A;
+            if (dd == 0) {
+                part_ml[pidx * 2 + 0] = M;
+                part_ml[pidx * 2 + 1] = L;
+            }
         }
+    }
+    // The padding tile's registers stay allocated to the end: reused earlier, they would make the
+    // combine above wait for those (discarded) loads.
+#pragma unroll
+    for (int w = 0; w < KW; ++w) {
+        asm volatile("" ::"v"(ta.k[w].x), "v"(ta.k[w].y), "v"(ta.k[w].z), "v"(ta.k[w].w));
+        asm volatile("" ::"v"(ta.v[w].x), "v"(ta.v[w].y), "v"(ta.v[w].z), "v"(ta.v[w].w));
     }
 }
 
 // Combines the nsplit partials of every query head: out = sum_s A_s 2^(m_s-M) / sum_s l_s 2^(m_s-M).
-// One block per head; the split weights are computed once (one thread per split) and the output
-// dimensions accumulate over splits with independent loads.
+// One block per head. Up to kFastSplits splits, every partial is requested at once (before the
+// control block is read) and held in registers; larger split counts loop over the splits.
 constexpr int kCombineThreads = 128;
 constexpr uint32_t kMaxSplits = 1024;
-template <int HD>
+constexpr int kFastSplits = 64;
+template <int HD, bool FAST>
 __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(const float* __restrict__ part_o,
                                                                   const float* __restrict__ part_ml, uint32_t nsplit,
                                                                   float* __restrict__ out, const vsl_ctrl* ctrl) {
     __shared__ float wts[kMaxSplits];
     __shared__ float red[kCombineThreads / 64];
     __shared__ float s_M, s_L;
-    if (ctrl->done) return;
     const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t base = (size_t)h * nsplit;
+    const uint32_t dd = tid < (uint32_t)HD ? tid : 0;
+    float o[FAST ? kFastSplits : 1];
+    float m0 = -INFINITY, l0 = 0.f;
+    if constexpr (FAST) {
+        if (tid < nsplit) {
+            m0 = part_ml[(base + tid) * 2];
+            l0 = part_ml[(base + tid) * 2 + 1];
+        }
+#pragma unroll
+        for (int s = 0; s < kFastSplits; ++s) o[s] = part_o[(base + (s < (int)nsplit ? s : 0)) * HD + dd];
+    }
+    const uint32_t done = ctrl->done;  // gates the store only (no branch to sink the loads behind)
     float mx = -INFINITY;
-    for (uint32_t s = tid; s < nsplit; s += kCombineThreads) {
-        const float m = part_ml[(base + s) * 2];
-        wts[s] = m;
-        mx = fmaxf(mx, m);
+    if constexpr (FAST) {
+        wts[tid] = m0;
+        mx = m0;
+    } else {
+        for (uint32_t s = tid; s < nsplit; s += kCombineThreads) {
+            const float m = part_ml[(base + s) * 2];
+            wts[s] = m;
+            mx = fmaxf(mx, m);
+        }
     }
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
@@ -498,11 +746,17 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(const float* _
     __syncthreads();
     const float M = s_M;
     float lsum = 0.f;
-    for (uint32_t s = tid; s < nsplit; s += kCombineThreads) {
-        const float m = wts[s];
-        const float f = m == -INFINITY ? 0.f : exp2f(m - M);
-        wts[s] = f;
-        lsum += part_ml[(base + s) * 2 + 1] * f;
+    if constexpr (FAST) {
+        const float f = (tid >= nsplit || m0 == -INFINITY) ? 0.f : exp2f(m0 - M);
+        wts[tid] = f;
+        lsum = l0 * f;
+    } else {
+        for (uint32_t s = tid; s < nsplit; s += kCombineThreads) {
+            const float m = wts[s];
+            const float f = m == -INFINITY ? 0.f : exp2f(m - M);
+            wts[s] = f;
+            lsum += part_ml[(base + s) * 2 + 1] * f;
+        }
     }
     lsum = wave_sum(lsum);
     __syncthreads();
@@ -515,8 +769,18 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(const float* _
     }
     __syncthreads();
     const float inv = 1.0f / s_L;
-    for (uint32_t dd = tid; dd < (uint32_t)HD; dd += kCombineThreads) {
-        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    if (tid >= (uint32_t)HD) return;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    if constexpr (FAST) {
+#pragma unroll
+        for (int s = 0; s < kFastSplits; s += 4) {
+            // splits past nsplit carry weight 0 (wts[s] was written for every s < kCombineThreads)
+            a0 = fmaf(o[s], wts[s], a0);
+            a1 = fmaf(o[s + 1], wts[s + 1], a1);
+            a2 = fmaf(o[s + 2], wts[s + 2], a2);
+            a3 = fmaf(o[s + 3], wts[s + 3], a3);
+        }
+    } else {
         uint32_t s = 0;
         for (; s + 4 <= nsplit; s += 4) {
             a0 = fmaf(part_o[(base + s) * HD + dd], wts[s], a0);
@@ -525,8 +789,8 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(const float* _
             a3 = fmaf(part_o[(base + s + 3) * HD + dd], wts[s + 3], a3);
         }
         for (; s < nsplit; ++s) a0 = fmaf(part_o[(base + s) * HD + dd], wts[s], a0);
-        out[(size_t)h * HD + dd] = ((a0 + a1) + (a2 + a3)) * inv;
     }
+    if (!done) out[(size_t)h * HD + dd] = ((a0 + a1) + (a2 + a3)) * inv;
 }
 
 template <class KT, int HD>
@@ -541,7 +805,10 @@ int launch_attn_g(uint32_t G, dim3 grid, hipStream_t s, const float* q, const vo
         default: return vsl_unsupported("vsl_attn_decode: GQA ratio %u (supported 1,2,4,8)", G);
     }
     HIP_TRY(hipGetLastError());
-    k_attn_combine<HD><<<n_q, kCombineThreads, 0, s>>>(po, pml, nsplit, out, ctrl);
+    if (nsplit <= (uint32_t)kFastSplits)
+        k_attn_combine<HD, true><<<n_q, kCombineThreads, 0, s>>>(po, pml, nsplit, out, ctrl);
+    else
+        k_attn_combine<HD, false><<<n_q, kCombineThreads, 0, s>>>(po, pml, nsplit, out, ctrl);
     HIP_TRY(hipGetLastError());
     return VSL_OK;
 }
@@ -807,10 +1074,10 @@ extern "C" int vsl_gemv(const void* W, int wdtype, uint32_t N, uint32_t K, const
         a.x = static_cast<const float*>(X);
         a.y = static_cast<float*>(Y);
         if (wdtype == VSL_DT_F16)
-            return ydtype == VSL_DT_F16 ? launch_gemv<WF16, 2, 8, EPI_STORE_F16>(a, 1u << 20, s)
-                                        : launch_gemv<WF16, 2, 8, EPI_STORE>(a, 1u << 20, s);
-        return ydtype == VSL_DT_F16 ? launch_gemv<WF32, 2, 8, EPI_STORE_F16>(a, 1u << 20, s)
-                                    : launch_gemv<WF32, 2, 8, EPI_STORE>(a, 1u << 20, s);
+            return ydtype == VSL_DT_F16 ? launch_gemv_k<WF16, 2, 4, EPI_STORE_F16>(a, 1u << 20, s)
+                                        : launch_gemv_k<WF16, 2, 4, EPI_STORE>(a, 1u << 20, s);
+        return ydtype == VSL_DT_F16 ? launch_gemv_k<WF32, 2, 4, EPI_STORE_F16>(a, 1u << 20, s)
+                                    : launch_gemv_k<WF32, 2, 4, EPI_STORE>(a, 1u << 20, s);
     }
 #define VSL_DISPATCH_XY(WT)                                                                                 \
     if (xdtype == VSL_DT_F16 && ydtype == VSL_DT_F16) return launch_gemv_multi<WT, vsl_half, vsl_half>(W, N, K, X, B, Y, s); \
@@ -839,12 +1106,12 @@ extern "C" int vsl_qkv_rope_append(const float* x, const float* gamma, float eps
     a.kc = kcache; a.vc = vcache; a.q_out = q_out; a.ctrl = ctrl;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (wdtype == VSL_DT_F16) {
-        if (kv_dtype == VSL_DT_F16) return launch_gemv<WF16, 2, 8, EPI_QKV, WF16>(a, 1u << 20, s);
-        return launch_gemv<WF16, 2, 8, EPI_QKV, WF32>(a, 1u << 20, s);
+        if (kv_dtype == VSL_DT_F16) return launch_gemv_k<WF16, 2, 4, EPI_QKV, WF16>(a, 1u << 20, s);
+        return launch_gemv_k<WF16, 2, 4, EPI_QKV, WF32>(a, 1u << 20, s);
     }
     if (wdtype == VSL_DT_F32) {
-        if (kv_dtype == VSL_DT_F16) return launch_gemv<WF32, 2, 8, EPI_QKV, WF16>(a, 1u << 20, s);
-        return launch_gemv<WF32, 2, 8, EPI_QKV, WF32>(a, 1u << 20, s);
+        if (kv_dtype == VSL_DT_F16) return launch_gemv_k<WF32, 2, 4, EPI_QKV, WF16>(a, 1u << 20, s);
+        return launch_gemv_k<WF32, 2, 4, EPI_QKV, WF32>(a, 1u << 20, s);
     }
     return vsl_unsupported("vsl_qkv_rope_append: dtype %d", wdtype);
 }
@@ -876,8 +1143,8 @@ extern "C" int vsl_gemv_residual(const void* W, int wdtype, uint32_t N, uint32_t
     GemvArgs a{};
     a.W = W; a.N = N; a.K = K; a.x = x; a.y = resid; a.ctrl = ctrl;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (wdtype == VSL_DT_F16) return launch_gemv<WF16, 2, 8, EPI_RESID>(a, 1u << 20, s);
-    if (wdtype == VSL_DT_F32) return launch_gemv<WF32, 2, 8, EPI_RESID>(a, 1u << 20, s);
+    if (wdtype == VSL_DT_F16) return launch_gemv_k<WF16, 1, 4, EPI_RESID>(a, 1u << 20, s);
+    if (wdtype == VSL_DT_F32) return launch_gemv_k<WF32, 1, 4, EPI_RESID>(a, 1u << 20, s);
     return vsl_unsupported("vsl_gemv_residual: dtype %d", wdtype);
 }
 
@@ -888,8 +1155,8 @@ extern "C" int vsl_norm_swiglu(const float* x, const float* gamma, float eps, co
     GemvArgs a{};
     a.W = Wgu; a.N = F; a.K = d; a.x = x; a.gamma = gamma; a.eps = eps; a.y = h_out; a.ctrl = ctrl;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (wdtype == VSL_DT_F16) return launch_gemv<WF16, 4, 4, EPI_SWIGLU>(a, 1u << 20, s);
-    if (wdtype == VSL_DT_F32) return launch_gemv<WF32, 4, 4, EPI_SWIGLU>(a, 1u << 20, s);
+    if (wdtype == VSL_DT_F16) return launch_gemv_k<WF16, 2, 4, EPI_SWIGLU>(a, 1u << 20, s);
+    if (wdtype == VSL_DT_F32) return launch_gemv_k<WF32, 2, 4, EPI_SWIGLU>(a, 1u << 20, s);
     return vsl_unsupported("vsl_norm_swiglu: dtype %d", wdtype);
 }
 
@@ -911,10 +1178,10 @@ extern "C" int vsl_lm_head_sample(const float* gamma, float eps, const void* W, 
     a.ws_val = ws_val; a.ws_idx = ws_idx; a.tokens = tokens; a.embed = embed; a.x_next = x;
     a.ctrl = ctrl;
     if (fused) {
-        int rc = wdtype == VSL_DT_F16 ? launch_gemv<WF16, 2, 8, EPI_ARGMAX>(a, kMaxLmBlocks, s)
-                                      : launch_gemv<WF32, 2, 8, EPI_ARGMAX>(a, kMaxLmBlocks, s);
+        int rc = wdtype == VSL_DT_F16 ? launch_gemv_k<WF16, 2, 4, EPI_ARGMAX>(a, kMaxLmBlocks, s)
+                                      : launch_gemv_k<WF32, 2, 4, EPI_ARGMAX>(a, kMaxLmBlocks, s);
         if (rc) return rc;
-        const uint32_t nb = gemv_blocks<2, EPI_ARGMAX>(V, kMaxLmBlocks);
+        const uint32_t nb = gemv_blocks_k<2, EPI_ARGMAX>(V, d, kMaxLmBlocks);
         if (embed_dtype == VSL_DT_F16)
             k_argmax_finish<WF16><<<1, kFinishThreads, 0, s>>>(ws_val, ws_idx, nb, V, d, embed, x, tokens, ctrl);
         else
@@ -925,8 +1192,8 @@ extern "C" int vsl_lm_head_sample(const float* gamma, float eps, const void* W, 
     if (sampler.mode != VSL_SAMPLE_TOPK_SEEDED) return vsl_invalid("vsl_lm_head_sample: sampler mode %d", sampler.mode);
     if (V > (uint32_t)(kSampBlock * kSampPer)) return vsl_unsupported("top-k sampling supports V <= %d", kSampBlock * kSampPer);
     // logits only (EPI_STORE with the norm prologue), then the sampling kernel
-    int rc = wdtype == VSL_DT_F16 ? launch_gemv<WF16, 2, 8, EPI_STORE>(a, 1u << 20, s)
-                                  : launch_gemv<WF32, 2, 8, EPI_STORE>(a, 1u << 20, s);
+    int rc = wdtype == VSL_DT_F16 ? launch_gemv_k<WF16, 2, 4, EPI_STORE>(a, 1u << 20, s)
+                                  : launch_gemv_k<WF32, 2, 4, EPI_STORE>(a, 1u << 20, s);
     if (rc) return rc;
     const uint64_t key = vsl_derive_key(sampler.seed, "sampler");
     if (embed_dtype == VSL_DT_F16)

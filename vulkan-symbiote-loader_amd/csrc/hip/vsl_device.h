@@ -54,6 +54,22 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Wave-wide sum through DPP lane moves (no LDS round trips): pairs and quads by quad_perm, rows of
+// 16 by row rotations, then rows folded by the row-15 / row-31 broadcasts so that lane 63 holds the
+// total, which is returned to every lane as a wave-uniform value.
+#define VSL_DPP_F(v, ctrl, row_mask) \
+    __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), (ctrl), (row_mask), 0xF, false))
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += VSL_DPP_F(v, 0xB1, 0xF);   // quad_perm [1,0,3,2]
+    v += VSL_DPP_F(v, 0x4E, 0xF);   // quad_perm [2,3,0,1]
+    v += VSL_DPP_F(v, 0x124, 0xF);  // row_ror:4
+    v += VSL_DPP_F(v, 0x128, 0xF);  // row_ror:8
+    v += VSL_DPP_F(v, 0x142, 0xA);  // row_bcast:15 into rows 1 and 3
+    v += VSL_DPP_F(v, 0x143, 0xC);  // row_bcast:31 into rows 2 and 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+#undef VSL_DPP_F
+
 // Sum across aligned groups of `W` lanes (W a power of two <= 64).
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
