@@ -23,8 +23,24 @@
 
 namespace {
 
-constexpr int kGemmThreads = 256;
-constexpr int BM = 128, BN = 128, BK = 32, LDS_STRIDE = BK + 8;  // halfs per LDS row (80 bytes)
+constexpr int BK = 64;  // K per pipeline stage
+constexpr int CH = 8;   // halfs per 16-byte chunk; a tile row holds BK / CH = 8 chunks
+
+// Tile configurations: block BM x BN, WAVES_M x WAVES_N waves, each wave a (BM/WAVES_M) x
+// (BN/WAVES_N) sub-tile of 32x32 MFMA fragments.
+//   GemmBig   128 x 256, 2 x 2 waves of 64 x 128 (8 accumulators per wave: long independent MFMA
+//             chains, 0.5 KB of LDS reads per MFMA) -- the wide projections;
+//   GemmMid   128 x 128, 4 x 2 waves of 32 x 64 (two waves per SIMD);
+//   GemmSmall  64 x 128, 2 x 2 waves of 32 x 64 (twice the tiles when the others leave CUs idle).
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_>
+struct GemmCfg {
+    static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_;
+    static constexpr int NT = 64 * WAVES_M * WAVES_N;
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
+};
+using GemmBig = GemmCfg<128, 256, 2, 2>;
+using GemmMid = GemmCfg<128, 128, 4, 2>;
+using GemmSmall = GemmCfg<64, 128, 2, 2>;
 
 __device__ __forceinline__ int d_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
 
@@ -34,119 +50,205 @@ __device__ __forceinline__ void split_f16(float v, vsl_half& hi, vsl_half& lo) {
     lo = (vsl_half)(v - (float)hi);
 }
 
-template <int EPI, bool AX2, bool CX2>
-__global__ __launch_bounds__(kGemmThreads) void k_gemm_f16(const vsl_half* __restrict__ A, const vsl_half* __restrict__ B,
-                                                           uint32_t M, uint32_t N, uint32_t K, void* __restrict__ C) {
+// LDS tiles are unpadded rows of BK halfs (128 bytes). gfx950's LDS serves 256 bytes (64 banks)
+// per cycle, i.e. 16 lanes of a 16-byte access: two rows. The 16-byte chunk c of row r is stored at
+// chunk position c ^ ((r >> 1) & 7): a fragment read (16 consecutive lanes = 16 consecutive rows,
+// one logical chunk) then covers all 16 bank groups (row parity x 8 positions), and so does a
+// store of two whole rows. No bank conflicts, no padding.
+__device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ ((r >> 1) & 7)) * CH); }
+
+// Block tile -> (m-tile, n-tile). Workgroups are dispatched to the 8 XCDs round-robin by block id;
+// each XCD gets a contiguous range of tiles, m-tiles fastest, so the blocks sharing a weight tile
+// share that XCD's L2. Returns false for the idle tail blocks of the last XCD ranges.
+__device__ __forceinline__ bool tile_of(uint32_t n_m, uint32_t n_tiles, uint32_t& mt, uint32_t& nt) {
+    const uint32_t b = blockIdx.x, xcd = b & 7, slot = b >> 3;
+    const uint32_t per = (n_tiles + 7) >> 3;
+    const uint32_t t = xcd * per + slot;
+    if (slot >= per || t >= n_tiles) return false;
+    mt = t % n_m;
+    nt = t / n_m;
+    return true;
+}
+
+// C[M][N] = A[M][K] * B[N][K]^T for one tile configuration (GemmCfg). Per K stage of 64: A (both
+// planes when split) and B tiles go global -> registers -> LDS (double buffered); each stage's
+// global loads are issued two stages ahead of its LDS stores.
+template <class G, int EPI, bool AX2, bool CX2>
+__global__ __launch_bounds__(G::NT) void k_gemm_f16(const vsl_half* __restrict__ A, const vsl_half* __restrict__ B,
+                                                    uint32_t M, uint32_t N, uint32_t K, void* __restrict__ C) {
+    constexpr int BM = G::BM, BN = G::BN, NT = G::NT, WM = G::WM, WN = G::WN, FM = G::FM, FN = G::FN;
     constexpr int AP = AX2 ? 2 : 1;  // A planes (hi, lo)
-    __shared__ __attribute__((aligned(16))) vsl_half As[2][AP][BM * LDS_STRIDE];
-    __shared__ __attribute__((aligned(16))) vsl_half Bs[2][BN * LDS_STRIDE];
+    constexpr int ACH = BM * BK / CH / NT;  // A chunks per thread per plane
+    constexpr int BCH = BN * BK / CH / NT;  // B chunks per thread
+    static_assert(EPI != VSL_EPI_SWIGLU || FN % 2 == 0, "SwiGLU waves pair gate and up fragments");
+    __shared__ __attribute__((aligned(16))) vsl_half As[2][AP][BM * BK];
+    __shared__ __attribute__((aligned(16))) vsl_half Bs[2][BN * BK];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const uint32_t m0 = blockIdx.y * BM;
+    const int wm = wave / G::WAVES_N, wn = wave % G::WAVES_N;
+    const uint32_t ncols = EPI == VSL_EPI_SWIGLU ? BN / 2 : BN;
+    const uint32_t n_m = (M + BM - 1) / BM, n_n = N / ncols;
+    uint32_t mt, nt;
+    if (!tile_of(n_m, n_m * n_n, mt, nt)) return;
+    const uint32_t m0 = mt * BM;
     // EPI_SWIGLU: the block covers 64 output columns; B-tile rows 0..63 are gate rows, 64..127 up rows.
-    const uint32_t nout0 = blockIdx.x * (EPI == VSL_EPI_SWIGLU ? BN / 2 : BN);
+    const uint32_t nout0 = nt * ncols;
     const size_t plane = (size_t)M * K;
 
-    // global -> register staging: each thread moves 2 x 16 bytes of each A plane and of B per K step
-    const int lr = tid >> 2, lk = (tid & 3) * 8;
     auto b_row = [&](int r) -> uint32_t {
         if constexpr (EPI == VSL_EPI_SWIGLU) return r < BN / 2 ? nout0 + r : N + nout0 + (r - BN / 2);
         else return nout0 + r;
     };
-    uint4 ra[AP][2], rb[2];
-    auto gload = [&](uint32_t k0) {
+    // Rows past M load row M-1 (never stored). K need only be a multiple of 32: chunks past K load
+    // chunk 0 of their row and are zeroed when stored to LDS (the mask is applied there, not at the
+    // load, so no select waits on a load in flight).
+    struct Stage {
+        uint4 a[AP][ACH], b[BCH];
+    };
+    auto gload = [&](Stage& st, uint32_t k0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t r = m0 + lr + i * 64;
+        for (int i = 0; i < ACH; ++i) {
+            const int c = tid + i * NT, r = c >> 3, ck = c & 7;
+            const uint32_t gr = m0 + r < M ? m0 + r : M - 1;
+            const uint32_t kk = k0 + ck * CH;
 #pragma unroll
             for (int p = 0; p < AP; ++p)
-                ra[p][i] = r < M ? *reinterpret_cast<const uint4*>(A + p * plane + (size_t)r * K + k0 + lk)
-                                 : make_uint4(0, 0, 0, 0);
-            rb[i] = *reinterpret_cast<const uint4*>(B + (size_t)b_row(lr + i * 64) * K + k0 + lk);
+                st.a[p][i] = *reinterpret_cast<const uint4*>(A + p * plane + (size_t)gr * K + (kk < K ? kk : 0));
+        }
+#pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+            const int c = tid + i * NT, r = c >> 3, ck = c & 7;
+            const uint32_t kk = k0 + ck * CH;
+            st.b[i] = *reinterpret_cast<const uint4*>(B + (size_t)b_row(r) * K + (kk < K ? kk : 0));
         }
     };
-    auto sstore = [&](int buf) {
+    // (masking by AND on the values: a select between the register set and a zero constant would
+    // be lowered as a select of addresses and keep the sets out of registers)
+    auto masked = [](uint4 v, uint32_t m) { return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m); };
+    auto sstore = [&](const Stage& st, int buf, uint32_t k0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < ACH; ++i) {
+            const int c = tid + i * NT, r = c >> 3, ck = c & 7;
+            const uint32_t m = k0 + ck * CH < K ? 0xFFFFFFFFu : 0u;
 #pragma unroll
-            for (int p = 0; p < AP; ++p)
-                *reinterpret_cast<uint4*>(&As[buf][p][(lr + i * 64) * LDS_STRIDE + lk]) = ra[p][i];
-            *reinterpret_cast<uint4*>(&Bs[buf][(lr + i * 64) * LDS_STRIDE + lk]) = rb[i];
+            for (int p = 0; p < AP; ++p) *reinterpret_cast<uint4*>(&As[buf][p][swz(r, ck)]) = masked(st.a[p][i], m);
+        }
+#pragma unroll
+        for (int i = 0; i < BCH; ++i) {
+            const int c = tid + i * NT, r = c >> 3, ck = c & 7;
+            const uint32_t m = k0 + ck * CH < K ? 0xFFFFFFFFu : 0u;
+            *reinterpret_cast<uint4*>(&Bs[buf][swz(r, ck)]) = masked(st.b[i], m);
         }
     };
 
-    float16v acc[2][2];
+    float16v acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-    // B-tile rows of this wave's two 32-column tiles
-    int bt[2];
-    if constexpr (EPI == VSL_EPI_SWIGLU) {
-        bt[0] = wn * 32;
-        bt[1] = BN / 2 + wn * 32;
-    } else {
-        bt[0] = wn * 64;
-        bt[1] = wn * 64 + 32;
+    // B-tile rows of this wave's FN 32-column fragments; for SwiGLU the first FN/2 are gate rows
+    // and the last FN/2 the matching up rows
+    int bt[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        if constexpr (EPI == VSL_EPI_SWIGLU)
+            bt[j] = (j < FN / 2 ? 0 : BN / 2) + wn * (WN / 2) + (j % (FN / 2)) * 32;
+        else
+            bt[j] = wn * WN + j * 32;
     }
 
-    const uint32_t nk = K / BK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (uint32_t kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
+    // Fragments of k-step ks+1 are read from LDS before the MFMAs of k-step ks are issued.
+    struct Frags {
+        half8 a[AP][FM], b[FN];
+    };
+    auto fload = [&](Frags& f, int buf, int ks) {
+        const int lc = ks * 2 + (lane >> 5);  // logical chunk of this lane's 8 k-slots
 #pragma unroll
-        for (int kc = 0; kc < BK; kc += 16) {
-            half8 af[AP][2], bf[2];
+        for (int i = 0; i < FM; ++i) {
+            const int r = wm * WM + i * 32 + (lane & 31);
 #pragma unroll
-            for (int p = 0; p < AP; ++p)
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    af[p][i] = *reinterpret_cast<const half8*>(
-                        &As[buf][p][(wm * 64 + i * 32 + (lane & 31)) * LDS_STRIDE + kc + (lane >> 5) * 8]);
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                bf[j] = *reinterpret_cast<const half8*>(&Bs[buf][(bt[j] + (lane & 31)) * LDS_STRIDE + kc + (lane >> 5) * 8]);
-#pragma unroll
-            for (int p = 0; p < AP; ++p)
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[p][i], bf[j], acc[i][j], 0, 0, 0);
+            for (int p = 0; p < AP; ++p) f.a[p][i] = *reinterpret_cast<const half8*>(&As[buf][p][swz(r, lc)]);
         }
-        if (kt + 1 < nk) sstore(buf ^ 1);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) f.b[j] = *reinterpret_cast<const half8*>(&Bs[buf][swz(bt[j] + (lane & 31), lc)]);
+    };
+    auto mfmas = [&](const Frags& f) {
+#pragma unroll
+        for (int p = 0; p < AP; ++p)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[p][i], f.b[j], acc[i][j], 0, 0, 0);
+    };
+    // One stage = four 16-wide k-steps; the next k-step's fragments are read before the current
+    // k-step's MFMAs are issued.
+    static_assert(BK == 64, "compute() walks four 16-wide k-steps");
+    auto compute = [&](int buf) {
+        Frags f0, f1;
+        fload(f0, buf, 0);
+        fload(f1, buf, 1);
+        mfmas(f0);
+        fload(f0, buf, 2);
+        mfmas(f1);
+        fload(f1, buf, 3);
+        mfmas(f0);
+        mfmas(f1);
+    };
+
+    // Pipeline: stage k's global loads are issued two stages before it is stored to LDS (register
+    // sets s0/s1 alternate), so each load has two stages of MFMA work to arrive. The stage count is
+    // rounded up to even (a padding stage is all zeros); loads for stages past the end re-read the
+    // last stage and are never stored, keeping every load unconditional.
+    const uint32_t nk = ((K + 2 * BK - 1) / (2 * BK)) * 2;
+    const uint32_t klast = (nk - 1) * BK;
+    auto kof = [&](uint32_t st) { return st < nk ? st * BK : klast; };
+    Stage s0, s1;
+    gload(s0, 0);
+    gload(s1, kof(1));
+    sstore(s0, 0, 0);
+    __syncthreads();
+    for (uint32_t kt = 0; kt < nk; kt += 2) {
+        gload(s0, kof(kt + 2));
+        __builtin_amdgcn_sched_barrier(0);
+        compute(0);
+        sstore(s1, 1, (kt + 1) * BK);
+        __syncthreads();
+        gload(s1, kof(kt + 3));
+        __builtin_amdgcn_sched_barrier(0);
+        compute(1);
+        sstore(s0, 0, (kt + 2) * BK);  // past the end: zeros, never read
         __syncthreads();
     }
 
     // epilogue
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < FM; ++i) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const uint32_t row = m0 + wm * 64 + i * 32 + d_row(v, lane);
+            const uint32_t row = m0 + wm * WM + i * 32 + d_row(v, lane);
             if (row >= M) continue;
             if constexpr (EPI == VSL_EPI_SWIGLU) {
-                const uint32_t col = nout0 + wn * 32 + (lane & 31);
-                const float h = silu(acc[i][0][v]) * acc[i][1][v];
                 vsl_half* Ch = reinterpret_cast<vsl_half*>(C);
-                if constexpr (CX2) {
-                    vsl_half hi, lo;
-                    split_f16(h, hi, lo);
-                    Ch[(size_t)row * N + col] = hi;
-                    Ch[(size_t)M * N + (size_t)row * N + col] = lo;
-                } else {
-                    Ch[(size_t)row * N + col] = (vsl_half)h;
+#pragma unroll
+                for (int j = 0; j < FN / 2; ++j) {
+                    const uint32_t col = nout0 + wn * (WN / 2) + j * 32 + (lane & 31);
+                    const float h = silu(acc[i][j][v]) * acc[i][j + FN / 2][v];
+                    if constexpr (CX2) {
+                        vsl_half hi, lo;
+                        split_f16(h, hi, lo);
+                        Ch[(size_t)row * N + col] = hi;
+                        Ch[(size_t)M * N + (size_t)row * N + col] = lo;
+                    } else {
+                        Ch[(size_t)row * N + col] = (vsl_half)h;
+                    }
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const uint32_t col = nout0 + wn * 64 + j * 32 + (lane & 31);
+                for (int j = 0; j < FN; ++j) {
+                    const uint32_t col = nout0 + wn * WN + j * 32 + (lane & 31);
                     const size_t o = (size_t)row * N + col;
                     if constexpr (EPI == VSL_EPI_STORE_F32) reinterpret_cast<float*>(C)[o] = acc[i][j][v];
                     else if constexpr (EPI == VSL_EPI_STORE_F16) reinterpret_cast<vsl_half*>(C)[o] = (vsl_half)acc[i][j][v];
@@ -157,9 +259,6 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm_f16(const vsl_half* __res
     }
 }
 
-// ---------------------------------------------------------------------------------------------
-// RoPE + split of the prefill QKV projection
-// ---------------------------------------------------------------------------------------------
 template <class KT, bool QX2>
 __global__ void k_rope_split(const float* __restrict__ qkv, uint32_t S, uint32_t n_q, uint32_t n_kv, uint32_t hd,
                              uint32_t pos0, const float* __restrict__ rc, const float* __restrict__ rs,
@@ -347,13 +446,33 @@ __global__ __launch_bounds__(64) void k_attn_prefill(const vsl_half* __restrict_
 
 }  // namespace
 
+template <class G, int EPI>
+static void launch_gemm_cfg(uint32_t blocks, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M,
+                            uint32_t N, uint32_t K, void* C, bool ax2, bool cx2) {
+    if (ax2 && cx2) k_gemm_f16<G, EPI, true, true><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C);
+    else if (ax2) k_gemm_f16<G, EPI, true, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C);
+    else if (cx2) k_gemm_f16<G, EPI, false, true><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C);
+    else k_gemm_f16<G, EPI, false, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C);
+}
+
+template <class G, int EPI>
+static uint32_t gemm_tiles(uint32_t M, uint32_t N) {
+    const uint32_t ncols = EPI == VSL_EPI_SWIGLU ? G::BN / 2 : G::BN;
+    return N % ncols ? 0u : ((M + G::BM - 1) / G::BM) * (N / ncols);
+}
+
+// Tile configuration by occupancy: the largest tiles that still give every CU a tile.
 template <int EPI>
-static void launch_gemm(dim3 grid, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N,
-                        uint32_t K, void* C, bool ax2, bool cx2) {
-    if (ax2 && cx2) k_gemm_f16<EPI, true, true><<<grid, kGemmThreads, 0, s>>>(a, b, M, N, K, C);
-    else if (ax2) k_gemm_f16<EPI, true, false><<<grid, kGemmThreads, 0, s>>>(a, b, M, N, K, C);
-    else if (cx2) k_gemm_f16<EPI, false, true><<<grid, kGemmThreads, 0, s>>>(a, b, M, N, K, C);
-    else k_gemm_f16<EPI, false, false><<<grid, kGemmThreads, 0, s>>>(a, b, M, N, K, C);
+static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N, uint32_t K,
+                       void* C, bool ax2, bool cx2) {
+    auto blocks = [](uint32_t tiles) { return ((tiles + 7) / 8) * 8; };  // whole XCD ranges (tile_of)
+    const uint32_t tb = gemm_tiles<GemmBig, EPI>(M, N), tm = gemm_tiles<GemmMid, EPI>(M, N);
+    const uint32_t ts = gemm_tiles<GemmSmall, EPI>(M, N);
+    if (tb >= 256) launch_gemm_cfg<GemmBig, EPI>(blocks(tb), s, a, b, M, N, K, C, ax2, cx2);
+    else if (tm >= 256) launch_gemm_cfg<GemmMid, EPI>(blocks(tm), s, a, b, M, N, K, C, ax2, cx2);
+    else if (ts) launch_gemm_cfg<GemmSmall, EPI>(blocks(ts), s, a, b, M, N, K, C, ax2, cx2);
+    else return vsl_invalid("vsl_gemm_f16: N=%u is not a multiple of the tile width", N);
+    return VSL_OK;
 }
 
 extern "C" int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
@@ -364,20 +483,21 @@ extern "C" int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N
     const int epi = epilogue & 0xFF;
     if (epilogue & ~(0xFF | VSL_GEMM_A_X2 | VSL_GEMM_C_X2)) return vsl_invalid("vsl_gemm_f16: flags 0x%x", epilogue);
     if (cx2 && epi != VSL_EPI_SWIGLU) return vsl_invalid("vsl_gemm_f16: VSL_GEMM_C_X2 needs VSL_EPI_SWIGLU");
-    if (K % BK) return vsl_invalid("vsl_gemm_f16: K=%u must be a multiple of %d", K, BK);
-    const uint32_t ncols = epi == VSL_EPI_SWIGLU ? BN / 2 : BN;
+    if (K % 32) return vsl_invalid("vsl_gemm_f16: K=%u must be a multiple of 32", K);
+    const uint32_t ncols = epi == VSL_EPI_SWIGLU ? 64 : 128;
     if (N % ncols) return vsl_invalid("vsl_gemm_f16: N=%u must be a multiple of %u", N, ncols);
-    dim3 grid(N / ncols, (M + BM - 1) / BM);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const vsl_half* a = static_cast<const vsl_half*>(A);
     const vsl_half* b = static_cast<const vsl_half*>(B);
+    int rc;
     switch (epi) {
-        case VSL_EPI_STORE_F32: launch_gemm<VSL_EPI_STORE_F32>(grid, s, a, b, M, N, K, C, ax2, false); break;
-        case VSL_EPI_STORE_F16: launch_gemm<VSL_EPI_STORE_F16>(grid, s, a, b, M, N, K, C, ax2, false); break;
-        case VSL_EPI_RESID: launch_gemm<VSL_EPI_RESID>(grid, s, a, b, M, N, K, C, ax2, false); break;
-        case VSL_EPI_SWIGLU: launch_gemm<VSL_EPI_SWIGLU>(grid, s, a, b, M, N, K, C, ax2, cx2); break;
+        case VSL_EPI_STORE_F32: rc = launch_gemm<VSL_EPI_STORE_F32>(s, a, b, M, N, K, C, ax2, false); break;
+        case VSL_EPI_STORE_F16: rc = launch_gemm<VSL_EPI_STORE_F16>(s, a, b, M, N, K, C, ax2, false); break;
+        case VSL_EPI_RESID: rc = launch_gemm<VSL_EPI_RESID>(s, a, b, M, N, K, C, ax2, false); break;
+        case VSL_EPI_SWIGLU: rc = launch_gemm<VSL_EPI_SWIGLU>(s, a, b, M, N, K, C, ax2, cx2); break;
         default: return vsl_invalid("vsl_gemm_f16: epilogue %d", epi);
     }
+    if (rc) return rc;
     HIP_TRY(hipGetLastError());
     return VSL_OK;
 }
