@@ -4,9 +4,9 @@
 //                  BK = 32, LDS double buffering, fused epilogues (fp32 / fp16 store, residual add,
 //                  SwiGLU over [Wgate; Wup]).
 // k_rope_split:    QKV GEMM output -> RoPE(q, k) at positions pos0+s -> q (fp16), K/V cache (fp16).
-// k_attn_prefill:  causal flash attention, one wavefront per (32 query rows, query head), computing
-//                  S^T = K Q^T and O^T = V^T P^T on MFMA so that every lane owns one query row's
-//                  softmax statistics and output column.
+// k_attn_prefill:  causal flash attention, one block per (32 query rows, KV head) with one wave per
+//                  query head of the group, computing S^T = K Q^T and O^T = V^T P^T on MFMA so that
+//                  every lane owns one query row's softmax statistics and output column.
 //
 // MFMA 32x32x16 f16 operand layout used here (lane l of a 64-lane wave):
 //   A (32 x 16): row l%32, 8 consecutive k-slots 8*(l/32)..+7
@@ -309,34 +309,88 @@ __global__ void k_rope_split(const float* __restrict__ qkv, uint32_t S, uint32_t
 // ---------------------------------------------------------------------------------------------
 // causal flash attention (prefill), fp16 in / fp16 out, fp32 softmax statistics
 // ---------------------------------------------------------------------------------------------
-template <int HD, bool QX2, bool OX2>
-__global__ __launch_bounds__(64) void k_attn_prefill(const vsl_half* __restrict__ q, const vsl_half* __restrict__ kc,
-                                                     const vsl_half* __restrict__ vc, uint32_t S, uint32_t pos0,
-                                                     uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
-                                                     vsl_half* __restrict__ out) {
-    constexpr int VT_STRIDE = 32 + 8;  // halfs per transposed-V row (one head dim, 32 positions)
-    constexpr int QP = QX2 ? 2 : 1;    // q planes; with split q the probabilities are split too
-    __shared__ __attribute__((aligned(16))) vsl_half Vt[HD * VT_STRIDE];
-    const int lane = threadIdx.x;
-    const uint32_t qb = blockIdx.x, h = blockIdx.y;
-    const uint32_t kvh = (uint32_t)(((uint64_t)h * n_kv) / n_q);
+// Causal flash attention for one chunk of S prompt rows at positions pos0.. (their K/V already in
+// the cache). Block = the G query heads of one KV head x 32 query rows, one wave per head: the
+// block stages each 64-position K/V tile in LDS once for all G heads (K row-major, swizzled; V
+// transposed so V^T is an MFMA A operand), one tile ahead in registers. Per tile each wave computes
+// S^T = K Q^T (two 32-position fragments), the online softmax of its 32 query rows (each lane owns
+// one row's statistics with its partner lane l^32), and O^T += V^T P^T.
+constexpr int kAttnTile = 64;  // KV positions per tile
+
+template <int HD>
+__device__ __forceinline__ int ksw(int r, int c) {
+    if constexpr (HD == 128) return r * HD + ((c ^ (r & 15)) * 8);       // 256-byte rows: 16 rows per bank sweep
+    else return r * HD + ((c ^ ((r >> 1) & 7)) * 8);                      // 128-byte rows: row pairs
+}
+
+template <int HD, int G, bool QX2, bool OX2>
+__global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restrict__ q, const vsl_half* __restrict__ kc,
+                                                         const vsl_half* __restrict__ vc, uint32_t S, uint32_t pos0,
+                                                         uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
+                                                         vsl_half* __restrict__ out) {
+    constexpr int TK = kAttnTile;
+    constexpr int NT = 64 * G;
+    constexpr int VTS = TK + 8;                 // halfs per V^T row (one head dim)
+    constexpr int CPR = HD / 8;                 // 16-byte chunks per K/V row
+    constexpr int NCH = TK * CPR / NT;          // chunks per thread per tile (K and V each)
+    constexpr int QP = QX2 ? 2 : 1;             // q planes; with split q the probabilities are split too
+    static_assert(NCH >= 1, "tile too small for the block");
+    __shared__ __attribute__((aligned(16))) vsl_half Ks[2][TK * HD];
+    __shared__ __attribute__((aligned(16))) vsl_half Vt[2][HD * VTS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t n_qb = gridDim.x;
+    const uint32_t qb = n_qb - 1 - blockIdx.x;  // the longest (latest) query blocks start first
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t h = kvh * G + wave;          // kv_head = head * n_kv / n_q
     const uint32_t s_base = qb * 32;
     const uint32_t my_s = s_base + (lane & 31);  // query row owned by this lane (stats, O^T column)
     const uint32_t qw = n_q * HD;
     const size_t qplane = (size_t)S * qw;
     const float sl2 = scale * 1.4426950408889634f;
+    const uint32_t last_s = min(S, s_base + 32) - 1;
+    const uint32_t kv_end = pos0 + last_s + 1;  // positions 0..kv_end-1 are visible to some row
+    const uint32_t my_pos = pos0 + my_s;
+    const uint32_t n_tiles = (kv_end + TK - 1) / TK;
+    const vsl_half* Kb = kc + (size_t)kvh * cap * HD;
+    const vsl_half* Vb = vc + (size_t)kvh * cap * HD;
 
-    // Q^T as the B operand of S^T = K Q^T: lane holds q row (l%32), hd slots 16c + 8*(l/32)..+7
+    // tile staging: chunk e of a tile is (position e / CPR, dims 8 * (e % CPR)); positions past
+    // kv_end read position 0 (in bounds) and their V is zeroed in LDS
+    struct Stage {
+        uint4 k[NCH], v[NCH];
+    };
+    auto gload = [&](Stage& st, uint32_t t) {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int e = tid + i * NT, r = e / CPR, c = e % CPR;
+            const uint32_t pos = t * TK + r;
+            const size_t off = (size_t)(pos < kv_end ? pos : 0) * HD + c * 8;
+            st.k[i] = *reinterpret_cast<const uint4*>(Kb + off);
+            st.v[i] = *reinterpret_cast<const uint4*>(Vb + off);
+        }
+    };
+    auto sstore = [&](const Stage& st, int buf, uint32_t t) {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+            const int e = tid + i * NT, r = e / CPR, c = e % CPR;
+            *reinterpret_cast<uint4*>(&Ks[buf][ksw<HD>(r, c)]) = st.k[i];
+            const uint32_t m = t * TK + r < kv_end ? 0xFFFFFFFFu : 0u;
+            const uint4 vm = make_uint4(st.v[i].x & m, st.v[i].y & m, st.v[i].z & m, st.v[i].w & m);
+            const half8 vh = __builtin_bit_cast(half8, vm);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) Vt[buf][(c * 8 + j) * VTS + r] = vh[j];
+        }
+    };
+
+    // Q^T as the B operand of S^T = K Q^T: lane holds q row (l%32), dims 16c + 8*(l/32)..+7
     half8 qf[QP][HD / 16];
 #pragma unroll
     for (int p = 0; p < QP; ++p)
 #pragma unroll
         for (int c = 0; c < HD / 16; ++c) {
-            if (my_s < S)
-                qf[p][c] = *reinterpret_cast<const half8*>(q + p * qplane + (size_t)my_s * qw + (size_t)h * HD + c * 16 +
-                                                           (lane >> 5) * 8);
-            else
-                qf[p][c] = half8{0, 0, 0, 0, 0, 0, 0, 0};
+            const uint32_t row = my_s < S ? my_s : S - 1;  // rows past S are never stored
+            qf[p][c] = *reinterpret_cast<const half8*>(q + p * qplane + (size_t)row * qw + (size_t)h * HD + c * 16 +
+                                                       (lane >> 5) * 8);
         }
     float16v o[HD / 32];
 #pragma unroll
@@ -345,86 +399,93 @@ __global__ __launch_bounds__(64) void k_attn_prefill(const vsl_half* __restrict_
         for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
     float m = -INFINITY, l = 0.f;
 
-    const uint32_t last_s = min(S, s_base + 32) - 1;
-    const uint32_t kv_end = pos0 + last_s + 1;  // positions 0..kv_end-1 are visible to some row
-    const vsl_half* Kb = kc + (size_t)kvh * cap * HD;
-    const vsl_half* Vb = vc + (size_t)kvh * cap * HD;
-    const uint32_t my_pos = pos0 + my_s;
-
-    for (uint32_t t0 = 0; t0 < kv_end; t0 += 32) {
-        // stage V^T for positions t0..t0+31 (zero beyond kv_end)
-        __syncthreads();
-        for (int e = lane; e < 32 * (HD / 8); e += 64) {
-            const int r = e / (HD / 8), c8 = (e % (HD / 8)) * 8;
-            half8 vv = (t0 + r < kv_end) ? *reinterpret_cast<const half8*>(Vb + (size_t)(t0 + r) * HD + c8)
-                                         : half8{0, 0, 0, 0, 0, 0, 0, 0};
+    auto compute = [&](int buf, uint32_t t) {
+        // S^T[kv][q] = sum_d K[kv][d] Q[q][d] for the tile's two 32-position halves
+        float16v st[2];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) Vt[(c8 + i) * VT_STRIDE + r] = vv[i];
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) st[kb][v] = 0.f;
+#pragma unroll
+            for (int c = 0; c < HD / 16; ++c) {
+                const half8 kf = *reinterpret_cast<const half8*>(&Ks[buf][ksw<HD>(kb * 32 + (lane & 31), 2 * c + (lane >> 5))]);
+#pragma unroll
+                for (int p = 0; p < QP; ++p) st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[p][c], st[kb], 0, 0, 0);
+            }
         }
-        // S^T[kv][q] = sum_d K[kv][d] Q[q][d]
-        float16v st;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) st[v] = 0.f;
-        const uint32_t krow = t0 + (lane & 31);
-#pragma unroll
-        for (int c = 0; c < HD / 16; ++c) {
-            half8 kf = krow < kv_end ? *reinterpret_cast<const half8*>(Kb + (size_t)krow * HD + c * 16 + (lane >> 5) * 8)
-                                     : half8{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-            for (int p = 0; p < QP; ++p) st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[p][c], st, 0, 0, 0);
-        }
-        // causal mask + online softmax over this lane's 16 kv values of its query row
+        // causal mask + online softmax over this lane's 32 values of its query row
         float bm = -INFINITY;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const uint32_t kvp = t0 + d_row(v, lane);
-            const float sc = (kvp <= my_pos && kvp < kv_end) ? st[v] * sl2 : -INFINITY;
-            st[v] = sc;
-            bm = fmaxf(bm, sc);
-        }
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t kvp = t * TK + kb * 32 + d_row(v, lane);
+                const float sc = kvp <= my_pos ? st[kb][v] * sl2 : -INFINITY;
+                st[kb][v] = sc;
+                bm = fmaxf(bm, sc);
+            }
         bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
         const float mn = fmaxf(m, bm);
         const float corr = (mn == -INFINITY) ? 1.f : exp2f(m - mn);
         float ps = 0.f;
-        half8 pf[QP][2];
+        half8 pf[QP][2][2];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const float pv = (st[v] == -INFINITY) ? 0.f : exp2f(st[v] - mn);
-            ps += pv;
-            if constexpr (QX2) {
-                vsl_half hi, lo;
-                split_f16(pv, hi, lo);
-                pf[0][v >> 3][v & 7] = hi;
-                pf[QP - 1][v >> 3][v & 7] = lo;
-            } else {
-                pf[0][v >> 3][v & 7] = (vsl_half)pv;
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float pv = (st[kb][v] == -INFINITY) ? 0.f : exp2f(st[kb][v] - mn);
+                ps += pv;
+                if constexpr (QX2) {
+                    vsl_half hi, lo;
+                    split_f16(pv, hi, lo);
+                    pf[0][kb][v >> 3][v & 7] = hi;
+                    pf[QP - 1][kb][v >> 3][v & 7] = lo;
+                } else {
+                    pf[0][kb][v >> 3][v & 7] = (vsl_half)pv;
+                }
             }
-        }
         ps += __shfl_xor(ps, 32, 64);
         l = l * corr + ps;
         m = mn;
 #pragma unroll
-        for (int t = 0; t < HD / 32; ++t)
+        for (int tt = 0; tt < HD / 32; ++tt)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) o[t][v] *= corr;
-        __syncthreads();
-        // O^T[dim][q] += sum_kv V^T[dim][kv] P^T[kv][q]; k-slots: v=0..7 -> MFMA 0, v=8..15 -> MFMA 1
+            for (int v = 0; v < 16; ++v) o[tt][v] *= corr;
+        // O^T[dim][q] += sum_kv V^T[dim][kv] P^T[kv][q]; P^T slots v = 0..7 / 8..15 of each half are
+        // the kv rows (v/4)*8 + (l/32)*4 + v%4, which the V^T operand reads to match
 #pragma unroll
-        for (int t = 0; t < HD / 32; ++t) {
-            const int dim = t * 32 + (lane & 31);
+        for (int tt = 0; tt < HD / 32; ++tt) {
+            const int dim = tt * 32 + (lane & 31);
 #pragma unroll
-            for (int half_i = 0; half_i < 2; ++half_i) {
-                // kv positions of slots v = 8*half_i + 0..7: rows d_row(v) = (v/4)*8 + (l/32)*4 + v%4
-                const int r0 = (half_i * 2) * 8 + (lane >> 5) * 4;
-                const int r1 = (half_i * 2 + 1) * 8 + (lane >> 5) * 4;
-                half4 a0 = *reinterpret_cast<const half4*>(&Vt[dim * VT_STRIDE + r0]);
-                half4 a1 = *reinterpret_cast<const half4*>(&Vt[dim * VT_STRIDE + r1]);
-                half8 af = half8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int p = 0; p < QP; ++p) o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, pf[p][half_i], o[t], 0, 0, 0);
-            }
+                for (int hi = 0; hi < 2; ++hi) {
+                    const int r0 = kb * 32 + (hi * 2) * 8 + (lane >> 5) * 4;
+                    const half4 a0 = *reinterpret_cast<const half4*>(&Vt[buf][dim * VTS + r0]);
+                    const half4 a1 = *reinterpret_cast<const half4*>(&Vt[buf][dim * VTS + r0 + 8]);
+                    const half8 af = half8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+#pragma unroll
+                    for (int p = 0; p < QP; ++p)
+                        o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, pf[p][kb][hi], o[tt], 0, 0, 0);
+                }
         }
+    };
+
+    // tile pipeline: tile t+1's global loads are issued before tile t's MFMAs and stored to the
+    // other LDS buffer after them; loads past the last tile re-read it and are never stored
+    Stage sg;
+    gload(sg, 0);
+    sstore(sg, 0, 0);
+    __syncthreads();
+    for (uint32_t t = 0; t < n_tiles; ++t) {
+        const int buf = t & 1;
+        gload(sg, t + 1 < n_tiles ? t + 1 : t);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(buf, t);
+        sstore(sg, buf ^ 1, t + 1);
+        __syncthreads();
     }
+
     if (my_s >= S) return;
     const float inv = l > 0.f ? 1.f / l : 0.f;
     vsl_half* orow = out + (size_t)my_s * qw + (size_t)h * HD;
@@ -531,14 +592,29 @@ extern "C" int vsl_rope_split_append(const float* qkv, uint32_t S, uint32_t n_q,
     return VSL_OK;
 }
 
+template <int HD, int G>
+static void launch_attn_prefill_g(dim3 grid, hipStream_t s, const vsl_half* q, const vsl_half* k, const vsl_half* v,
+                                  uint32_t S, uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
+                                  vsl_half* o, bool qx2, bool ox2) {
+    constexpr int NT = 64 * G;
+    if (qx2 && ox2) k_attn_prefill<HD, G, true, true><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
+    else if (qx2) k_attn_prefill<HD, G, true, false><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
+    else if (ox2) k_attn_prefill<HD, G, false, true><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
+    else k_attn_prefill<HD, G, false, false><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
+}
+
 template <int HD>
-static void launch_attn_prefill(dim3 grid, hipStream_t s, const vsl_half* q, const vsl_half* k, const vsl_half* v,
-                                uint32_t S, uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
-                                vsl_half* o, bool qx2, bool ox2) {
-    if (qx2 && ox2) k_attn_prefill<HD, true, true><<<grid, 64, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
-    else if (qx2) k_attn_prefill<HD, true, false><<<grid, 64, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
-    else if (ox2) k_attn_prefill<HD, false, true><<<grid, 64, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
-    else k_attn_prefill<HD, false, false><<<grid, 64, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
+static int launch_attn_prefill(dim3 grid, hipStream_t s, const vsl_half* q, const vsl_half* k, const vsl_half* v,
+                               uint32_t S, uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
+                               vsl_half* o, bool qx2, bool ox2) {
+    switch (n_q / n_kv) {
+        case 1: launch_attn_prefill_g<HD, 1>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2); break;
+        case 2: launch_attn_prefill_g<HD, 2>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2); break;
+        case 4: launch_attn_prefill_g<HD, 4>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2); break;
+        case 8: launch_attn_prefill_g<HD, 8>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2); break;
+        default: return vsl_unsupported("vsl_attn_prefill: GQA ratio %u (supported 1, 2, 4, 8)", n_q / n_kv);
+    }
+    return VSL_OK;
 }
 
 extern "C" int vsl_attn_prefill(const void* q, int q_dtype, const void* kcache, const void* vcache, uint32_t S,
@@ -553,19 +629,21 @@ extern "C" int vsl_attn_prefill(const void* q, int q_dtype, const void* kcache, 
     }
     if ((q_dtype != VSL_DT_F16 && q_dtype != VSL_DT_F16X2) || (out_dtype != VSL_DT_F16 && out_dtype != VSL_DT_F16X2))
         return vsl_unsupported("vsl_attn_prefill: dtypes %d/%d", q_dtype, out_dtype);
-    dim3 grid((S + 31) / 32, n_q);
+    dim3 grid((S + 31) / 32, n_kv);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool qx2 = q_dtype == VSL_DT_F16X2, ox2 = out_dtype == VSL_DT_F16X2;
     const vsl_half* qq = static_cast<const vsl_half*>(q);
     const vsl_half* kk = static_cast<const vsl_half*>(kcache);
     const vsl_half* vv = static_cast<const vsl_half*>(vcache);
     vsl_half* oo = static_cast<vsl_half*>(out);
+    int rc;
     if (hd == 128)
-        launch_attn_prefill<128>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, ox2);
+        rc = launch_attn_prefill<128>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, ox2);
     else if (hd == 64)
-        launch_attn_prefill<64>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, ox2);
+        rc = launch_attn_prefill<64>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, ox2);
     else
         return vsl_unsupported("vsl_attn_prefill: head_dim %u", hd);
+    if (rc) return rc;
     HIP_TRY(hipGetLastError());
     return VSL_OK;
 }
