@@ -96,6 +96,70 @@ def cpu_baseline(eng, cfg, prompt, seconds):
                       f"weights ({secs:.1f} s, {threads} threads, fp16 weights / fp32 math)"}
 
 
+def run_sweep(a):
+    """GEMV sweep: W [N,K] fp16 ~N(0,0.02), X [K,B] fp16 ~N(0,1), fp32 accumulate, fp16 Y."""
+    import ctypes
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (use --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+    vsl = load_package()
+    H = vsl.hip()
+    P = ctypes.c_void_p
+    arena = P()
+    vsl.check(H.vsl_arena_create(0, 1 << 30, ctypes.byref(arena)))
+
+    def alloc(n):
+        p = P()
+        vsl.check(H.vsl_arena_alloc(arena, n, 256, ctypes.byref(p)))
+        return p
+
+    rot_bytes = 512 << 20
+    wmax = 32000 * 4096 * 2
+    ncopy = -(-rot_bytes // wmax) + 1
+    wbuf = alloc(ncopy * wmax if ncopy * wmax >= rot_bytes else rot_bytes + wmax)
+    wtotal = max(ncopy * wmax, rot_bytes + wmax)
+    vsl.check(H.vsl_fill_normal(wbuf, vsl.VSL_DT_F16, wtotal // 2, 1, b"sweep.W", 0.0, 0.02, None))
+    xbuf = alloc(14336 * 16 * 2)
+    vsl.check(H.vsl_fill_normal(xbuf, vsl.VSL_DT_F16, 14336 * 16, 2, b"sweep.X", 0.0, 1.0, None))
+    ybuf = alloc(32000 * 16 * 2)
+    e0, e1 = P(), P()
+    vsl.check(H.vsl_event_create(ctypes.byref(e0)))
+    vsl.check(H.vsl_event_create(ctypes.byref(e1)))
+    rows = []
+    for (N, K) in [(4096, 4096), (14336, 4096), (4096, 14336), (32000, 4096)]:
+        wsz = N * K * 2
+        copies = max(2, -(-rot_bytes // wsz))
+        ptrs = [P(wbuf.value + (i * wsz) % (wtotal - wsz)) for i in range(copies)]
+        for B in (1, 4, 16):
+            # X as B contiguous K-vectors (vsl_gemv_batched); Y [B][N] fp16
+            args = lambda w: (w, N, K, xbuf, B, ybuf, vsl.VSL_DT_F16, None)
+            for w in ptrs[:2]:
+                vsl.check(H.vsl_gemv_batched(*args(w)))
+            reps = max(copies * 4, 64)
+            vsl.check(H.vsl_event_record(e0, None))
+            for i in range(reps):
+                vsl.check(H.vsl_gemv_batched(*args(ptrs[i % copies])))
+            vsl.check(H.vsl_event_record(e1, None))
+            vsl.check(H.vsl_event_sync(e1))
+            ms = ctypes.c_float()
+            vsl.check(H.vsl_event_elapsed_ms(e0, e1, ctypes.byref(ms)))
+            us = ms.value * 1e3 / reps
+            nbytes = 2 * N * K + 2 * K * B + 2 * N * B
+            rows.append({"N": N, "K": K, "B": B, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1),
+                         "hbm_frac": round(nbytes / us / 1e3 / (PEAK_HBM / 1e9), 4),
+                         "tflops": round(2 * N * K * B / us / 1e6, 2)})
+    vsl.check(H.vsl_arena_destroy(arena))
+    geo = float(np.exp(np.mean([np.log(r["gbps"]) for r in rows])))
+    out = {"metric": "GEMV sweep HBM GB/s (geometric mean over 12 shapes), fp16 W/X/Y, fp32 accumulate",
+           "value": round(geo, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f16",
+           "data": "synthetic: W ~N(0,0.02), X ~N(0,1) fp16 (Philox on device); W rotated over >= 512 MB",
+           "config": {"workload": "GEMV / skinny-GEMM sweep y = W X, (N,K) in {(4096,4096),(14336,4096),"
+                                  "(4096,14336),(32000,4096)}, B in {1,4,16}"},
+           "shapes": rows}
+    print(json.dumps(out), flush=True)
+
+
 def run_long(a):
     """Long-context workload: 8B-class fp16, prompt 8192 (2048-row chunks), KV capacity 32768."""
     if a.gpus != 1:
@@ -166,6 +230,10 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="launch each decode step's kernels directly instead of replaying the captured hipGraph "
                          "(same kernels; used under rocprofv3, whose graph-launch interception crashes here)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="the standalone fp16 GEMV / skinny-GEMM sweep instead: Y = W X for (N, K) in "
+                         "{(4096,4096), (14336,4096), (4096,14336), (32000,4096)} and B in {1, 4, 16}, W rotated "
+                         "over >= 512 MB of distinct copies so the 256 MB MALL cannot serve it")
     ap.add_argument("--long", action="store_true",
                     help="the long-context workload instead: 8192-token prompt prefilled in 2048-token chunks "
                          "into a 32768-position KV cache, greedy decode (default 128 steps), then the same "
@@ -173,6 +241,9 @@ def main():
     a = ap.parse_args()
     if a.long:
         run_long(a)
+        return
+    if a.sweep:
+        run_sweep(a)
         return
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (use --gpus 1)",

@@ -51,25 +51,37 @@ def test_gemv_sweep(vsl, orc, dev, H, N, K, B):
     X = rng.normal(0, 1, (K, B)).astype(np.float16)
     ref = orc.gemm_nt(W, X.astype(np.float32))
     dW = dev.put(W)
-    if B == 1:
+    if B == 1:  # the decode GEMV (fp32 activation)
         dX = dev.put(X.astype(np.float32))
         dY = dev.empty((N, 1), np.float32)
         ok(vsl, H.vsl_gemv(dev.p(dW), vsl.VSL_DT_F16, N, K, dev.p(dX), vsl.VSL_DT_F32, 1, dev.p(dY),
                            vsl.VSL_DT_F32, None))
         y = dev.get(dY)
         assert rel_err(y, ref) < 1e-5
-    else:
-        dX = dev.put(X)
-        dY = dev.empty((N, B), np.float16)
-        ok(vsl, H.vsl_gemv(dev.p(dW), vsl.VSL_DT_F16, N, K, dev.p(dX), vsl.VSL_DT_F16, B, dev.p(dY),
-                           vsl.VSL_DT_F16, None))
-        y = dev.get(dY).astype(np.float32)
-        # fp16 output: within half an fp16 ulp of the fp32-accumulated value, plus accumulation noise
-        assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -11 + 1e-4 * np.max(np.abs(ref)))
+    # the sweep as specified: fp16 X, fp16 Y
+    dX = dev.put(X)
+    dY = dev.empty((N, B), np.float16)
+    ok(vsl, H.vsl_gemv(dev.p(dW), vsl.VSL_DT_F16, N, K, dev.p(dX), vsl.VSL_DT_F16, B, dev.p(dY),
+                       vsl.VSL_DT_F16, None))
+    y = dev.get(dY).astype(np.float32)
+    # fp16 output: within half an fp16 ulp of the fp32-accumulated value, plus accumulation noise
+    assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -11 + 1e-4 * np.max(np.abs(ref)))
+    # fp32 output of the same product
+    dY32 = dev.empty((N, B), np.float32)
+    ok(vsl, H.vsl_gemv(dev.p(dW), vsl.VSL_DT_F16, N, K, dev.p(dX), vsl.VSL_DT_F16, B, dev.p(dY32),
+                       vsl.VSL_DT_F32, None))
+    assert rel_err(dev.get(dY32), ref) < 1e-5
+    # batch of B contiguous activation vectors: X [B][K], Y [B][N]
+    dXt = dev.put(np.ascontiguousarray(X.T))
+    dYt = dev.empty((B, N), np.float32)
+    ok(vsl, H.vsl_gemv_batched(dev.p(dW), N, K, dev.p(dXt), B, dev.p(dYt), vsl.VSL_DT_F32, None))
+    assert rel_err(dev.get(dYt).T, ref) < 1e-5
 
 
 def test_gemv_rejects_bad_shapes(vsl, dev, H):
     d = dev.empty((16,), np.float32)
+    assert H.vsl_gemv_batched(dev.p(d), 4, 1024, dev.p(d), 1, dev.p(d), 0, None) == -100  # K % 2048
+    assert H.vsl_gemv_batched(dev.p(d), 4, 2048, dev.p(d), 0, dev.p(d), 0, None) == -100  # B < 1
     assert H.vsl_gemv(dev.p(d), 1, 4, 12, dev.p(d), 0, 1, dev.p(d), 0, None) == -100  # K % 8
     assert H.vsl_gemv(dev.p(d), 1, 4, 16, dev.p(d), 0, 17, dev.p(d), 0, None) == -100  # B > 16
     assert H.vsl_gemv(None, 1, 4, 16, dev.p(d), 0, 1, dev.p(d), 0, None) == -100

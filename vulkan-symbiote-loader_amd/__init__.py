@@ -116,6 +116,7 @@ _HIP_SIGS = {
     "vsl_embed": (_I32, [_P, _I32, _U32, _U32, _P, _U32, _P, _P]),
     "vsl_rmsnorm": (_I32, [_P, _P, _U32, _U32, _F32, _P, _I32, _P]),
     "vsl_gemv": (_I32, [_P, _I32, _U32, _U32, _P, _I32, _U32, _P, _I32, _P]),
+    "vsl_gemv_batched": (_I32, [_P, _U32, _U32, _P, _U32, _P, _I32, _P]),
     "vsl_qkv_rope_append": (_I32, [_P, _P, _F32, _P, _I32, _U32, _U32, _U32, _U32, _P, _P, _P, _P, _I32, _U32, _P,
                                    _P, _P]),
     "vsl_attn_decode": (_I32, [_P, _P, _P, _I32, _U32, _U32, _U32, _U32, _F32, _U32, _P, _P, _P, _P, _P]),

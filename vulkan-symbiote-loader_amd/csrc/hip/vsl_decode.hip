@@ -1014,9 +1014,114 @@ int launch_gemv_multi(const void* W, uint32_t N, uint32_t K, const void* X, uint
     return VSL_OK;
 }
 
-// fp16 -> fp32 staging of a single activation column (sweep B=1 with f16 X)
-__global__ void k_h2f(const vsl_half* x, float* y, uint32_t n) {
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) y[i] = (float)x[i];
+// ---------------------------------------------------------------------------------------------
+// skinny GEMM on MFMA (the fp16 GEMV sweep): Y[N][B] = W[N][K] X[K][B], X fp16 [K][B] row-major,
+// 1 <= B <= 16, fp32 accumulation. v_mfma_f32_16x16x32_f16 with A = 16 rows of W (lane l: row
+// l%16, k-slots 8*(l/16)..+7 -- one 16-byte load) and B = X (lane l: column l%16, the same
+// k-slots -- eight 2-byte loads, L1/L2 resident); D lane l holds rows 4*(l/16)..+3 of column l%16.
+// Block = kSkR x 16 rows x 8 waves (each wave's X operand serves its kSkR row groups); wave w
+// accumulates the K range [w K/8, (w+1) K/8) in groups of U 32-wide steps, double-buffered (the next group's W loads issued before the current group's
+// MFMAs); the 8 partial tiles are summed in LDS in wave order (deterministic). HBM traffic is W
+// once; columns past B load column B-1 and are masked to zero.
+constexpr int kSkWaves = 8, kSkU = 4, kSkR = 1;              // kSkR row groups of 16 per wave
+constexpr uint32_t kSkRows = 16 * kSkR;                      // rows per block
+constexpr uint32_t kSkKAlign = kSkWaves * 32 * kSkU * 2;  // K multiple: whole group pairs per wave
+
+// VEC_MAJOR: X holds B vectors of K ([B][K]) and Y B vectors of N ([B][N]) -- a batch of
+// activation vectors, each contiguous -- so a lane's X operand is one 16-byte load; otherwise X is
+// [K][B] and Y [N][B] (row-major products), eight 2-byte loads per operand.
+template <typename YT, bool VEC_MAJOR>
+__global__ __launch_bounds__(kSkWaves * 64) void k_skinny(const vsl_half* __restrict__ W, uint32_t N, uint32_t K,
+                                                         const vsl_half* __restrict__ X, uint32_t B, YT* __restrict__ Y) {
+    __shared__ float part[kSkWaves][kSkRows][17];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t row = blockIdx.x * kSkRows + (lane & 15);  // + 16 per row group
+    const uint32_t ksub = (lane >> 4) * 8;
+    const uint32_t col = lane & 15;
+    const uint32_t bc = col < B ? col : B - 1;
+    const uint32_t bmask = col < B ? 0xFFFFFFFFu : 0u;
+    const uint32_t kw = K / kSkWaves;
+    const uint32_t k_begin = wave * kw;
+    const uint32_t n_groups = kw / (32 * kSkU);
+    const vsl_half* wrow[kSkR];
+#pragma unroll
+    for (int r = 0; r < kSkR; ++r) {
+        const uint32_t rr = row + 16 * r;
+        wrow[r] = W + (size_t)(rr < N ? rr : N - 1) * K;  // rows past N: never stored
+    }
+
+    struct Group {
+        uint4 a[kSkR][kSkU];
+        uint4 xv[kSkU];              // VEC_MAJOR
+        vsl_half x[kSkU][VEC_MAJOR ? 1 : 8];
+    };
+    auto issue = [&](Group& g, uint32_t j) {
+#pragma unroll
+        for (int u = 0; u < kSkU; ++u) {
+            const uint32_t k = k_begin + (j * kSkU + u) * 32 + ksub;
+#pragma unroll
+            for (int r = 0; r < kSkR; ++r) g.a[r][u] = load16<true>(wrow[r] + k);
+            if constexpr (VEC_MAJOR) {
+                g.xv[u] = load16<false>(X + (size_t)bc * K + k);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) g.x[u][i] = X[(size_t)(k + i) * B + bc];
+            }
+        }
+    };
+    float4v acc[kSkR];
+#pragma unroll
+    for (int r = 0; r < kSkR; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](const Group& g) {
+#pragma unroll
+        for (int u = 0; u < kSkU; ++u) {
+            uint4 xr;
+            if constexpr (VEC_MAJOR) {
+                xr = g.xv[u];
+            } else {
+                half8 xb;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) xb[i] = g.x[u][i];
+                xr = __builtin_bit_cast(uint4, xb);
+            }
+            xr = make_uint4(xr.x & bmask, xr.y & bmask, xr.z & bmask, xr.w & bmask);
+#pragma unroll
+            for (int r = 0; r < kSkR; ++r)
+                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, g.a[r][u]),
+                                                                __builtin_bit_cast(half8, xr), acc[r], 0, 0, 0);
+        }
+    };
+    Group ga, gb;
+    issue(ga, 0);
+    for (uint32_t j = 0; j < n_groups; j += 2) {
+        issue(gb, j + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(ga);
+        issue(ga, j + 2 < n_groups ? j + 2 : j + 1);  // past the end: re-read, never consumed
+        __builtin_amdgcn_sched_barrier(0);
+        consume(gb);
+    }
+#pragma unroll
+    for (int r = 0; r < kSkR; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[wave][16 * r + (lane >> 4) * 4 + i][col] = acc[r][i];
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < kSkRows * 16; e += kSkWaves * 64) {
+        const uint32_t m = e >> 4, n = e & 15;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kSkWaves; ++w) v += part[w][m][n];
+        const uint32_t r = blockIdx.x * kSkRows + m;
+        if (r < N && n < B) store_elem(Y + (VEC_MAJOR ? (size_t)n * N + r : (size_t)r * B + n), v);
+    }
+}
+
+template <typename YT, bool VEC_MAJOR>
+int launch_skinny(const void* W, uint32_t N, uint32_t K, const void* X, uint32_t B, void* Y, hipStream_t s) {
+    k_skinny<YT, VEC_MAJOR><<<(N + kSkRows - 1) / kSkRows, kSkWaves * 64, 0, s>>>(
+        static_cast<const vsl_half*>(W), N, K, static_cast<const vsl_half*>(X), B, static_cast<YT*>(Y));
+    HIP_TRY(hipGetLastError());
+    return VSL_OK;
 }
 
 }  // namespace
@@ -1065,8 +1170,12 @@ extern "C" int vsl_gemv(const void* W, int wdtype, uint32_t N, uint32_t K, const
         (ydtype != VSL_DT_F16 && ydtype != VSL_DT_F32))
         return vsl_unsupported("vsl_gemv: dtype combination %d/%d/%d", wdtype, xdtype, ydtype);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (wdtype == VSL_DT_F16 && xdtype == VSL_DT_F16 && K % kSkKAlign == 0)
+        return ydtype == VSL_DT_F16 ? launch_skinny<vsl_half, false>(W, N, K, X, B, Y, s)
+                                    : launch_skinny<float, false>(W, N, K, X, B, Y, s);
     if (B == 1) {
-        if (xdtype == VSL_DT_F16) return vsl_unsupported("vsl_gemv: B=1 expects fp32 X (use the f16 path via B>1)");
+        if (xdtype == VSL_DT_F16)
+            return vsl_unsupported("vsl_gemv: B=1 with fp16 X needs K %% %u == 0 (else pass fp32 X)", kSkKAlign);
         GemvArgs a{};
         a.W = W;
         a.N = N;
@@ -1089,6 +1198,18 @@ extern "C" int vsl_gemv(const void* W, int wdtype, uint32_t N, uint32_t K, const
     }
     VSL_DISPATCH_XY(WF32)
 #undef VSL_DISPATCH_XY
+}
+
+extern "C" int vsl_gemv_batched(const void* W, uint32_t N, uint32_t K, const void* X, uint32_t B, void* Y, int ydtype,
+                                void* stream) {
+    if (!W || !X || !Y) return vsl_invalid("vsl_gemv_batched: null pointer");
+    if (N == 0 || K == 0) return vsl_invalid("vsl_gemv_batched: empty shape");
+    if (B < 1 || B > 16) return vsl_invalid("vsl_gemv_batched: B=%u must be in [1,16]", B);
+    if (K % kSkKAlign) return vsl_invalid("vsl_gemv_batched: K=%u must be a multiple of %u", K, kSkKAlign);
+    if (ydtype != VSL_DT_F16 && ydtype != VSL_DT_F32) return vsl_unsupported("vsl_gemv_batched: Y dtype %d", ydtype);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return ydtype == VSL_DT_F16 ? launch_skinny<vsl_half, true>(W, N, K, X, B, Y, s)
+                                : launch_skinny<float, true>(W, N, K, X, B, Y, s);
 }
 
 extern "C" int vsl_qkv_rope_append(const float* x, const float* gamma, float eps, const void* Wqkv, int wdtype,
