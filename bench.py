@@ -29,7 +29,7 @@ KV_CAPACITY = 4096
 # HBM bytes per launch of the dominant decode kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
 # passes summarised in profiles/decode_8b_rocprof.md (FETCH_SIZE scaled x1.9999 by a 1 GiB copy).
 # Re-measure with the commands listed there whenever the kernel changes.
-DOMINANT_TRAFFIC_BYTES = 235_220_000 + 57_000
+DOMINANT_TRAFFIC_BYTES = 235_240_000 + 115_000
 
 
 def load_package():
