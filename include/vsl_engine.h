@@ -31,7 +31,9 @@ typedef struct vsl_model_spec {
     uint32_t max_position_embeddings;
     float rope_theta, rms_eps;
     float init_std;    /* synthetic weights only: N(0, init_std) */
-    uint32_t dtype;    /* VSL_DT_F32 / VSL_DT_F16 for the linear weights */
+    uint32_t dtype;    /* storage of the linear weights: VSL_WF_F32 (== VSL_DT_F32) or VSL_WF_F16
+                          (== VSL_DT_F16); vsl_write_synthetic_gguf also takes VSL_WF_Q4_0 / Q4_1 /
+                          Q8_0 (every 2-D weight block-quantized from the fp32 draws) */
     uint32_t head_dim; /* filled by vsl_engine_get_config; ignored on input */
 } vsl_model_spec;
 
@@ -45,6 +47,8 @@ typedef struct vsl_engine_options {
     uint32_t prefill_split;  /* prefill activations carried as hi/lo fp16 pairs: bit 0 QKV input, bit 1
                                 attention q/probabilities, bit 2 O input, bit 3 gate/up input, bit 4
                                 down input; vsl_engine_default_options sets all five */
+    uint32_t dequant_f32;    /* block-quantized GGUF weights expand to fp32 packs (the exact values of
+                                dequantize_tensor, GGUFLoader.cpp:1121-1223) instead of fp16 packs */
 } vsl_engine_options;
 
 typedef struct vsl_gen_params {
@@ -103,7 +107,8 @@ int vsl_engine_benchmark(vsl_engine* e, uint32_t warmup, uint32_t tokens, uint32
 int vsl_engine_read_tensor(vsl_engine* e, const char* name, void* dst, uint64_t bytes, int* dtype_out);
 
 /* GGUF writer: synthetic Llama-style model with the reference's tensor names.
- * convention 0 = the reference's tensor-type ids (F32 6, F16 48), 1 = ggml ids (F32 0, F16 1). */
+ * convention 0 = the reference's tensor-type ids (F32 6, F16 48, Q4_0 13, Q4_1 14, Q8_0 17) and
+ * block layout, 1 = ggml ids (F32 0, F16 1, Q4_0 2, Q4_1 3, Q8_0 8) and ggml's block layout. */
 int vsl_write_synthetic_gguf(const char* path, const vsl_model_spec* spec, uint64_t seed, int convention);
 /* the host synthetic generator (same stream as vsl_fill_normal) */
 int vsl_synthetic_fill_host(void* out, int dtype, uint64_t n, uint64_t seed, const char* name, float mean,
@@ -120,7 +125,8 @@ int vsl_gguf_model_config(vsl_gguf* g, vsl_model_spec* out);
 /* -30 when the tensor does not exist */
 int vsl_gguf_tensor(vsl_gguf* g, const char* name, uint64_t* data_offset, uint64_t* data_size, uint32_t* raw_type,
                     uint32_t* n_dims, uint64_t dims[4]);
-/* returns the element count, or the reference's read codes (-11 read, -12 type, -20 quantized, -30 missing) */
+/* returns the element count, or the reference's read codes (-11 read, -12 type, -20 quantized, -30 missing);
+ * Q4_0 / Q4_1 / Q8_0 tensors are dequantized (dequantize_tensor, GGUFLoader.cpp:1121-1223) */
 int64_t vsl_gguf_read_f32(vsl_gguf* g, const char* name, float* out, uint64_t cap);
 
 /* ConfigManager (ConfigManager.h:133-270): parse CLI args / a TOML file into the singleton and read

@@ -106,6 +106,34 @@ int vsl_fill_normal(void* dst, int dtype, uint64_t n, uint64_t seed, const char*
 int vsl_fill_const(void* dst, int dtype, uint64_t n, float value, void* stream);
 
 /* ------------------------------------------------------------------------------------------
+ * GGUF weight storage expanded in HBM.  Replaces the dequant-on-load of
+ * GGUFLoaderImpl::read_tensor_data (vk_symbiote/src/GGUFLoader.cpp:761-793, which calls
+ * dequantize_tensor :1121-1223 and returns floats for the upload): here the raw blocks are
+ * uploaded and expanded on the device.
+ * ------------------------------------------------------------------------------------------ */
+/* storage formats (independent of either file's type ids) */
+enum { VSL_WF_F32 = 0, VSL_WF_F16 = 1, VSL_WF_Q4_0 = 2, VSL_WF_Q4_1 = 3, VSL_WF_Q8_0 = 4 };
+/* block layout of the quantized formats:
+ *  VSL_QL_REFERENCE  files with the reference's ids (Q4_0 = 13, Q4_1 = 14, Q8_0 = 17): byte i of
+ *                    the 16 nibble bytes holds elements 2i (low nibble) and 2i+1 (high nibble), as
+ *                    dequantize_tensor reads them (:1163-1168); fp16 scales converted by its local
+ *                    helper (:1132-1149), which drops the sign of a subnormal or zero scale
+ *  VSL_QL_GGML       files with ggml's ids (2, 3, 8): byte j holds elements j (low) and j + 16
+ *                    (high); scales are exact binary16
+ * Each block is 32 elements: Q4_0 = fp16 d + 16 bytes, x = (nibble - 8) d; Q4_1 = fp16 d, fp16 m
+ * + 16 bytes, x = nibble d + m; Q8_0 = fp16 d + 32 int8, x = q d. */
+enum { VSL_QL_REFERENCE = 0, VSL_QL_GGML = 1 };
+/* bytes of n elements stored in `fmt` (quantized: ceil(n / 32) whole blocks, as
+ * calculate_tensor_data_size, GGUFLoader.cpp:1111-1116); 0 for an unknown format */
+uint64_t vsl_weight_bytes(int fmt, uint64_t n);
+/* Expand n elements in `src_fmt` (device memory, vsl_weight_bytes(src_fmt, n) bytes) into dst as
+ * VSL_DT_F32 (the exact dequantized values) or VSL_DT_F16 (those values rounded to nearest even).
+ * F16 / F32 sources are converted elementwise (layout ignored).  src needs 2-byte alignment (4 for
+ * F32), dst 16-byte alignment; src and dst must not overlap. */
+int vsl_convert_weights(const void* src, int src_fmt, int layout, uint64_t n, void* dst, int dst_dtype,
+                        void* stream);
+
+/* ------------------------------------------------------------------------------------------
  * Decode control block (device memory).  One per engine; read by every decode kernel.
  * ------------------------------------------------------------------------------------------ */
 typedef struct vsl_ctrl {

@@ -46,6 +46,7 @@ _SIGS = {
                                     ctypes.POINTER(_U64), ctypes.POINTER(_U32), ctypes.POINTER(_U64),
                                     ctypes.POINTER(_U64)]),
     "orc_gguf_read_f32": (ctypes.c_int64, [_P, ctypes.c_char_p, _P, _U64]),
+    "orc_dequant": (ctypes.c_int64, [_P, _U64, _U32, _I32, _U64, _P]),
     "orc_gguf_get_u32": (_I32, [_P, ctypes.c_char_p, ctypes.POINTER(_U32)]),
     "orc_gguf_get_f32": (_I32, [_P, ctypes.c_char_p, ctypes.POINTER(_F32)]),
     "orc_gguf_model_config": (None, [_P, ctypes.POINTER(Config)]),

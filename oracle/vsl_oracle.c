@@ -22,6 +22,11 @@
  *                            Wq/Wk; committed golden token ids and logits
  *   orc_sample               greedy = lowest index of the max; seeded top-k vs a numpy restatement
  *                            of Utils.cpp:140-172 driven by the Philox stream
+ *   orc_dequant              hand-assembled Q4_0 / Q4_1 / Q8_0 blocks with literal expected values
+ *                            (nibble order of each convention, every int8 code, the scale helper's
+ *                            unsigned subnormals, partial and truncated final blocks, -20 for
+ *                            other quantized ids) and a bound |x - dq(q(x))| <= d/2 against an
+ *                            independent numpy quantizer
  */
 #define _GNU_SOURCE
 #include "vsl_oracle.h"
@@ -229,7 +234,8 @@ typedef struct {
     uint64_t dims[4];
     uint32_t raw_type;
     uint64_t offset, data_offset, data_size, n_elem;
-    int kind; /* 0 f32, 1 f16, -1 unsupported */
+    int kind;  /* 0 f32, 1 f16, -1 unsupported */
+    int quant; /* 1 for a block-quantized type that orc_dequant expands to fp32 */
 } gti;
 
 struct orc_gguf {
@@ -303,6 +309,66 @@ static uint64_t ggml_type_size(uint32_t t, uint64_t n) {
         case 30: return n * 2;               /* BF16 */
         default: return 0;
     }
+}
+
+/* Block formats expanded by orc_dequant: 0 Q4_0, 1 Q4_1, 2 Q8_0, -1 anything else.  Reference
+ * ids Q4_0 = 13, Q4_1 = 14, Q8_0 = 17 (GGUFLoader.h:18-73); ggml ids 2, 3, 8 (ggml's published
+ * type enum, which the reference does not use). */
+static int quant_format(uint32_t raw_type, int convention) {
+    if (convention == 0) return raw_type == 13 ? 0 : raw_type == 14 ? 1 : raw_type == 17 ? 2 : -1;
+    return raw_type == 2 ? 0 : raw_type == 3 ? 1 : raw_type == 8 ? 2 : -1;
+}
+
+/* The scale conversion local to dequantize_tensor (GGUFLoader.cpp:1132-1149).  It differs from
+ * IEEE binary16 only where the exponent field is 0: a subnormal becomes mantissa * 2^-24 with
+ * its sign dropped, and -0 becomes +0.  Infinities and NaNs keep their sign. */
+static float ref_block_scale(uint16_t h) {
+    const uint32_t exp = (h >> 10) & 0x1F, man = h & 0x3FF;
+    if (exp == 0) return man == 0 ? 0.0f : (float)man * 5.9604644775390625e-08f; /* exact */
+    return orc_h2f(h);
+}
+
+/* dequantize_tensor (GGUFLoader.cpp:1121-1223) for reference-convention files; for ggml-id files
+ * the same three formats with ggml's published block layout.
+ *   Q4_0  fp16 d, 16 bytes   x = (nibble - 8) * d
+ *   Q4_1  fp16 d, fp16 m, 16 bytes   x = nibble * d + m
+ *   Q8_0  fp16 d, 32 int8    x = q * d
+ * Nibble order: the reference reads byte i as elements 2i (low nibble) and 2i+1 (high nibble)
+ * (:1163-1168, :1187-1192); ggml stores element j < 16 in the low nibble of byte j and element
+ * j + 16 in its high nibble.  Scales: the reference's helper above, ggml's exact binary16.
+ * Every product q * d is exact in binary32 (at most 8 + 11 significant bits), so the result does
+ * not depend on evaluation order or FMA contraction.
+ * Blocks are read while a whole block remains in `size` bytes (the loop guard at :1157, :1178,
+ * :1203); the last block may be partial (n not a multiple of 32).  Returns the number of floats
+ * written, which is below n when the data runs out, or -20 for any other type. */
+int64_t orc_dequant(const void* data, uint64_t size, uint32_t raw_type, int convention, uint64_t n, float* out) {
+    const int q = quant_format(raw_type, convention);
+    if (q < 0) return -20;
+    const uint8_t* p = (const uint8_t*)data;
+    const uint64_t bb = q == 0 ? 18 : (q == 1 ? 20 : 34);
+    const uint64_t nb = (n + 31) / 32;
+    uint64_t w = 0;
+    for (uint64_t b = 0; b < nb && (b + 1) * bb <= size; ++b) {
+        const uint8_t* blk = p + b * bb;
+        uint16_t hd, hm = 0;
+        memcpy(&hd, blk, 2);
+        if (q == 1) memcpy(&hm, blk + 2, 2);
+        const float d = convention == 0 ? ref_block_scale(hd) : orc_h2f(hd);
+        const float m = q != 1 ? 0.0f : (convention == 0 ? ref_block_scale(hm) : orc_h2f(hm));
+        const uint8_t* qs = blk + (q == 1 ? 4 : 2);
+        for (int j = 0; j < 32 && w < n; ++j) {
+            float v;
+            if (q == 2) {
+                v = (float)(int8_t)qs[j] * d;
+            } else {
+                const int nib = convention == 0 ? ((j & 1) ? qs[j >> 1] >> 4 : qs[j >> 1] & 15)
+                                                : (j < 16 ? qs[j] & 15 : qs[j - 16] >> 4);
+                v = q == 0 ? (float)(nib - 8) * d : (float)nib * d + m;
+            }
+            out[w++] = v;
+        }
+    }
+    return (int64_t)w;
 }
 
 static const gkv* find_kv(const orc_gguf* g, const char* key) {
@@ -407,9 +473,12 @@ int orc_gguf_open(const char* path, orc_gguf** out) {
         if (g->convention == 0) {
             t->data_size = ref_type_size(t->raw_type, t->n_elem);
             t->kind = t->raw_type == 6 ? ORC_F32 : (t->raw_type == 48 ? ORC_F16 : -1);
+            t->quant = quant_format(t->raw_type, 0) >= 0;
         } else {
             t->data_size = ggml_type_size(t->raw_type, t->n_elem);
             t->kind = t->raw_type == 0 ? ORC_F32 : (t->raw_type == 1 ? ORC_F16 : -1);
+            /* ggml blocks never straddle rows: ne0 must be a whole number of blocks */
+            t->quant = quant_format(t->raw_type, 1) >= 0 && t->n_dims > 0 && t->dims[0] % 32 == 0;
         }
     }
     *out = g;
@@ -456,6 +525,14 @@ int64_t orc_gguf_read_f32(const orc_gguf* g, const char* name, float* out, uint6
     const gti* t = &g->tis[i];
     const void* p = tensor_ptr(g, t);
     if (!p) return -11;
+    if (t->quant) {
+        if (t->n_elem > cap) return -11;
+        return orc_dequant(p, t->data_size, t->raw_type, g->convention, t->n_elem, out);
+    }
+    if (quant_format(t->raw_type, g->convention) >= 0 ||
+        (g->convention == 0 ? (t->raw_type >= 13 && t->raw_type <= 53 && t->raw_type != 48)
+                            : (t->raw_type >= 2 && t->raw_type != 30)))
+        return -20; /* other quantized ids reach dequantize_tensor's default case (:1219-1220) */
     if (t->kind < 0) return -12;
     if (t->n_elem > cap) return -11;
     if (t->kind == ORC_F32) {
@@ -663,9 +740,19 @@ int orc_model_from_gguf(const char* path, orc_model** out) {
     m->gguf = g;
     for (uint64_t i = 0; i < g->n_tensors; ++i) {
         const gti* t = &g->tis[i];
-        if (t->kind < 0) continue;
+        if (t->kind < 0 && !t->quant) continue;
         const void* p = tensor_ptr(g, t);
         if (!p) { orc_model_free(m); return -11; }
+        if (t->quant) { /* dequant-on-load: an owned fp32 copy */
+            float* f = (float*)malloc((t->n_elem ? t->n_elem : 1) * sizeof(float));
+            own(m, f);
+            if (orc_dequant(p, t->data_size, t->raw_type, g->convention, t->n_elem, f) != (int64_t)t->n_elem) {
+                orc_model_free(m);
+                return -11;
+            }
+            orc_model_set_tensor(m, t->name, f, ORC_F32, 0);
+            continue;
+        }
         orc_model_set_tensor(m, t->name, p, t->kind, 0);
     }
     if (orc_model_check(m)) { orc_model_free(m); return -30; }

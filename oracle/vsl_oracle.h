@@ -74,8 +74,12 @@ int orc_gguf_find(const orc_gguf* g, const char* name);
 int orc_gguf_tensor_info(const orc_gguf* g, int idx, char* name_out, size_t name_cap,
                          uint32_t* n_dims, uint64_t dims[4], uint32_t* raw_type,
                          uint64_t* data_offset, uint64_t* data_size);
-/* read tensor as fp32 (GGUFLoaderImpl::read_tensor_data semantics); returns element count or <0 */
+/* read tensor as fp32 (GGUFLoaderImpl::read_tensor_data semantics, Q4_0/Q4_1/Q8_0 dequantized);
+ * returns element count or <0 (-20 for other quantized types) */
 int64_t orc_gguf_read_f32(const orc_gguf* g, const char* name, float* out, uint64_t cap);
+/* dequantize_tensor (GGUFLoader.cpp:1121-1223): raw_type in the file's convention (0 reference
+ * ids 13/14/17, 1 ggml ids 2/3/8); returns floats written (fewer than n when size runs out) or -20 */
+int64_t orc_dequant(const void* data, uint64_t size, uint32_t raw_type, int convention, uint64_t n, float* out);
 /* metadata scalars; return 0 when found with the exact type, -1 otherwise */
 int orc_gguf_get_u32(const orc_gguf* g, const char* key, uint32_t* v);
 int orc_gguf_get_f32(const orc_gguf* g, const char* key, float* v);

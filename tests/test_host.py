@@ -104,7 +104,7 @@ def test_product_gguf_error_codes(vsl, tmp_path):
     ti.write_bytes(data[:hdr + 10])
     assert _gguf(vsl, ti)[0] == -4
     q = tmp_path / "q.gguf"
-    q.write_bytes(build_gguf([("t", [32], 17, b"\0" * 34)], [])[0])  # Q8_0 in the reference's ids
+    q.write_bytes(build_gguf([("t", [32], 15, b"\0" * 22)], [])[0])  # Q5_0: dequantize_tensor's -20
     rc, h = _gguf(vsl, q)
     assert rc == 0
     out = np.zeros(64, np.float32)

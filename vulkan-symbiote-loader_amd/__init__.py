@@ -21,6 +21,8 @@ HIP_LIB = os.path.join(LIB_DIR, "libvsl_hip.so")
 ENGINE_LIB = os.path.join(LIB_DIR, "libvsl_engine.so")
 
 VSL_DT_F32, VSL_DT_F16, VSL_DT_F16X2 = 0, 1, 2
+VSL_WF_F32, VSL_WF_F16, VSL_WF_Q4_0, VSL_WF_Q4_1, VSL_WF_Q8_0 = 0, 1, 2, 3, 4
+VSL_QL_REFERENCE, VSL_QL_GGML = 0, 1
 GEMM_A_X2, GEMM_C_X2 = 0x100, 0x200
 SAMPLE_GREEDY, SAMPLE_REFERENCE, SAMPLE_TOPK_SEEDED = 0, 1, 2
 EPI_STORE_F32, EPI_STORE_F16, EPI_RESID, EPI_SWIGLU = 0, 1, 2, 3
@@ -44,7 +46,8 @@ class ModelSpec(ctypes.Structure):
 class EngineOptions(ctypes.Structure):
     _fields_ = [("device", ctypes.c_int32), ("kv_capacity", ctypes.c_uint32), ("use_graph", ctypes.c_uint32),
                 ("prefill_chunk", ctypes.c_uint32), ("attn_splits", ctypes.c_uint32),
-                ("batched_prefill", ctypes.c_uint32), ("prefill_split", ctypes.c_uint32)]
+                ("batched_prefill", ctypes.c_uint32), ("prefill_split", ctypes.c_uint32),
+                ("dequant_f32", ctypes.c_uint32)]
 
 
 class GenParams(ctypes.Structure):
@@ -89,6 +92,8 @@ _HIP_SIGS = {
     "vsl_set_device": (_I32, [_I32]),
     "vsl_device_sync": (_I32, []),
     "vsl_arena_create": (_I32, [_I32, _U64, ctypes.POINTER(_P)]),
+    "vsl_weight_bytes": (_U64, [_I32, _U64]),
+    "vsl_convert_weights": (_I32, [_P, _I32, _I32, _U64, _P, _I32, _P]),
     "vsl_arena_destroy": (_I32, [_P]),
     "vsl_arena_alloc": (_I32, [_P, _U64, _U64, ctypes.POINTER(_P)]),
     "vsl_arena_free": (_I32, [_P, _P]),
@@ -244,7 +249,8 @@ class Engine:
     """VulkanSymbioteEngine on one MI355X."""
 
     def __init__(self, gguf_path=None, spec=None, seed=0, device=0, kv_capacity=0, use_graph=True,
-                 prefill_chunk=0, attn_splits=0, batched_prefill=True, init_std=0.02, prefill_split=None):
+                 prefill_chunk=0, attn_splits=0, batched_prefill=True, init_std=0.02, prefill_split=None,
+                 dequant_f32=False):
         self._lib = engine_lib()
         opt = EngineOptions()
         self._lib.vsl_engine_default_options(ctypes.byref(opt))
@@ -252,6 +258,7 @@ class Engine:
         opt.prefill_chunk, opt.attn_splits, opt.batched_prefill = prefill_chunk, attn_splits, int(bool(batched_prefill))
         if prefill_split is not None:
             opt.prefill_split = prefill_split
+        opt.dequant_f32 = int(bool(dequant_f32))
         h = ctypes.c_void_p()
         if gguf_path is not None:
             rc = self._lib.vsl_engine_open(str(gguf_path).encode(), ctypes.byref(opt), ctypes.byref(h))

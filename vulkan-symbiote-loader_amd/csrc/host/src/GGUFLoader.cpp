@@ -138,6 +138,27 @@ uint64_t ggml_type_size(uint32_t t, uint64_t n) {
     }
 }
 
+// The scale helper local to dequantize_tensor (GGUFLoader.cpp:1132-1149).  Where the exponent
+// field is 0 it returns ldexp(mantissa, -24) with no sign (so -0 reads as +0 and a negative
+// subnormal as positive); every other pattern converts exactly.
+float reference_block_scale(uint16_t h) {
+    if (((h >> 10) & 0x1F) == 0) return static_cast<float>(h & 0x3FF) * 5.9604644775390625e-08f;
+    return half_to_float(h);
+}
+
+constexpr uint64_t kBlock = 32;
+
+uint64_t block_bytes(int fmt) {
+    return fmt == VSL_WF_Q4_0 ? 18 : fmt == VSL_WF_Q4_1 ? 20 : fmt == VSL_WF_Q8_0 ? 34 : 0;
+}
+
+// element index held by nibble `hi` (0 low, 1 high) of byte i in a 4-bit block
+inline uint32_t nibble_element(uint32_t i, uint32_t hi, bool ref_layout) {
+    return ref_layout ? 2 * i + hi : i + 16 * hi;
+}
+
+}  // namespace
+
 float half_to_float(uint16_t h) {
     uint32_t sign = static_cast<uint32_t>(h >> 15) << 31, e = (h >> 10) & 0x1F, m = h & 0x3FF, bits;
     if (e == 0) {
@@ -158,7 +179,109 @@ float half_to_float(uint16_t h) {
     return f;
 }
 
-}  // namespace
+uint16_t float_to_half(float f) {  // round to nearest even
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u, a = x & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | ((a & 0x7FFFFFu) ? (0x200u | ((a & 0x7FFFFFu) >> 13)) : 0));
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
+    if (a < 0x38800000u) {
+        if (a < 0x33000000u) return (uint16_t)sign;
+        uint32_t e = a >> 23, m = (a & 0x7FFFFFu) | 0x800000u, sh = 126 - e;
+        uint32_t q = m >> sh, rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+        if (rem > half || (rem == half && (q & 1))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = (((a >> 23) - 112) << 10) | ((a & 0x7FFFFFu) >> 13), rem = a & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1))) q++;
+    return (uint16_t)(sign | q);
+}
+
+uint64 dequantize_blocks(const uint8_t* src, uint64 src_bytes, int fmt, int layout, uint64 n, float* out) {
+    const uint64_t bb = block_bytes(fmt);
+    if (!bb) return 0;
+    const bool ref = layout == VSL_QL_REFERENCE;
+    auto scale = [&](const uint8_t* p) {
+        uint16_t h;
+        std::memcpy(&h, p, 2);
+        return ref ? reference_block_scale(h) : half_to_float(h);
+    };
+    uint64_t done = 0;
+    for (uint64_t b = 0; done < n && (b + 1) * bb <= src_bytes; ++b) {
+        const uint8_t* blk = src + b * bb;
+        const uint64_t cnt = std::min<uint64_t>(kBlock, n - done);
+        float v[kBlock];
+        const float d = scale(blk);
+        if (fmt == VSL_WF_Q8_0) {
+            for (uint32_t j = 0; j < kBlock; ++j) v[j] = static_cast<float>(static_cast<int8_t>(blk[2 + j])) * d;
+        } else {
+            // Q4_0 is (nibble - 8) * d with no addend: adding +0 would turn a -0 product into +0
+            const bool with_min = fmt == VSL_WF_Q4_1;
+            const float m = with_min ? scale(blk + 2) : 0.0f;
+            const uint8_t* qs = blk + (with_min ? 4 : 2);
+            for (uint32_t i = 0; i < 16; ++i)
+                for (uint32_t hi = 0; hi < 2; ++hi) {
+                    const int nib = (qs[i] >> (4 * hi)) & 15;
+                    v[nibble_element(i, hi, ref)] =
+                        with_min ? static_cast<float>(nib) * d + m : static_cast<float>(nib - 8) * d;
+                }
+        }
+        std::memcpy(out + done, v, cnt * sizeof(float));
+        done += cnt;
+    }
+    return done;
+}
+
+std::vector<uint8_t> quantize_blocks(const float* x, uint64 n, int fmt, int layout) {
+    const uint64_t bb = block_bytes(fmt), nb = (n + kBlock - 1) / kBlock;
+    std::vector<uint8_t> out(nb * bb, 0);
+    if (!bb) return {};
+    const bool ref = layout == VSL_QL_REFERENCE;
+    for (uint64_t b = 0; b < nb; ++b) {
+        float v[kBlock] = {0};
+        const uint64_t cnt = std::min<uint64_t>(kBlock, n - b * kBlock);
+        std::memcpy(v, x + b * kBlock, cnt * sizeof(float));
+        uint8_t* blk = out.data() + b * bb;
+        auto put_half = [](uint8_t* p, float f) {
+            const uint16_t h = float_to_half(f);
+            std::memcpy(p, &h, 2);
+            return half_to_float(h);  // the scale the reader will see
+        };
+        if (fmt == VSL_WF_Q8_0) {
+            float amax = 0.0f;
+            for (float f : v) amax = std::max(amax, std::fabs(f));
+            const float d = put_half(blk, amax / 127.0f);
+            const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+            for (uint32_t j = 0; j < kBlock; ++j) {
+                const float q = std::nearbyint(v[j] * inv);
+                blk[2 + j] = static_cast<uint8_t>(static_cast<int8_t>(std::min(127.0f, std::max(-128.0f, q))));
+            }
+            continue;
+        }
+        uint8_t nib[kBlock];
+        if (fmt == VSL_WF_Q4_0) {
+            float ext = 0.0f;
+            for (float f : v)
+                if (std::fabs(f) > std::fabs(ext)) ext = f;
+            const float d = put_half(blk, ext / -8.0f);
+            const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+            for (uint32_t j = 0; j < kBlock; ++j)
+                nib[j] = static_cast<uint8_t>(std::min(15.0f, std::max(0.0f, std::floor(v[j] * inv + 8.5f))));
+        } else {
+            float lo = v[0], hi = v[0];
+            for (float f : v) { lo = std::min(lo, f); hi = std::max(hi, f); }
+            const float d = put_half(blk, (hi - lo) / 15.0f);
+            const float m = put_half(blk + 2, lo);
+            const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+            for (uint32_t j = 0; j < kBlock; ++j)
+                nib[j] = static_cast<uint8_t>(std::min(15.0f, std::max(0.0f, std::floor((v[j] - m) * inv + 0.5f))));
+        }
+        uint8_t* qs = blk + (fmt == VSL_WF_Q4_1 ? 4 : 2);
+        for (uint32_t i = 0; i < 16; ++i)
+            qs[i] = static_cast<uint8_t>(nib[nibble_element(i, 0, ref)] | (nib[nibble_element(i, 1, ref)] << 4));
+    }
+    return out;
+}
 
 GGUFLoader::GGUFLoader(const Path& file_path) : file_path_(file_path) {}
 GGUFLoader::~GGUFLoader() { close(); }
@@ -342,6 +465,33 @@ int GGUFLoader::storage_dtype(const GGUFTensorInfo& t) const {
     return -1;
 }
 
+int GGUFLoader::weight_format(const GGUFTensorInfo& t) const {
+    const uint32_t id = static_cast<uint32_t>(t.data_type);
+    if (convention_ == GGUFConvention::REFERENCE) {
+        switch (id) {
+            case 6: return VSL_WF_F32;
+            case 48: return VSL_WF_F16;
+            case 13: return VSL_WF_Q4_0;
+            case 14: return VSL_WF_Q4_1;
+            case 17: return VSL_WF_Q8_0;
+            default: return -1;
+        }
+    }
+    switch (id) {
+        case 0: return VSL_WF_F32;
+        case 1: return VSL_WF_F16;
+        case 2: case 3: case 8:
+            // ggml never splits a block across rows
+            if (t.dimensions.empty() || t.dimensions[0] % kBlock) return -1;
+            return id == 2 ? VSL_WF_Q4_0 : (id == 3 ? VSL_WF_Q4_1 : VSL_WF_Q8_0);
+        default: return -1;
+    }
+}
+
+int GGUFLoader::block_layout() const {
+    return convention_ == GGUFConvention::GGML ? VSL_QL_GGML : VSL_QL_REFERENCE;
+}
+
 const uint8_t* GGUFLoader::tensor_bytes(const GGUFTensorInfo& t) const {
     if (!map_ || t.data_offset + t.data_size > size_ || t.data_offset < data_start_) return nullptr;
     return map_ + t.data_offset;
@@ -364,6 +514,14 @@ Expected<std::vector<float>> GGUFLoader::read_tensor_data(const GGUFTensorInfo& 
             std::memcpy(&h, p + 2 * i, 2);
             r[i] = half_to_float(h);
         }
+        return r;
+    }
+    const int wf = weight_format(t);
+    if (wf >= VSL_WF_Q4_0) {  // read_tensor_data -> dequantize_tensor (:775-777)
+        uint64_t n = 1;
+        for (auto x : t.dimensions) n *= x;
+        std::vector<float> r(n);
+        r.resize(dequantize_blocks(p, t.data_size, wf, block_layout(), n, r.data()));
         return r;
     }
     const uint32_t id = static_cast<uint32_t>(t.data_type);
@@ -433,7 +591,11 @@ void GGUFWriter::add_string(const std::string& key, const std::string& v) {
 }
 void GGUFWriter::add_tensor(const std::string& name, const std::vector<uint64_t>& dims, bool is_f16, const void* data,
                             uint64_t bytes) {
-    tensors_.push_back(T{name, dims, is_f16, data, bytes});
+    tensors_.push_back(T{name, dims, is_f16 ? VSL_WF_F16 : VSL_WF_F32, data, bytes});
+}
+void GGUFWriter::add_tensor_format(const std::string& name, const std::vector<uint64_t>& dims, int fmt,
+                                   const void* data, uint64_t bytes) {
+    tensors_.push_back(T{name, dims, fmt, data, bytes});
 }
 
 ExpectedVoid GGUFWriter::write(const Path& path) const {
@@ -486,7 +648,9 @@ ExpectedVoid GGUFWriter::write(const Path& path) const {
         uint32_t nd = static_cast<uint32_t>(t.dims.size());
         put(&nd, 4);
         for (auto d : t.dims) put(&d, 8);
-        uint32_t ty = conv_ == GGUFConvention::GGML ? (t.is_f16 ? 1u : 0u) : (t.is_f16 ? 48u : 6u);
+        // type ids per format F32, F16, Q4_0, Q4_1, Q8_0
+        static const uint32_t kRefIds[5] = {6, 48, 13, 14, 17}, kGgmlIds[5] = {0, 1, 2, 3, 8};
+        const uint32_t ty = (conv_ == GGUFConvention::GGML ? kGgmlIds : kRefIds)[t.fmt];
         put(&ty, 4);
         put(&off, 8);
         offs.push_back(off);

@@ -52,40 +52,6 @@ void philox(uint32_t c[4], uint32_t k0, uint32_t k1) {
     }
 }
 
-uint16_t float_to_half(float f) {  // round to nearest even
-    uint32_t x;
-    std::memcpy(&x, &f, 4);
-    uint32_t sign = (x >> 16) & 0x8000u, a = x & 0x7FFFFFFFu;
-    if (a >= 0x7F800000u) return (uint16_t)(sign | 0x7C00u | ((a & 0x7FFFFFu) ? (0x200u | ((a & 0x7FFFFFu) >> 13)) : 0));
-    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);
-    if (a < 0x38800000u) {
-        if (a < 0x33000000u) return (uint16_t)sign;
-        uint32_t e = a >> 23, m = (a & 0x7FFFFFu) | 0x800000u, sh = 126 - e;
-        uint32_t q = m >> sh, rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
-        if (rem > half || (rem == half && (q & 1))) q++;
-        return (uint16_t)(sign | q);
-    }
-    uint32_t q = (((a >> 23) - 112) << 10) | ((a & 0x7FFFFFu) >> 13), rem = a & 0x1FFFu;
-    if (rem > 0x1000u || (rem == 0x1000u && (q & 1))) q++;
-    return (uint16_t)(sign | q);
-}
-
-float half_to_float_h(uint16_t h) {
-    uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1F, m = h & 0x3FF, bits;
-    if (e == 0) {
-        if (m == 0) bits = sign;
-        else {
-            float v = (float)m * 5.9604644775390625e-08f;
-            std::memcpy(&bits, &v, 4);
-            bits |= sign;
-        }
-    } else if (e == 31) bits = sign | 0x7F800000u | (m << 13);
-    else bits = sign | ((e + 112u) << 23) | (m << 13);
-    float f;
-    std::memcpy(&f, &bits, 4);
-    return f;
-}
-
 std::string layer_name(uint32_t l, const char* suffix) { return "blk." + std::to_string(l) + "." + suffix; }
 
 uint64_t align256(uint64_t n) { return (n + 255) & ~uint64_t(255); }
@@ -149,8 +115,21 @@ ExpectedVoid write_synthetic_gguf(const Path& path, const SyntheticSpec& spec, G
     w.add_f32("llama.rope.freq_base", c.rope_theta);
     w.add_f32("llama.attention.layer_norm_rms_epsilon", c.rms_epsilon);
     std::vector<std::vector<uint8_t>> store;
+    const bool quant = spec.quant_format >= VSL_WF_Q4_0 && spec.quant_format <= VSL_WF_Q8_0;
+    if (spec.quant_format >= 0 && !quant) return kErrInvalid;
+    // ggml blocks never straddle rows: every ne0 (d, and F for ffn_down) must be whole blocks
+    if (quant && conv == GGUFConvention::GGML && (c.hidden_size % 32 || c.intermediate_size % 32)) return kErrInvalid;
+    const int layout = conv == GGUFConvention::GGML ? VSL_QL_GGML : VSL_QL_REFERENCE;
     auto add_rand = [&](const std::string& name, uint64_t ne0, uint64_t ne1) {
-        const uint64_t n = ne0 * ne1, es = spec.fp16 ? 2 : 4;
+        const uint64_t n = ne0 * ne1;
+        if (quant) {
+            std::vector<float> x(n);
+            synthetic_fill_host(x.data(), false, n, spec.seed, name, 0.0f, spec.init_std);
+            store.push_back(quantize_blocks(x.data(), n, spec.quant_format, layout));
+            w.add_tensor_format(name, {ne0, ne1}, spec.quant_format, store.back().data(), store.back().size());
+            return;
+        }
+        const uint64_t es = spec.fp16 ? 2 : 4;
         store.emplace_back(n * es);
         synthetic_fill_host(store.back().data(), spec.fp16, n, spec.seed, name, 0.0f, spec.init_std);
         w.add_tensor(name, {ne0, ne1}, spec.fp16, store.back().data(), n * es);
@@ -227,10 +206,17 @@ VulkanSymbioteEngine::VulkanSymbioteEngine(const Path& model_path, const EngineO
     const GGUFTensorInfo* q = loader_->get_tensor("blk.0.attn_q.weight");
     const GGUFTensorInfo* e = loader_->get_tensor("token_embd.weight");
     if (!q || !e) throw std::runtime_error("Failed to load model: blk.0.attn_q.weight / token_embd.weight missing");
-    const int wdt = loader_->storage_dtype(*q), edt = loader_->storage_dtype(*e);
-    if (wdt < 0 || edt < 0) throw std::runtime_error("Failed to load model: unsupported tensor type (F32/F16 only)");
+    const int qf = loader_->weight_format(*q), ef = loader_->weight_format(*e);
+    if (qf < 0 || ef < 0)
+        throw std::runtime_error("Failed to load model: unsupported tensor type (F32, F16, Q4_0, Q4_1, Q8_0)");
+    // F32 / F16 packs keep the stored type; block-quantized weights expand to fp16, or to fp32 on request
+    auto pack_dtype = [&](int wf) {
+        if (wf == VSL_WF_F32) return static_cast<int>(VSL_DT_F32);
+        if (wf == VSL_WF_F16) return static_cast<int>(VSL_DT_F16);
+        return static_cast<int>(options_.dequant_f32 ? VSL_DT_F32 : VSL_DT_F16);
+    };
     try {
-        init_device(cfg, wdt == VSL_DT_F16, edt);
+        init_device(cfg, pack_dtype(qf) == VSL_DT_F16, pack_dtype(ef));
         load_weights_from_gguf();
     } catch (...) {
         release();
@@ -465,47 +451,68 @@ void VulkanSymbioteEngine::load_weights_from_gguf() {
             if (p.tensor_name == name) return p;
         return PackMetadata{};
     };
-    auto need = [&](const std::string& name, uint64_t elems, int want_dt) -> const GGUFTensorInfo& {
+    // Formats other than the pack dtype (block-quantized, or F16 <-> F32) cross PCIe in their stored
+    // form into a device staging slot and are expanded there by vsl_convert_weights.
+    std::unique_ptr<vsl_arena, int (*)(vsl_arena*)> conv_arena(nullptr, vsl_arena_destroy);
+    void* dstage[2] = {nullptr, nullptr};
+    auto upload_convert = [&](void* dst, const uint8_t* src, int fmt, uint64_t n, int dst_dt) {
+        if (!conv_arena) {
+            vsl_arena* a = nullptr;
+            check(vsl_arena_create(options_.device, 2 * kStageBytes + (1u << 20), &a), "staging arena");
+            conv_arena.reset(a);
+            for (auto& p : dstage) check(vsl_arena_alloc(a, kStageBytes, 256, &p), "staging alloc");
+        }
+        // elements per slot: whole blocks for the quantized formats
+        const uint64_t per = fmt >= VSL_WF_Q4_0 ? kStageBytes / vsl_weight_bytes(fmt, 32) * 32
+                                                : kStageBytes / vsl_weight_bytes(fmt, 1);
+        const uint64_t es = dst_dt == VSL_DT_F16 ? 2 : 4;
+        for (uint64_t e0 = 0; e0 < n; e0 += per) {
+            const uint64_t cnt = std::min(per, n - e0), off = vsl_weight_bytes(fmt, e0),
+                           len = vsl_weight_bytes(fmt, cnt);
+            if (pending[slot]) check(vsl_event_sync(ev_[2 + slot]), "staging wait");
+            std::memcpy(stage[slot], src + off, len);
+            check(vsl_pack_upload(dstage[slot], stage[slot], len, upload_stream_, nullptr), "vsl_pack_upload");
+            check(vsl_convert_weights(dstage[slot], fmt, g.block_layout(), cnt, static_cast<char*>(dst) + e0 * es,
+                                      dst_dt, upload_stream_),
+                  "vsl_convert_weights");
+            check(vsl_event_record(ev_[2 + slot], upload_stream_), "staging event");
+            pending[slot] = true;
+            slot ^= 1;
+        }
+    };
+    auto need = [&](const std::string& name, uint64_t elems) -> const GGUFTensorInfo& {
         const GGUFTensorInfo* t = g.get_tensor(name);
         if (!t) throw std::runtime_error("missing tensor " + name);
         uint64_t n = 1;
         for (auto x : t->dimensions) n *= x;
         if (n != elems) throw std::runtime_error("tensor " + name + " has " + std::to_string(n) + " elements, expected " + std::to_string(elems));
-        if (want_dt >= 0 && g.storage_dtype(*t) != want_dt)
-            throw std::runtime_error("tensor " + name + " storage type does not match the model's linear weights");
-        if (g.storage_dtype(*t) < 0) throw std::runtime_error("tensor " + name + " has an unsupported type");
-        if (!g.tensor_bytes(*t)) throw std::runtime_error("tensor " + name + " data out of range");
+        if (g.weight_format(*t) < 0) throw std::runtime_error("tensor " + name + " has an unsupported type");
+        if (!g.tensor_bytes(*t) || t->data_size < vsl_weight_bytes(g.weight_format(*t), n))
+            throw std::runtime_error("tensor " + name + " data out of range");
         return *t;
     };
-    auto load_linear = [&](void* dst, const std::string& name, uint64_t elems) {
-        const GGUFTensorInfo& t = need(name, elems, wdt_);
-        upload(dst, g.tensor_bytes(t), t.data_size);
-        pack_manager_.register_pack(meta_of(name), dst, t.data_size, wdt_);
+    // a weight tensor into a pack of dtype `dt`: raw bytes when stored in that dtype, else expanded
+    auto load_weight = [&](void* dst, const std::string& name, uint64_t elems, int dt) {
+        const GGUFTensorInfo& t = need(name, elems);
+        const int fmt = g.weight_format(t);
+        if (fmt == (dt == VSL_DT_F16 ? VSL_WF_F16 : VSL_WF_F32))
+            upload(dst, g.tensor_bytes(t), vsl_weight_bytes(fmt, elems));
+        else
+            upload_convert(dst, g.tensor_bytes(t), fmt, elems, dt);
+        pack_manager_.register_pack(meta_of(name), dst, elems * (dt == VSL_DT_F16 ? 2 : 4), dt);
     };
+    auto load_linear = [&](void* dst, const std::string& name, uint64_t elems) { load_weight(dst, name, elems, wdt_); };
     std::vector<std::vector<float>> norm_host;
     norm_host.reserve(2 * c.num_layers + 1);
     auto load_norm = [&](float* dst, const std::string& name) {
-        const GGUFTensorInfo& t = need(name, d, -1);
-        norm_host.emplace_back(d);
-        std::vector<float>& h = norm_host.back();
-        const uint8_t* src = g.tensor_bytes(t);
-        if (g.storage_dtype(t) == VSL_DT_F32) {
-            std::memcpy(h.data(), src, d * 4);
-        } else {
-            for (uint64_t i = 0; i < d; ++i) {
-                uint16_t v;
-                std::memcpy(&v, src + 2 * i, 2);
-                h[i] = half_to_float_h(v);
-            }
-        }
-        check(vsl_copy_h2d(dst, h.data(), d * 4, upload_stream_), "norm upload");
+        const GGUFTensorInfo& t = need(name, d);
+        auto r = g.read_tensor_data(t, true);  // F32 copied, F16 converted, blocks dequantized
+        if (!r.has_value() || r.value().size() != d) throw std::runtime_error("cannot read " + name);
+        norm_host.push_back(std::move(r.value()));
+        check(vsl_copy_h2d(dst, norm_host.back().data(), d * 4, upload_stream_), "norm upload");
         pack_manager_.register_pack(meta_of(name), dst, d * 4, VSL_DT_F32);
     };
-    {
-        const GGUFTensorInfo& t = need("token_embd.weight", V * d, edt_);
-        upload(embed_, g.tensor_bytes(t), t.data_size);
-        pack_manager_.register_pack(meta_of("token_embd.weight"), embed_, t.data_size, edt_);
-    }
+    load_weight(embed_, "token_embd.weight", V * d, edt_);
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         Layer& y = layers_[l];
         const uint64_t es = wdt_ == VSL_DT_F16 ? 2 : 4;
@@ -529,11 +536,15 @@ void VulkanSymbioteEngine::load_weights_from_gguf() {
     }
     if (g.get_tensor("output.weight")) {
         load_linear(out_w_, "output.weight", V * d);
-    } else {
-        if (edt_ != wdt_) throw std::runtime_error("tied output projection needs token_embd in the linear weight type");
+    } else if (edt_ == wdt_) {  // tied output projection
         check(vsl_copy_d2d(out_w_, embed_, V * d * (wdt_ == VSL_DT_F16 ? 2 : 4), upload_stream_), "tied output");
+    } else {
+        check(vsl_convert_weights(embed_, edt_ == VSL_DT_F16 ? VSL_WF_F16 : VSL_WF_F32, VSL_QL_REFERENCE, V * d,
+                                  out_w_, wdt_, upload_stream_),
+              "tied output");
     }
     check(vsl_stream_sync(upload_stream_), "upload sync");
+    conv_arena.reset();
     vsl_host_pinned_free(stage[0]);
     vsl_host_pinned_free(stage[1]);
 }

@@ -41,6 +41,7 @@ static EngineOptions to_options(const vsl_engine_options* o) {
     e.attn_splits = o->attn_splits;
     e.batched_prefill = o->batched_prefill != 0;
     e.prefill_split = o->prefill_split & EngineOptions::kPrefillSplitAll;
+    e.dequant_f32 = o->dequant_f32 != 0;
     return e;
 }
 
@@ -78,6 +79,9 @@ extern "C" int vsl_engine_open_synthetic(const vsl_model_spec* spec, uint64_t se
     if (!spec || !out) return fail(VSL_E_INVALID, "vsl_engine_open_synthetic: null argument");
     *out = nullptr;
     try {
+        if (spec->dtype > VSL_DT_F16)
+            return fail(VSL_E_UNSUPPORTED, "vsl_engine_open_synthetic: weights are F32 or F16 (quantized "
+                                           "models are opened from a GGUF file)");
         SyntheticSpec s;
         s.config = to_config(spec);
         s.fp16 = spec->dtype == VSL_DT_F16;
@@ -293,9 +297,11 @@ extern "C" int vsl_engine_read_tensor(vsl_engine* e, const char* name, void* dst
 
 extern "C" int vsl_write_synthetic_gguf(const char* path, const vsl_model_spec* spec, uint64_t seed, int convention) {
     if (!path || !spec) return fail(VSL_E_INVALID, "vsl_write_synthetic_gguf: null argument");
+    if (spec->dtype > VSL_WF_Q8_0) return fail(VSL_E_INVALID, "vsl_write_synthetic_gguf: unknown weight format");
     SyntheticSpec s;
     s.config = to_config(spec);
     s.fp16 = spec->dtype == VSL_DT_F16;
+    s.quant_format = spec->dtype >= VSL_WF_Q4_0 ? static_cast<int>(spec->dtype) : -1;
     s.init_std = spec->init_std > 0 ? spec->init_std : 0.02f;
     s.seed = seed;
     auto r = write_synthetic_gguf(Path(path), s, convention == 1 ? GGUFConvention::GGML : GGUFConvention::REFERENCE);

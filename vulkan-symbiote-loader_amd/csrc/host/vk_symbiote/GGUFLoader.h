@@ -11,7 +11,10 @@
 //    The convention is taken from the key "vsl.tensor_type_convention" when present, else
 //    inferred from the ids in the file;
 //  - F16 tensors are converted by read_tensor_data (the reference routes id 48 into its
-//    quantized branch, which rejects it with -20).
+//    quantized branch, which rejects it with -20);
+//  - Q4_0 / Q4_1 / Q8_0 are dequantized as dequantize_tensor does (GGUFLoader.cpp:1121-1223) in
+//    files with the reference's ids, and with ggml's published block layout in files with ggml's
+//    ids (which the reference cannot read at all).
 #pragma once
 
 #include <cstdint>
@@ -104,6 +107,11 @@ class GGUFLoader {
     int storage_dtype(const GGUFTensorInfo& t) const;
     // mapped raw bytes of a tensor (nullptr if out of range)
     const uint8_t* tensor_bytes(const GGUFTensorInfo& t) const;
+    // VSL_WF_* storage format of a tensor that vsl_convert_weights can expand (F32, F16, Q4_0, Q4_1,
+    // Q8_0), -1 otherwise.  A ggml-id quantized tensor needs ne0 to be a whole number of blocks.
+    int weight_format(const GGUFTensorInfo& t) const;
+    // VSL_QL_REFERENCE or VSL_QL_GGML: block layout of this file's quantized tensors
+    int block_layout() const;
 
    private:
     Path file_path_;
@@ -122,6 +130,21 @@ class GGUFLoader {
     std::mutex cache_mu_;
 };
 
+// IEEE binary16 <-> binary32 (every case exact / round to nearest even; the reference's
+// convert_fp16_to_fp32, GGUFLoader.cpp:1225-1262, gives the same values except for NaN payloads).
+float half_to_float(uint16_t h);
+uint16_t float_to_half(float f);
+// dequantize_tensor (GGUFLoader.cpp:1121-1223) on the host, for read_tensor_data: expands Q4_0 /
+// Q4_1 / Q8_0 blocks (fmt = VSL_WF_*) in the given block layout (VSL_QL_*).  Whole blocks are read
+// while they fit in src_bytes, the last one possibly partial; returns the number of floats written
+// (below n when the data runs out, as the reference's loop guard does).
+uint64 dequantize_blocks(const uint8_t* src, uint64 src_bytes, int fmt, int layout, uint64 n, float* out);
+// Quantize n floats into ceil(n / 32) blocks of `fmt` (a short last block is zero padded).  Q8_0:
+// d = max|x| / 127, q = round(x / d); Q4_0: d = -(the value of largest magnitude) / 8,
+// nibble = clamp(floor(x / d + 8.5)); Q4_1: d = (max - min) / 15, m = min,
+// nibble = clamp(floor((x - m) / d + 0.5)).  Used for synthetic files and fixtures.
+std::vector<uint8_t> quantize_blocks(const float* x, uint64 n, int fmt, int layout);
+
 // Minimal GGUF writer (v3) for synthetic models and fixtures.
 class GGUFWriter {
    public:
@@ -132,6 +155,9 @@ class GGUFWriter {
     // data: raw bytes in the storage type (is_f16 ? binary16 : binary32); dims ne0-first
     void add_tensor(const std::string& name, const std::vector<uint64_t>& dims, bool is_f16, const void* data,
                     uint64_t bytes);
+    // data: raw bytes in storage format fmt (VSL_WF_*: F32, F16, or blocks from quantize_blocks)
+    void add_tensor_format(const std::string& name, const std::vector<uint64_t>& dims, int fmt, const void* data,
+                           uint64_t bytes);
     ExpectedVoid write(const Path& path) const;
 
    private:
@@ -143,7 +169,7 @@ class GGUFWriter {
     struct T {
         std::string name;
         std::vector<uint64_t> dims;
-        bool is_f16;
+        int fmt;  // VSL_WF_*
         const void* data;
         uint64_t bytes;
     };

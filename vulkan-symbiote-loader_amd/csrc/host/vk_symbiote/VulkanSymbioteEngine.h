@@ -70,6 +70,9 @@ struct EngineOptions {
     // inputs) instead of one rounded fp16 value: bit 0 QKV GEMM input, bit 1 attention (q and the
     // probabilities), bit 2 O-projection input, bit 3 gate/up GEMM input, bit 4 down-projection input.
     uint32_t prefill_split = kPrefillSplitAll;
+    // Block-quantized GGUF weights (Q4_0 / Q4_1 / Q8_0) are expanded at load into fp16 packs, or into
+    // fp32 packs holding exactly the values the reference's dequantize_tensor returns when set.
+    bool dequant_f32 = false;
     bool verbose = false;
     static constexpr uint32_t kPrefillSplitAll = 0x1F;
 };
@@ -79,6 +82,9 @@ struct EngineOptions {
 struct SyntheticSpec {
     ModelConfig config;
     bool fp16 = true;
+    // write_synthetic_gguf only: VSL_WF_Q4_0 / Q4_1 / Q8_0 stores every 2-D weight (embeddings and
+    // output included) block-quantized from the fp32 draws; -1 keeps F16 / F32 per `fp16`
+    int quant_format = -1;
     float init_std = 0.02f;
     uint64_t seed = 0;
 };
