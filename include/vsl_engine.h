@@ -77,7 +77,8 @@ int vsl_engine_close(vsl_engine* e);
  * number of generated tokens. */
 int vsl_engine_generate_ids(vsl_engine* e, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
                             const vsl_gen_params* params, uint32_t* out_tokens, float* out_logits, uint32_t* n_out);
-/* generate(prompt, max_tokens, temperature): text in, prompt + decoded tokens out (NUL-terminated) */
+/* generate(prompt, max_tokens, temperature): text in, prompt + decode({id}) of each generated token out
+ * (NUL-terminated), with the tokenizer of the model file (the byte fallback for synthetic engines) */
 int vsl_engine_generate_text(vsl_engine* e, const char* prompt, uint32_t max_tokens, float temperature, char* out,
                              uint64_t out_cap, uint64_t* out_len);
 
@@ -110,6 +111,13 @@ int vsl_engine_read_tensor(vsl_engine* e, const char* name, void* dst, uint64_t 
  * convention 0 = the reference's tensor-type ids (F32 6, F16 48, Q4_0 13, Q4_1 14, Q8_0 17) and
  * block layout, 1 = ggml ids (F32 0, F16 1, Q4_0 2, Q4_1 3, Q8_0 8) and ggml's block layout. */
 int vsl_write_synthetic_gguf(const char* path, const vsl_model_spec* spec, uint64_t seed, int convention);
+/* the same with a vocabulary: n_tokens strings (tokens[i], token_lens[i] bytes each, may hold any
+ * byte) written as the array "tokenizer.ggml.tokens", or with keyed = 1 as one string key
+ * "tokenizer.ggml.tokens.<i>" per token (the layout the reference's Tokenizer::from_gguf scans for,
+ * Tokenizer.cpp:55-74) */
+int vsl_write_synthetic_gguf_vocab(const char* path, const vsl_model_spec* spec, uint64_t seed, int convention,
+                                   const char* const* tokens, const uint64_t* token_lens, uint32_t n_tokens,
+                                   int keyed);
 /* the host synthetic generator (same stream as vsl_fill_normal) */
 int vsl_synthetic_fill_host(void* out, int dtype, uint64_t n, uint64_t seed, const char* name, float mean,
                             float stddev);
@@ -128,6 +136,24 @@ int vsl_gguf_tensor(vsl_gguf* g, const char* name, uint64_t* data_offset, uint64
 /* returns the element count, or the reference's read codes (-11 read, -12 type, -20 quantized, -30 missing);
  * Q4_0 / Q4_1 / Q8_0 tensors are dequantized (dequantize_tensor, GGUFLoader.cpp:1121-1223) */
 int64_t vsl_gguf_read_f32(vsl_gguf* g, const char* name, float* out, uint64_t cap);
+
+/* Tokenizer (vk_symbiote/include/vk_symbiote/Tokenizer.h:7-22): the vocabulary of a GGUF file
+ * (array "tokenizer.ggml.tokens", else keys "tokenizer.ggml.tokens.<id>"), or the 256-byte fallback
+ * when gguf_path is NULL or the file has neither (the reference also falls back on an unreadable
+ * file).  encode / decode follow Tokenizer.cpp:131-198: whitespace-split words, a word found in the
+ * vocabulary is one id, else one id per byte (found, or (signed byte * 31) % 31000 + 1000); an empty
+ * text gives [0]; decode joins vocab[id % vocab_size] with single spaces.
+ * vsl_tokenizer_encode writes min(*n_out, cap) ids and sets *n_out to the full count;
+ * vsl_tokenizer_decode writes at most cap bytes (no terminator) and sets *len_out to the full
+ * length.  source: 0 bytes, 1 array, 2 keys. */
+typedef struct vsl_tokenizer vsl_tokenizer;
+int vsl_tokenizer_open(const char* gguf_path, vsl_tokenizer** out);
+int vsl_tokenizer_close(vsl_tokenizer* t);
+int vsl_tokenizer_info(vsl_tokenizer* t, uint32_t* vocab_size, int* source);
+int vsl_tokenizer_encode(vsl_tokenizer* t, const char* text, uint64_t text_len, uint32_t* ids, uint64_t cap,
+                         uint64_t* n_out);
+int vsl_tokenizer_decode(vsl_tokenizer* t, const uint32_t* ids, uint64_t n, char* out, uint64_t cap,
+                         uint64_t* len_out);
 
 /* ConfigManager (ConfigManager.h:133-270): parse CLI args / a TOML file into the singleton and read
  * the fields the engine uses.  enable_gpu is 0 after --disable-gpu; opening an engine then fails. */

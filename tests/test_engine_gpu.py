@@ -57,6 +57,26 @@ def test_tiny_stop_on_eos_capacity_and_text(vsl, orc, tiny_path):
         assert out == "hello world" + "".join(chr(t % 256) for t in ref)
 
 
+def test_text_path_with_gguf_vocabulary(vsl, orc, tmp_path):
+    """generate(text) with the model file's vocabulary (array and keyed layouts): the prompt encoded
+    by the oracle's tokenizer, greedy ids from the oracle model (EOS 0/2 stops), and the output
+    prompt + decode({id}) of each generated token, byte for byte."""
+    from oracle import tokenizer as otok
+    vocab = [b"<unk>", b"<s>", b"</s>"] + [bytes([i]) for i in range(32, 127)] + \
+            [b"tok%d" % i for i in range(TINY["vocab_size"] - 98)]
+    for keyed in (False, True):
+        p = tmp_path / f"tiny_vocab_{int(keyed)}.gguf"
+        vsl.write_synthetic_gguf(p, TINY, seed=0, vocab=vocab, keyed=keyed)
+        tok = otok.from_gguf(p)
+        m = orc.Model(p)
+        with vsl.Engine(p, kv_capacity=64) as e:
+            for prompt in (b"hello world", b"tok5 tok77 zz\xc3\xa9", b"   "):
+                ref = m.generate(np.array(tok.encode(prompt), np.uint32), 20, stop_on_eos=True)
+                want = prompt + b"".join(tok.decode([int(t)]) for t in ref)
+                assert e.generate(prompt, max_tokens=20, temperature=0.0, raw=True) == want
+        m.close()
+
+
 def test_tiny_seeded_topk(vsl, orc, tiny_path):
     g = np.load(GOLD)
     m = orc.Model(tiny_path)

@@ -165,6 +165,13 @@ _ENGINE_SIGS = {
                                     ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "vsl_engine_read_tensor": (_I32, [_P, ctypes.c_char_p, _P, _U64, ctypes.POINTER(ctypes.c_int)]),
     "vsl_write_synthetic_gguf": (_I32, [ctypes.c_char_p, ctypes.POINTER(ModelSpec), _U64, _I32]),
+    "vsl_write_synthetic_gguf_vocab": (_I32, [ctypes.c_char_p, ctypes.POINTER(ModelSpec), _U64, _I32,
+                                              ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_U64), _U32, _I32]),
+    "vsl_tokenizer_open": (_I32, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "vsl_tokenizer_close": (_I32, [_P]),
+    "vsl_tokenizer_info": (_I32, [_P, ctypes.POINTER(_U32), ctypes.POINTER(ctypes.c_int)]),
+    "vsl_tokenizer_encode": (_I32, [_P, ctypes.c_char_p, _U64, _P, _U64, ctypes.POINTER(_U64)]),
+    "vsl_tokenizer_decode": (_I32, [_P, _P, _U64, _P, _U64, ctypes.POINTER(_U64)]),
     "vsl_synthetic_fill_host": (_I32, [_P, _I32, _U64, _U64, ctypes.c_char_p, _F32, _F32]),
     "vsl_gguf_open": (_I32, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "vsl_gguf_close": (_I32, [_P]),
@@ -231,11 +238,64 @@ def make_spec(cfg, init_std=0.02):
     return s
 
 
-def write_synthetic_gguf(path, cfg, seed=0, convention="reference", init_std=0.02):
+def write_synthetic_gguf(path, cfg, seed=0, convention="reference", init_std=0.02, vocab=None, keyed=False):
+    """cfg["dtype"]: VSL_WF_* storage of the 2-D weights. vocab: optional list of token strings or
+    bytes, written as the array tokenizer.ggml.tokens (keyed=True: one key tokenizer.ggml.tokens.<id>
+    per token)."""
     lib = engine_lib()
     spec = make_spec(cfg, init_std)
     conv = {"reference": 0, "ggml": 1}[convention]
-    check(lib.vsl_write_synthetic_gguf(str(path).encode(), ctypes.byref(spec), seed, conv), lib)
+    if vocab is None:
+        check(lib.vsl_write_synthetic_gguf(str(path).encode(), ctypes.byref(spec), seed, conv), lib)
+        return
+    toks = [t if isinstance(t, bytes) else t.encode() for t in vocab]
+    arr = (ctypes.c_char_p * max(len(toks), 1))(*toks)
+    lens = (_U64 * max(len(toks), 1))(*[len(t) for t in toks])
+    check(lib.vsl_write_synthetic_gguf_vocab(str(path).encode(), ctypes.byref(spec), seed, conv, arr, lens,
+                                             len(toks), int(bool(keyed))), lib)
+
+
+class Tokenizer:
+    """Tokenizer::from_gguf (path) or the 256-byte fallback (path None). Text is bytes or str (UTF-8)."""
+
+    SOURCES = ("bytes", "array", "keys")
+
+    def __init__(self, gguf_path=None):
+        self._lib = engine_lib()
+        h = ctypes.c_void_p()
+        check(self._lib.vsl_tokenizer_open(None if gguf_path is None else str(gguf_path).encode(), ctypes.byref(h)),
+              self._lib)
+        self._h = h
+        v, src = _U32(), ctypes.c_int()
+        check(self._lib.vsl_tokenizer_info(self._h, ctypes.byref(v), ctypes.byref(src)), self._lib)
+        self.vocab_size, self.source = v.value, self.SOURCES[src.value]
+
+    def encode(self, text):
+        b = text if isinstance(text, bytes) else text.encode()
+        n = _U64()
+        check(self._lib.vsl_tokenizer_encode(self._h, b, len(b), None, 0, ctypes.byref(n)), self._lib)
+        out = np.zeros(max(n.value, 1), dtype=np.uint32)
+        check(self._lib.vsl_tokenizer_encode(self._h, b, len(b), _ptr(out), n.value, ctypes.byref(n)), self._lib)
+        return out[:n.value]
+
+    def decode(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        n = _U64()
+        check(self._lib.vsl_tokenizer_decode(self._h, _ptr(ids), ids.size, None, 0, ctypes.byref(n)), self._lib)
+        buf = ctypes.create_string_buffer(max(n.value, 1))
+        check(self._lib.vsl_tokenizer_decode(self._h, _ptr(ids), ids.size, buf, n.value, ctypes.byref(n)), self._lib)
+        return buf.raw[:n.value]
+
+    def close(self):
+        if self._h:
+            self._lib.vsl_tokenizer_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
 
 
 def synthetic_fill_host(n, dtype, seed, name, mean=0.0, std=0.02):
@@ -332,14 +392,21 @@ class Engine:
         check(self._lib.vsl_engine_time_op(self._h, op, iterations, ctypes.byref(ms)), self._lib)
         return ms.value
 
-    def generate(self, text, max_tokens=256, temperature=0.7):
+    def generate(self, text, max_tokens=256, temperature=0.7, raw=False):
+        """generate(): prompt + decode({id}) per generated token. Returns bytes when raw, else a str
+        decoded as latin-1 (bytes kept 1:1, as the byte tokenizer emits them)."""
+        b = text if isinstance(text, bytes) else text.encode()
         need = ctypes.c_uint64(0)
-        cap = len(text) + 2 * max_tokens + 64
-        buf = ctypes.create_string_buffer(cap)
-        check(self._lib.vsl_engine_generate_text(self._h, text.encode(), max_tokens, temperature, buf, cap,
-                                                 ctypes.byref(need)), self._lib)
-        # one byte per generated token (the reference's byte tokenizer): latin-1 keeps bytes 1:1
-        return buf.raw[:need.value].decode("latin-1")
+        cap = len(b) + 2 * max_tokens + 64
+        for _ in range(2):  # a longer vocabulary text than the first guess: run again with its size
+            buf = ctypes.create_string_buffer(cap)
+            check(self._lib.vsl_engine_generate_text(self._h, b, max_tokens, temperature, buf, cap,
+                                                     ctypes.byref(need)), self._lib)
+            if need.value < cap:
+                break
+            cap = need.value + 1
+        out = buf.raw[:need.value]
+        return out if raw else out.decode("latin-1")
 
     def last_stats(self):
         s = GenStats()

@@ -589,6 +589,21 @@ void GGUFWriter::add_string(const std::string& key, const std::string& v) {
     std::memcpy(kv.bytes.data() + 8, v.data(), v.size());
     kvs_.push_back(std::move(kv));
 }
+void GGUFWriter::add_string_array(const std::string& key, const std::vector<std::string>& v) {
+    KV kv{key, 9, std::vector<uint8_t>(12)};
+    const uint32_t et = 8;
+    const uint64_t cnt = v.size();
+    std::memcpy(kv.bytes.data(), &et, 4);
+    std::memcpy(kv.bytes.data() + 4, &cnt, 8);
+    for (const std::string& s : v) {
+        const uint64_t l = s.size();
+        const size_t o = kv.bytes.size();
+        kv.bytes.resize(o + 8 + s.size());
+        std::memcpy(kv.bytes.data() + o, &l, 8);
+        std::memcpy(kv.bytes.data() + o + 8, s.data(), s.size());
+    }
+    kvs_.push_back(std::move(kv));
+}
 void GGUFWriter::add_tensor(const std::string& name, const std::vector<uint64_t>& dims, bool is_f16, const void* data,
                             uint64_t bytes) {
     tensors_.push_back(T{name, dims, is_f16 ? VSL_WF_F16 : VSL_WF_F32, data, bytes});

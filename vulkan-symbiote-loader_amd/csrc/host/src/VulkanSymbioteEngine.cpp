@@ -114,6 +114,14 @@ ExpectedVoid write_synthetic_gguf(const Path& path, const SyntheticSpec& spec, G
     w.add_u32("llama.context_length", c.max_position_embeddings);
     w.add_f32("llama.rope.freq_base", c.rope_theta);
     w.add_f32("llama.attention.layer_norm_rms_epsilon", c.rms_epsilon);
+    if (!spec.vocab.empty()) {
+        if (spec.vocab_keyed) {
+            for (size_t i = 0; i < spec.vocab.size(); ++i)
+                w.add_string("tokenizer.ggml.tokens." + std::to_string(i), spec.vocab[i]);
+        } else {
+            w.add_string_array("tokenizer.ggml.tokens", spec.vocab);
+        }
+    }
     std::vector<std::vector<uint8_t>> store;
     const bool quant = spec.quant_format >= VSL_WF_Q4_0 && spec.quant_format <= VSL_WF_Q8_0;
     if (spec.quant_format >= 0 && !quant) return kErrInvalid;
@@ -158,27 +166,6 @@ ExpectedVoid write_synthetic_gguf(const Path& path, const SyntheticSpec& spec, G
     return w.write(path);
 }
 
-// Tokenizer.cpp:113-129 + :131-178 (vocabulary branch over the 256 single-byte tokens) and
-// :180-198: every non-whitespace byte is one token; decode joins bytes (id % 256) with spaces.
-std::vector<uint32_t> simple_encode(const std::string& text) {
-    std::vector<uint32_t> ids;
-    std::istringstream iss(text);
-    std::string word;
-    while (iss >> word)
-        for (unsigned char ch : word) ids.push_back(ch);
-    if (ids.empty()) ids.push_back(0);
-    return ids;
-}
-
-std::string simple_decode(const std::vector<uint32_t>& tokens) {
-    std::string r;
-    for (size_t i = 0; i < tokens.size(); ++i) {
-        r += static_cast<char>(tokens[i] % 256);
-        if (i + 1 < tokens.size()) r += ' ';
-    }
-    return r;
-}
-
 void BenchmarkStats::print() const {
     std::printf("[Benchmark] avg %.2f tok/s (min %.2f, max %.2f, std %.2f), latency %.3f ms, peak HBM %.2f GB\n",
                 avg_tokens_per_sec, min_tokens_per_sec, max_tokens_per_sec, std_dev_tokens_per_sec, avg_latency_ms,
@@ -215,6 +202,7 @@ VulkanSymbioteEngine::VulkanSymbioteEngine(const Path& model_path, const EngineO
         if (wf == VSL_WF_F16) return static_cast<int>(VSL_DT_F16);
         return static_cast<int>(options_.dequant_f32 ? VSL_DT_F32 : VSL_DT_F16);
     };
+    tokenizer_ = Tokenizer::from_gguf(model_path);  // VulkanSymbioteEngine.cpp:1140
     try {
         init_device(cfg, pack_dtype(qf) == VSL_DT_F16, pack_dtype(ef));
         load_weights_from_gguf();
@@ -225,6 +213,7 @@ VulkanSymbioteEngine::VulkanSymbioteEngine(const Path& model_path, const EngineO
 }
 
 VulkanSymbioteEngine::VulkanSymbioteEngine(const SyntheticSpec& spec, const EngineOptions& options) : options_(options) {
+    tokenizer_ = Tokenizer::create_simple_tokenizer();
     try {
         init_device(spec.config, spec.fp16, spec.fp16 ? VSL_DT_F16 : VSL_DT_F32);
         init_synthetic_weights(spec);
@@ -795,8 +784,8 @@ double VulkanSymbioteEngine::time_op(int op, uint32_t iterations) {
     return (double)ms / ((double)iterations * per_round);
 }
 
-std::vector<uint32_t> VulkanSymbioteEngine::encode(const std::string& text) { return simple_encode(text); }
-std::string VulkanSymbioteEngine::decode(const std::vector<uint32_t>& tokens) { return simple_decode(tokens); }
+std::vector<uint32_t> VulkanSymbioteEngine::encode(const std::string& text) { return tokenizer_->encode(text); }
+std::string VulkanSymbioteEngine::decode(const std::vector<uint32_t>& tokens) { return tokenizer_->decode(tokens); }
 
 std::string VulkanSymbioteEngine::generate(const std::string& prompt, uint32_t max_tokens, float temperature) {
     clear_kv_cache();

@@ -309,6 +309,71 @@ extern "C" int vsl_write_synthetic_gguf(const char* path, const vsl_model_spec* 
     return VSL_OK;
 }
 
+extern "C" int vsl_write_synthetic_gguf_vocab(const char* path, const vsl_model_spec* spec, uint64_t seed,
+                                              int convention, const char* const* tokens, const uint64_t* token_lens,
+                                              uint32_t n_tokens, int keyed) {
+    if (!path || !spec || (n_tokens && (!tokens || !token_lens)))
+        return fail(VSL_E_INVALID, "vsl_write_synthetic_gguf_vocab: null argument");
+    if (spec->dtype > VSL_WF_Q8_0) return fail(VSL_E_INVALID, "vsl_write_synthetic_gguf_vocab: unknown weight format");
+    SyntheticSpec s;
+    s.config = to_config(spec);
+    s.fp16 = spec->dtype == VSL_DT_F16;
+    s.quant_format = spec->dtype >= VSL_WF_Q4_0 ? static_cast<int>(spec->dtype) : -1;
+    s.init_std = spec->init_std > 0 ? spec->init_std : 0.02f;
+    s.seed = seed;
+    for (uint32_t i = 0; i < n_tokens; ++i) {
+        if (!tokens[i] && token_lens[i]) return fail(VSL_E_INVALID, "vsl_write_synthetic_gguf_vocab: null token");
+        s.vocab.emplace_back(tokens[i] ? tokens[i] : "", static_cast<size_t>(token_lens[i]));
+    }
+    s.vocab_keyed = keyed != 0;
+    auto r = write_synthetic_gguf(Path(path), s, convention == 1 ? GGUFConvention::GGML : GGUFConvention::REFERENCE);
+    if (!r.has_value()) return fail(r.error(), "vsl_write_synthetic_gguf_vocab: write failed");
+    return VSL_OK;
+}
+
+// Tokenizer
+struct vsl_tokenizer {
+    std::unique_ptr<Tokenizer> impl;
+};
+
+extern "C" int vsl_tokenizer_open(const char* gguf_path, vsl_tokenizer** out) {
+    if (!out) return fail(VSL_E_INVALID, "vsl_tokenizer_open: null argument");
+    auto t = std::make_unique<vsl_tokenizer>();
+    t->impl = gguf_path ? Tokenizer::from_gguf(Path(gguf_path)) : Tokenizer::create_simple_tokenizer();
+    *out = t.release();
+    return VSL_OK;
+}
+
+extern "C" int vsl_tokenizer_close(vsl_tokenizer* t) {
+    delete t;
+    return VSL_OK;
+}
+
+extern "C" int vsl_tokenizer_info(vsl_tokenizer* t, uint32_t* vocab_size, int* source) {
+    if (!t) return fail(VSL_E_INVALID, "vsl_tokenizer_info: null handle");
+    if (vocab_size) *vocab_size = t->impl->vocab_size();
+    if (source) *source = static_cast<int>(t->impl->source());
+    return VSL_OK;
+}
+
+extern "C" int vsl_tokenizer_encode(vsl_tokenizer* t, const char* text, uint64_t text_len, uint32_t* ids, uint64_t cap,
+                                    uint64_t* n_out) {
+    if (!t || (!text && text_len) || (!ids && cap) || !n_out) return fail(VSL_E_INVALID, "vsl_tokenizer_encode: null argument");
+    const std::vector<uint32_t> r = t->impl->encode(std::string(text ? text : "", static_cast<size_t>(text_len)));
+    for (uint64_t i = 0; i < r.size() && i < cap; ++i) ids[i] = r[i];
+    *n_out = r.size();
+    return VSL_OK;
+}
+
+extern "C" int vsl_tokenizer_decode(vsl_tokenizer* t, const uint32_t* ids, uint64_t n, char* out, uint64_t cap,
+                                    uint64_t* len_out) {
+    if (!t || (!ids && n) || (!out && cap) || !len_out) return fail(VSL_E_INVALID, "vsl_tokenizer_decode: null argument");
+    const std::string r = t->impl->decode(std::vector<uint32_t>(ids, ids + n));
+    if (cap) std::memcpy(out, r.data(), static_cast<size_t>(std::min<uint64_t>(cap, r.size())));
+    *len_out = r.size();
+    return VSL_OK;
+}
+
 extern "C" int vsl_synthetic_fill_host(void* out, int dtype, uint64_t n, uint64_t seed, const char* name, float mean,
                                        float stddev) {
     if (!out || !name) return fail(VSL_E_INVALID, "vsl_synthetic_fill_host: null argument");

@@ -152,6 +152,7 @@ class GGUFWriter {
     void add_u32(const std::string& key, uint32_t v);
     void add_f32(const std::string& key, float v);
     void add_string(const std::string& key, const std::string& v);
+    void add_string_array(const std::string& key, const std::vector<std::string>& v);
     // data: raw bytes in the storage type (is_f16 ? binary16 : binary32); dims ne0-first
     void add_tensor(const std::string& name, const std::vector<uint64_t>& dims, bool is_f16, const void* data,
                     uint64_t bytes);

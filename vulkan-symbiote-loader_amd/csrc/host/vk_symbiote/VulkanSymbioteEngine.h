@@ -21,6 +21,7 @@
 #include "Common.h"
 #include "GGUFLoader.h"
 #include "NomadPack.h"
+#include "Tokenizer.h"
 
 struct vsl_arena;
 struct vsl_graph;
@@ -85,6 +86,10 @@ struct SyntheticSpec {
     // write_synthetic_gguf only: VSL_WF_Q4_0 / Q4_1 / Q8_0 stores every 2-D weight (embeddings and
     // output included) block-quantized from the fp32 draws; -1 keeps F16 / F32 per `fp16`
     int quant_format = -1;
+    // write_synthetic_gguf only: a vocabulary, written as the string array "tokenizer.ggml.tokens"
+    // or, with vocab_keyed, as one string key "tokenizer.ggml.tokens.<id>" per entry
+    std::vector<std::string> vocab;
+    bool vocab_keyed = false;
     float init_std = 0.02f;
     uint64_t seed = 0;
 };
@@ -117,6 +122,7 @@ class VulkanSymbioteEngine {
     std::string generate(const std::string& prompt, uint32_t max_tokens = 256, float temperature = 0.7f);
     std::vector<uint32_t> encode(const std::string& text);
     std::string decode(const std::vector<uint32_t>& tokens);
+    const Tokenizer& tokenizer() const { return *tokenizer_; }
 
     // Token-id entry point.  Returns the number of generated tokens (<0 on error).
     // logits_out (optional) receives one vocab-sized row per generated token: the logits that
@@ -178,6 +184,7 @@ class VulkanSymbioteEngine {
     GenerationTimings timings_;
     PackManager pack_manager_;
     std::unique_ptr<GGUFLoader> loader_;
+    std::unique_ptr<Tokenizer> tokenizer_;
 
     int wdt_ = 1, kvdt_ = 1, edt_ = 1;  // VSL_DT_* of linear weights, KV cache, embedding
     uint32_t cap_ = 0, nsplit_ = 32;
@@ -240,8 +247,5 @@ ExpectedVoid write_synthetic_gguf(const Path& path, const SyntheticSpec& spec, G
 void synthetic_fill_host(void* out, bool fp16, uint64_t n, uint64_t seed, const std::string& name, float mean,
                          float stddev);
 
-// The reference's fallback byte tokenizer (Tokenizer.cpp:113-198).
-std::vector<uint32_t> simple_encode(const std::string& text);
-std::string simple_decode(const std::vector<uint32_t>& tokens);
 
 }  // namespace vk_symbiote
