@@ -212,6 +212,21 @@ def run_long(a):
         "decode_launch": "eager" if a.eager else "hipGraph replay",
     }
     eng.close()
+    # the same decode with the windowed long-context mode at the reference's parameters (window 512,
+    # 16 global tokens, from sequence length 8193 on): every decode step attends 529 positions
+    win = (512, 16, 8192)
+    eng = vsl.Engine(spec=CFG, seed=0, kv_capacity=cap, prefill_chunk=chunk, use_graph=not a.eager, window=win)
+    eng.begin(prompt, 3)
+    eng.decode(2)
+    eng.finish()
+    win_s, _ = timed()
+    eng.close()
+    n_att = win[1] + win[0] + 1
+    win_bytes = sum(decode_bytes(CFG, n_prompt + i if n_prompt + i <= win[2] else n_att) for i in range(1, steps + 1))
+    out["window_decode_tok_s"] = round(steps / win_s, 2)
+    out["window_decode_hbm_gbps"] = round(win_bytes / win_s / 1e9, 1)
+    out["window_decode_hbm_frac"] = round(win_bytes / win_s / PEAK_HBM, 4)
+    out["window"] = {"sparse_window": win[0], "sparse_global": win[1], "sparse_threshold": win[2]}
     print(json.dumps(out), flush=True)
 
 

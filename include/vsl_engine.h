@@ -49,6 +49,12 @@ typedef struct vsl_engine_options {
                                 down input; vsl_engine_default_options sets all five */
     uint32_t dequant_f32;    /* block-quantized GGUF weights expand to fp32 packs (the exact values of
                                 dequantize_tensor, GGUFLoader.cpp:1121-1223) instead of fp16 packs */
+    uint32_t sparse_attention;  /* 1 = windowed long-context mode (use_sparse_attention, Common.h:70-75):
+                                   a query at position p with p + 1 > sparse_threshold attends to the
+                                   first sparse_global keys and the sparse_window keys before it only */
+    uint32_t sparse_window;     /* vsl_engine_default_options: 512 */
+    uint32_t sparse_global;     /* 16 */
+    uint32_t sparse_threshold;  /* 8192 (the reference's seq_len > 8192, VulkanSymbioteEngine.cpp:788) */
 } vsl_engine_options;
 
 typedef struct vsl_gen_params {

@@ -199,6 +199,18 @@ int vsl_attn_decode(const float* q, const void* kcache, const void* vcache, int 
                     uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* part_o,
                     float* part_ml, float* out, vsl_ctrl* ctrl, void* stream);
 
+/* Windowed long-context mode (the reference's use_sparse_attention, Common.h:70-75, switched on
+ * above `seq_len > 8192` at VulkanSymbioteEngine.cpp:788; sparse_attention.comp:77-100 sliding
+ * window + global tokens).  With p = ctrl->pos: while p + 1 <= threshold the query attends to every
+ * key 0..p (as vsl_attn_decode); past it, to the keys k < n_global and p - window <= k <= p only.
+ * Replaces sparse_attention_with_weights (VulkanSymbioteEngine.cpp:2592-2724), whose shader drops
+ * the global tokens and zeroes scores past index 512; those defects are not reproduced.
+ * window + n_global < 2^31. */
+int vsl_attn_decode_window(const float* q, const void* kcache, const void* vcache, int kv_dtype, uint32_t n_q,
+                           uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* part_o,
+                           float* part_ml, float* out, vsl_ctrl* ctrl, uint32_t window, uint32_t n_global,
+                           uint32_t threshold, void* stream);
+
 /* y[N] += W[N][K] x[K]  (O projection / FFN down projection with the residual add fused) */
 int vsl_gemv_residual(const void* W, int wdtype, uint32_t N, uint32_t K, const float* x, float* resid,
                       vsl_ctrl* ctrl, void* stream);
@@ -256,6 +268,12 @@ int vsl_rope_split_append(const float* qkv, uint32_t S, uint32_t n_q, uint32_t n
 int vsl_attn_prefill(const void* q, int q_dtype, const void* kcache, const void* vcache, uint32_t S,
                      uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale,
                      void* out, int out_dtype, void* stream);
+/* The same with the windowed mode of vsl_attn_decode_window applied per row: the row at position
+ * p attends to 0..p while p + 1 <= threshold, else to k < n_global and p - window <= k <= p. */
+int vsl_attn_prefill_window(const void* q, int q_dtype, const void* kcache, const void* vcache, uint32_t S,
+                            uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale,
+                            void* out, int out_dtype, uint32_t window, uint32_t n_global, uint32_t threshold,
+                            void* stream);
 
 /* ------------------------------------------------------------------------------------------
  * hipGraph helpers (each decode step is captured once and replayed).

@@ -47,6 +47,8 @@ _SIGS = {
                                     ctypes.POINTER(_U64)]),
     "orc_gguf_read_f32": (ctypes.c_int64, [_P, ctypes.c_char_p, _P, _U64]),
     "orc_dequant": (ctypes.c_int64, [_P, _U64, _U32, _I32, _U64, _P]),
+    "orc_attention_decode_window": (None, [_P, _P, _P, _U32, _U32, _U32, _U32, _U32, _F32, _U32, _U32, _U32, _P]),
+    "orc_model_set_window": (None, [_P, _U32, _U32, _U32]),
     "orc_gguf_get_u32": (_I32, [_P, ctypes.c_char_p, ctypes.POINTER(_U32)]),
     "orc_gguf_get_f32": (_I32, [_P, ctypes.c_char_p, ctypes.POINTER(_F32)]),
     "orc_gguf_model_config": (None, [_P, ctypes.POINTER(Config)]),
@@ -144,6 +146,10 @@ class Model:
         c = Config()
         L.orc_model_config(self.h, ctypes.byref(c))
         self.config = config_dict(c)
+
+    def set_window(self, window, n_global, threshold):
+        """Windowed attention from sequence length threshold + 1 on (threshold None: dense)."""
+        lib().orc_model_set_window(self.h, window, n_global, 0xFFFFFFFF if threshold is None else threshold)
 
     def set_tensor(self, name, arr, copy=False):
         arr = np.ascontiguousarray(arr)
@@ -247,12 +253,18 @@ def gemm_nt(W, X):
     return Y
 
 
-def attention_decode(q, kc, vc, n_q, n_kv, hd, cap, length, scale):
+def attention_decode(q, kc, vc, n_q, n_kv, hd, cap, length, scale, window=None):
+    """window: None (dense) or (window, n_global, threshold)."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     kc = np.ascontiguousarray(kc, dtype=np.float32)
     vc = np.ascontiguousarray(vc, dtype=np.float32)
     out = np.empty(n_q * hd, dtype=np.float32)
-    lib().orc_attention_decode(ptr(q), ptr(kc), ptr(vc), n_q, n_kv, hd, cap, length, scale, ptr(out))
+    if window is None:
+        lib().orc_attention_decode(ptr(q), ptr(kc), ptr(vc), n_q, n_kv, hd, cap, length, scale, ptr(out))
+    else:
+        w, g, t = window
+        lib().orc_attention_decode_window(ptr(q), ptr(kc), ptr(vc), n_q, n_kv, hd, cap, length, scale, w, g, t,
+                                          ptr(out))
     return out
 
 

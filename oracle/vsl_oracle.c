@@ -15,6 +15,9 @@
  *   orc_rope                 pos 0 identity, norm preservation, <R_m q, R_n k> depends on m-n only,
  *                            and the adjacent-pair convention against a hand-rotated vector
  *   orc_attention_decode     one-key attention == V, uniform scores == mean of V, brute force fp64
+ *   windowed attention       uniform scores over one-hot values give 1/|A| exactly on the attended
+ *                            set A, written out literally per (len, window, globals, threshold);
+ *                            keys outside A perturbed without effect; threshold not reached == dense
  *   orc_gemm_nt              fp64 numpy matmul on the GEMV-sweep shapes (reduced N)
  *   orc_swiglu               closed forms silu(0)=0, silu(x)->x
  *   orc_forward / generate   tiny-config logits vs an independent transformers LlamaForCausalLM
@@ -607,6 +610,7 @@ typedef struct {
 
 struct orc_model {
     orc_config cfg;
+    uint32_t win, n_global, win_threshold; /* windowed attention; win_threshold UINT32_MAX = dense */
     wref tok_embd, output;
     float* out_norm;
     orc_layer* layers;
@@ -629,7 +633,14 @@ orc_model* orc_model_new(const orc_config* cfg) {
     m->cfg = *cfg;
     if (m->cfg.head_dim == 0 && m->cfg.num_heads) m->cfg.head_dim = m->cfg.hidden_size / m->cfg.num_heads;
     m->layers = (orc_layer*)calloc(cfg->num_layers ? cfg->num_layers : 1, sizeof(orc_layer));
+    m->win_threshold = UINT32_MAX;
     return m;
+}
+
+void orc_model_set_window(orc_model* m, uint32_t window, uint32_t n_global, uint32_t threshold) {
+    m->win = window;
+    m->n_global = n_global;
+    m->win_threshold = threshold;
 }
 
 void orc_model_free(orc_model* m) {
@@ -898,6 +909,25 @@ void orc_gemm_nt(const void* Wp, int wtype, uint32_t N, uint32_t K, const float*
 void orc_attention_decode(const float* q, const float* kc, const float* vc, uint32_t n_q,
                           uint32_t n_kv, uint32_t hd, uint32_t cap, uint32_t len, float scale,
                           float* out) {
+    orc_attention_decode_window(q, kc, vc, n_q, n_kv, hd, cap, len, scale, 0, 0, UINT32_MAX, out);
+}
+
+/* Key k is attended by the query at position p = len - 1 when k <= p and, once len > threshold
+ * (the reference switches to its sparse path when seq_len > 8192, VulkanSymbioteEngine.cpp:788),
+ * when k < n_global (the global tokens) or k >= p - window (the sliding window,
+ * sparse_attention.comp:84-85 window_start = pos - window_size).  The reference's shader takes
+ * the contiguous range [min(global_end, window_start), ...) and clamps it to 1024-blocks
+ * (:94-131), which drops the global tokens; that is not restated. */
+static int window_keeps(uint32_t k, uint32_t len, uint32_t window, uint32_t n_global, uint32_t threshold) {
+    const uint32_t p = len - 1;
+    if (k > p) return 0;
+    if (threshold == UINT32_MAX || len <= threshold) return 1;
+    return k < n_global || (uint64_t)k + window >= p;
+}
+
+void orc_attention_decode_window(const float* q, const float* kc, const float* vc, uint32_t n_q,
+                                 uint32_t n_kv, uint32_t hd, uint32_t cap, uint32_t len, float scale,
+                                 uint32_t window, uint32_t n_global, uint32_t threshold, float* out) {
 #pragma omp parallel for schedule(static)
     for (int64_t hh = 0; hh < (int64_t)n_q; ++hh) {
         uint32_t h = (uint32_t)hh;
@@ -906,6 +936,7 @@ void orc_attention_decode(const float* q, const float* kc, const float* vc, uint
         double* sc = (double*)malloc((size_t)len * sizeof(double));
         double mx = -INFINITY;
         for (uint32_t t = 0; t < len; ++t) {
+            if (!window_keeps(t, len, window, n_global, threshold)) continue;
             const float* kt = kc + ((size_t)kvh * cap + t) * hd;
             double s = 0.0;
             for (uint32_t d = 0; d < hd; ++d) s += (double)qh[d] * (double)kt[d];
@@ -915,12 +946,13 @@ void orc_attention_decode(const float* q, const float* kc, const float* vc, uint
         }
         double sum = 0.0;
         for (uint32_t t = 0; t < len; ++t) {
-            sc[t] = exp(sc[t] - mx);
+            sc[t] = window_keeps(t, len, window, n_global, threshold) ? exp(sc[t] - mx) : 0.0;
             sum += sc[t];
         }
         for (uint32_t d = 0; d < hd; ++d) {
             double acc = 0.0;
-            for (uint32_t t = 0; t < len; ++t) acc += sc[t] * (double)vc[((size_t)kvh * cap + t) * hd + d];
+            for (uint32_t t = 0; t < len; ++t)
+                if (sc[t] != 0.0) acc += sc[t] * (double)vc[((size_t)kvh * cap + t) * hd + d];
             out[(size_t)h * hd + d] = (float)(acc / sum);
         }
         free(sc);
@@ -1089,7 +1121,8 @@ int orc_forward(const orc_model* m, orc_state* s, uint32_t token, uint32_t pos, 
                 s->kc[l][((size_t)h * s->cap + pos) * hd + j] = kv;
                 s->vc[l][((size_t)h * s->cap + pos) * hd + j] = vv;
             }
-        orc_attention_decode(s->q, s->kc[l], s->vc[l], nq, nkv, hd, s->cap, pos + 1, scale, s->o);
+        orc_attention_decode_window(s->q, s->kc[l], s->vc[l], nq, nkv, hd, s->cap, pos + 1, scale, m->win,
+                                    m->n_global, m->win_threshold, s->o);
         gemv(&L->o, d, (uint64_t)nq * hd, s->o, s->tmp);
         for (uint32_t i = 0; i < d; ++i) s->x[i] += s->tmp[i];
         orc_rmsnorm(s->x, L->ffn_norm, d, c->rms_eps, s->n);

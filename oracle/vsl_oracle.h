@@ -131,6 +131,12 @@ void orc_gemm_nt(const void* W, int wtype, uint32_t N, uint32_t K, const float* 
 void orc_attention_decode(const float* q, const float* kc, const float* vc, uint32_t n_q,
                           uint32_t n_kv, uint32_t hd, uint32_t cap, uint32_t len, float scale,
                           float* out);
+/* windowed mode: once len > threshold, the query at p = len - 1 attends to k < n_global and
+ * k >= p - window only (threshold UINT32_MAX: dense) */
+void orc_attention_decode_window(const float* q, const float* kc, const float* vc, uint32_t n_q,
+                                 uint32_t n_kv, uint32_t hd, uint32_t cap, uint32_t len, float scale,
+                                 uint32_t window, uint32_t n_global, uint32_t threshold, float* out);
+void orc_model_set_window(orc_model* m, uint32_t window, uint32_t n_global, uint32_t threshold);
 void orc_swiglu(const float* gate, const float* up, uint32_t n, float* h);
 uint32_t orc_sample(const float* logits, uint32_t n, int sampler, float temperature,
                     uint32_t top_k, uint64_t seed, uint64_t step);

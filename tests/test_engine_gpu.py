@@ -123,6 +123,48 @@ def _parity(vsl, orc, cfg, n_prompt, n_new, batched, kv_capacity, seed=0):
     return prompt, toks, lg, ref_toks, ref_lg
 
 
+def test_windowed_mode_tiny(vsl, orc, tiny_path):
+    """Windowed long-context mode with small parameters so that the run crosses the threshold
+    (window 8, 4 global tokens, threshold 24; prompt 16 + 32 tokens): greedy tokens identical to the
+    oracle with the same window and logits within 1e-4 relative; the steps before the threshold equal
+    the dense run, the later ones differ from it."""
+    g = np.load(GOLD)
+    m = orc.Model(tiny_path)
+    m.set_window(8, 4, 24)
+    ref_toks, ref_lg = m.generate(g["prompt"], 32, logits=True)
+    m.close()
+    with vsl.Engine(tiny_path, kv_capacity=64, window=(8, 4, 24)) as e:
+        toks, lg = e.generate_ids(g["prompt"], 32, return_logits=True)
+        assert e.config["dtype"] == 0
+    with vsl.Engine(tiny_path, kv_capacity=64) as e:
+        dtoks, dlg = e.generate_ids(g["prompt"], 32, return_logits=True)
+    scale = np.max(np.abs(ref_lg))
+    assert np.array_equal(toks, ref_toks)
+    assert np.max(np.abs(lg - ref_lg)) < 1e-4 * scale
+    # step i samples from position 15 + i: windowed once 16 + i > 24
+    assert np.max(np.abs(lg[:9] - dlg[:9])) < 1e-4 * scale
+    assert np.max(np.abs(lg[9:] - dlg[9:])) > 1e-2 * scale
+
+
+def test_windowed_mode_1b_batched_prefill(vsl, orc):
+    """1B fp16 with the MFMA prefill crossing the threshold inside the prompt (window 16, 4 globals,
+    threshold 64, prompt 128): greedy 32 tokens identical to the oracle over the resident weights
+    with the same window, logits within max-abs 2e-2."""
+    cfg = vsl.LLAMA_1B
+    win = (16, 4, 64)
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=512, batched_prefill=True, window=win) as e:
+        prompt = orc.random_ids(128, cfg["vocab_size"], 1)
+        toks, lg = e.generate_ids(prompt, 32, return_logits=True)
+        m = _oracle_from_engine(orc, e, cfg)
+    m.set_window(*win)
+    rt, rl = m.generate(prompt, 32, kv_f16=True, logits=True)
+    m.close()
+    first, margins = _report(toks, rt, lg, rl)
+    n = min(len(toks), len(rt), first if first is not None else 32)
+    assert np.max(np.abs(lg[:n] - rl[:n])) < 2e-2, np.max(np.abs(lg[:n] - rl[:n]))
+    assert first is None, f"first mismatch at step {first}, oracle top1-top2 margin {margins[first]:.5f}"
+
+
 def _report(toks, ref_toks, lg, ref_lg):
     n = min(len(toks), len(ref_toks))
     first = next((i for i in range(n) if toks[i] != ref_toks[i]), None)

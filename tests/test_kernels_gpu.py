@@ -179,6 +179,77 @@ def test_attn_decode(vsl, orc, dev, H, kvdt, hd, nq, nkv, length, nsplit):
     assert rel_err(dev.get(out), ref) < 2e-5
 
 
+@pytest.mark.parametrize("kvdt,hd,nq,nkv", [(1, 128, 32, 8), (0, 64, 4, 4)])
+@pytest.mark.parametrize("length,window,n_glob,thr", [
+    (300, 64, 4, 100),    # windowed: globals 0..3 and keys 235..299
+    (300, 64, 4, 300),    # threshold not passed: dense
+    (1025, 100, 16, 0),   # windowed from the start; 16 globals span a whole tile
+    (70, 64, 4, 0),       # window and globals leave out key 4 only
+    (69, 64, 4, 0),       # window and globals cover every key: dense
+    (2000, 512, 16, 8),   # the reference's window and globals
+])
+@pytest.mark.parametrize("nsplit", [32, 7])
+def test_attn_decode_window(vsl, orc, dev, H, kvdt, hd, nq, nkv, length, window, n_glob, thr, nsplit):
+    """Windowed decode attention (virtual positions remapped past the globals) against the oracle's
+    windowed attention; keys outside the window are filled with large values that would dominate."""
+    rng = np.random.default_rng(length + window + hd)
+    cap = 2048
+    kvnp = np.float16 if kvdt == 1 else np.float32
+    K = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float32)
+    V = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float32)
+    q = rng.normal(0, 1, nq * hd).astype(np.float32)
+    p = length - 1
+    if length > thr and p > n_glob + window:
+        hidden = slice(n_glob, p - window)
+        K[:, hidden] = np.repeat(q.reshape(nq, hd)[::nq // nkv][:, None, :], p - window - n_glob, axis=1) * 4
+        V[:, hidden] = 100.0
+    K, V = K.astype(kvnp), V.astype(kvnp)
+    scale = 1.0 / math.sqrt(hd)
+    po = dev.empty((nq * nsplit * hd,), np.float32)
+    pml = dev.empty((nq * nsplit * 2,), np.float32)
+    out = dev.empty((nq * hd,), np.float32)
+    c = ctrl_buf(vsl, dev, H, p, cap=cap)
+    ok(vsl, H.vsl_attn_decode_window(dev.p(dev.put(q)), dev.p(dev.put(K)), dev.p(dev.put(V)), kvdt, nq, nkv, hd,
+                                     cap, scale, nsplit, dev.p(po), dev.p(pml), dev.p(out), dev.p(c), window, n_glob,
+                                     thr, None))
+    ref = orc.attention_decode(q, K.astype(np.float32), V.astype(np.float32), nq, nkv, hd, cap, length, scale,
+                               window=(window, n_glob, thr))
+    assert rel_err(dev.get(out), ref) < 2e-5
+
+
+@pytest.mark.parametrize("hd,nq,nkv,S,pos0,window,n_glob,thr,x2", [
+    (64, 8, 8, 300, 100, 64, 4, 150, False),      # rows 100..149 dense, 150..399 windowed, tiles skipped
+    (128, 32, 8, 200, 0, 100, 70, 60, False),     # globals over two tiles; a block straddles the threshold
+    (128, 32, 8, 160, 300, 32, 0, 0, True),       # every row windowed, no globals, split q / out
+    (64, 8, 8, 96, 0, 512, 16, 8192, False),      # threshold not reached: dense
+])
+def test_attn_prefill_window(vsl, orc, dev, H, hd, nq, nkv, S, pos0, window, n_glob, thr, x2):
+    rng = np.random.default_rng(hd + S + pos0 + window)
+    cap = 512
+    Q = rng.normal(0, 1, (S, nq * hd)).astype(np.float32)
+    K = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16)
+    V = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16)
+    if x2:
+        hi = Q.astype(np.float16)
+        lo = (Q - hi.astype(np.float32)).astype(np.float16)
+        qd, qdt, odt = np.concatenate([hi, lo]), 2, 2
+    else:
+        qd, qdt, odt = Q.astype(np.float16), 1, 1
+        Q = qd.astype(np.float32)
+    out = dev.empty(((2 if x2 else 1) * S, nq * hd), np.float16)
+    scale = 1.0 / math.sqrt(hd)
+    ok(vsl, H.vsl_attn_prefill_window(dev.p(dev.put(qd)), qdt, dev.p(dev.put(K)), dev.p(dev.put(V)), S, pos0, nq,
+                                      nkv, hd, cap, scale, dev.p(out), odt, window, n_glob, thr, None))
+    O = dev.get(out).astype(np.float32)
+    if x2:
+        O = O[:S] + O[S:]
+    Kf, Vf = K.astype(np.float32), V.astype(np.float32)
+    for s in sorted(set(list(range(0, S, max(1, S // 11))) + [S - 1, min(S - 1, max(0, thr - pos0 - 1)),
+                                                             min(S - 1, max(0, thr - pos0))])):
+        ref = orc.attention_decode(Q[s], Kf, Vf, nq, nkv, hd, cap, pos0 + s + 1, scale, window=(window, n_glob, thr))
+        assert rel_err(O[s], ref) < (1e-4 if x2 else 4e-3), s
+
+
 def test_gemv_residual_and_swiglu(vsl, orc, dev, H):
     rng = np.random.default_rng(9)
     d, F = 4096, 14336

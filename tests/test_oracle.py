@@ -261,6 +261,50 @@ def test_attention_closed_forms(orc):
     assert np.allclose(out[0], vc[0, 5], atol=1e-4)
 
 
+@pytest.mark.parametrize("length,window,n_global,threshold,attended", [
+    # threshold not passed (len <= threshold): every key 0..p
+    (32, 8, 4, 32, list(range(32))),
+    # p = 39: globals 0..3 and the window 31..39
+    (40, 8, 4, 32, [0, 1, 2, 3] + list(range(31, 40))),
+    # p = 13: window 5..13 and globals 0..3 leave out key 4 only
+    (14, 8, 4, 8, [0, 1, 2, 3] + list(range(5, 14))),
+    # window and globals overlap: 0..p
+    (12, 8, 4, 8, list(range(12))),
+    # no global tokens, window 0: the query attends to itself only
+    (50, 0, 0, 1, [49]),
+    # threshold 0: windowed from the first position on
+    (64, 3, 2, 0, [0, 1, 60, 61, 62, 63]),
+])
+def test_windowed_attention_sets(orc, length, window, n_global, threshold, attended):
+    """Equal keys give uniform weights, and the values are one-hot in the key position, so the
+    output is exactly 1/|A| on the attended set A and 0 elsewhere."""
+    nq, nkv, hd, cap = 4, 2, 64, 64
+    rng = np.random.default_rng(7)
+    q = rng.normal(0, 1, nq * hd).astype(np.float32)
+    kc = np.repeat(rng.normal(0, 1, (nkv, 1, hd)).astype(np.float32), cap, axis=1)
+    vc = np.zeros((nkv, cap, hd), np.float32)
+    for t in range(cap):
+        vc[:, t, t] = 1.0
+    out = orc.attention_decode(q, kc, vc, nq, nkv, hd, cap, length, 0.125,
+                               window=(window, n_global, threshold)).reshape(nq, hd)
+    want = np.zeros(hd, np.float32)
+    want[attended] = 1.0 / len(attended)
+    for h in range(nq):
+        assert np.allclose(out[h], want, atol=1e-7), (h, np.nonzero(out[h])[0])
+    # keys outside the set (and their values) do not matter
+    kc2, vc2 = kc.copy(), vc.copy()
+    outside = [t for t in range(length) if t not in attended]
+    kc2[:, outside] = rng.normal(0, 5, (nkv, len(outside), hd))
+    vc2[:, outside] = rng.normal(0, 5, (nkv, len(outside), hd))
+    out2 = orc.attention_decode(q, kc2, vc2, nq, nkv, hd, cap, length, 0.125,
+                                window=(window, n_global, threshold)).reshape(nq, hd)
+    assert np.array_equal(out, out2)
+    # an unreached threshold is the dense kernel
+    dense = orc.attention_decode(q, kc2, vc2, nq, nkv, hd, cap, length, 0.125)
+    unreached = orc.attention_decode(q, kc2, vc2, nq, nkv, hd, cap, length, 0.125, window=(window, n_global, length))
+    assert np.array_equal(dense, unreached)
+
+
 def test_gemm_matches_numpy(orc):
     rng = np.random.default_rng(4)
     for (N, K, B) in [(64, 4096, 1), (96, 14336, 4), (40, 4096, 16)]:

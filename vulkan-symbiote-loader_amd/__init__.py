@@ -47,7 +47,9 @@ class EngineOptions(ctypes.Structure):
     _fields_ = [("device", ctypes.c_int32), ("kv_capacity", ctypes.c_uint32), ("use_graph", ctypes.c_uint32),
                 ("prefill_chunk", ctypes.c_uint32), ("attn_splits", ctypes.c_uint32),
                 ("batched_prefill", ctypes.c_uint32), ("prefill_split", ctypes.c_uint32),
-                ("dequant_f32", ctypes.c_uint32)]
+                ("dequant_f32", ctypes.c_uint32), ("sparse_attention", ctypes.c_uint32),
+                ("sparse_window", ctypes.c_uint32), ("sparse_global", ctypes.c_uint32),
+                ("sparse_threshold", ctypes.c_uint32)]
 
 
 class GenParams(ctypes.Structure):
@@ -94,6 +96,10 @@ _HIP_SIGS = {
     "vsl_arena_create": (_I32, [_I32, _U64, ctypes.POINTER(_P)]),
     "vsl_weight_bytes": (_U64, [_I32, _U64]),
     "vsl_convert_weights": (_I32, [_P, _I32, _I32, _U64, _P, _I32, _P]),
+    "vsl_attn_decode_window": (_I32, [_P, _P, _P, _I32, _U32, _U32, _U32, _U32, _F32, _U32, _P, _P, _P, _P,
+                                      _U32, _U32, _U32, _P]),
+    "vsl_attn_prefill_window": (_I32, [_P, _I32, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F32, _P, _I32,
+                                       _U32, _U32, _U32, _P]),
     "vsl_arena_destroy": (_I32, [_P]),
     "vsl_arena_alloc": (_I32, [_P, _U64, _U64, ctypes.POINTER(_P)]),
     "vsl_arena_free": (_I32, [_P, _P]),
@@ -310,7 +316,9 @@ class Engine:
 
     def __init__(self, gguf_path=None, spec=None, seed=0, device=0, kv_capacity=0, use_graph=True,
                  prefill_chunk=0, attn_splits=0, batched_prefill=True, init_std=0.02, prefill_split=None,
-                 dequant_f32=False):
+                 dequant_f32=False, window=None):
+        """window: None (dense attention) or (sparse_window, sparse_global, sparse_threshold) for the
+        windowed long-context mode; (512, 16, 8192) are the reference's values."""
         self._lib = engine_lib()
         opt = EngineOptions()
         self._lib.vsl_engine_default_options(ctypes.byref(opt))
@@ -319,6 +327,9 @@ class Engine:
         if prefill_split is not None:
             opt.prefill_split = prefill_split
         opt.dequant_f32 = int(bool(dequant_f32))
+        if window is not None:
+            opt.sparse_attention = 1
+            opt.sparse_window, opt.sparse_global, opt.sparse_threshold = window
         h = ctypes.c_void_p()
         if gguf_path is not None:
             rc = self._lib.vsl_engine_open(str(gguf_path).encode(), ctypes.byref(opt), ctypes.byref(h))

@@ -533,12 +533,17 @@ constexpr float kLog2e = 1.4426950408889634f;
 // depend on the sequence length, so its first tile is requested before the control block is read,
 // and every next tile before the current one is consumed (two register buffers, as in the GEMV).
 // Positions at or past the length are masked by selects; tiles past the cache read position 0.
-template <class KT, int HD, int G>
+//
+// WIN: the windowed mode. The query at position p attends to every key k <= p while p + 1 <= thr;
+// past that, to the n_glob first keys and the win keys before p (k >= p - win) only. The tiles
+// then run over that set as virtual positions v (v < n_glob -> k = v, else k = v + p - win - n_glob),
+// which depend on p, so the first tiles are requested after the control block is read.
+template <class KT, int HD, int G, bool WIN>
 __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict__ q, const void* __restrict__ kcache,
                                                         const void* __restrict__ vcache, uint32_t n_q, uint32_t n_kv,
                                                         uint32_t cap, float scale, uint32_t nsplit,
                                                         float* __restrict__ part_o, float* __restrict__ part_ml,
-                                                        vsl_ctrl* ctrl) {
+                                                        vsl_ctrl* ctrl, uint32_t win, uint32_t n_glob, uint32_t thr) {
     typedef typename KT::T T;
     constexpr int LPP = HD / 8;            // lanes per position, 8 elements per lane
     constexpr int SLOTS = 64 / LPP;        // positions per wave per tile
@@ -557,12 +562,14 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
     struct Tile {
         uint4 k[KW], v[KW];
     };
+    uint32_t shift = 0;  // WIN: key position = virtual position + shift past the n_glob first keys
     auto position = [&](uint32_t j) { return (j * nsplit + split) * NSLOT + wave * SLOTS + slot; };
     // positions at or past `limit` read position 0 instead (in bounds, and the same cache lines
     // for every such lane)
     auto issue = [&](Tile& b, uint32_t j, uint32_t limit) {
         uint32_t t = position(j);
         t = t < limit ? t : 0;
+        if constexpr (WIN) t = t < n_glob ? t : t + shift;
         const T* kp = Kb + (size_t)t * HD + sub * 8;
         const T* vp = Vb + (size_t)t * HD + sub * 8;
 #pragma unroll
@@ -583,12 +590,25 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
         qr[g][1] = *reinterpret_cast<const float4*>(qp + 4);
     }
     Tile ta, tb;
-    issue(ta, 0, cap);
-    issue(tb, 1, cap);
+    if constexpr (!WIN) {
+        issue(ta, 0, cap);
+        issue(tb, 1, cap);
+    }
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t done = ctrl->done;
     const uint32_t pos = ctrl->pos;
     const uint32_t len = pos < cap ? pos + 1 : cap;  // pos >= cap only with done set
+    // keys attended (virtual positions 0 .. n_att-1)
+    uint32_t n_att = len;
+    if constexpr (WIN) {
+        const uint32_t p = len - 1;  // the query position (clamped with `len` when done)
+        if (len > thr && p > n_glob + win) {  // otherwise the two ranges cover 0..p
+            n_att = n_glob + win + 1;
+            shift = p - win - n_glob;
+        }
+        issue(ta, 0, n_att);
+        issue(tb, 1, n_att);
+    }
 
     float qv[G][8];
 #pragma unroll
@@ -608,7 +628,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
     }
 
     auto consume = [&](const Tile& b, uint32_t j) {
-        const bool valid = position(j) < len;
+        const bool valid = position(j) < n_att;
         float kf[8], vf[8];
         if constexpr (KW == 1) {
             unpack(b.k[0], KT(), kf);
@@ -638,19 +658,19 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
     };
 
     consume(ta, 0);
-    issue(ta, 2, len);
+    issue(ta, 2, n_att);
     __builtin_amdgcn_sched_barrier(0);
     consume(tb, 1);
-    const uint32_t total = (len + NSLOT - 1) / NSLOT;  // tiles holding positions < len
+    const uint32_t total = (n_att + NSLOT - 1) / NSLOT;  // tiles holding positions < n_att
     const uint32_t mine = total > split ? (total - 1 - split) / nsplit + 1 : 0;
     // tiles 2 .. mine-1 in pairs with a single loop exit (an odd remainder is padded with one
     // masked tile); the tile issued by the last pair is never consumed
     const uint32_t n_pairs = mine > 2 ? (mine - 1) / 2 : 0;
     for (uint32_t pp = 0; pp < n_pairs; ++pp) {
-        issue(tb, 2 * pp + 3, len);
+        issue(tb, 2 * pp + 3, n_att);
         __builtin_amdgcn_sched_barrier(0);
         consume(ta, 2 * pp + 2);
-        issue(ta, 2 * pp + 4, len);
+        issue(ta, 2 * pp + 4, n_att);
         __builtin_amdgcn_sched_barrier(0);
         consume(tb, 2 * pp + 3);
     }
@@ -793,15 +813,32 @@ __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(const float* _
     if (!done) out[(size_t)h * HD + dd] = ((a0 + a1) + (a2 + a3)) * inv;
 }
 
+struct AttnWindow {
+    bool on;
+    uint32_t win, n_glob, thr;
+};
+
+template <class KT, int HD, int G>
+void launch_attn_w(dim3 grid, hipStream_t s, const float* q, const void* kc, const void* vc, uint32_t n_q,
+                   uint32_t n_kv, uint32_t cap, float scale, uint32_t nsplit, float* po, float* pml, vsl_ctrl* ctrl,
+                   const AttnWindow& w) {
+    if (w.on)
+        k_attn_decode<KT, HD, G, true><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl,
+                                                               w.win, w.n_glob, w.thr);
+    else
+        k_attn_decode<KT, HD, G, false><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl,
+                                                                0, 0, 0);
+}
+
 template <class KT, int HD>
 int launch_attn_g(uint32_t G, dim3 grid, hipStream_t s, const float* q, const void* kc, const void* vc, uint32_t n_q,
                   uint32_t n_kv, uint32_t cap, float scale, uint32_t nsplit, float* po, float* pml, float* out,
-                  vsl_ctrl* ctrl) {
+                  vsl_ctrl* ctrl, const AttnWindow& w) {
     switch (G) {
-        case 1: k_attn_decode<KT, HD, 1><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl); break;
-        case 2: k_attn_decode<KT, HD, 2><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl); break;
-        case 4: k_attn_decode<KT, HD, 4><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl); break;
-        case 8: k_attn_decode<KT, HD, 8><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl); break;
+        case 1: launch_attn_w<KT, HD, 1>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+        case 2: launch_attn_w<KT, HD, 2>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+        case 4: launch_attn_w<KT, HD, 4>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+        case 8: launch_attn_w<KT, HD, 8>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
         default: return vsl_unsupported("vsl_attn_decode: GQA ratio %u (supported 1,2,4,8)", G);
     }
     HIP_TRY(hipGetLastError());
@@ -1237,9 +1274,9 @@ extern "C" int vsl_qkv_rope_append(const float* x, const float* gamma, float eps
     return vsl_unsupported("vsl_qkv_rope_append: dtype %d", wdtype);
 }
 
-extern "C" int vsl_attn_decode(const float* q, const void* kcache, const void* vcache, int kv_dtype, uint32_t n_q,
-                               uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* part_o,
-                               float* part_ml, float* out, vsl_ctrl* ctrl, void* stream) {
+static int attn_decode(const float* q, const void* kcache, const void* vcache, int kv_dtype, uint32_t n_q,
+                       uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* part_o,
+                       float* part_ml, float* out, vsl_ctrl* ctrl, const AttnWindow& w, void* stream) {
     if (!q || !kcache || !vcache || !part_o || !part_ml || !out || !ctrl)
         return vsl_invalid("vsl_attn_decode: null pointer");
     if (n_kv == 0 || n_q % n_kv) return vsl_invalid("vsl_attn_decode: n_q=%u not a multiple of n_kv=%u", n_q, n_kv);
@@ -1248,13 +1285,30 @@ extern "C" int vsl_attn_decode(const float* q, const void* kcache, const void* v
     dim3 grid(nsplit, n_kv);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (kv_dtype == VSL_DT_F16) {
-        if (hd == 128) return launch_attn_g<WF16, 128>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl);
-        if (hd == 64) return launch_attn_g<WF16, 64>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl);
+        if (hd == 128) return launch_attn_g<WF16, 128>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl, w);
+        if (hd == 64) return launch_attn_g<WF16, 64>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl, w);
     } else if (kv_dtype == VSL_DT_F32) {
-        if (hd == 128) return launch_attn_g<WF32, 128>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl);
-        if (hd == 64) return launch_attn_g<WF32, 64>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl);
+        if (hd == 128) return launch_attn_g<WF32, 128>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl, w);
+        if (hd == 64) return launch_attn_g<WF32, 64>(G, grid, s, q, kcache, vcache, n_q, n_kv, cap, scale, nsplit, part_o, part_ml, out, ctrl, w);
     }
     return vsl_unsupported("vsl_attn_decode: head_dim %u / kv dtype %d (supported 64,128 / f16,f32)", hd, kv_dtype);
+}
+
+extern "C" int vsl_attn_decode(const float* q, const void* kcache, const void* vcache, int kv_dtype, uint32_t n_q,
+                               uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* part_o,
+                               float* part_ml, float* out, vsl_ctrl* ctrl, void* stream) {
+    return attn_decode(q, kcache, vcache, kv_dtype, n_q, n_kv, hd, cap, scale, nsplit, part_o, part_ml, out, ctrl,
+                       AttnWindow{false, 0, 0, 0}, stream);
+}
+
+extern "C" int vsl_attn_decode_window(const float* q, const void* kcache, const void* vcache, int kv_dtype,
+                                      uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale,
+                                      uint32_t nsplit, float* part_o, float* part_ml, float* out, vsl_ctrl* ctrl,
+                                      uint32_t window, uint32_t n_global, uint32_t threshold, void* stream) {
+    if ((uint64_t)window + n_global >= 0x80000000ull)
+        return vsl_invalid("vsl_attn_decode_window: window %u + global %u too large", window, n_global);
+    return attn_decode(q, kcache, vcache, kv_dtype, n_q, n_kv, hd, cap, scale, nsplit, part_o, part_ml, out, ctrl,
+                       AttnWindow{true, window, n_global, threshold}, stream);
 }
 
 extern "C" int vsl_gemv_residual(const void* W, int wdtype, uint32_t N, uint32_t K, const float* x, float* resid,

@@ -323,11 +323,12 @@ __device__ __forceinline__ int ksw(int r, int c) {
     else return r * HD + ((c ^ ((r >> 1) & 7)) * 8);                      // 128-byte rows: row pairs
 }
 
-template <int HD, int G, bool QX2, bool OX2>
+template <int HD, int G, bool QX2, bool OX2, bool WIN>
 __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restrict__ q, const vsl_half* __restrict__ kc,
                                                          const vsl_half* __restrict__ vc, uint32_t S, uint32_t pos0,
                                                          uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
-                                                         vsl_half* __restrict__ out) {
+                                                         vsl_half* __restrict__ out, uint32_t win, uint32_t n_glob,
+                                                         uint32_t thr) {
     constexpr int TK = kAttnTile;
     constexpr int NT = 64 * G;
     constexpr int VTS = TK + 8;                 // halfs per V^T row (one head dim)
@@ -351,6 +352,20 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     const uint32_t kv_end = pos0 + last_s + 1;  // positions 0..kv_end-1 are visible to some row
     const uint32_t my_pos = pos0 + my_s;
     const uint32_t n_tiles = (kv_end + TK - 1) / TK;
+    // Windowed rows (position p with p + 1 > thr) see the keys k < n_glob and k >= p - win only.
+    // When the block's first row is windowed, every row is, and the key tiles below the first row's
+    // window and past the global tiles are skipped: virtual tile vt runs over [0, n_gt) and then
+    // [t_lo, n_tiles).
+    const uint32_t p_first = pos0 + s_base;
+    uint32_t n_gt = n_tiles, t_lo = n_tiles;
+    if (WIN && p_first + 1 > thr && p_first > win) {
+        t_lo = (p_first - win) / TK;
+        n_gt = min((n_glob + TK - 1) / TK, t_lo);
+    }
+    const uint32_t n_vt = n_gt + (n_tiles - t_lo);
+    auto phys = [&](uint32_t vt) { return vt < n_gt ? vt : vt - n_gt + t_lo; };
+    // this lane's row: keys below my_lo (and not global) are masked
+    const uint32_t my_lo = (WIN && my_pos + 1 > thr && my_pos > win) ? my_pos - win : 0;
     const vsl_half* Kb = kc + (size_t)kvh * cap * HD;
     const vsl_half* Vb = vc + (size_t)kvh * cap * HD;
 
@@ -420,7 +435,8 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t kvp = t * TK + kb * 32 + d_row(v, lane);
-                const float sc = kvp <= my_pos ? st[kb][v] * sl2 : -INFINITY;
+                const bool seen = WIN ? kvp <= my_pos && (kvp >= my_lo || kvp < n_glob) : kvp <= my_pos;
+                const float sc = seen ? st[kb][v] * sl2 : -INFINITY;
                 st[kb][v] = sc;
                 bm = fmaxf(bm, sc);
             }
@@ -474,15 +490,16 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     // tile pipeline: tile t+1's global loads are issued before tile t's MFMAs and stored to the
     // other LDS buffer after them; loads past the last tile re-read it and are never stored
     Stage sg;
-    gload(sg, 0);
-    sstore(sg, 0, 0);
+    gload(sg, phys(0));
+    sstore(sg, 0, phys(0));
     __syncthreads();
-    for (uint32_t t = 0; t < n_tiles; ++t) {
+    for (uint32_t t = 0; t < n_vt; ++t) {
         const int buf = t & 1;
-        gload(sg, t + 1 < n_tiles ? t + 1 : t);
+        const uint32_t next = phys(t + 1 < n_vt ? t + 1 : t);
+        gload(sg, next);
         __builtin_amdgcn_sched_barrier(0);
-        compute(buf, t);
-        sstore(sg, buf ^ 1, t + 1);
+        compute(buf, phys(t));
+        sstore(sg, buf ^ 1, next);
         __syncthreads();
     }
 
@@ -592,34 +609,51 @@ extern "C" int vsl_rope_split_append(const float* qkv, uint32_t S, uint32_t n_q,
     return VSL_OK;
 }
 
+struct PrefillWindow {
+    bool on;
+    uint32_t win, n_glob, thr;
+};
+
+template <int HD, int G, bool WIN>
+static void launch_attn_prefill_w(dim3 grid, hipStream_t s, const vsl_half* q, const vsl_half* k, const vsl_half* v,
+                                  uint32_t S, uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
+                                  vsl_half* o, bool qx2, bool ox2, const PrefillWindow& w) {
+    constexpr int NT = 64 * G;
+    if (qx2 && ox2)
+        k_attn_prefill<HD, G, true, true, WIN><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+    else if (qx2)
+        k_attn_prefill<HD, G, true, false, WIN><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+    else if (ox2)
+        k_attn_prefill<HD, G, false, true, WIN><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+    else
+        k_attn_prefill<HD, G, false, false, WIN><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+}
+
 template <int HD, int G>
 static void launch_attn_prefill_g(dim3 grid, hipStream_t s, const vsl_half* q, const vsl_half* k, const vsl_half* v,
                                   uint32_t S, uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
-                                  vsl_half* o, bool qx2, bool ox2) {
-    constexpr int NT = 64 * G;
-    if (qx2 && ox2) k_attn_prefill<HD, G, true, true><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
-    else if (qx2) k_attn_prefill<HD, G, true, false><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
-    else if (ox2) k_attn_prefill<HD, G, false, true><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
-    else k_attn_prefill<HD, G, false, false><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o);
+                                  vsl_half* o, bool qx2, bool ox2, const PrefillWindow& w) {
+    if (w.on) launch_attn_prefill_w<HD, G, true>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w);
+    else launch_attn_prefill_w<HD, G, false>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w);
 }
 
 template <int HD>
 static int launch_attn_prefill(dim3 grid, hipStream_t s, const vsl_half* q, const vsl_half* k, const vsl_half* v,
                                uint32_t S, uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
-                               vsl_half* o, bool qx2, bool ox2) {
+                               vsl_half* o, bool qx2, bool ox2, const PrefillWindow& w) {
     switch (n_q / n_kv) {
-        case 1: launch_attn_prefill_g<HD, 1>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2); break;
-        case 2: launch_attn_prefill_g<HD, 2>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2); break;
-        case 4: launch_attn_prefill_g<HD, 4>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2); break;
-        case 8: launch_attn_prefill_g<HD, 8>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2); break;
+        case 1: launch_attn_prefill_g<HD, 1>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w); break;
+        case 2: launch_attn_prefill_g<HD, 2>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w); break;
+        case 4: launch_attn_prefill_g<HD, 4>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w); break;
+        case 8: launch_attn_prefill_g<HD, 8>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w); break;
         default: return vsl_unsupported("vsl_attn_prefill: GQA ratio %u (supported 1, 2, 4, 8)", n_q / n_kv);
     }
     return VSL_OK;
 }
 
-extern "C" int vsl_attn_prefill(const void* q, int q_dtype, const void* kcache, const void* vcache, uint32_t S,
-                                uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale,
-                                void* out, int out_dtype, void* stream) {
+static int attn_prefill(const void* q, int q_dtype, const void* kcache, const void* vcache, uint32_t S, uint32_t pos0,
+                        uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, void* out, int out_dtype,
+                        const PrefillWindow& w, void* stream) {
     if (!q || !kcache || !vcache || !out) return vsl_invalid("vsl_attn_prefill: null pointer");
     if (S == 0) return VSL_OK;
     if (n_kv == 0 || n_q % n_kv) return vsl_invalid("vsl_attn_prefill: n_q=%u n_kv=%u", n_q, n_kv);
@@ -638,12 +672,29 @@ extern "C" int vsl_attn_prefill(const void* q, int q_dtype, const void* kcache, 
     vsl_half* oo = static_cast<vsl_half*>(out);
     int rc;
     if (hd == 128)
-        rc = launch_attn_prefill<128>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, ox2);
+        rc = launch_attn_prefill<128>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, ox2, w);
     else if (hd == 64)
-        rc = launch_attn_prefill<64>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, ox2);
+        rc = launch_attn_prefill<64>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, ox2, w);
     else
         return vsl_unsupported("vsl_attn_prefill: head_dim %u", hd);
     if (rc) return rc;
     HIP_TRY(hipGetLastError());
     return VSL_OK;
+}
+
+extern "C" int vsl_attn_prefill(const void* q, int q_dtype, const void* kcache, const void* vcache, uint32_t S,
+                                uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale,
+                                void* out, int out_dtype, void* stream) {
+    return attn_prefill(q, q_dtype, kcache, vcache, S, pos0, n_q, n_kv, hd, cap, scale, out, out_dtype,
+                        PrefillWindow{false, 0, 0, 0}, stream);
+}
+
+extern "C" int vsl_attn_prefill_window(const void* q, int q_dtype, const void* kcache, const void* vcache, uint32_t S,
+                                       uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap,
+                                       float scale, void* out, int out_dtype, uint32_t window, uint32_t n_global,
+                                       uint32_t threshold, void* stream) {
+    if ((uint64_t)window + n_global >= 0x80000000ull)
+        return vsl_invalid("vsl_attn_prefill_window: window %u + global %u too large", window, n_global);
+    return attn_prefill(q, q_dtype, kcache, vcache, S, pos0, n_q, n_kv, hd, cap, scale, out, out_dtype,
+                        PrefillWindow{true, window, n_global, threshold}, stream);
 }

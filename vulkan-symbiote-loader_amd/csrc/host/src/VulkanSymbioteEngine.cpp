@@ -240,6 +240,16 @@ void VulkanSymbioteEngine::release() {
     pack_manager_.clear();
 }
 
+int VulkanSymbioteEngine::attend(const Layer& y, float scale) {
+    const uint32_t nq = config_.num_attention_heads, nkv = config_.num_key_value_heads, hd = config_.head_dim;
+    if (config_.use_sparse_attention)
+        return vsl_attn_decode_window(q_, y.kc, y.vc, kvdt_, nq, nkv, hd, cap_, scale, nsplit_, part_o_, part_ml_,
+                                      attn_, ctrl_, config_.sparse_window_size, config_.sparse_global_tokens,
+                                      config_.sparse_threshold, stream_);
+    return vsl_attn_decode(q_, y.kc, y.vc, kvdt_, nq, nkv, hd, cap_, scale, nsplit_, part_o_, part_ml_, attn_, ctrl_,
+                           stream_);
+}
+
 void VulkanSymbioteEngine::init_device(const ModelConfig& cfg, bool fp16_weights, int embed_dtype) {
     if (!ConfigManager::instance().performance().enable_gpu)
         throw std::runtime_error("GPU disabled (--disable-gpu): this backend runs on MI355X only and has no CPU path");
@@ -249,6 +259,13 @@ void VulkanSymbioteEngine::init_device(const ModelConfig& cfg, bool fp16_weights
         throw std::runtime_error("invalid model configuration");
     config_.head_dim = cfg.hidden_size / cfg.num_attention_heads;
     config_.use_fp16 = fp16_weights;
+    // windowed long-context mode: off unless asked for (exact dense attention at every length)
+    config_.use_sparse_attention = options_.sparse_attention;
+    config_.sparse_window_size = options_.sparse_window;
+    config_.sparse_global_tokens = options_.sparse_global;
+    config_.sparse_threshold = options_.sparse_threshold;
+    if ((uint64_t)options_.sparse_window + options_.sparse_global >= 0x80000000ull)
+        throw std::runtime_error("sparse window + global tokens too large");
     wdt_ = fp16_weights ? VSL_DT_F16 : VSL_DT_F32;
     kvdt_ = wdt_;  // fp16 models keep an fp16 KV cache; fp32 models keep fp32
     edt_ = embed_dtype;
@@ -547,8 +564,7 @@ void VulkanSymbioteEngine::enqueue_layers(uint32_t l0, uint32_t l1) {
         const Layer& y = layers_[l];
         check(vsl_qkv_rope_append(x_, y.attn_norm, eps, y.wqkv, wdt_, d, nq, nkv, hd, rope_cos_, rope_sin_, y.kc, y.vc,
                                   kvdt_, cap_, q_, ctrl_, stream_), "vsl_qkv_rope_append");
-        check(vsl_attn_decode(q_, y.kc, y.vc, kvdt_, nq, nkv, hd, cap_, scale, nsplit_, part_o_, part_ml_, attn_,
-                              ctrl_, stream_), "vsl_attn_decode");
+        check(attend(y, scale), "vsl_attn_decode");
         check(vsl_gemv_residual(y.wo, wdt_, d, nq * hd, attn_, x_, ctrl_, stream_), "vsl_gemv_residual(o)");
         check(vsl_norm_swiglu(x_, y.ffn_norm, eps, y.wgu, wdt_, d, F, h_, ctrl_, stream_), "vsl_norm_swiglu");
         check(vsl_gemv_residual(y.wdown, wdt_, d, F, h_, x_, ctrl_, stream_), "vsl_gemv_residual(down)");
@@ -631,8 +647,14 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
             check(vsl_gemm_f16(pxn_, y.wqkv, S, (nq + 2 * nkv) * hd, d, pqkv_, g_qkv, stream_), "gemm qkv");
             check(vsl_rope_split_append(pqkv_, S, nq, nkv, hd, c0, rope_cos_, rope_sin_, pq_, qdt, y.kc, y.vc, kvdt_,
                                         cap_, stream_), "vsl_rope_split_append");
-            check(vsl_attn_prefill(pq_, qdt, y.kc, y.vc, S, c0, nq, nkv, hd, cap_, scale, pattn_, odt, stream_),
-                  "vsl_attn_prefill");
+            if (config_.use_sparse_attention)
+                check(vsl_attn_prefill_window(pq_, qdt, y.kc, y.vc, S, c0, nq, nkv, hd, cap_, scale, pattn_, odt,
+                                              config_.sparse_window_size, config_.sparse_global_tokens,
+                                              config_.sparse_threshold, stream_),
+                      "vsl_attn_prefill_window");
+            else
+                check(vsl_attn_prefill(pq_, qdt, y.kc, y.vc, S, c0, nq, nkv, hd, cap_, scale, pattn_, odt, stream_),
+                      "vsl_attn_prefill");
             check(vsl_gemm_f16(pattn_, y.wo, S, d, nq * hd, px_, g_o, stream_), "gemm o");
             check(vsl_rmsnorm(px_, y.ffn_norm, S, d, eps, pxn_, n2, stream_), "vsl_rmsnorm");
             check(vsl_gemm_f16(pxn_, y.wgu, S, F, d, ph_, g_gu, stream_), "gemm gate/up");
@@ -758,8 +780,7 @@ double VulkanSymbioteEngine::time_op(int op, uint32_t iterations) {
                                           y.vc, kvdt_, cap_, q_, ctrl_, stream_), "qkv");
                 break;
             case 1:
-                check(vsl_attn_decode(q_, y.kc, y.vc, kvdt_, nq, nkv, hd, cap_, scale, nsplit_, part_o_, part_ml_,
-                                      attn_, ctrl_, stream_), "attn");
+                check(attend(y, scale), "attn");
                 break;
             case 2: check(vsl_gemv_residual(y.wo, wdt_, d, nq * hd, attn_, x_, ctrl_, stream_), "o"); break;
             case 3: check(vsl_norm_swiglu(x_, y.ffn_norm, eps, y.wgu, wdt_, d, F, h_, ctrl_, stream_), "gate/up"); break;

@@ -29,6 +29,10 @@ extern "C" void vsl_engine_default_options(vsl_engine_options* o) {
     o->use_graph = 1;
     o->batched_prefill = 1;
     o->prefill_split = EngineOptions::kPrefillSplitAll;
+    const EngineOptions d;
+    o->sparse_window = d.sparse_window;
+    o->sparse_global = d.sparse_global;
+    o->sparse_threshold = d.sparse_threshold;
 }
 
 static EngineOptions to_options(const vsl_engine_options* o) {
@@ -42,6 +46,10 @@ static EngineOptions to_options(const vsl_engine_options* o) {
     e.batched_prefill = o->batched_prefill != 0;
     e.prefill_split = o->prefill_split & EngineOptions::kPrefillSplitAll;
     e.dequant_f32 = o->dequant_f32 != 0;
+    e.sparse_attention = o->sparse_attention != 0;
+    e.sparse_window = o->sparse_window;
+    e.sparse_global = o->sparse_global;
+    e.sparse_threshold = o->sparse_threshold;
     return e;
 }
 

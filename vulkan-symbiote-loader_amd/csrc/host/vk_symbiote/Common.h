@@ -39,13 +39,16 @@ struct ModelConfig {
     bool use_fp16 = true;
     float rms_epsilon = 1e-5f;
 
-    // Windowed long-context mode of the reference (Common.h:70-75).  Parsed and kept for API
-    // compatibility; this backend always runs exact dense causal attention.
+    // Windowed long-context mode of the reference (Common.h:70-75).  The engine sets these from
+    // EngineOptions (off unless asked for); sparse_threshold is the reference's fixed
+    // `seq_len > 8192` switch (VulkanSymbioteEngine.cpp:788).  sparse_block_size and
+    // use_ring_attention are kept for API compatibility (the reference never reads them).
     bool use_sparse_attention = true;
     uint32 sparse_window_size = 512;
     uint32 sparse_global_tokens = 16;
     uint32 sparse_block_size = 1024;
     bool use_ring_attention = true;
+    uint32 sparse_threshold = 8192;
 };
 
 struct InferenceParams {

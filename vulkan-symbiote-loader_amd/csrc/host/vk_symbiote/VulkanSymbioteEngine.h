@@ -74,6 +74,14 @@ struct EngineOptions {
     // Block-quantized GGUF weights (Q4_0 / Q4_1 / Q8_0) are expanded at load into fp16 packs, or into
     // fp32 packs holding exactly the values the reference's dequantize_tensor returns when set.
     bool dequant_f32 = false;
+    // Windowed long-context mode (the reference's use_sparse_attention, Common.h:70-75, taken when
+    // seq_len > 8192, VulkanSymbioteEngine.cpp:788): a query at position p with p + 1 > threshold
+    // attends to the first sparse_global keys and to the sparse_window keys before it (and itself)
+    // only.  Off by default: every length then runs exact dense causal attention.
+    bool sparse_attention = false;
+    uint32_t sparse_window = 512;
+    uint32_t sparse_global = 16;
+    uint32_t sparse_threshold = 8192;
     bool verbose = false;
     static constexpr uint32_t kPrefillSplitAll = 0x1F;
 };
@@ -236,6 +244,7 @@ class VulkanSymbioteEngine {
     vsl_graph* step_graph(const SamplingParams& p);
     void release();
     void check(int rc, const char* what) const;
+    int attend(const Layer& y, float scale);  // decode attention of one layer (dense or windowed)
 };
 
 // Writes a synthetic Llama-style GGUF (tensor names as the reference reads them,
