@@ -113,6 +113,27 @@ int vsl_engine_benchmark(vsl_engine* e, uint32_t warmup, uint32_t tokens, uint32
 /* device -> host copy of one resident pack (GGUF tensor name); *dtype_out = VSL_DT_* */
 int vsl_engine_read_tensor(vsl_engine* e, const char* name, void* dst, uint64_t bytes, int* dtype_out);
 
+/* Pack metadata (PackMetadata, NomadPack.h:33-44, as GGUFLoader::generate_packs fills it,
+ * GGUFLoader.cpp:730-751: one pack per tensor, pack_id = std::hash(name), type by name :1302-1315,
+ * layer from "blk.<n>" :1264-1272, priority :1279-1300).  For an engine's packs also where each one
+ * lives: device pointer, resident bytes (after any expansion), dtype and tier (VRAM_HOT = 0). */
+typedef struct vsl_pack_info {
+    uint64_t pack_id;
+    int32_t type;           /* PackType: 0..3 attention Q/K/V/O, 4 gate (and up), 6 down, 7 norm,
+                               10 embedding, 11 head, 255 unknown */
+    uint32_t layer_idx, head_idx, alignment;
+    uint64_t compressed_size, decompressed_size, file_offset;
+    float base_priority;
+    int32_t tier;           /* engine packs: MemoryTier; GGUF packs: -1 */
+    int32_t dtype;          /* engine packs: VSL_DT_*; GGUF packs: -1 */
+    uint32_t n_dimensions;
+    uint64_t resident_bytes; /* engine packs: bytes in HBM; GGUF packs: 0 */
+    void* device_ptr;        /* engine packs: the pack's HBM address; GGUF packs: NULL */
+} vsl_pack_info;
+int vsl_engine_pack_count(vsl_engine* e, uint64_t* n);
+/* name receives the tensor name (NUL-terminated, truncated to name_cap) */
+int vsl_engine_pack(vsl_engine* e, uint64_t idx, vsl_pack_info* out, char* name, uint64_t name_cap);
+
 /* GGUF writer: synthetic Llama-style model with the reference's tensor names.
  * convention 0 = the reference's tensor-type ids (F32 6, F16 48, Q4_0 13, Q4_1 14, Q8_0 17) and
  * block layout, 1 = ggml ids (F32 0, F16 1, Q4_0 2, Q4_1 3, Q8_0 8) and ggml's block layout. */
@@ -139,6 +160,9 @@ int vsl_gguf_model_config(vsl_gguf* g, vsl_model_spec* out);
 /* -30 when the tensor does not exist */
 int vsl_gguf_tensor(vsl_gguf* g, const char* name, uint64_t* data_offset, uint64_t* data_size, uint32_t* raw_type,
                     uint32_t* n_dims, uint64_t dims[4]);
+/* GGUFLoader::generate_packs: the packs of every tensor, in file order */
+int vsl_gguf_pack_count(vsl_gguf* g, uint64_t* n);
+int vsl_gguf_pack(vsl_gguf* g, uint64_t idx, vsl_pack_info* out, char* name, uint64_t name_cap);
 /* returns the element count, or the reference's read codes (-11 read, -12 type, -20 quantized, -30 missing);
  * Q4_0 / Q4_1 / Q8_0 tensors are dequantized (dequantize_tensor, GGUFLoader.cpp:1121-1223) */
 int64_t vsl_gguf_read_f32(vsl_gguf* g, const char* name, float* out, uint64_t cap);

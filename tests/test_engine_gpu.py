@@ -211,6 +211,22 @@ def test_engine_stats_and_packs(vsl):
         e.generate_ids(np.arange(1, 17, dtype=np.uint32), 8)
         s = e.last_stats()
         assert s["prompt_tokens"] == 16 and s["generated_tokens"] == 8 and s["decode_ms"] > 0
+        # one resident pack per tensor, each in HBM (tier VRAM_HOT) inside the arena, sized as stored
+        packs = e.packs()
+        assert len(packs) == 9 * L + 3
+        assert sum(p["resident_bytes"] for p in packs) == wb
+        assert all(p["tier"] == 0 and p["device_ptr"] for p in packs)
+        by = {p["name"]: p for p in packs}
+        assert by["blk.3.ffn_down.weight"]["resident_bytes"] == 2 * d * F and by["blk.3.ffn_down.weight"]["dtype"] == 1
+        assert by["blk.3.ffn_norm.weight"]["dtype"] == 0 and by["blk.3.ffn_norm.weight"]["resident_bytes"] == 4 * d
+        assert (by["blk.3.attn_q.weight"]["type"], by["blk.3.attn_q.weight"]["layer_idx"]) == (0, 3)
+        assert by["blk.3.ffn_up.weight"]["type"] == 4 and by["output_norm.weight"]["type"] == 11
+        # the q/k/v packs of a layer are contiguous (one fused GEMV reads them as one matrix)
+        q, k, v = (by[f"blk.7.attn_{x}.weight"] for x in "qkv")
+        assert k["device_ptr"] == q["device_ptr"] + q["resident_bytes"]
+        assert v["device_ptr"] == k["device_ptr"] + k["resident_bytes"]
+        st = e.vram_stats()
+        assert st["used_size"] >= wb
 
 
 @pytest.mark.slow

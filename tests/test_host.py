@@ -195,3 +195,54 @@ def test_config_manager_args_and_toml(vsl, tmp_path):
     t2.write_text("[memory]\nvram_budget_gb = 1000\n")
     assert L.vsl_config_load_file(str(t2).encode()) != 0  # validate_config: VRAM above 288 GB
     L.vsl_config_reset()
+
+
+def _gguf_packs(vsl, path):
+    L = vsl.engine_lib()
+    g = ctypes.c_void_p()
+    assert L.vsl_gguf_open(str(path).encode(), ctypes.byref(g)) == 0
+    try:
+        n = ctypes.c_uint64()
+        assert L.vsl_gguf_pack_count(g, ctypes.byref(n)) == 0
+        out = {}
+        for i in range(n.value):
+            info, name = vsl.PackInfo(), ctypes.create_string_buffer(256)
+            assert L.vsl_gguf_pack(g, i, ctypes.byref(info), name, 256) == 0
+            out[name.value.decode()] = info
+        assert L.vsl_gguf_pack(g, n.value, ctypes.byref(vsl.PackInfo()), None, 0) == -30
+        return out
+    finally:
+        L.vsl_gguf_close(g)
+
+
+# name -> (PackType, layer, priority), by the reference's rules (GGUFLoader.cpp:1264-1315): type by
+# substring in a fixed order (ffn_up files under the gate type; only attn_norm / ffn_norm are norms,
+# so output_norm is HEAD); layer = the first "blk.<digits>" anywhere; priority 0.5, +0.2 "attn",
+# +0.3 "token_embd"/"output", +0.1 layer < 4, capped at 1.0
+PACK_RULES = {
+    "token_embd.weight": (10, 0, 0.9), "output.weight": (11, 0, 0.9), "output_norm.weight": (11, 0, 0.9),
+    "blk.0.attn_q.weight": (0, 0, 0.8), "blk.3.attn_k.weight": (1, 3, 0.8), "blk.4.attn_v.weight": (2, 4, 0.7),
+    "blk.17.attn_output.weight": (3, 17, 1.0), "blk.2.ffn_gate.weight": (4, 2, 0.6),
+    "blk.5.ffn_up.weight": (4, 5, 0.5), "blk.9.ffn_down.weight": (6, 9, 0.5), "blk.1.attn_norm.weight": (7, 1, 0.8),
+    "blk.12.ffn_norm.weight": (7, 12, 0.5), "x.blk.y.blk.21.misc": (255, 21, 0.5), "rope_freqs.weight": (255, 0, 0.6),
+}
+
+
+def test_pack_metadata_rules(vsl, tmp_path):
+    tensors = [(n, [4 + i], 6, np.arange(4 + i, dtype=np.float32).tobytes()) for i, n in enumerate(PACK_RULES)]
+    data, start, offs = build_gguf(tensors, [("llama.embedding_length", 4, struct.pack("<I", 64))])
+    p = tmp_path / "packs.gguf"
+    p.write_bytes(data)
+    packs = _gguf_packs(vsl, p)
+    assert set(packs) == set(PACK_RULES)
+    ids = set()
+    for (name, dims, _, raw), off in zip(tensors, offs):
+        info = packs[name]
+        t, layer, prio = PACK_RULES[name]
+        assert (info.type, info.layer_idx, info.head_idx, info.alignment) == (t, layer, 0, 256), name
+        assert abs(info.base_priority - prio) < 1e-6, (name, info.base_priority)
+        assert info.compressed_size == info.decompressed_size == len(raw)
+        assert info.file_offset == start + off
+        assert (info.tier, info.dtype, info.resident_bytes, info.device_ptr) == (-1, -1, 0, None)
+        ids.add(info.pack_id)
+    assert len(ids) == len(PACK_RULES) and 0 not in ids  # std::hash of distinct names

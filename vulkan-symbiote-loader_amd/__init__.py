@@ -43,6 +43,15 @@ class ModelSpec(ctypes.Structure):
                 ("dtype", ctypes.c_uint32), ("head_dim", ctypes.c_uint32)]
 
 
+class PackInfo(ctypes.Structure):
+    _fields_ = [("pack_id", ctypes.c_uint64), ("type", ctypes.c_int32), ("layer_idx", ctypes.c_uint32),
+                ("head_idx", ctypes.c_uint32), ("alignment", ctypes.c_uint32), ("compressed_size", ctypes.c_uint64),
+                ("decompressed_size", ctypes.c_uint64), ("file_offset", ctypes.c_uint64),
+                ("base_priority", ctypes.c_float), ("tier", ctypes.c_int32), ("dtype", ctypes.c_int32),
+                ("n_dimensions", ctypes.c_uint32), ("resident_bytes", ctypes.c_uint64),
+                ("device_ptr", ctypes.c_void_p)]
+
+
 class EngineOptions(ctypes.Structure):
     _fields_ = [("device", ctypes.c_int32), ("kv_capacity", ctypes.c_uint32), ("use_graph", ctypes.c_uint32),
                 ("prefill_chunk", ctypes.c_uint32), ("attn_splits", ctypes.c_uint32),
@@ -173,6 +182,10 @@ _ENGINE_SIGS = {
     "vsl_write_synthetic_gguf": (_I32, [ctypes.c_char_p, ctypes.POINTER(ModelSpec), _U64, _I32]),
     "vsl_write_synthetic_gguf_vocab": (_I32, [ctypes.c_char_p, ctypes.POINTER(ModelSpec), _U64, _I32,
                                               ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_U64), _U32, _I32]),
+    "vsl_engine_pack_count": (_I32, [_P, ctypes.POINTER(_U64)]),
+    "vsl_engine_pack": (_I32, [_P, _U64, ctypes.POINTER(PackInfo), ctypes.c_char_p, _U64]),
+    "vsl_gguf_pack_count": (_I32, [_P, ctypes.POINTER(_U64)]),
+    "vsl_gguf_pack": (_I32, [_P, _U64, ctypes.POINTER(PackInfo), ctypes.c_char_p, _U64]),
     "vsl_tokenizer_open": (_I32, [ctypes.c_char_p, ctypes.POINTER(_P)]),
     "vsl_tokenizer_close": (_I32, [_P]),
     "vsl_tokenizer_info": (_I32, [_P, ctypes.POINTER(_U32), ctypes.POINTER(ctypes.c_int)]),
@@ -444,6 +457,19 @@ class Engine:
         check(self._lib.vsl_engine_benchmark(self._h, warmup, tokens, iterations, ctypes.byref(a), ctypes.byref(lo),
                                              ctypes.byref(hi)), self._lib)
         return a.value, lo.value, hi.value
+
+    def packs(self):
+        """Resident packs: [{name, type, layer_idx, priority, bytes, dtype, tier, device_ptr, ...}]."""
+        n = _U64()
+        check(self._lib.vsl_engine_pack_count(self._h, ctypes.byref(n)), self._lib)
+        out = []
+        for i in range(n.value):
+            info, name = PackInfo(), ctypes.create_string_buffer(256)
+            check(self._lib.vsl_engine_pack(self._h, i, ctypes.byref(info), name, 256), self._lib)
+            d = {f: getattr(info, f) for f, _ in PackInfo._fields_}
+            d["name"] = name.value.decode()
+            out.append(d)
+        return out
 
     def read_tensor(self, name, nbytes):
         buf = np.empty(nbytes, dtype=np.uint8)

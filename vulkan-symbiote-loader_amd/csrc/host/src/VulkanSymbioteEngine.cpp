@@ -404,8 +404,9 @@ void VulkanSymbioteEngine::init_synthetic_weights(const SyntheticSpec& spec) {
         PackMetadata m;
         m.pack_id = std::hash<std::string>{}(name);
         m.tensor_name = name;
-        m.type = PackType::NORM_GAMMA;
+        m.type = classify_tensor_type(name);
         m.layer_idx = extract_layer_index(name);
+        m.base_priority = calculate_pack_priority(name);
         m.decompressed_size = m.compressed_size = d * 4;
         m.n_dimensions = 1;
         m.dimensions = {d};

@@ -1,4 +1,5 @@
 // engine_capi.cpp -- extern "C" wrapper of VulkanSymbioteEngine / GGUF writer / ConfigManager.
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -339,6 +340,47 @@ extern "C" int vsl_write_synthetic_gguf_vocab(const char* path, const vsl_model_
     return VSL_OK;
 }
 
+// Packs
+static void fill_pack(const PackMetadata& m, vsl_pack_info* o, char* name, uint64_t cap) {
+    std::memset(o, 0, sizeof(*o));
+    o->pack_id = m.pack_id;
+    o->type = static_cast<int32_t>(m.type);
+    o->layer_idx = m.layer_idx;
+    o->head_idx = m.head_idx;
+    o->alignment = m.alignment;
+    o->compressed_size = m.compressed_size;
+    o->decompressed_size = m.decompressed_size;
+    o->file_offset = m.file_offset;
+    o->base_priority = m.base_priority;
+    o->tier = -1;
+    o->dtype = -1;
+    o->n_dimensions = m.n_dimensions;
+    if (name && cap) {
+        const size_t n = std::min<size_t>(m.tensor_name.size(), static_cast<size_t>(cap - 1));
+        std::memcpy(name, m.tensor_name.data(), n);
+        name[n] = 0;
+    }
+}
+
+extern "C" int vsl_engine_pack_count(vsl_engine* e, uint64_t* n) {
+    if (!e || !n) return fail(VSL_E_INVALID, "vsl_engine_pack_count: null argument");
+    *n = e->impl->packs().size();
+    return VSL_OK;
+}
+
+extern "C" int vsl_engine_pack(vsl_engine* e, uint64_t idx, vsl_pack_info* out, char* name, uint64_t name_cap) {
+    if (!e || !out) return fail(VSL_E_INVALID, "vsl_engine_pack: null argument");
+    const auto& packs = e->impl->packs();
+    if (idx >= packs.size()) return fail(kErrNotFound, "vsl_engine_pack: index out of range");
+    const ResidentPack& p = packs[idx];
+    fill_pack(p.meta, out, name, name_cap);
+    out->tier = static_cast<int32_t>(p.tier);
+    out->dtype = p.dtype;
+    out->resident_bytes = p.bytes;
+    out->device_ptr = p.device_ptr;
+    return VSL_OK;
+}
+
 // Tokenizer
 struct vsl_tokenizer {
     std::unique_ptr<Tokenizer> impl;
@@ -442,6 +484,20 @@ extern "C" int vsl_gguf_open(const char* path, vsl_gguf** out) {
     auto r = g->impl->load();
     if (!r.has_value()) return fail(r.error(), std::string("vsl_gguf_open: cannot parse ") + path);
     *out = g.release();
+    return VSL_OK;
+}
+
+extern "C" int vsl_gguf_pack_count(vsl_gguf* g, uint64_t* n) {
+    if (!g || !n) return fail(VSL_E_INVALID, "vsl_gguf_pack_count: null argument");
+    *n = g->impl->tensor_count();
+    return VSL_OK;
+}
+
+extern "C" int vsl_gguf_pack(vsl_gguf* g, uint64_t idx, vsl_pack_info* out, char* name, uint64_t name_cap) {
+    if (!g || !out) return fail(VSL_E_INVALID, "vsl_gguf_pack: null argument");
+    const std::vector<PackMetadata> packs = g->impl->generate_packs(g->impl->get_model_config());
+    if (idx >= packs.size()) return fail(kErrNotFound, "vsl_gguf_pack: index out of range");
+    fill_pack(packs[idx], out, name, name_cap);
     return VSL_OK;
 }
 
