@@ -335,6 +335,56 @@ def test_gemm_f16(vsl, dev, H, M, N, K, epi):
     assert rel_err(y, ref) < tol
 
 
+@pytest.mark.parametrize("M,N,K,epi,ax2,cx2", [
+    (512, 14336, 2048, 3, False, False),   # SwiGLU over [Wgate; Wup]: 2 x 112 tiles of 256 x 256
+    (512, 14336, 2048, 3, True, True),     # split A (hi/lo planes) and split output
+    (777, 14336, 1024, 3, True, False),    # ragged M
+    (2048, 6144, 4096, 0, False, False),   # fp32 store
+    (2048, 6144, 4096, 0, True, False),
+    (1024, 12288, 128, 2, False, False),   # residual add; four K stages (one pass over the buffers)
+    (1536, 8192, 256, 1, True, False),     # fp16 store; split A, four stages
+    (2048, 4096, 1024, 2, True, False),    # 128 x 256 tiles (16 x 16 of them), split A
+    (1536, 4096, 512, 3, False, True),     # 128 x 256 tiles, SwiGLU with split output
+])
+def test_gemm_dma(vsl, orc, dev, H, M, N, K, epi, ax2, cx2):
+    """Shapes whose 256 x 256 (or 128 x 256) tiles cover >= 192 CUs run the direct-to-LDS GEMM:
+    sampled rows (the first, the last, and random ones) against a float64 product."""
+    rng = np.random.default_rng(M + N + K + epi + 7 * ax2)
+    nb = 2 * N if epi == 3 else N
+    Af = rng.normal(0, 1, (M, K)).astype(np.float32)
+    B = rng.normal(0, 0.02, (nb, K)).astype(np.float16)
+    if ax2:
+        hi = Af.astype(np.float16)
+        lo = (Af - hi.astype(np.float32)).astype(np.float16)
+        Ad = np.concatenate([hi, lo])
+        Aref = hi.astype(np.float64) + lo.astype(np.float64)
+    else:
+        Ad = Af.astype(np.float16)
+        Aref = Ad.astype(np.float64)
+    if epi == 1:
+        C = dev.empty((M, N), np.float16)
+    elif epi == 3:
+        C = dev.empty(((2 if cx2 else 1) * M, N), np.float16)
+    else:
+        C0 = rng.normal(0, 1, (M, N)).astype(np.float32) if epi == 2 else np.zeros((M, N), np.float32)
+        C = dev.put(C0)
+    flags = (0x100 if ax2 else 0) | (0x200 if cx2 else 0)
+    ok(vsl, H.vsl_gemm_f16(dev.p(dev.put(Ad)), dev.p(dev.put(B)), M, N, K, dev.p(C), epi | flags, None))
+    out = dev.get(C).astype(np.float64)
+    rows = np.unique(np.concatenate([[0, M - 1, M // 2], rng.integers(0, M, 40)]))
+    prod = Aref[rows] @ B.astype(np.float64).T
+    if epi == 3:
+        ref = orc.swiglu(prod[:, :N].astype(np.float32).ravel(), prod[:, N:].astype(np.float32).ravel())
+        ref = ref.reshape(len(rows), N)
+        got = out[rows] + (out[M + rows] if cx2 else 0.0)
+        assert rel_err(got, ref) < (2.0 ** -18 if cx2 else 2.0 ** -9)
+    elif epi == 1:
+        assert rel_err(out[rows], prod) < 2.0 ** -10
+    else:
+        ref = prod + (C0[rows] if epi == 2 else 0.0)
+        assert rel_err(out[rows], ref) < 1e-5
+
+
 def test_gemm_f16_swiglu(vsl, orc, dev, H):
     rng = np.random.default_rng(21)
     M, F, K = 130, 512, 2048

@@ -1,0 +1,359 @@
+// vsl_gemm_dma.hip -- prefill GEMM with direct-to-LDS loads: C[M][N] = A[M][K] * B[N][K]^T on
+// v_mfma_f32_32x32x16_f16, for the shapes whose tiles fill the chip.
+//
+// Pipeline: BK = 32 per stage, four LDS stage buffers (separate __shared__ arrays). Stage s + 3 is
+// requested with global_load_lds_dwordx4 (64 lanes x 16 bytes straight into LDS, no register
+// staging and no ds_write) while stage s is computed; before computing stage s a wave waits for
+// its own loads of that stage (s_waitcnt vmcnt with the two younger stages still in flight) and
+// the block meets at a barrier, after which every wave's part of the stage is in LDS and every
+// wave has finished reading the buffer the next request overwrites. The compiler does not add
+// waits of its own for loads into the other three buffers.
+//
+// Block = 4 waves (2 x 2), block tile BM x BN, wave tile (BM/2) x (BN/2) of 32 x 32 fragments.
+// LDS rows are BK = 32 halfs (64 bytes, four 16-byte chunks); chunk c of row r sits at chunk
+// position c ^ ((r >> 2) & 3) of its row: a fragment read (16 lanes = 16 consecutive rows, one
+// logical chunk) then touches all 16 bank groups of a 256-byte LDS cycle. Since a load instruction
+// writes its 64 lanes' chunks contiguously, the swizzle is applied by choosing which global chunk
+// each lane fetches.
+//
+// With a split A (VSL_DT_F16X2) a stage holds the hi and the lo A tiles and one B tile: both MFMAs
+// of a fragment pair read the same B fragment, and B crosses L2 once (the stage grows from 32 to
+// 48 KB, so two stage buffers instead of four).
+#include <hip/hip_runtime.h>
+
+#include "vsl_device.h"
+#include "vsl_internal.h"
+
+namespace {
+
+constexpr uint32_t kKAlign = 128;  // K granularity: NBUF * BK for every configuration
+constexpr int kThreads = 256;
+
+// 16 bytes per lane from global memory straight into LDS: lane i writes lds + 16 i (lds is
+// wave-uniform). Only the device pass sees the builtin: in the host pass it would invalidate the
+// kernel and drop its launch stub.
+// The source is a wave-uniform base plus a 32-bit per-lane byte offset (the saddr + voffset form,
+// one VGPR per load).
+__device__ __forceinline__ void lds_load16(const vsl_half* base, uint32_t byte_off, vsl_half* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(base) + byte_off, lds, 16, 0, 0);
+#else
+    (void)base;
+    (void)byte_off;
+    (void)lds;
+#endif
+}
+
+// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt not waited)
+#define VSL_VMCNT_WAIT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt not waited)
+#define VSL_LGKM_WAIT0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
+
+// Block tile BM x BN, BK halfs of K per stage, AP planes of A per stage (2: the hi and lo planes of
+// a split A share the stage's B tile), NBUF stage buffers (together at most 128 KB of LDS).
+template <int BM_, int BN_, int BK_, int AP_>
+struct DmaCfg {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, AP = AP_;
+    static constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 32, FN = WN / 32;
+    static constexpr int CPR = BK / 8;                  // 16-byte chunks per tile row
+    static constexpr int ACH = BM * BK / 8 / kThreads;  // 16-byte chunks per thread per stage, per A plane
+    static constexpr int BCH = BN * BK / 8 / kThreads;
+    static constexpr int STAGE = (AP * BM + BN) * BK;   // halfs per stage buffer
+    static constexpr int NBUF = STAGE * 2 * 4 <= 128 * 1024 ? 4 : 2;
+    static constexpr int KS = BK / 16;                  // MFMA k-steps per stage
+    static_assert(STAGE * 2 * NBUF <= 128 * 1024, "stage buffers exceed 128 KB");
+};
+
+__device__ __forceinline__ int d_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
+
+__device__ __forceinline__ void split_f16(float v, vsl_half& hi, vsl_half& lo) {
+    hi = (vsl_half)v;
+    lo = (vsl_half)(v - (float)hi);
+}
+
+// LDS chunk position (16-byte units) of logical chunk c of tile row r. A 256-byte LDS cycle serves
+// 16 lanes of a 16-byte read, i.e. 4 rows of 64 bytes (BK 32) or 2 rows of 128 bytes (BK 64); the
+// chunk index is xor-ed with the row's position among the 16 rows of a fragment read so that those
+// 16 reads fall in distinct bank groups.
+template <int CPR>
+__device__ __forceinline__ int chunk_pos(int r, int c) {
+    if constexpr (CPR == 4) return r * 4 + (c ^ ((r >> 2) & 3));
+    else return r * 8 + (c ^ ((r >> 1) & 7));
+}
+
+template <class G, int EPI, bool AX2, bool CX2>
+__global__ __launch_bounds__(kThreads) void k_gemm_dma(const vsl_half* __restrict__ A, const vsl_half* __restrict__ B,
+                                                       uint32_t M, uint32_t N, uint32_t K, void* __restrict__ C) {
+    constexpr int BM = G::BM, BN = G::BN, BK = G::BK, WM = G::WM, WN = G::WN, FM = G::FM, FN = G::FN;
+    constexpr int ACH = G::ACH, BCH = G::BCH, STAGE = G::STAGE, CPR = G::CPR, NBUF = G::NBUF, KS = G::KS;
+    constexpr int AP = G::AP;
+    static_assert(AP == (AX2 ? 2 : 1), "configuration / plane count mismatch");
+    static_assert(EPI != VSL_EPI_SWIGLU || FN % 2 == 0, "SwiGLU waves pair gate and up fragments");
+    __shared__ __attribute__((aligned(16))) vsl_half L0[STAGE];
+    __shared__ __attribute__((aligned(16))) vsl_half L1[STAGE];
+    __shared__ __attribute__((aligned(16))) vsl_half L2[NBUF > 2 ? STAGE : 8];
+    __shared__ __attribute__((aligned(16))) vsl_half L3[NBUF > 2 ? STAGE : 8];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const uint32_t ncols = EPI == VSL_EPI_SWIGLU ? BN / 2 : BN;
+    const uint32_t n_m = (M + BM - 1) / BM, n_tiles = n_m * (N / ncols);
+    // XCD-aware tile order: workgroups go to the 8 XCDs round-robin by block id; each XCD takes a
+    // contiguous range of tiles, m fastest, so blocks sharing a B tile share an L2
+    const uint32_t b = blockIdx.x, xcd = b & 7, slot = b >> 3, per = (n_tiles + 7) >> 3;
+    const uint32_t t = xcd * per + slot;
+    if (slot >= per || t >= n_tiles) return;
+    const uint32_t mt = t % n_m, nt = t / n_m;
+    const uint32_t m0 = mt * BM, nout0 = nt * ncols;
+
+    // per-thread load sources (byte offsets without the stage's k0): load j of a stage covers
+    // chunk positions j*256 + tid; position P holds row P/CPR and the logical chunk whose swizzled
+    // position is P%CPR (the xor is its own inverse).
+    // Byte offsets fit in 32 bits: rows * K * 2 < 2^32 is checked by the launcher.
+    auto unswz = [](int P, int& r, int& c) {
+        r = P / CPR;
+        c = chunk_pos<CPR>(r, P % CPR) - r * CPR;
+    };
+    uint32_t a_off[ACH], b_off[BCH];
+#pragma unroll
+    for (int j = 0; j < ACH; ++j) {
+        int r, c;
+        unswz(j * kThreads + tid, r, c);
+        const uint32_t gr = m0 + r < M ? m0 + r : M - 1;  // rows past M re-read row M-1 (never stored)
+        a_off[j] = (gr * K + c * 8) * 2;
+    }
+#pragma unroll
+    for (int j = 0; j < BCH; ++j) {
+        int r, c;
+        unswz(j * kThreads + tid, r, c);
+        uint32_t br;
+        if constexpr (EPI == VSL_EPI_SWIGLU) br = r < BN / 2 ? nout0 + r : N + nout0 + (r - BN / 2);
+        else br = nout0 + r;
+        b_off[j] = (br * K + c * 8) * 2;
+    }
+    const uint32_t nst = K / BK;
+    const size_t plane = (size_t)M * K;
+    // stages past the end re-load the last stage into a buffer that is not read again, keeping the
+    // number of loads in flight the same at every wait
+    auto issue = [&](vsl_half* L, uint32_t st) {
+        const uint32_t k0 = (st < nst ? st : nst - 1) * BK;
+        const vsl_half* Bp = B + k0;
+#pragma unroll
+        for (int p = 0; p < AP; ++p) {
+            const vsl_half* Ap = A + p * plane + k0;
+#pragma unroll
+            for (int j = 0; j < ACH; ++j) lds_load16(Ap, a_off[j], L + p * BM * BK + (j * kThreads + wave * 64) * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < BCH; ++j) lds_load16(Bp, b_off[j], L + AP * BM * BK + (j * kThreads + wave * 64) * 8);
+    };
+
+    float16v acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+    // B-tile rows of this wave's fragments; for SwiGLU the first FN/2 are gate rows, the last FN/2
+    // the matching up rows
+    int bt[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        if constexpr (EPI == VSL_EPI_SWIGLU) bt[j] = (j < FN / 2 ? 0 : BN / 2) + wn * (WN / 2) + (j % (FN / 2)) * 32;
+        else bt[j] = wn * WN + j * 32;
+    }
+    struct Frags {
+        half8 a[AP][FM], b[FN];
+    };
+    auto fload = [&](Frags& f, const vsl_half* L, int ks) {
+        const int lc = ks * 2 + (lane >> 5);  // logical chunk of this lane's 8 k-slots
+#pragma unroll
+        for (int p = 0; p < AP; ++p)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                f.a[p][i] = *reinterpret_cast<const half8*>(
+                    L + p * BM * BK + chunk_pos<CPR>(wm * WM + i * 32 + (lane & 31), lc) * 8);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+            f.b[j] = *reinterpret_cast<const half8*>(L + AP * BM * BK + chunk_pos<CPR>(bt[j] + (lane & 31), lc) * 8);
+    };
+    auto mfmas = [&](const Frags& f) {
+#pragma unroll
+        for (int p = 0; p < AP; ++p)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[p][i], f.b[j], acc[i][j], 0, 0, 0);
+    };
+    constexpr int kPerStage = AP * ACH + BCH;  // loads per thread per stage
+    // Stage s in buffer Lc, k-steps 0..KS-1 alternating between the fragment sets f0 / f1; k-step
+    // 0 was requested during the previous stage. Each k-step requests the next one's fragments and
+    // then issues its MFMAs (the reads land meanwhile). Before the last k-step's MFMAs: wait for this
+    // wave's reads (Lc is fully read) and for its loads of stage s+1, meet at the barrier (every
+    // wave has read Lc, every load of stage s+1 is in LDS), request stage s+NBUF into Lc, and
+    // request stage s+1's first k-step from Ln. The stage count is a multiple of NBUF
+    // (K % (NBUF * BK) == 0), so no step is ever skipped.
+    Frags f0, f1;
+    auto step = [&](vsl_half* Lc, const vsl_half* Ln, uint32_t s) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            Frags& cur = (ks & 1) ? f1 : f0;
+            Frags& nxt = (ks & 1) ? f0 : f1;
+            if (ks < KS - 1) {
+                fload(nxt, Lc, ks + 1);
+            } else {
+                VSL_LGKM_WAIT0();
+                VSL_VMCNT_WAIT((NBUF - 2) * kPerStage);
+                __builtin_amdgcn_s_barrier();
+                issue(Lc, s + NBUF);
+                fload(nxt, Ln, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(cur);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    issue(L0, 0);
+    issue(L1, 1);
+    if constexpr (NBUF == 4) {
+        issue(L2, 2);
+        issue(L3, 3);
+    }
+    VSL_VMCNT_WAIT((NBUF - 1) * kPerStage);
+    __builtin_amdgcn_s_barrier();
+    fload(f0, L0, 0);
+    if constexpr (NBUF == 4) {
+        for (uint32_t s = 0; s < nst; s += 4) {
+            step(L0, L1, s);
+            step(L1, L2, s + 1);
+            step(L2, L3, s + 2);
+            step(L3, L0, s + 3);
+        }
+    } else {
+        for (uint32_t s = 0; s < nst; s += 2) {
+            step(L0, L1, s);
+            step(L1, L0, s + 1);
+        }
+    }
+    VSL_VMCNT_WAIT(0);  // the trailing loads land before the block's LDS is released
+
+    // epilogue. Accumulators are read through v_accvgpr_read with an AGPR operand: with 256 of them
+    // live, the epilogue's arithmetic would otherwise have the register allocator place some in
+    // arch VGPRs and spill inside the main loop.
+    auto rd = [](const float16v& a, int v) {
+        float x;
+        asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(x) : "a"(a[v]));
+        return x;
+    };
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const uint32_t row = m0 + wm * WM + i * 32 + d_row(v, lane);
+            if (row >= M) continue;
+            if constexpr (EPI == VSL_EPI_SWIGLU) {
+                vsl_half* Ch = reinterpret_cast<vsl_half*>(C);
+#pragma unroll
+                for (int j = 0; j < FN / 2; ++j) {
+                    const uint32_t col = nout0 + wn * (WN / 2) + j * 32 + (lane & 31);
+                    const float h = silu(rd(acc[i][j], v)) * rd(acc[i][j + FN / 2], v);
+                    if constexpr (CX2) {
+                        vsl_half hi, lo;
+                        split_f16(h, hi, lo);
+                        Ch[(size_t)row * N + col] = hi;
+                        Ch[(size_t)M * N + (size_t)row * N + col] = lo;
+                    } else {
+                        Ch[(size_t)row * N + col] = (vsl_half)h;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const uint32_t col = nout0 + wn * WN + j * 32 + (lane & 31);
+                    const size_t o = (size_t)row * N + col;
+                    const float x = rd(acc[i][j], v);
+                    if constexpr (EPI == VSL_EPI_STORE_F32) reinterpret_cast<float*>(C)[o] = x;
+                    else if constexpr (EPI == VSL_EPI_STORE_F16) reinterpret_cast<vsl_half*>(C)[o] = (vsl_half)x;
+                    else reinterpret_cast<float*>(C)[o] += x;
+                }
+            }
+        }
+    }
+}
+
+template <int BM, int BN>
+struct DmaPair {  // the one-plane and the split-A configuration of a block tile
+    using One = DmaCfg<BM, BN, 32, 1>;
+    using Two = DmaCfg<BM, BN, 32, 2>;
+};
+using DmaBig = DmaPair<256, 256>;
+using DmaMid = DmaPair<128, 256>;
+
+template <class G, int EPI>
+uint32_t dma_tiles(uint32_t M, uint32_t N) {
+    const uint32_t ncols = EPI == VSL_EPI_SWIGLU ? G::BN / 2 : G::BN;
+    return N % ncols ? 0u : ((M + G::BM - 1) / G::BM) * (N / ncols);
+}
+
+template <class P, int EPI>
+void launch_cfg(uint32_t tiles, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N,
+                uint32_t K, void* C, bool ax2, bool cx2) {
+    const uint32_t blocks = ((tiles + 7) / 8) * 8;  // whole XCD ranges
+    using One = typename P::One;
+    using Two = typename P::Two;
+    if (ax2 && cx2) k_gemm_dma<Two, EPI, true, true><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C);
+    else if (ax2) k_gemm_dma<Two, EPI, true, false><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C);
+    else if (cx2) k_gemm_dma<One, EPI, false, true><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C);
+    else k_gemm_dma<One, EPI, false, false><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C);
+}
+
+template <int EPI>
+int launch_epi(int cfg, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N, uint32_t K,
+               void* C, bool ax2, bool cx2) {
+    if (cfg == 0) {
+        const uint32_t t = dma_tiles<DmaBig::One, EPI>(M, N);
+        if (!t) return -1;
+        launch_cfg<DmaBig, EPI>(t, s, a, b, M, N, K, C, ax2, cx2);
+    } else {
+        const uint32_t t = dma_tiles<DmaMid::One, EPI>(M, N);
+        if (!t) return -1;
+        launch_cfg<DmaMid, EPI>(t, s, a, b, M, N, K, C, ax2, cx2);
+    }
+    return 0;
+}
+
+}  // namespace
+
+// Tiles of the direct-to-LDS GEMM for a shape: config 0 is 256 x 256, config 1 is 128 x 256; 0 when
+// the shape does not fit the configuration (N not a multiple of the tile width, K not of 128).
+uint32_t vsl_gemm_dma_tiles(int cfg, uint32_t M, uint32_t N, uint32_t K, int epi) {
+    if (K % kKAlign || K == 0) return 0;
+    const uint64_t brows = epi == VSL_EPI_SWIGLU ? 2ull * N : N;
+    if (((uint64_t)M * K * 2) >> 32 || (brows * K * 2) >> 32) return 0;
+    const bool sw = epi == VSL_EPI_SWIGLU;
+    if (cfg == 0)
+        return sw ? dma_tiles<DmaBig::One, VSL_EPI_SWIGLU>(M, N) : dma_tiles<DmaBig::One, VSL_EPI_STORE_F32>(M, N);
+    return sw ? dma_tiles<DmaMid::One, VSL_EPI_SWIGLU>(M, N) : dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
+}
+
+// Launches the direct-to-LDS GEMM; returns 0, or -1 when the shape does not fit `cfg`.
+int vsl_gemm_dma_launch(int cfg, void* stream, const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K,
+                        void* C, int epi, bool ax2, bool cx2) {
+    if (K % kKAlign || K == 0) return -1;
+    const uint64_t brows = epi == VSL_EPI_SWIGLU ? 2ull * N : N;
+    if (((uint64_t)M * K * 2) >> 32 || (brows * K * 2) >> 32) return -1;  // 32-bit byte offsets
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const vsl_half* a = static_cast<const vsl_half*>(A);
+    const vsl_half* b = static_cast<const vsl_half*>(B);
+    switch (epi) {
+        case VSL_EPI_STORE_F32: return launch_epi<VSL_EPI_STORE_F32>(cfg, s, a, b, M, N, K, C, ax2, false);
+        case VSL_EPI_STORE_F16: return launch_epi<VSL_EPI_STORE_F16>(cfg, s, a, b, M, N, K, C, ax2, false);
+        case VSL_EPI_RESID: return launch_epi<VSL_EPI_RESID>(cfg, s, a, b, M, N, K, C, ax2, false);
+        case VSL_EPI_SWIGLU: return launch_epi<VSL_EPI_SWIGLU>(cfg, s, a, b, M, N, K, C, ax2, cx2);
+        default: return -1;
+    }
+}

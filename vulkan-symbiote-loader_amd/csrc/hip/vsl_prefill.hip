@@ -539,11 +539,20 @@ static uint32_t gemm_tiles(uint32_t M, uint32_t N) {
     return N % ncols ? 0u : ((M + G::BM - 1) / G::BM) * (N / ncols);
 }
 
+constexpr uint32_t kDmaMinTiles = 192;
+
 // Tile configuration by occupancy: the largest tiles that still give every CU a tile.
 template <int EPI>
 static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N, uint32_t K,
                        void* C, bool ax2, bool cx2) {
     auto blocks = [](uint32_t tiles) { return ((tiles + 7) / 8) * 8; };  // whole XCD ranges (tile_of)
+    // shapes whose 256 x 256 (else 128 x 256) tiles cover at least three quarters of the CUs take
+    // the direct-to-LDS kernel
+    for (int cfg = 0; cfg < 2; ++cfg)
+        if (vsl_gemm_dma_tiles(cfg, M, N, K, EPI) >= kDmaMinTiles)
+            return vsl_gemm_dma_launch(cfg, s, a, b, M, N, K, C, EPI, ax2, cx2) == 0
+                       ? VSL_OK
+                       : vsl_invalid("vsl_gemm_f16: shape %ux%ux%u does not fit the direct-to-LDS tiles", M, N, K);
     const uint32_t tb = gemm_tiles<GemmBig, EPI>(M, N), tm = gemm_tiles<GemmMid, EPI>(M, N);
     const uint32_t ts = gemm_tiles<GemmSmall, EPI>(M, N);
     if (tb >= 256) launch_gemm_cfg<GemmBig, EPI>(blocks(tb), s, a, b, M, N, K, C, ax2, cx2);
