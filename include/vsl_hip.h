@@ -254,6 +254,14 @@ enum { VSL_EPI_STORE_F32 = 0, VSL_EPI_STORE_F16 = 1, VSL_EPI_RESID = 2, VSL_EPI_
 enum { VSL_GEMM_A_X2 = 0x100, VSL_GEMM_C_X2 = 0x200 };
 int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
                  void* stream);
+/* The same with an fp32 workspace (16-byte aligned): shapes whose output tiles would leave CUs idle
+ * (e.g. M = 512 against N = 4096) are split over K, the partials summed in a fixed order by a second
+ * launch that applies the epilogue (not for VSL_EPI_SWIGLU).  vsl_gemm_f16_ws_bytes gives the bytes a
+ * shape uses (0: no split, the workspace is not touched); with less than that the call runs
+ * unsplit. */
+int vsl_gemm_f16_ws(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
+                    void* workspace, uint64_t ws_bytes, void* stream);
+uint64_t vsl_gemm_f16_ws_bytes(uint32_t M, uint32_t N, uint32_t K, int epilogue);
 
 /* Q/K/V split of a prefill QKV GEMM output (f32 [S][(n_q+2 n_kv) hd]) with RoPE at positions
  * pos0..pos0+S-1: q -> q_out [S][n_q][hd] (q_dtype VSL_DT_F16 or VSL_DT_F16X2), k/v -> caches at

@@ -385,6 +385,44 @@ def test_gemm_dma(vsl, orc, dev, H, M, N, K, epi, ax2, cx2):
         assert rel_err(out[rows], ref) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K,epi,ax2", [
+    (512, 4096, 14336, 2, True),   # down projection of a 512-row chunk: residual add, split A
+    (512, 6144, 4096, 0, True),    # QKV: fp32 store
+    (512, 4096, 4096, 1, False),   # fp16 store
+    (300, 4096, 2048, 2, False),   # ragged M
+])
+def test_gemm_splitk(vsl, dev, H, M, N, K, epi, ax2):
+    """Narrow shapes through vsl_gemm_f16_ws: split over K into a workspace, reduced in order with the
+    epilogue; a too-small workspace runs unsplit with the same result (to rounding)."""
+    rng = np.random.default_rng(M + N + K + epi)
+    Af = rng.normal(0, 1, (M, K)).astype(np.float32)
+    B = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    if ax2:
+        hi = Af.astype(np.float16)
+        lo = (Af - hi.astype(np.float32)).astype(np.float16)
+        Ad, Aref = np.concatenate([hi, lo]), hi.astype(np.float64) + lo.astype(np.float64)
+    else:
+        Ad = Af.astype(np.float16)
+        Aref = Ad.astype(np.float64)
+    flags = epi | (0x100 if ax2 else 0)
+    need = H.vsl_gemm_f16_ws_bytes(M, N, K, flags)
+    assert need > 0 and need % (4 * M * N) == 0
+    ws = dev.empty((need // 4 + 4,), np.float32)
+    C0 = rng.normal(0, 1, (M, N)).astype(np.float32) if epi == 2 else np.zeros((M, N), np.float32)
+    outs = []
+    for ws_bytes in (need, need - 4):  # the second call runs unsplit
+        C = dev.empty((M, N), np.float16) if epi == 1 else dev.put(C0)
+        ok(vsl, H.vsl_gemm_f16_ws(dev.p(dev.put(Ad)), dev.p(dev.put(B)), M, N, K, dev.p(C), flags, dev.p(ws),
+                                  ws_bytes, None))
+        outs.append(dev.get(C).astype(np.float64))
+    rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, 40)]))
+    ref = Aref[rows] @ B.astype(np.float64).T + (C0[rows] if epi == 2 else 0.0)
+    for out in outs:
+        assert rel_err(out[rows], ref) < (2.0 ** -10 if epi == 1 else 1e-5)
+    # a shape that fills the chip with whole tiles needs no workspace
+    assert H.vsl_gemm_f16_ws_bytes(2048, 6144, 4096, 0) == 0
+
+
 def test_gemm_f16_swiglu(vsl, orc, dev, H):
     rng = np.random.default_rng(21)
     M, F, K = 130, 512, 2048

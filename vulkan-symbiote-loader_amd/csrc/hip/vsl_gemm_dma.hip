@@ -81,9 +81,13 @@ __device__ __forceinline__ int chunk_pos(int r, int c) {
     else return r * 8 + (c ^ ((r >> 1) & 7));
 }
 
-template <class G, int EPI, bool AX2, bool CX2>
+// SK (split K): the block's work item is (k chunk, tile); it multiplies K / ksplit of K and stores
+// the fp32 partial tile to ws[chunk][M][N]; k_splitk_reduce sums the chunks in order and applies the
+// epilogue (SwiGLU is not split).
+template <class G, int EPI, bool AX2, bool CX2, bool SK>
 __global__ __launch_bounds__(kThreads) void k_gemm_dma(const vsl_half* __restrict__ A, const vsl_half* __restrict__ B,
-                                                       uint32_t M, uint32_t N, uint32_t K, void* __restrict__ C) {
+                                                       uint32_t M, uint32_t N, uint32_t K, void* __restrict__ C,
+                                                       float* __restrict__ ws, uint32_t ksplit) {
     constexpr int BM = G::BM, BN = G::BN, BK = G::BK, WM = G::WM, WN = G::WN, FM = G::FM, FN = G::FN;
     constexpr int ACH = G::ACH, BCH = G::BCH, STAGE = G::STAGE, CPR = G::CPR, NBUF = G::NBUF, KS = G::KS;
     constexpr int AP = G::AP;
@@ -97,15 +101,21 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(const vsl_half* __restric
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
+    static_assert(!SK || EPI != VSL_EPI_SWIGLU, "SwiGLU is not split over K");
     const uint32_t ncols = EPI == VSL_EPI_SWIGLU ? BN / 2 : BN;
     const uint32_t n_m = (M + BM - 1) / BM, n_tiles = n_m * (N / ncols);
+    const uint32_t n_items = SK ? n_tiles * ksplit : n_tiles;
     // XCD-aware tile order: workgroups go to the 8 XCDs round-robin by block id; each XCD takes a
-    // contiguous range of tiles, m fastest, so blocks sharing a B tile share an L2
-    const uint32_t b = blockIdx.x, xcd = b & 7, slot = b >> 3, per = (n_tiles + 7) >> 3;
-    const uint32_t t = xcd * per + slot;
-    if (slot >= per || t >= n_tiles) return;
+    // contiguous range of work items, m fastest, so blocks sharing a B tile share an L2
+    const uint32_t b = blockIdx.x, xcd = b & 7, slot = b >> 3, per = (n_items + 7) >> 3;
+    const uint32_t item = xcd * per + slot;
+    if (slot >= per || item >= n_items) return;
+    const uint32_t kc = SK ? item / n_tiles : 0, t = SK ? item % n_tiles : item;
     const uint32_t mt = t % n_m, nt = t / n_m;
     const uint32_t m0 = mt * BM, nout0 = nt * ncols;
+    const uint32_t kspan = SK ? K / ksplit : K;  // K range of this block: [kc * kspan, (kc + 1) * kspan)
+    A += (size_t)kc * kspan;
+    B += (size_t)kc * kspan;
 
     // per-thread load sources (byte offsets without the stage's k0): load j of a stage covers
     // chunk positions j*256 + tid; position P holds row P/CPR and the logical chunk whose swizzled
@@ -132,7 +142,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(const vsl_half* __restric
         else br = nout0 + r;
         b_off[j] = (br * K + c * 8) * 2;
     }
-    const uint32_t nst = K / BK;
+    const uint32_t nst = kspan / BK;
     const size_t plane = (size_t)M * K;
     // stages past the end re-load the last stage into a buffer that is not read again, keeping the
     // number of loads in flight the same at every wait
@@ -255,7 +265,13 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(const vsl_half* __restric
         for (int v = 0; v < 16; ++v) {
             const uint32_t row = m0 + wm * WM + i * 32 + d_row(v, lane);
             if (row >= M) continue;
-            if constexpr (EPI == VSL_EPI_SWIGLU) {
+            if constexpr (SK) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    const uint32_t col = nout0 + wn * WN + j * 32 + (lane & 31);
+                    ws[((size_t)kc * M + row) * N + col] = rd(acc[i][j], v);
+                }
+            } else if constexpr (EPI == VSL_EPI_SWIGLU) {
                 vsl_half* Ch = reinterpret_cast<vsl_half*>(C);
 #pragma unroll
                 for (int j = 0; j < FN / 2; ++j) {
@@ -285,6 +301,26 @@ __global__ __launch_bounds__(kThreads) void k_gemm_dma(const vsl_half* __restric
     }
 }
 
+// C = epilogue(sum over k chunks of ws[chunk]), four consecutive elements per thread, chunks added
+// in order (the result does not depend on scheduling).
+template <int EPI>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, uint32_t ksplit, uint64_t MN,
+                                                       void* __restrict__ C) {
+    const uint64_t e = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (e >= MN) return;
+    float4v sum = *reinterpret_cast<const float4v*>(ws + e);
+    for (uint32_t k = 1; k < ksplit; ++k) sum += *reinterpret_cast<const float4v*>(ws + k * MN + e);
+    if constexpr (EPI == VSL_EPI_STORE_F32) {
+        *reinterpret_cast<float4v*>(static_cast<float*>(C) + e) = sum;
+    } else if constexpr (EPI == VSL_EPI_STORE_F16) {
+        *reinterpret_cast<half4*>(static_cast<vsl_half*>(C) + e) =
+            half4{(vsl_half)sum[0], (vsl_half)sum[1], (vsl_half)sum[2], (vsl_half)sum[3]};
+    } else {
+        float4v* c = reinterpret_cast<float4v*>(static_cast<float*>(C) + e);
+        *c = *c + sum;
+    }
+}
+
 template <int BM, int BN>
 struct DmaPair {  // the one-plane and the split-A configuration of a block tile
     using One = DmaCfg<BM, BN, 32, 1>;
@@ -305,10 +341,23 @@ void launch_cfg(uint32_t tiles, hipStream_t s, const vsl_half* a, const vsl_half
     const uint32_t blocks = ((tiles + 7) / 8) * 8;  // whole XCD ranges
     using One = typename P::One;
     using Two = typename P::Two;
-    if (ax2 && cx2) k_gemm_dma<Two, EPI, true, true><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C);
-    else if (ax2) k_gemm_dma<Two, EPI, true, false><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C);
-    else if (cx2) k_gemm_dma<One, EPI, false, true><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C);
-    else k_gemm_dma<One, EPI, false, false><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C);
+    if (ax2 && cx2) k_gemm_dma<Two, EPI, true, true, false><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+    else if (ax2) k_gemm_dma<Two, EPI, true, false, false><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+    else if (cx2) k_gemm_dma<One, EPI, false, true, false><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+    else k_gemm_dma<One, EPI, false, false, false><<<blocks, kThreads, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+}
+
+// split-K GEMM (partials, the epilogue's type only selects the reduce kernel)
+template <class P>
+void launch_splitk(uint32_t items, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N,
+                   uint32_t K, float* ws, uint32_t ksplit, bool ax2) {
+    const uint32_t blocks = ((items + 7) / 8) * 8;
+    if (ax2)
+        k_gemm_dma<typename P::Two, VSL_EPI_STORE_F32, true, false, true><<<blocks, kThreads, 0, s>>>(
+            a, b, M, N, K, nullptr, ws, ksplit);
+    else
+        k_gemm_dma<typename P::One, VSL_EPI_STORE_F32, false, false, true><<<blocks, kThreads, 0, s>>>(
+            a, b, M, N, K, nullptr, ws, ksplit);
 }
 
 template <int EPI>
@@ -338,6 +387,41 @@ uint32_t vsl_gemm_dma_tiles(int cfg, uint32_t M, uint32_t N, uint32_t K, int epi
     if (cfg == 0)
         return sw ? dma_tiles<DmaBig::One, VSL_EPI_SWIGLU>(M, N) : dma_tiles<DmaBig::One, VSL_EPI_STORE_F32>(M, N);
     return sw ? dma_tiles<DmaMid::One, VSL_EPI_SWIGLU>(M, N) : dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
+}
+
+// Split-K plan for shapes whose tiles leave CUs idle: the 128 x 256 tiling with the smallest split
+// in {2, 4, 8} that gives >= min_items work items and >= 512 of K (whole 128-wide stage groups) per
+// chunk. Returns the split (0: none) and the fp32 workspace bytes it needs.
+uint32_t vsl_gemm_splitk_plan(uint32_t M, uint32_t N, uint32_t K, int epi, uint32_t min_items, uint64_t* ws_bytes) {
+    if (ws_bytes) *ws_bytes = 0;
+    if (epi == VSL_EPI_SWIGLU || N % 4) return 0;
+    const uint32_t tiles = dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
+    if (!tiles || ((uint64_t)M * K * 2) >> 32 || ((uint64_t)N * K * 2) >> 32) return 0;
+    for (uint32_t ks : {2u, 4u, 8u}) {
+        if (K % (ks * kKAlign) || K / ks < 512) continue;
+        if (tiles * ks >= min_items) {
+            if (ws_bytes) *ws_bytes = (uint64_t)ks * M * N * 4;
+            return ks;
+        }
+    }
+    return 0;
+}
+
+int vsl_gemm_splitk_launch(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
+                           uint32_t K, void* C, int epi, bool ax2, float* ws) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint32_t tiles = dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
+    launch_splitk<DmaMid>(tiles * ksplit, s, static_cast<const vsl_half*>(A), static_cast<const vsl_half*>(B), M, N,
+                          K, ws, ksplit, ax2);
+    const uint64_t MN = (uint64_t)M * N;
+    const uint32_t rblocks = (uint32_t)((MN / 4 + 255) / 256);
+    switch (epi) {
+        case VSL_EPI_STORE_F32: k_splitk_reduce<VSL_EPI_STORE_F32><<<rblocks, 256, 0, s>>>(ws, ksplit, MN, C); break;
+        case VSL_EPI_STORE_F16: k_splitk_reduce<VSL_EPI_STORE_F16><<<rblocks, 256, 0, s>>>(ws, ksplit, MN, C); break;
+        case VSL_EPI_RESID: k_splitk_reduce<VSL_EPI_RESID><<<rblocks, 256, 0, s>>>(ws, ksplit, MN, C); break;
+        default: return -1;
+    }
+    return 0;
 }
 
 // Launches the direct-to-LDS GEMM; returns 0, or -1 when the shape does not fit `cfg`.

@@ -544,7 +544,7 @@ constexpr uint32_t kDmaMinTiles = 192;
 // Tile configuration by occupancy: the largest tiles that still give every CU a tile.
 template <int EPI>
 static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N, uint32_t K,
-                       void* C, bool ax2, bool cx2) {
+                       void* C, bool ax2, bool cx2, float* ws, uint64_t ws_bytes) {
     auto blocks = [](uint32_t tiles) { return ((tiles + 7) / 8) * 8; };  // whole XCD ranges (tile_of)
     // shapes whose 256 x 256 (else 128 x 256) tiles cover at least three quarters of the CUs take
     // the direct-to-LDS kernel
@@ -553,6 +553,16 @@ static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint
             return vsl_gemm_dma_launch(cfg, s, a, b, M, N, K, C, EPI, ax2, cx2) == 0
                        ? VSL_OK
                        : vsl_invalid("vsl_gemm_f16: shape %ux%ux%u does not fit the direct-to-LDS tiles", M, N, K);
+    // otherwise, with a workspace, split K over enough blocks
+    if (ws) {
+        uint64_t need = 0;
+        const uint32_t ks = vsl_gemm_splitk_plan(M, N, K, EPI, kDmaMinTiles, &need);
+        if (ks && need <= ws_bytes) {
+            if (vsl_gemm_splitk_launch(ks, s, a, b, M, N, K, C, EPI, ax2, ws))
+                return vsl_invalid("vsl_gemm_f16: split-K epilogue %d", EPI);
+            return VSL_OK;
+        }
+    }
     const uint32_t tb = gemm_tiles<GemmBig, EPI>(M, N), tm = gemm_tiles<GemmMid, EPI>(M, N);
     const uint32_t ts = gemm_tiles<GemmSmall, EPI>(M, N);
     if (tb >= 256) launch_gemm_cfg<GemmBig, EPI>(blocks(tb), s, a, b, M, N, K, C, ax2, cx2);
@@ -562,8 +572,8 @@ static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint
     return VSL_OK;
 }
 
-extern "C" int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
-                            void* stream) {
+static int gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
+                    float* ws, uint64_t ws_bytes, void* stream) {
     if (!A || !B || !C) return vsl_invalid("vsl_gemm_f16: null pointer");
     if (M == 0) return VSL_OK;
     const bool ax2 = (epilogue & VSL_GEMM_A_X2) != 0, cx2 = (epilogue & VSL_GEMM_C_X2) != 0;
@@ -578,15 +588,35 @@ extern "C" int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N
     const vsl_half* b = static_cast<const vsl_half*>(B);
     int rc;
     switch (epi) {
-        case VSL_EPI_STORE_F32: rc = launch_gemm<VSL_EPI_STORE_F32>(s, a, b, M, N, K, C, ax2, false); break;
-        case VSL_EPI_STORE_F16: rc = launch_gemm<VSL_EPI_STORE_F16>(s, a, b, M, N, K, C, ax2, false); break;
-        case VSL_EPI_RESID: rc = launch_gemm<VSL_EPI_RESID>(s, a, b, M, N, K, C, ax2, false); break;
-        case VSL_EPI_SWIGLU: rc = launch_gemm<VSL_EPI_SWIGLU>(s, a, b, M, N, K, C, ax2, cx2); break;
+        case VSL_EPI_STORE_F32: rc = launch_gemm<VSL_EPI_STORE_F32>(s, a, b, M, N, K, C, ax2, false, ws, ws_bytes); break;
+        case VSL_EPI_STORE_F16: rc = launch_gemm<VSL_EPI_STORE_F16>(s, a, b, M, N, K, C, ax2, false, ws, ws_bytes); break;
+        case VSL_EPI_RESID: rc = launch_gemm<VSL_EPI_RESID>(s, a, b, M, N, K, C, ax2, false, ws, ws_bytes); break;
+        case VSL_EPI_SWIGLU: rc = launch_gemm<VSL_EPI_SWIGLU>(s, a, b, M, N, K, C, ax2, cx2, ws, ws_bytes); break;
         default: return vsl_invalid("vsl_gemm_f16: epilogue %d", epi);
     }
     if (rc) return rc;
     HIP_TRY(hipGetLastError());
     return VSL_OK;
+}
+
+extern "C" int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
+                            void* stream) {
+    return gemm_f16(A, B, M, N, K, C, epilogue, nullptr, 0, stream);
+}
+
+extern "C" int vsl_gemm_f16_ws(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C,
+                               int epilogue, void* workspace, uint64_t ws_bytes, void* stream) {
+    if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15))
+        return vsl_invalid("vsl_gemm_f16_ws: workspace must be 16-byte aligned");
+    return gemm_f16(A, B, M, N, K, C, epilogue, static_cast<float*>(workspace), workspace ? ws_bytes : 0, stream);
+}
+
+extern "C" uint64_t vsl_gemm_f16_ws_bytes(uint32_t M, uint32_t N, uint32_t K, int epilogue) {
+    const int epi = epilogue & 0xFF;
+    for (int cfg = 0; cfg < 2; ++cfg)
+        if (vsl_gemm_dma_tiles(cfg, M, N, K, epi) >= kDmaMinTiles) return 0;
+    uint64_t need = 0;
+    return vsl_gemm_splitk_plan(M, N, K, epi, kDmaMinTiles, &need) ? need : 0;
 }
 
 extern "C" int vsl_rope_split_append(const float* qkv, uint32_t S, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t pos0,

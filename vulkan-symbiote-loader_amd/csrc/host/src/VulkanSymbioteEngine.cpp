@@ -352,6 +352,15 @@ void VulkanSymbioteEngine::plan_and_allocate() {
         add(2 * ch * nq * hd * 2, &pq_);
         add(2 * ch * nq * hd * 2, &pattn_);
         add(2 * ch * F * 2, &ph_);
+        // split-K workspace of the narrow prefill GEMMs (QKV, O, down), the largest any chunk size
+        // up to ch needs
+        gws_bytes_ = 0;
+        for (uint32_t S = 1; S <= ch; ++S) {
+            gws_bytes_ = std::max<uint64_t>(gws_bytes_, vsl_gemm_f16_ws_bytes(S, (nq + 2 * nkv) * hd, d, VSL_EPI_STORE_F32));
+            gws_bytes_ = std::max<uint64_t>(gws_bytes_, vsl_gemm_f16_ws_bytes(S, d, nq * hd, VSL_EPI_RESID));
+            gws_bytes_ = std::max<uint64_t>(gws_bytes_, vsl_gemm_f16_ws_bytes(S, d, F, VSL_EPI_RESID));
+        }
+        if (gws_bytes_) add(gws_bytes_, &gws_);
     }
     uint64_t total = (1ull << 20);
     for (auto& r : reqs) total += r.bytes;
@@ -645,7 +654,8 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
         for (uint32_t l = 0; l < c.num_layers; ++l) {
             const Layer& y = layers_[l];
             check(vsl_rmsnorm(px_, y.attn_norm, S, d, eps, pxn_, n1, stream_), "vsl_rmsnorm");
-            check(vsl_gemm_f16(pxn_, y.wqkv, S, (nq + 2 * nkv) * hd, d, pqkv_, g_qkv, stream_), "gemm qkv");
+            check(vsl_gemm_f16_ws(pxn_, y.wqkv, S, (nq + 2 * nkv) * hd, d, pqkv_, g_qkv, gws_, gws_bytes_, stream_),
+                  "gemm qkv");
             check(vsl_rope_split_append(pqkv_, S, nq, nkv, hd, c0, rope_cos_, rope_sin_, pq_, qdt, y.kc, y.vc, kvdt_,
                                         cap_, stream_), "vsl_rope_split_append");
             if (config_.use_sparse_attention)
@@ -656,10 +666,10 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
             else
                 check(vsl_attn_prefill(pq_, qdt, y.kc, y.vc, S, c0, nq, nkv, hd, cap_, scale, pattn_, odt, stream_),
                       "vsl_attn_prefill");
-            check(vsl_gemm_f16(pattn_, y.wo, S, d, nq * hd, px_, g_o, stream_), "gemm o");
+            check(vsl_gemm_f16_ws(pattn_, y.wo, S, d, nq * hd, px_, g_o, gws_, gws_bytes_, stream_), "gemm o");
             check(vsl_rmsnorm(px_, y.ffn_norm, S, d, eps, pxn_, n2, stream_), "vsl_rmsnorm");
             check(vsl_gemm_f16(pxn_, y.wgu, S, F, d, ph_, g_gu, stream_), "gemm gate/up");
-            check(vsl_gemm_f16(ph_, y.wdown, S, d, F, px_, g_dn, stream_), "gemm down");
+            check(vsl_gemm_f16_ws(ph_, y.wdown, S, d, F, px_, g_dn, gws_, gws_bytes_, stream_), "gemm down");
         }
     }
     check(vsl_copy_d2d(x_, px_ + (size_t)(last_rows - 1) * d, (size_t)d * 4, stream_), "last row");

@@ -222,6 +222,8 @@ class VulkanSymbioteEngine {
     uint32_t chunk_ = 0;
     float *px_ = nullptr, *pqkv_ = nullptr;
     void *pxn_ = nullptr, *pq_ = nullptr, *pattn_ = nullptr, *ph_ = nullptr;
+    void* gws_ = nullptr;  // split-K workspace of the prefill GEMMs
+    uint64_t gws_bytes_ = 0;
     // pinned host mirrors
     uint32_t* host_tokens_ = nullptr;
     vsl_ctrl* host_ctrl_ = nullptr;
