@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <type_traits>
 
 #include "vsl_device.h"
 #include "vsl_hip.h"
@@ -64,24 +65,34 @@ __device__ __forceinline__ void lds_barrier() {
 // The block's activation slice lives in registers between its loads and the LDS store, so that
 // the loads can be issued ahead of the first weight tile (vector loads complete in issue order:
 // waiting for the activations then never waits for the weights behind them).
-template <int WAVES>
+template <int WAVES, int XPT>
 struct XStage {
-    static constexpr uint32_t NT = WAVES * 64;
-    static constexpr int XPT = 8;  // float4 per thread: K <= 8192 at 4 waves, K <= 16384 at 8 waves
+    static constexpr uint32_t NT = WAVES * 64;  // XPT float4 per thread: K <= XPT * NT * 4
     float4 xr[XPT];
     float4 gr[XPT];
 
     // Branch-free, with indexes past K clamped to 0: the waits that later consume these registers
     // then count exactly the loads issued after them.
+    // (the gains only when there is a norm; these loads all precede the first weight tile, so a
+    // uniform branch here changes no wait of the weight pipeline)
     __device__ __forceinline__ void load(const float* __restrict__ x, const float* __restrict__ gamma, uint32_t K) {
         const uint32_t tid = threadIdx.x;
-        const float* g = gamma ? gamma : x;
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
             const uint32_t i = (j * NT + tid) * 4;
             const uint32_t ic = i < K ? i : 0;
             xr[j] = *reinterpret_cast<const float4*>(x + ic);
-            gr[j] = *reinterpret_cast<const float4*>(g + ic);
+        }
+        if (gamma) {
+#pragma unroll
+            for (int j = 0; j < XPT; ++j) {
+                const uint32_t i = (j * NT + tid) * 4;
+                const uint32_t ic = i < K ? i : 0;
+                gr[j] = *reinterpret_cast<const float4*>(gamma + ic);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < XPT; ++j) gr[j] = make_float4(1.f, 1.f, 1.f, 1.f);
         }
     }
     // RMS-normalise (rms_norm.comp:24-34) when gamma is given, and store to LDS as fp32
@@ -180,7 +191,7 @@ __device__ void finish_token(uint32_t tok, uint32_t V, uint32_t d, const void* e
 // buffers: tile t+1 is requested before tile t is consumed, so every wave keeps one tile in
 // flight at all times, including across its row-group boundaries. Operands the epilogue reads
 // from memory (residual rows, RoPE angles) are requested together with each tile.
-template <class WT, int R, int U, int EPI, class ET, int WAVES>
+template <class WT, int R, int U, int EPI, class ET, int WAVES, int XPT>
 __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
     __shared__ float red[WAVES];
     __shared__ float bval[WAVES];
@@ -368,11 +379,12 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
 
     // Prologue: activation and gain loads, then the first weight tile, then the control block; the
     // staging, the norm and the control-block latency all complete under the weight fetch.
-    XStage<WAVES> st;
+    XStage<WAVES, XPT> st;
     st.load(a.x, a.gamma, a.K);
     uint4 wa[R][U], wb[R][U];
     float pa[R], pb[R];
     issue_w(wa, 0);
+    issue_w(wb, 1);
     __builtin_amdgcn_sched_barrier(0);
     if (a.ctrl) {
         if (a.ctrl->done) return;
@@ -388,23 +400,29 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
         }
     }
     issue_pf(pa, 0);  // the RoPE angles depend on pos
+    issue_pf(pb, 1);
     st.store(a.gamma, a.eps, a.K, xs, red);
 
     // Straight-line pairs with a single loop exit: the compiler's memory-counter waits merge over
     // every control-flow edge, so a conditional issue, a skipped consume or a mid-loop exit would
-    // leave a buffer's loads pending on some edge and serialise the pipeline. An odd tile count is
-    // padded with one tile past the wave's last group (clamped addresses, no output rows), and the
-    // tile issued by the last pair is never consumed.
-    const uint32_t n_pairs = (n_tiles + 1) / 2;
-    // (sched_barrier: keep each issue ahead of the previous tile's arithmetic in the schedule)
-    for (uint32_t p = 0; p < n_pairs; ++p) {
-        issue(wb, pb, 2 * p + 1);
-        __builtin_amdgcn_sched_barrier(0);
+    // leave a buffer's loads pending on some edge and serialise the pipeline. Both buffers are
+    // requested before the staging, so two tiles are in flight from the start; a buffer is refilled
+    // right after it is consumed, and the last pair (peeled) is consumed without refills, so no
+    // load is outstanding when the wave ends. An odd tile count is padded with one tile past the
+    // wave's last group, and a wave without groups consumes one pair of such tiles (clamped
+    // addresses, no output rows).
+    const uint32_t n_pairs = n_tiles ? (n_tiles + 1) / 2 : 1;
+    // (sched_barrier: keep each issue ahead of the next tile's arithmetic in the schedule)
+    for (uint32_t p = 0; p + 1 < n_pairs; ++p) {
         consume(wa, pa, 2 * p);
         issue(wa, pa, 2 * p + 2);
         __builtin_amdgcn_sched_barrier(0);
         consume(wb, pb, 2 * p + 1);
+        issue(wb, pb, 2 * p + 3);
+        __builtin_amdgcn_sched_barrier(0);
     }
+    consume(wa, pa, 2 * n_pairs - 2);
+    consume(wb, pb, 2 * n_pairs - 1);
 
     if constexpr (EPI == EPI_ARGMAX) {
         // per-block partial argmax; k_argmax_finish reduces the partials in the next launch (a
@@ -456,17 +474,19 @@ __global__ __launch_bounds__(kFinishThreads) void k_argmax_finish(const float* _
     finish_token<ET>(bidx[0], V, d, embed, x_next, tokens, ctrl);
 }
 
-// Upper bound on a decode GEMV's grid: blocks-per-CU x the current device's CU count, 4 by default
-// (16 waves per CU at 4-wave blocks: one resident round), VSL_GEMV_BLOCKS_PER_CU overrides it and
-// 0 removes the bound. A bounded grid strides over the row groups, staging the activation vector
-// once per block instead of once per few groups.
-uint32_t gemv_grid_cap() {
-    static int per_cu = -1;
-    if (per_cu < 0) {
+// Upper bound on a decode GEMV's grid: blocks-per-CU x the current device's CU count, by default the
+// blocks that keep 16 waves per CU (one resident round); VSL_GEMV_BLOCKS_PER_CU overrides it and 0
+// removes the bound. A bounded grid strides over the row groups, staging the activation vector once
+// per block instead of once per few groups.
+uint32_t gemv_grid_cap(int waves) {
+    static int per_cu_env = -2;
+    if (per_cu_env == -2) {
         const char* e = getenv("VSL_GEMV_BLOCKS_PER_CU");
-        per_cu = e ? atoi(e) : 4;
-        if (per_cu < 0) per_cu = 0;
+        per_cu_env = e ? atoi(e) : -1;
+        if (e && per_cu_env < 0) per_cu_env = 0;
     }
+    // default: 16 resident waves per CU
+    const int per_cu = per_cu_env >= 0 ? per_cu_env : (waves >= 16 ? 1 : 16 / waves);
     if (per_cu == 0) return 0xFFFFFFFFu;
     static int cus[64] = {0};
     int dev = 0;
@@ -485,16 +505,29 @@ uint32_t gemv_blocks(uint32_t N, uint32_t max_blocks) {
     const uint32_t groups = (N + RG - 1) / RG;
     uint32_t blocks = (groups + WAVES - 1) / WAVES;
     if (blocks > max_blocks) blocks = max_blocks;
-    const uint32_t cap = gemv_grid_cap();
+    const uint32_t cap = gemv_grid_cap(WAVES);
     if (blocks > cap) blocks = cap;
     return blocks == 0 ? 1 : blocks;
 }
 
+constexpr uint32_t kMaxK = 16384;  // activation vector held in LDS as fp32 (64 KB)
+
+// XPT: float4 of the activation vector staged per thread, the smallest power of two covering K
 template <class WT, int R, int U, int EPI, int WAVES, class ET = WF32>
 int launch_gemv(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
     const uint32_t blocks = gemv_blocks<R, EPI, WAVES>(a.N, max_blocks);
     const size_t lds = (size_t)a.K * sizeof(float);
-    k_gemv_dec<WT, R, U, EPI, ET, WAVES><<<blocks, WAVES * 64, lds, s>>>(a);
+    const uint32_t per = WAVES * 64 * 4;
+    if (a.K <= per)
+        k_gemv_dec<WT, R, U, EPI, ET, WAVES, 1><<<blocks, WAVES * 64, lds, s>>>(a);
+    else if (a.K <= 2 * per)
+        k_gemv_dec<WT, R, U, EPI, ET, WAVES, 2><<<blocks, WAVES * 64, lds, s>>>(a);
+    else if (a.K <= 4 * per)
+        k_gemv_dec<WT, R, U, EPI, ET, WAVES, 4><<<blocks, WAVES * 64, lds, s>>>(a);
+    else if (WAVES * 64 * 4 * 4 < kMaxK && a.K <= 8 * per)
+        k_gemv_dec<WT, R, U, EPI, ET, WAVES, (WAVES * 64 * 4 * 4 < kMaxK ? 8 : 4)><<<blocks, WAVES * 64, lds, s>>>(a);
+    else
+        return vsl_invalid("decode GEMV: K=%u exceeds the %u-wave staging", a.K, (unsigned)WAVES);
     HIP_TRY(hipGetLastError());
     return VSL_OK;
 }
@@ -503,18 +536,40 @@ int launch_gemv(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
 // columns, 8-wave blocks keep 16 waves resident per CU within the 160 KB of LDS.
 constexpr uint32_t kWideK = 8192;
 
+int gemv_waves_env() {
+    static int w = -1;
+    if (w < 0) {
+        const char* e = getenv("VSL_GEMV_WAVES");
+        w = e ? atoi(e) : 0;
+        if (w != 4 && w != 8 && w != 16) w = 0;
+    }
+    return w;
+}
+
 template <class WT, int R, int U, int EPI, class ET = WF32>
 int launch_gemv_k(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
+    switch (gemv_waves_env()) {
+        case 16: return launch_gemv<WT, R, U, EPI, 16, ET>(a, max_blocks, s);
+        case 8: return launch_gemv<WT, R, U, EPI, 8, ET>(a, max_blocks, s);
+        case 4: if (a.K <= kWideK) return launch_gemv<WT, R, U, EPI, 4, ET>(a, max_blocks, s); break;
+        default: break;
+    }
     return a.K > kWideK ? launch_gemv<WT, R, U, EPI, 8, ET>(a, max_blocks, s)
                         : launch_gemv<WT, R, U, EPI, 4, ET>(a, max_blocks, s);
 }
 
 template <int R, int EPI>
 uint32_t gemv_blocks_k(uint32_t N, uint32_t K, uint32_t max_blocks) {
+    // the grid launch_gemv_k chooses
+    switch (gemv_waves_env()) {
+        case 16: return gemv_blocks<R, EPI, 16>(N, max_blocks);
+        case 8: return gemv_blocks<R, EPI, 8>(N, max_blocks);
+        case 4: if (K <= kWideK) return gemv_blocks<R, EPI, 4>(N, max_blocks); break;
+        default: break;
+    }
     return K > kWideK ? gemv_blocks<R, EPI, 8>(N, max_blocks) : gemv_blocks<R, EPI, 4>(N, max_blocks);
 }
 
-constexpr uint32_t kMaxK = 16384;  // activation vector held in LDS as fp32 (64 KB)
 
 int check_gemv_shape(uint32_t N, uint32_t K, const char* who) {
     if (N == 0 || K == 0) return vsl_invalid("%s: empty shape", who);
@@ -528,29 +583,36 @@ int check_gemv_shape(uint32_t N, uint32_t K, const char* who) {
 // ---------------------------------------------------------------------------------------------
 constexpr float kLog2e = 1.4426950408889634f;
 
-// Block (split s, KV head h). Positions are taken in tiles of NSLOT (one position per LPP-lane
-// group); block s owns tiles s, s + nsplit, s + 2 nsplit, ... A block's tile addresses do not
-// depend on the sequence length, so its first tile is requested before the control block is read,
-// and every next tile before the current one is consumed (two register buffers, as in the GEMV).
-// Positions at or past the length are masked by selects; tiles past the cache read position 0.
+// Block (split s, KV head h), WAVES waves. A lane group of LPP lanes holds one position (8 head
+// dims per lane), a wave SLOTS positions, the block NSLOT; a tile is P such rows of the block
+// (P positions per lane, TILE positions), so P x 32 bytes per lane are in flight per tile. Block s
+// owns tiles s, s + nsplit, s + 2 nsplit, ... A block's tile addresses do not depend on the
+// sequence length, so its first two tiles are requested before the control block is read, and
+// every next tile before the current one is consumed (two register buffers, as in the GEMV).
+// Positions at or past the length are masked by selects; their loads read position 0.
 //
 // WIN: the windowed mode. The query at position p attends to every key k <= p while p + 1 <= thr;
 // past that, to the n_glob first keys and the win keys before p (k >= p - win) only. The tiles
 // then run over that set as virtual positions v (v < n_glob -> k = v, else k = v + p - win - n_glob),
 // which depend on p, so the first tiles are requested after the control block is read.
-template <class KT, int HD, int G, bool WIN>
-__global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict__ q, const void* __restrict__ kcache,
-                                                        const void* __restrict__ vcache, uint32_t n_q, uint32_t n_kv,
-                                                        uint32_t cap, float scale, uint32_t nsplit,
-                                                        float* __restrict__ part_o, float* __restrict__ part_ml,
-                                                        vsl_ctrl* ctrl, uint32_t win, uint32_t n_glob, uint32_t thr) {
+//
+// Output: the split's softmax partials per query head, part_ml = (m, l) and part_o = sum_k 2^(s_k - m)
+// v_k (scores in log2 units), merged by k_attn_combine.
+template <class KT, int HD, int G, bool WIN, int WAVES, int P>
+__global__ __launch_bounds__(WAVES * 64) void k_attn_decode(const float* __restrict__ q, const void* __restrict__ kcache,
+                                                            const void* __restrict__ vcache, uint32_t n_q, uint32_t n_kv,
+                                                            uint32_t cap, float scale, uint32_t nsplit,
+                                                            float* __restrict__ part_o, float* __restrict__ part_ml,
+                                                            vsl_ctrl* ctrl, uint32_t win, uint32_t n_glob, uint32_t thr) {
     typedef typename KT::T T;
+    constexpr int NT = WAVES * 64;
     constexpr int LPP = HD / 8;            // lanes per position, 8 elements per lane
-    constexpr int SLOTS = 64 / LPP;        // positions per wave per tile
-    constexpr int NSLOT = kWaves * SLOTS;  // positions per tile
-    constexpr int KW = sizeof(T) * 8 / 16; // 16-byte loads per lane per row (1 fp16, 2 fp32)
-    __shared__ float s_ml[NSLOT][G][2];
-    __shared__ float s_acc[NSLOT][G][HD];
+    constexpr int SLOTS = 64 / LPP;        // positions per wave per row
+    constexpr int NSLOT = WAVES * SLOTS;   // positions per row of the block
+    constexpr uint32_t TILE = NSLOT * P;   // positions per tile
+    constexpr int KW = sizeof(T) * 8 / 16; // 16-byte loads per lane per position (1 fp16, 2 fp32)
+    __shared__ float s_ml[WAVES][G][2];
+    __shared__ float s_acc[WAVES][G][HD];
 
     const uint32_t kvh = blockIdx.y, split = blockIdx.x;
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -560,22 +622,27 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
     const T* Vb = static_cast<const T*>(vcache) + (size_t)kvh * cap * HD;
 
     struct Tile {
-        uint4 k[KW], v[KW];
+        uint4 k[P][KW], v[P][KW];
     };
     uint32_t shift = 0;  // WIN: key position = virtual position + shift past the n_glob first keys
-    auto position = [&](uint32_t j) { return (j * nsplit + split) * NSLOT + wave * SLOTS + slot; };
+    auto position = [&](uint32_t j, int p) {
+        return (j * nsplit + split) * TILE + (uint32_t)p * NSLOT + wave * SLOTS + slot;
+    };
     // positions at or past `limit` read position 0 instead (in bounds, and the same cache lines
     // for every such lane)
     auto issue = [&](Tile& b, uint32_t j, uint32_t limit) {
-        uint32_t t = position(j);
-        t = t < limit ? t : 0;
-        if constexpr (WIN) t = t < n_glob ? t : t + shift;
-        const T* kp = Kb + (size_t)t * HD + sub * 8;
-        const T* vp = Vb + (size_t)t * HD + sub * 8;
 #pragma unroll
-        for (int w = 0; w < KW; ++w) {
-            b.k[w] = load16<false>(kp + w * (8 / KW));
-            b.v[w] = load16<false>(vp + w * (8 / KW));
+        for (int p = 0; p < P; ++p) {
+            uint32_t t = position(j, p);
+            t = t < limit ? t : 0;
+            if constexpr (WIN) t = t < n_glob ? t : t + shift;
+            const T* kp = Kb + (size_t)t * HD + sub * 8;
+            const T* vp = Vb + (size_t)t * HD + sub * 8;
+#pragma unroll
+            for (int w = 0; w < KW; ++w) {
+                b.k[p][w] = load16<false>(kp + w * (8 / KW));
+                b.v[p][w] = load16<false>(vp + w * (8 / KW));
+            }
         }
     };
 
@@ -627,76 +694,121 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
         for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
     }
 
+    // Per tile: the P scores of every head (DPP sums over the position's lane group), one running
+    // maximum update and one rescale of the accumulators, then the P weighted values.
     auto consume = [&](const Tile& b, uint32_t j) {
-        const bool valid = position(j) < n_att;
-        float kf[8], vf[8];
-        if constexpr (KW == 1) {
-            unpack(b.k[0], KT(), kf);
-            unpack(b.v[0], KT(), vf);
-        } else {
-            unpack(b.k[0], KT(), kf);
-            unpack(b.k[1], KT(), kf + 4);
-            unpack(b.v[0], KT(), vf);
-            unpack(b.v[1], KT(), vf + 4);
+        float kf[P][8], vf[P][8];
+        bool valid[P];
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            valid[p] = position(j, p) < n_att;
+            if constexpr (KW == 1) {
+                unpack(b.k[p][0], KT(), kf[p]);
+                unpack(b.v[p][0], KT(), vf[p]);
+            } else {
+                unpack(b.k[p][0], KT(), kf[p]);
+                unpack(b.k[p][1], KT(), kf[p] + 4);
+                unpack(b.v[p][0], KT(), vf[p]);
+                unpack(b.v[p][1], KT(), vf[p] + 4);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vf[p][i] = valid[p] ? vf[p][i] : 0.f;  // cache memory past len is arbitrary
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vf[i] = valid ? vf[i] : 0.f;  // cache memory past len is arbitrary
-#pragma unroll
         for (int g = 0; g < G; ++g) {
-            float sc = 0.f;
+            float sc[P];
+            float mt = m[g];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) sc = fmaf(qv[g][i], kf[i], sc);
-            sc = group_sum<LPP>(sc);
-            const float mn = valid ? fmaxf(m[g], sc) : m[g];
-            const float corr = valid ? exp2f(m[g] - mn) : 1.f;
-            const float p = valid ? exp2f(sc - mn) : 0.f;
-            l[g] = l[g] * corr + p;
+            for (int p = 0; p < P; ++p) {
+                float d = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[i], acc[g][i] * corr);
-            m[g] = mn;
+                for (int i = 0; i < 8; ++i) d = fmaf(qv[g][i], kf[p][i], d);
+                sc[p] = group_sum_dpp<LPP>(d);
+                mt = valid[p] ? fmaxf(mt, sc[p]) : mt;
+            }
+            // m = -inf: 0 (nothing accumulated yet); no valid key so far: keep (mt - mt would be NaN)
+            const float corr = mt == -INFINITY ? 1.f : fast_exp2(m[g] - mt);
+            float ls = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[g][i] *= corr;
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const float pr = valid[p] ? fast_exp2(sc[p] - mt) : 0.f;
+                ls += pr;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(pr, vf[p][i], acc[g][i]);
+            }
+            l[g] = fmaf(l[g], corr, ls);
+            m[g] = mt;
         }
     };
 
-    consume(ta, 0);
-    issue(ta, 2, n_att);
-    __builtin_amdgcn_sched_barrier(0);
-    consume(tb, 1);
-    const uint32_t total = (n_att + NSLOT - 1) / NSLOT;  // tiles holding positions < n_att
+    const uint32_t total = (n_att + TILE - 1) / TILE;  // tiles holding positions < n_att
     const uint32_t mine = total > split ? (total - 1 - split) / nsplit + 1 : 0;
-    // tiles 2 .. mine-1 in pairs with a single loop exit (an odd remainder is padded with one
-    // masked tile); the tile issued by the last pair is never consumed
-    const uint32_t n_pairs = mine > 2 ? (mine - 1) / 2 : 0;
-    for (uint32_t pp = 0; pp < n_pairs; ++pp) {
+    // pairs with a single loop exit, each buffer refilled right after it is consumed; the last pair
+    // (peeled) is consumed without refills so that no load is outstanding past it (tiles past the
+    // block's own are masked: their positions are >= n_att)
+    const uint32_t n_pairs = mine ? (mine + 1) / 2 : 1;
+    for (uint32_t pp = 0; pp + 1 < n_pairs; ++pp) {
+        consume(ta, 2 * pp);
+        issue(ta, 2 * pp + 2, n_att);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(tb, 2 * pp + 1);
         issue(tb, 2 * pp + 3, n_att);
         __builtin_amdgcn_sched_barrier(0);
-        consume(ta, 2 * pp + 2);
-        issue(ta, 2 * pp + 4, n_att);
-        __builtin_amdgcn_sched_barrier(0);
-        consume(tb, 2 * pp + 3);
     }
+    consume(ta, 2 * n_pairs - 2);
+    consume(tb, 2 * n_pairs - 1);
 
-    // per-slot partials -> LDS -> block combine
-    const uint32_t sl = wave * SLOTS + slot;
+    // merge the wave's SLOTS position groups (lanes sub + LPP * slot hold the same dims): pairs of
+    // lanes at distances LPP .. 32, merged symmetrically so that both lanes of a pair agree
+    auto merge_pairs = [&](auto xc) {
+        constexpr int X = decltype(xc)::value;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        if (sub == 0) {
-            s_ml[sl][g][0] = m[g];
-            s_ml[sl][g][1] = l[g];
+        for (int g = 0; g < G; ++g) {
+            float ma, mb, la, lb;
+            lane_pair<X>(m[g], ma, mb);
+            lane_pair<X>(l[g], la, lb);
+            const float M = fmaxf(ma, mb);
+            const float fa = ma == -INFINITY ? 0.f : fast_exp2(ma - M);
+            const float fb = mb == -INFINITY ? 0.f : fast_exp2(mb - M);
+            l[g] = la * fa + lb * fb;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float aa, ab;
+                lane_pair<X>(acc[g][i], aa, ab);
+                acc[g][i] = aa * fa + ab * fb;
+            }
+            m[g] = M;
         }
+    };
+    if constexpr (LPP == 8) merge_pairs(std::integral_constant<int, 8>());
+    merge_pairs(std::integral_constant<int, 16>());
+    merge_pairs(std::integral_constant<int, 32>());
+    if (slot == 0) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s_acc[sl][g][sub * 8 + i] = acc[g][i];
+        for (int g = 0; g < G; ++g) {
+            if (sub == 0) {
+                s_ml[wave][g][0] = m[g];
+                s_ml[wave][g][1] = l[g];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s_acc[wave][g][sub * 8 + i] = acc[g][i];
+        }
     }
-    lds_barrier();  // (no wait on the unconsumed tile's loads)
-    for (uint32_t e = threadIdx.x; e < (uint32_t)(G * HD); e += kBlock) {
+    lds_barrier();
+    for (uint32_t e = threadIdx.x; e < (uint32_t)(G * HD); e += NT) {
         const uint32_t g = e / HD, dd = e % HD;
         float M = -INFINITY;
-        for (int s = 0; s < NSLOT; ++s) M = fmaxf(M, s_ml[s][g][0]);
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, s_ml[w][g][0]);
         float L = 0.f, A = 0.f;
         if (M != -INFINITY) {
-            for (int s = 0; s < NSLOT; ++s) {
-                const float f = exp2f(s_ml[s][g][0] - M);
-                L += s_ml[s][g][1] * f;
-                A += s_acc[s][g][dd] * f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                const float f = exp2f(s_ml[w][g][0] - M);
+                L += s_ml[w][g][1] * f;
+                A += s_acc[w][g][dd] * f;
             }
         }
         const size_t pidx = (size_t)(h0 + g) * nsplit + split;
@@ -707,13 +819,6 @@ __global__ __launch_bounds__(kBlock) void k_attn_decode(const float* __restrict_
                 part_ml[pidx * 2 + 1] = L;
             }
         }
-    }
-    // The padding tile's registers stay allocated to the end: reused earlier, they would make the
-    // combine above wait for those (discarded) loads.
-#pragma unroll
-    for (int w = 0; w < KW; ++w) {
-        asm volatile("" ::"v"(ta.k[w].x), "v"(ta.k[w].y), "v"(ta.k[w].z), "v"(ta.k[w].w));
-        asm volatile("" ::"v"(ta.v[w].x), "v"(ta.v[w].y), "v"(ta.v[w].z), "v"(ta.v[w].w));
     }
 }
 
@@ -818,16 +923,40 @@ struct AttnWindow {
     uint32_t win, n_glob, thr;
 };
 
+// Launch shape of k_attn_decode (waves per block, positions per lane per tile); VSL_ATTN_SHAPE picks
+// another for measurements: 1 = 4 x 2, 2 = 8 x 1, 3 = 8 x 2 (dense attention only).
+int attn_shape_env() {
+    static int cfg = -1;
+    if (cfg < 0) {
+        const char* e = getenv("VSL_ATTN_SHAPE");
+        cfg = e ? atoi(e) : 0;
+        if (cfg < 0 || cfg > 3) cfg = 0;
+    }
+    return cfg;
+}
+
+template <class KT, int HD, int G, bool WIN, int WAVES, int P>
+void launch_attn_shape(dim3 grid, hipStream_t s, const float* q, const void* kc, const void* vc, uint32_t n_q,
+                       uint32_t n_kv, uint32_t cap, float scale, uint32_t nsplit, float* po, float* pml,
+                       vsl_ctrl* ctrl, const AttnWindow& w) {
+    k_attn_decode<KT, HD, G, WIN, WAVES, P><<<grid, WAVES * 64, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po,
+                                                                        pml, ctrl, w.win, w.n_glob, w.thr);
+}
+
 template <class KT, int HD, int G>
 void launch_attn_w(dim3 grid, hipStream_t s, const float* q, const void* kc, const void* vc, uint32_t n_q,
                    uint32_t n_kv, uint32_t cap, float scale, uint32_t nsplit, float* po, float* pml, vsl_ctrl* ctrl,
                    const AttnWindow& w) {
-    if (w.on)
-        k_attn_decode<KT, HD, G, true><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl,
-                                                               w.win, w.n_glob, w.thr);
-    else
-        k_attn_decode<KT, HD, G, false><<<grid, kBlock, 0, s>>>(q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl,
-                                                                0, 0, 0);
+    if (w.on) {
+        launch_attn_shape<KT, HD, G, true, 4, 1>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w);
+        return;
+    }
+    switch (attn_shape_env()) {
+        case 1: launch_attn_shape<KT, HD, G, false, 4, 2>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+        case 2: launch_attn_shape<KT, HD, G, false, 8, 1>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+        case 3: launch_attn_shape<KT, HD, G, false, 8, 2>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+        default: launch_attn_shape<KT, HD, G, false, 4, 1>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+    }
 }
 
 template <class KT, int HD>

@@ -70,6 +70,43 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 }
 #undef VSL_DPP_F
 
+// Sum across aligned groups of W = 8 or 16 lanes with DPP row operations (VALU only, every lane of
+// the group ends with the sum): quad sums by quad_perm, then the other quad of the half row by
+// row_half_mirror (lane i <- 7 - i), then the other half row by row_mirror (lane i <- 15 - i).
+template <int W>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+    static_assert(W == 8 || W == 16, "DPP group sums over 8 or 16 lanes");
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));   // [1,0,3,2]
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));   // [2,3,0,1]
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));  // half mirror
+    if constexpr (W == 16)
+        v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));  // mirror
+    return v;
+}
+
+// The values of lanes i and i ^ X for X = 8 (row_ror:8 within a 16-lane row), 16 (v_permlane16_swap)
+// or 32 (v_permlane32_swap), as an (a, b) pair that is the same in both lanes (a: the lane with the
+// X bit clear). VALU only.
+template <int X>
+__device__ __forceinline__ void lane_pair(float v, float& a, float& b) {
+    static_assert(X == 8 || X == 16 || X == 32, "lane pairs at distance 8, 16 or 32");
+    if constexpr (X == 8) {
+        const float o = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+        const bool lo = (threadIdx.x & 8) == 0;
+        a = lo ? v : o;
+        b = lo ? o : v;
+    } else {
+        const uint32_t u = __float_as_uint(v);
+        const auto r = X == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                               : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        a = __uint_as_float(r[0]);
+        b = __uint_as_float(r[1]);
+    }
+}
+
+// 2^x by the hardware instruction (no denormal rescaling: results below 2^-126 flush to 0)
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // Sum across aligned groups of `W` lanes (W a power of two <= 64).
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
