@@ -923,17 +923,10 @@ struct AttnWindow {
     uint32_t win, n_glob, thr;
 };
 
-// Launch shape of k_attn_decode (waves per block, positions per lane per tile); VSL_ATTN_SHAPE picks
-// another for measurements: 1 = 4 x 2, 2 = 8 x 1, 3 = 8 x 2 (dense attention only).
-int attn_shape_env() {
-    static int cfg = -1;
-    if (cfg < 0) {
-        const char* e = getenv("VSL_ATTN_SHAPE");
-        cfg = e ? atoi(e) : 0;
-        if (cfg < 0 || cfg > 3) cfg = 0;
-    }
-    return cfg;
-}
+// Launch shape of k_attn_decode: 4 waves, one position per lane per tile (measured on the 8B
+// workload against 4 x 2, 8 x 1 and 8 x 2 at 1K and 8K context: more positions per block lengthen
+// the per-block latency chain more than they save in block count).
+constexpr int kAttnWaves = 4, kAttnP = 1;
 
 template <class KT, int HD, int G, bool WIN, int WAVES, int P>
 void launch_attn_shape(dim3 grid, hipStream_t s, const float* q, const void* kc, const void* vc, uint32_t n_q,
@@ -947,16 +940,12 @@ template <class KT, int HD, int G>
 void launch_attn_w(dim3 grid, hipStream_t s, const float* q, const void* kc, const void* vc, uint32_t n_q,
                    uint32_t n_kv, uint32_t cap, float scale, uint32_t nsplit, float* po, float* pml, vsl_ctrl* ctrl,
                    const AttnWindow& w) {
-    if (w.on) {
-        launch_attn_shape<KT, HD, G, true, 4, 1>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w);
-        return;
-    }
-    switch (attn_shape_env()) {
-        case 1: launch_attn_shape<KT, HD, G, false, 4, 2>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
-        case 2: launch_attn_shape<KT, HD, G, false, 8, 1>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
-        case 3: launch_attn_shape<KT, HD, G, false, 8, 2>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
-        default: launch_attn_shape<KT, HD, G, false, 4, 1>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
-    }
+    if (w.on)
+        launch_attn_shape<KT, HD, G, true, kAttnWaves, kAttnP>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml,
+                                                               ctrl, w);
+    else
+        launch_attn_shape<KT, HD, G, false, kAttnWaves, kAttnP>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po,
+                                                                pml, ctrl, w);
 }
 
 template <class KT, int HD>
