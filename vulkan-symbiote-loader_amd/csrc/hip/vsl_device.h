@@ -34,6 +34,45 @@ __device__ __forceinline__ uint4 load16(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16 bytes per lane from global memory straight into LDS: lane i writes lds + 16 i (lds is
+// wave-uniform). Only the device pass sees the builtin: in the host pass it would invalidate the
+// kernel and drop its launch stub.
+// The source is a wave-uniform base plus a 32-bit per-lane byte offset (the saddr + voffset form,
+// one VGPR per load).
+__device__ __forceinline__ void lds_load16(const vsl_half* base, uint32_t byte_off, vsl_half* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(base) + byte_off, lds, 16, 0, 0);
+#else
+    (void)base;
+    (void)byte_off;
+    (void)lds;
+#endif
+}
+
+// LDS transpose read (ds_read_b64_tr_b16): within each group of 16 lanes, lane i receives as its
+// value j element i%4 of the four 16-bit values at the address given by lane 4j + i/4 of the group
+// (layout measured on gfx950). p must point into LDS, 8-byte aligned.
+__device__ __forceinline__ half4 lds_read_tr16(const vsl_half* p) {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    const s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p));
+    return __builtin_bit_cast(half4, v);
+}
+
+// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt not waited)
+#define VSL_VMCNT_WAIT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt not waited)
+#define VSL_LGKM_WAIT0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
+
+// hi/lo split of an fp32 value into two binary16 values (hi + lo carries ~22 significant bits).
+// hi passes through an empty register asm: stored and subtracted, it is then the same rounded value
+// (the backend otherwise may pack the stored hi with a second conversion of v whose rounding need
+// not match the one lo was derived from, measured as one fp16 ulp of error in vector stores).
+__device__ __forceinline__ void split_f16(float v, vsl_half& hi, vsl_half& lo) {
+    hi = (vsl_half)v;
+    asm volatile("" : "+v"(hi));
+    lo = (vsl_half)(v - (float)hi);
+}
+
 // Unpack a 16-byte vector of weights into fp32 values.
 __device__ __forceinline__ void unpack(const uint4& v, WF16, float* out) {
     const half8 h = __builtin_bit_cast(half8, v);

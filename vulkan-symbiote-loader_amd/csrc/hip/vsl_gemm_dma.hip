@@ -29,26 +29,6 @@ namespace {
 constexpr uint32_t kKAlign = 128;  // K granularity: NBUF * BK for every configuration
 constexpr int kThreads = 256;
 
-// 16 bytes per lane from global memory straight into LDS: lane i writes lds + 16 i (lds is
-// wave-uniform). Only the device pass sees the builtin: in the host pass it would invalidate the
-// kernel and drop its launch stub.
-// The source is a wave-uniform base plus a 32-bit per-lane byte offset (the saddr + voffset form,
-// one VGPR per load).
-__device__ __forceinline__ void lds_load16(const vsl_half* base, uint32_t byte_off, vsl_half* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(base) + byte_off, lds, 16, 0, 0);
-#else
-    (void)base;
-    (void)byte_off;
-    (void)lds;
-#endif
-}
-
-// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt not waited)
-#define VSL_VMCNT_WAIT(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14))
-// s_waitcnt lgkmcnt(0) (vmcnt and expcnt not waited)
-#define VSL_LGKM_WAIT0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
-
 // Block tile BM x BN, BK halfs of K per stage, AP planes of A per stage (2: the hi and lo planes of
 // a split A share the stage's B tile), NBUF stage buffers (together at most 128 KB of LDS).
 template <int BM_, int BN_, int BK_, int AP_>
@@ -65,11 +45,6 @@ struct DmaCfg {
 };
 
 __device__ __forceinline__ int d_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
-
-__device__ __forceinline__ void split_f16(float v, vsl_half& hi, vsl_half& lo) {
-    hi = (vsl_half)v;
-    lo = (vsl_half)(v - (float)hi);
-}
 
 // LDS chunk position (16-byte units) of logical chunk c of tile row r. A 256-byte LDS cycle serves
 // 16 lanes of a 16-byte read, i.e. 4 rows of 64 bytes (BK 32) or 2 rows of 128 bytes (BK 64); the

@@ -44,12 +44,6 @@ using GemmSmall = GemmCfg<64, 128, 2, 2>;
 
 __device__ __forceinline__ int d_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
 
-// hi/lo split of an fp32 value into two binary16 values (hi + lo carries ~22 significant bits)
-__device__ __forceinline__ void split_f16(float v, vsl_half& hi, vsl_half& lo) {
-    hi = (vsl_half)v;
-    lo = (vsl_half)(v - (float)hi);
-}
-
 // LDS tiles are unpadded rows of BK halfs (128 bytes). gfx950's LDS serves 256 bytes (64 banks)
 // per cycle, i.e. 16 lanes of a 16-byte access: two rows. The 16-byte chunk c of row r is stored at
 // chunk position c ^ ((r >> 1) & 7): a fragment read (16 consecutive lanes = 16 consecutive rows,
@@ -310,11 +304,13 @@ __global__ void k_rope_split(const float* __restrict__ qkv, uint32_t S, uint32_t
 // causal flash attention (prefill), fp16 in / fp16 out, fp32 softmax statistics
 // ---------------------------------------------------------------------------------------------
 // Causal flash attention for one chunk of S prompt rows at positions pos0.. (their K/V already in
-// the cache). Block = the G query heads of one KV head x 32 query rows, one wave per head: the
-// block stages each 64-position K/V tile in LDS once for all G heads (K row-major, swizzled; V
-// transposed so V^T is an MFMA A operand), one tile ahead in registers. Per tile each wave computes
-// S^T = K Q^T (two 32-position fragments), the online softmax of its 32 query rows (each lane owns
-// one row's statistics with its partner lane l^32), and O^T += V^T P^T.
+// the cache). Block = the G query heads of one KV head x 32 query rows, one wave per head: each
+// 64-position K/V tile is copied once for all G heads straight from the cache into LDS
+// (global_load_lds, two tile buffers, the next tile requested before the current one is computed),
+// both row-major with the chunk swizzle of ksw. Per tile each wave computes S^T = K Q^T (two
+// 32-position fragments), the online softmax of its 32 query rows (each lane owns one row's
+// statistics with its partner lane l^32), and O^T += V^T P^T, whose V^T operand is gathered from
+// the row-major V tile (eight 2-byte reads per fragment, spread over the banks by the swizzle).
 constexpr int kAttnTile = 64;  // KV positions per tile
 
 template <int HD>
@@ -331,14 +327,13 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
                                                          uint32_t thr) {
     constexpr int TK = kAttnTile;
     constexpr int NT = 64 * G;
-    constexpr int VTS = TK + 8;                 // halfs per V^T row (one head dim)
     constexpr int CPR = HD / 8;                 // 16-byte chunks per K/V row
     constexpr int NCH = TK * CPR / NT;          // chunks per thread per tile (K and V each)
     constexpr int QP = QX2 ? 2 : 1;             // q planes; with split q the probabilities are split too
-    static_assert(NCH >= 1, "tile too small for the block");
+    static_assert(NCH >= 1 && TK * CPR % NT == 0, "tile does not divide over the block");
     __shared__ __attribute__((aligned(16))) vsl_half Ks[2][TK * HD];
-    __shared__ __attribute__((aligned(16))) vsl_half Vt[2][HD * VTS];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ __attribute__((aligned(16))) vsl_half Vs[2][TK * HD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n_qb = gridDim.x;
     const uint32_t qb = n_qb - 1 - blockIdx.x;  // the longest (latest) query blocks start first
     const uint32_t kvh = blockIdx.y;
@@ -369,31 +364,25 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     const vsl_half* Kb = kc + (size_t)kvh * cap * HD;
     const vsl_half* Vb = vc + (size_t)kvh * cap * HD;
 
-    // tile staging: chunk e of a tile is (position e / CPR, dims 8 * (e % CPR)); positions past
-    // kv_end read position 0 (in bounds) and their V is zeroed in LDS
-    struct Stage {
-        uint4 k[NCH], v[NCH];
-    };
-    auto gload = [&](Stage& st, uint32_t t) {
+    // Tile copy: LDS chunk position P = i * NT + tid holds row P / CPR and the logical chunk whose
+    // swizzled position is P % CPR (the swizzle is an xor, its own inverse). Positions past kv_end
+    // copy position 0 (in bounds; finite values whose probabilities are 0).
+    uint32_t roff[NCH];  // byte offset of the chunk within a tile, without the tile's first row
+    int rrow[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const int P = i * NT + tid, r = P / CPR;
+        const int c = (ksw<HD>(r, P % CPR) - r * HD) / 8;
+        rrow[i] = r;
+        roff[i] = (uint32_t)(c * 8 * 2);
+    }
+    auto issue = [&](int buf, uint32_t t) {
 #pragma unroll
         for (int i = 0; i < NCH; ++i) {
-            const int e = tid + i * NT, r = e / CPR, c = e % CPR;
-            const uint32_t pos = t * TK + r;
-            const size_t off = (size_t)(pos < kv_end ? pos : 0) * HD + c * 8;
-            st.k[i] = *reinterpret_cast<const uint4*>(Kb + off);
-            st.v[i] = *reinterpret_cast<const uint4*>(Vb + off);
-        }
-    };
-    auto sstore = [&](const Stage& st, int buf, uint32_t t) {
-#pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            const int e = tid + i * NT, r = e / CPR, c = e % CPR;
-            *reinterpret_cast<uint4*>(&Ks[buf][ksw<HD>(r, c)]) = st.k[i];
-            const uint32_t m = t * TK + r < kv_end ? 0xFFFFFFFFu : 0u;
-            const uint4 vm = make_uint4(st.v[i].x & m, st.v[i].y & m, st.v[i].z & m, st.v[i].w & m);
-            const half8 vh = __builtin_bit_cast(half8, vm);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) Vt[buf][(c * 8 + j) * VTS + r] = vh[j];
+            const uint32_t pos = t * TK + rrow[i];
+            const uint32_t off = (pos < kv_end ? pos : 0u) * (HD * 2) + roff[i];
+            lds_load16(Kb, off, &Ks[buf][(i * NT + wave * 64) * 8]);
+            lds_load16(Vb, off, &Vs[buf][(i * NT + wave * 64) * 8]);
         }
     };
 
@@ -414,6 +403,11 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
         for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
     float m = -INFINITY, l = 0.f;
 
+    // Lazy rescaling: m is the reference maximum of this lane's row (probabilities are taken as
+    // 2^(score - m)); it is raised, and the accumulators rescaled, only when a tile's maximum exceeds
+    // it by more than kLazy (log2 units) in some lane of the wave, so every probability stays below
+    // 2^kLazy and most tiles skip the rescale. The quotient O / l does not depend on m.
+    constexpr float kLazy = 8.f;
     auto compute = [&](int buf, uint32_t t) {
         // S^T[kv][q] = sum_d K[kv][d] Q[q][d] for the tile's two 32-position halves
         float16v st[2];
@@ -421,35 +415,54 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) st[kb][v] = 0.f;
+            half8 kf[HD / 16];
 #pragma unroll
-            for (int c = 0; c < HD / 16; ++c) {
-                const half8 kf = *reinterpret_cast<const half8*>(&Ks[buf][ksw<HD>(kb * 32 + (lane & 31), 2 * c + (lane >> 5))]);
+            for (int c = 0; c < HD / 16; ++c)
+                kf[c] = *reinterpret_cast<const half8*>(&Ks[buf][ksw<HD>(kb * 32 + (lane & 31), 2 * c + (lane >> 5))]);
 #pragma unroll
-                for (int p = 0; p < QP; ++p) st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[p][c], st[kb], 0, 0, 0);
-            }
+            for (int c = 0; c < HD / 16; ++c)
+#pragma unroll
+                for (int p = 0; p < QP; ++p) st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[p][c], st[kb], 0, 0, 0);
         }
-        // causal mask + online softmax over this lane's 32 values of its query row
+        // causal (and window) mask, only on tiles that reach past the block's first row
+        const bool full = !WIN && t * TK + TK - 1 <= p_first;
         float bm = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const uint32_t kvp = t * TK + kb * 32 + d_row(v, lane);
-                const bool seen = WIN ? kvp <= my_pos && (kvp >= my_lo || kvp < n_glob) : kvp <= my_pos;
-                const float sc = seen ? st[kb][v] * sl2 : -INFINITY;
+                float sc = st[kb][v] * sl2;
+                if (!full) {
+                    const uint32_t kvp = t * TK + kb * 32 + d_row(v, lane);
+                    const bool seen = WIN ? kvp <= my_pos && (kvp >= my_lo || kvp < n_glob) : kvp <= my_pos;
+                    sc = seen ? sc : -INFINITY;
+                }
                 st[kb][v] = sc;
                 bm = fmaxf(bm, sc);
             }
-        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-        const float mn = fmaxf(m, bm);
-        const float corr = (mn == -INFINITY) ? 1.f : exp2f(m - mn);
+        {
+            float ba, bb;
+            lane_pair<32>(bm, ba, bb);
+            bm = fmaxf(ba, bb);
+        }
+        const bool raise = bm > m + kLazy;  // m = -inf: any finite tile maximum raises it
+        if (__builtin_amdgcn_ballot_w64(raise)) {
+            const float mn = raise ? bm : m;
+            const float corr = mn == -INFINITY ? 1.f : fast_exp2(m - mn);  // m = -inf: 0
+            l *= corr;
+            m = mn;
+#pragma unroll
+            for (int tt = 0; tt < HD / 32; ++tt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[tt][v] *= corr;
+        }
         float ps = 0.f;
         half8 pf[QP][2][2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const float pv = (st[kb][v] == -INFINITY) ? 0.f : exp2f(st[kb][v] - mn);
+                const float pv = (st[kb][v] == -INFINITY) ? 0.f : fast_exp2(st[kb][v] - m);
                 ps += pv;
                 if constexpr (QX2) {
                     vsl_half hi, lo;
@@ -460,26 +473,31 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
                     pf[0][kb][v >> 3][v & 7] = (vsl_half)pv;
                 }
             }
-        ps += __shfl_xor(ps, 32, 64);
-        l = l * corr + ps;
-        m = mn;
-#pragma unroll
-        for (int tt = 0; tt < HD / 32; ++tt)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) o[tt][v] *= corr;
+        {
+            float pa, pb;
+            lane_pair<32>(ps, pa, pb);
+            ps = pa + pb;
+        }
+        l += ps;
         // O^T[dim][q] += sum_kv V^T[dim][kv] P^T[kv][q]; P^T slots v = 0..7 / 8..15 of each half are
-        // the kv rows (v/4)*8 + (l/32)*4 + v%4, which the V^T operand reads to match
+        // the kv rows (v/4)*8 + (l/32)*4 + v%4, which the V^T operand reads to match: lane l needs
+        // V[r0 + j][dim] and V[r0 + 8 + j][dim] (j = 0..3) for dim = 32 tt + l%32, r0 = 32 kb + 16 hi
+        // + 4 (l/32). ds_read_b64_tr_b16 gives lane i of a 16-lane group element i%4 of the 8-byte
+        // row addressed by lane 4j + i/4 of the group as its value j, so lane i addresses
+        // V[r0 + i/4][d0 + 4 (i%4) .. +3] with d0 the group's first dim: value j is V[r0 + j][d0 + i].
+        const vsl_half* Vt = Vs[buf];
+        const int gi = lane & 15, gdim = ((lane >> 4) & 1) * 16 + 4 * (gi & 3);
 #pragma unroll
         for (int tt = 0; tt < HD / 32; ++tt) {
-            const int dim = tt * 32 + (lane & 31);
+            const int d = tt * 32 + gdim;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int hi = 0; hi < 2; ++hi) {
-                    const int r0 = kb * 32 + (hi * 2) * 8 + (lane >> 5) * 4;
-                    const half4 a0 = *reinterpret_cast<const half4*>(&Vt[buf][dim * VTS + r0]);
-                    const half4 a1 = *reinterpret_cast<const half4*>(&Vt[buf][dim * VTS + r0 + 8]);
-                    const half8 af = half8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+                    const int r = kb * 32 + hi * 16 + (lane >> 5) * 4 + (gi >> 2);
+                    const half4 x0 = lds_read_tr16(Vt + ksw<HD>(r, d >> 3) + (d & 7));
+                    const half4 x1 = lds_read_tr16(Vt + ksw<HD>(r + 8, d >> 3) + (d & 7));
+                    const half8 af = half8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
 #pragma unroll
                     for (int p = 0; p < QP; ++p)
                         o[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, pf[p][kb][hi], o[tt], 0, 0, 0);
@@ -487,38 +505,46 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
         }
     };
 
-    // tile pipeline: tile t+1's global loads are issued before tile t's MFMAs and stored to the
-    // other LDS buffer after them; loads past the last tile re-read it and are never stored
-    Stage sg;
-    gload(sg, phys(0));
-    sstore(sg, 0, phys(0));
+    // Tile pipeline: tile t+1 is requested into the other buffer before tile t is computed; after
+    // it, each wave waits for its own copies and the block meets at a barrier (every copy of t+1 is
+    // in LDS, every wave has finished reading buffer t, which the next request overwrites). The
+    // request past the last tile re-copies it into the buffer that is not read again.
+    issue(0, phys(0));
+    VSL_VMCNT_WAIT(0);
     __syncthreads();
     for (uint32_t t = 0; t < n_vt; ++t) {
         const int buf = t & 1;
-        const uint32_t next = phys(t + 1 < n_vt ? t + 1 : t);
-        gload(sg, next);
-        __builtin_amdgcn_sched_barrier(0);
+        issue(buf ^ 1, phys(t + 1 < n_vt ? t + 1 : t));
         compute(buf, phys(t));
-        sstore(sg, buf ^ 1, next);
+        VSL_VMCNT_WAIT(0);
         __syncthreads();
     }
 
     if (my_s >= S) return;
     const float inv = l > 0.f ? 1.f / l : 0.f;
     vsl_half* orow = out + (size_t)my_s * qw + (size_t)h * HD;
+    // element v of O^T fragment t is dim 32 t + d_row(v, lane): runs of 4 consecutive dims (v%4), so
+    // each run is one 8-byte store per plane
 #pragma unroll
     for (int t = 0; t < HD / 32; ++t)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const float val = o[t][v] * inv;
-            if constexpr (OX2) {
-                vsl_half hi, lo;
-                split_f16(val, hi, lo);
-                orow[t * 32 + d_row(v, lane)] = hi;
-                orow[qplane + t * 32 + d_row(v, lane)] = lo;
-            } else {
-                orow[t * 32 + d_row(v, lane)] = (vsl_half)val;
+        for (int v0 = 0; v0 < 16; v0 += 4) {
+            half4 hv, lv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float val = o[t][v0 + i] * inv;
+                if constexpr (OX2) {
+                    vsl_half hi, lo;
+                    split_f16(val, hi, lo);
+                    hv[i] = hi;
+                    lv[i] = lo;
+                } else {
+                    hv[i] = (vsl_half)val;
+                }
             }
+            const int dim = t * 32 + d_row(v0, lane);
+            *reinterpret_cast<half4*>(orow + dim) = hv;
+            if constexpr (OX2) *reinterpret_cast<half4*>(orow + qplane + dim) = lv;
         }
 }
 
