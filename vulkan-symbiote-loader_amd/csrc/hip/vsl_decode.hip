@@ -1093,12 +1093,69 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float* x, const f
     for (uint32_t i = threadIdx.x; i < d; i += kBlock) {
         const float v = xr[i] * inv * (gamma ? gamma[i] : 1.0f);
         if constexpr (X2) {
-            const vsl_half hi = (vsl_half)v;
+            vsl_half hi, lo;
+            split_f16(v, hi, lo);
             out[(size_t)blockIdx.x * d + i] = hi;
-            out[(size_t)rows * d + (size_t)blockIdx.x * d + i] = (vsl_half)(v - (float)hi);
+            out[(size_t)rows * d + (size_t)blockIdx.x * d + i] = lo;
         } else {
             store_elem(out + (size_t)blockIdx.x * d + i, v);
         }
+    }
+}
+
+// One row per wave, held in registers: NV float4 per lane (d = 256 NV), 16-byte loads of x and the
+// gains, the sum of squares by DPP, 8-byte (fp16 / split) or 16-byte (fp32) stores. No LDS, no
+// barrier: one memory round trip per row.
+template <typename OT, bool X2, int NV>
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_wave(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                         uint32_t rows, float eps, OT* __restrict__ out) {
+    constexpr uint32_t d = 256 * NV;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * d;
+    float4 v[NV], g[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) v[j] = *reinterpret_cast<const float4*>(xr + (j * 64 + lane) * 4);
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        g[j] = gamma ? *reinterpret_cast<const float4*>(gamma + (j * 64 + lane) * 4) : make_float4(1.f, 1.f, 1.f, 1.f);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    const float inv = 1.0f / sqrtf(wave_sum_dpp(ss) / (float)d + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const size_t o = (size_t)row * d + (j * 64 + lane) * 4;
+        const float4 y = make_float4(v[j].x * inv * g[j].x, v[j].y * inv * g[j].y, v[j].z * inv * g[j].z,
+                                     v[j].w * inv * g[j].w);
+        if constexpr (X2) {
+            vsl_half h0, h1, h2, h3, l0, l1, l2, l3;
+            split_f16(y.x, h0, l0);
+            split_f16(y.y, h1, l1);
+            split_f16(y.z, h2, l2);
+            split_f16(y.w, h3, l3);
+            *reinterpret_cast<half4*>(out + o) = half4{h0, h1, h2, h3};
+            *reinterpret_cast<half4*>(out + (size_t)rows * d + o) = half4{l0, l1, l2, l3};
+        } else if constexpr (sizeof(OT) == 2) {
+            *reinterpret_cast<half4*>(out + o) = half4{(vsl_half)y.x, (vsl_half)y.y, (vsl_half)y.z, (vsl_half)y.w};
+        } else {
+            *reinterpret_cast<float4*>(out + o) = y;
+        }
+    }
+}
+
+template <typename OT, bool X2>
+void launch_rmsnorm(const float* x, const float* gamma, uint32_t rows, uint32_t d, float eps, OT* out, hipStream_t s) {
+    const uint32_t wb = (rows + kWaves - 1) / kWaves;
+    switch (d) {
+        case 256: k_rmsnorm_wave<OT, X2, 1><<<wb, kBlock, 0, s>>>(x, gamma, rows, eps, out); return;
+        case 512: k_rmsnorm_wave<OT, X2, 2><<<wb, kBlock, 0, s>>>(x, gamma, rows, eps, out); return;
+        case 1024: k_rmsnorm_wave<OT, X2, 4><<<wb, kBlock, 0, s>>>(x, gamma, rows, eps, out); return;
+        case 2048: k_rmsnorm_wave<OT, X2, 8><<<wb, kBlock, 0, s>>>(x, gamma, rows, eps, out); return;
+        case 4096: k_rmsnorm_wave<OT, X2, 16><<<wb, kBlock, 0, s>>>(x, gamma, rows, eps, out); return;
+        case 8192: k_rmsnorm_wave<OT, X2, 32><<<wb, kBlock, 0, s>>>(x, gamma, rows, eps, out); return;
+        default: k_rmsnorm_rows<OT, X2><<<rows, kBlock, 0, s>>>(x, gamma, rows, d, eps, out); return;
     }
 }
 
@@ -1305,11 +1362,11 @@ extern "C" int vsl_rmsnorm(const float* x, const float* gamma, uint32_t rows, ui
     if (rows == 0) return VSL_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (out_dtype == VSL_DT_F16)
-        k_rmsnorm_rows<vsl_half, false><<<rows, kBlock, 0, s>>>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out));
+        launch_rmsnorm<vsl_half, false>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out), s);
     else if (out_dtype == VSL_DT_F16X2)
-        k_rmsnorm_rows<vsl_half, true><<<rows, kBlock, 0, s>>>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out));
+        launch_rmsnorm<vsl_half, true>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out), s);
     else if (out_dtype == VSL_DT_F32)
-        k_rmsnorm_rows<float, false><<<rows, kBlock, 0, s>>>(x, gamma, rows, d, eps, static_cast<float*>(out));
+        launch_rmsnorm<float, false>(x, gamma, rows, d, eps, static_cast<float*>(out), s);
     else
         return vsl_unsupported("vsl_rmsnorm: dtype %d", out_dtype);
     HIP_TRY(hipGetLastError());
