@@ -27,9 +27,9 @@ CFG = dict(hidden_size=4096, num_layers=32, num_heads=32, num_kv_heads=8, interm
 KV_CAPACITY = 4096
 
 # HBM bytes per launch of the dominant decode kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
-# passes summarised in profiles/decode_8b_rocprof.md (FETCH_SIZE scaled x1.9999 by a 1 GiB copy).
+# passes summarised in profiles/llama8b_decode_prefill_rocprof.md (FETCH_SIZE scaled x1.9999 by a 1 GiB copy).
 # Re-measure with the commands listed there whenever the kernel changes.
-DOMINANT_TRAFFIC_BYTES = 235_240_000 + 115_000
+DOMINANT_TRAFFIC_BYTES = 235_290_000 + 115_000
 
 
 def load_package():
@@ -360,7 +360,7 @@ def main():
                            "frac": round(achieved / PEAK_HBM, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
                            "algorithmic_bytes": dom["bytes"],
                            "kernel": "k_gemv_dec<EPI_SWIGLU> (ffn norm + [Wgate;Wup] GEMV + SwiGLU)",
-                           "traffic_source": "profiles/decode_8b_rocprof.md"}
+                           "traffic_source": "profiles/llama8b_decode_prefill_rocprof.md"}
         out["decode_ops"] = ops
 
     if not a.no_cpu_baseline:
