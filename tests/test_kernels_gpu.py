@@ -570,6 +570,36 @@ def test_rmsnorm_split_planes(vsl, orc, dev, H):
     assert np.array_equal(o[0], ref.astype(np.float16).astype(np.float32)) or rel_err(o[0], ref) < 2.0 ** -11
 
 
+@pytest.mark.parametrize("d", [256, 512, 1024, 2048, 4096, 8192, 1000])
+@pytest.mark.parametrize("rows", [1, 6])
+@pytest.mark.parametrize("odt", [0, 1, 2])
+def test_rmsnorm_rows_widths(vsl, orc, dev, H, d, rows, odt):
+    """Row RMSNorm for every width the one-row-per-wave kernel holds in registers (256 .. 8192) and a
+    width that takes the block-per-row kernel (1000), row counts that leave waves of a block without
+    a row, fp32 / fp16 / split outputs, with and without gains. The split reproduces the fp32 result
+    and its hi plane is a nearest binary16 of hi + lo."""
+    rng = np.random.default_rng(d + rows + 7 * odt)
+    x = rng.normal(0, 2, (rows, d)).astype(np.float32)
+    g = rng.normal(1, 0.1, d).astype(np.float32) if odt != 1 else None
+    planes = 2 if odt == 2 else 1
+    out = dev.empty((planes, rows, d), np.float32 if odt == 0 else np.float16)
+    ok(vsl, H.vsl_rmsnorm(dev.p(dev.put(x)), dev.p(dev.put(g)) if g is not None else None, rows, d, 1e-5, dev.p(out),
+                          odt, None))
+    o = dev.get(out).astype(np.float64)
+    gg = g if g is not None else np.ones(d, np.float32)
+    ref = np.stack([orc.rmsnorm(x[r], gg, 1e-5) for r in range(rows)]).astype(np.float64)
+    if odt == 0:
+        assert rel_err(o[0], ref) < 2e-6
+    elif odt == 1:
+        assert rel_err(o[0], ref) < 2.0 ** -11
+    else:
+        assert rel_err(o[0] + o[1], ref) < 2e-6
+        # hi is a nearest binary16 of hi + lo: |lo| is at most half the fp16 spacing at hi (a split
+        # whose stored hi came from a different rounding than lo leaves up to a whole spacing)
+        hi16 = o[0].astype(np.float16)
+        assert np.all(np.abs(o[1]) <= 0.5 * np.spacing(np.abs(hi16)).astype(np.float64))
+
+
 @pytest.mark.parametrize("M,N,K,epi", [(77, 256, 4096, 0), (130, 512, 2048, 2), (200, 4096, 14336, 2)])
 def test_gemm_split_a(vsl, dev, H, M, N, K, epi):
     rng = np.random.default_rng(M + N + K)
