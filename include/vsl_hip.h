@@ -270,6 +270,28 @@ int vsl_rope_split_append(const float* qkv, uint32_t S, uint32_t n_q, uint32_t n
                           uint32_t pos0, const float* rope_cos, const float* rope_sin, void* q_out, int q_dtype,
                           void* kcache, void* vcache, int kv_dtype, uint32_t cap, void* stream);
 
+/* The attention stage's entry for S prompt rows (forward_layer_with_weights,
+ * VulkanSymbioteEngine.cpp:777-806, normed -> attention_with_weights): the QKV projection of A
+ * [S][K] against Wqkv [(n_q+2 n_kv) hd][K] followed by vsl_rope_split_append.  `a_flags` is 0 or
+ * VSL_GEMM_A_X2.  When the shape splits over K (workspace as for vsl_gemm_f16_ws), the partials are
+ * summed, rotated and stored by one launch and qkv is not touched; otherwise qkv (f32 [S][(n_q+2 n_kv)
+ * hd]) receives the projection first.  Checks (capacity, dtypes) happen before anything is launched. */
+int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uint32_t S, uint32_t K, int a_flags,
+                                 uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t pos0, const float* rope_cos,
+                                 const float* rope_sin, void* q_out, int q_dtype, void* kcache, void* vcache,
+                                 int kv_dtype, uint32_t cap, float* qkv, void* workspace, uint64_t ws_bytes,
+                                 void* stream);
+
+/* A residual projection and the RMSNorm that starts the next stage (forward_layer_with_weights,
+ * VulkanSymbioteEngine.cpp:777-806: the attention output feeds the FFN's norm, the FFN output the
+ * next layer's attention norm): x [M][N] f32 += A [M][K] B [N][K]^T, then xn = rmsnorm(x) * gamma as
+ * vsl_rmsnorm (xn_dtype F16, F16X2 or F32).  When the shape splits over K, one launch sums the
+ * partials in order, adds them to x and normalizes the rows; otherwise the residual GEMM is followed
+ * by vsl_rmsnorm. */
+int vsl_gemm_f16_resid_rmsnorm(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, int a_flags,
+                               float* x, const float* gamma, float eps, void* xn, int xn_dtype, void* workspace,
+                               uint64_t ws_bytes, void* stream);
+
 /* Causal prefill attention for S queries at positions pos0..pos0+S-1 against cache positions
  * 0..pos0+s: q [S][n_q][hd] (q_dtype F16 or F16X2), caches f16 [n_kv][cap][hd],
  * out [S][n_q*hd] (out_dtype F16 or F16X2).  With F16X2 q the probabilities are split as well. */

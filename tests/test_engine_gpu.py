@@ -248,12 +248,34 @@ def test_llama_8b_long_context(vsl):
         s3 = e.generate_ids(prompt, 32, mode="topk", temperature=0.7, top_k=40, seed=8)
     with vsl.Engine(spec=cfg, seed=0, kv_capacity=32768, batched_prefill=False) as e:
         rt, rl = e.generate_ids(prompt, n_new, return_logits=True)
+    _assert_matches_tokenwise(toks, lg, rt, rl)
+    assert np.array_equal(s1, s2) and not np.array_equal(s1, s3)
+    assert len(s1) == 32 and int(s1.max()) < V and int(s3.max()) < V
+
+
+def _assert_matches_tokenwise(toks, lg, rt, rl):
+    """Greedy tokens identical up to the first step whose per-token reference top1-top2 margin is below
+    4e-2 (a near-tie either path may break either way); logits within max-abs 2e-2 up to and including
+    that step."""
+    n_new = len(rt)
     srt = np.sort(rl, axis=1)
     margins = srt[:, -1] - srt[:, -2]
     tie = next((i for i in range(n_new) if margins[i] < 4e-2), n_new)
     n = next((i for i in range(tie) if toks[i] != rt[i]), tie)
     assert n == tie, f"greedy mismatch at step {n} (reference margin {margins[n]:.4f})"
-    last = min(tie + 1, n_new)  # logits agree up to and including the first near-tie step
+    last = min(tie + 1, n_new)
     assert np.max(np.abs(lg[:last] - rl[:last])) < 2e-2, np.max(np.abs(lg[:last] - rl[:last]))
-    assert np.array_equal(s1, s2) and not np.array_equal(s1, s3)
-    assert len(s1) == 32 and int(s1.max()) < V and int(s3.max()) < V
+
+
+def test_llama_8b_prefill_512_matches_tokenwise(vsl):
+    """The 8B-class 512-token prefill as one MFMA chunk -- QKV, O and down projections split over K,
+    their sums fused with RoPE + the Q/K/V split and with the residual add + the next RMSNorm --
+    against the per-token path (the decode kernels the oracle pins at small sizes) on the same
+    weights, 32 greedy tokens."""
+    cfg = vsl.LLAMA_8B
+    prompt = np.random.default_rng(5).integers(0, cfg["vocab_size"], 512).astype(np.uint32)
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=1024, batched_prefill=True) as e:
+        toks, lg = e.generate_ids(prompt, 32, return_logits=True)
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=1024, batched_prefill=False) as e:
+        rt, rl = e.generate_ids(prompt, 32, return_logits=True)
+    _assert_matches_tokenwise(toks, lg, rt, rl)

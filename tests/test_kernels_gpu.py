@@ -656,3 +656,161 @@ def test_attn_prefill_split(vsl, orc, dev, H, hd, nq, nkv, S, pos0):
     for s in range(0, S, max(1, S // 7)):
         ref = orc.attention_decode(Qf[s], K, V, nq, nkv, hd, cap, pos0 + s + 1, scale)
         assert rel_err(O[0][s] + O[1][s], ref) < 2e-5
+
+
+# ------------------------------------------------------------------------------------------
+# prefill projections fused with the step that consumes them
+# ------------------------------------------------------------------------------------------
+def _act(rng, M, K, ax2):
+    """fp16 activations (or split hi/lo planes) and the fp64 values they stand for."""
+    Af = rng.normal(0, 1, (M, K)).astype(np.float32)
+    if ax2:
+        hi, lo = split_np(Af)
+        return np.concatenate([hi, lo]), hi.astype(np.float64) + lo.astype(np.float64)
+    Ad = Af.astype(np.float16)
+    return Ad, Ad.astype(np.float64)
+
+
+@pytest.mark.parametrize("S,K,nq,nkv,hd,pos0,ax2,qx2,kvdt", [
+    (512, 4096, 32, 8, 128, 0, True, True, 1),     # 512-row chunk of the 8B-class model: K split 2
+    (512, 4096, 32, 8, 128, 100, False, False, 1),  # later chunk, fp16 q
+    (300, 4096, 32, 8, 128, 7, True, True, 0),     # ragged rows (K split 4), fp32 cache
+    (256, 4096, 32, 8, 64, 0, False, True, 1),     # head_dim 64 (K split 8)
+])
+def test_gemm_qkv_rope_append(vsl, orc, dev, H, S, K, nq, nkv, hd, pos0, ax2, qx2, kvdt):
+    """QKV projection + RoPE + Q/K/V split through one entry point. With the workspace the split-K
+    partials are summed, rotated and stored by one launch: its q, k and v equal those of the unfused
+    composition (the projection into an fp32 buffer through the same workspace, then
+    vsl_rope_split_append) exactly, since both add the same partials in the same order, and match the
+    oracle's RoPE of the fp64 projection. Without the workspace the entry runs unsplit through the
+    buffer. Cache positions outside pos0..pos0+S-1 are left alone."""
+    rng = np.random.default_rng(S + hd + pos0)
+    cap, theta = 1024, 500000.0
+    N = (nq + 2 * nkv) * hd
+    Ad, Aref = _act(rng, S, K, ax2)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    cs, sn = rope_tables(cap, hd, theta)
+    kvnp = np.float16 if kvdt == 1 else np.float32
+    K0 = rng.normal(0, 1, (nkv, cap, hd)).astype(kvnp)
+    need = H.vsl_gemm_f16_ws_bytes(S, N, K, 0)
+    assert need > 0
+    ws = dev.empty((need // 4,), np.float32)
+    dA, dW, dcs, dsn = dev.put(Ad), dev.put(W), dev.put(cs), dev.put(sn)
+    qkv = dev.empty((S, N), np.float32)
+    qdt, aflag = (2 if qx2 else 1), (0x100 if ax2 else 0)
+    outs = []
+    for mode in ("fused", "unfused", "unsplit"):
+        q = dev.empty(((2 if qx2 else 1) * S, nq * hd), np.float16)
+        kc, vc = dev.put(K0), dev.put(K0)
+        if mode == "unfused":
+            ok(vsl, H.vsl_gemm_f16_ws(dev.p(dA), dev.p(dW), S, N, K, dev.p(qkv), aflag, dev.p(ws), need, None))
+            ok(vsl, H.vsl_rope_split_append(dev.p(qkv), S, nq, nkv, hd, pos0, dev.p(dcs), dev.p(dsn), dev.p(q), qdt,
+                                            dev.p(kc), dev.p(vc), kvdt, cap, None))
+        else:
+            ok(vsl, H.vsl_gemm_f16_qkv_rope_append(dev.p(dA), dev.p(dW), S, K, aflag, nq, nkv, hd, pos0, dev.p(dcs),
+                                                   dev.p(dsn), dev.p(q), qdt, dev.p(kc), dev.p(vc), kvdt, cap,
+                                                   dev.p(qkv), dev.p(ws) if mode == "fused" else None,
+                                                   need if mode == "fused" else 0, None))
+        outs.append((dev.get(q).astype(np.float64), dev.get(kc).astype(np.float64), dev.get(vc).astype(np.float64)))
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(a, b)
+    for q, kc, vc in (outs[0], outs[2]):
+        Q = (q[:S] + q[S:]) if qx2 else q
+        outside = np.ones(cap, bool)
+        outside[pos0:pos0 + S] = False
+        assert np.array_equal(kc[:, outside], K0[:, outside].astype(np.float64))
+        assert np.array_equal(vc[:, outside], K0[:, outside].astype(np.float64))
+        qt = 2e-5 if qx2 else 2.0 ** -10
+        kt = 2.0 ** -10 if kvdt == 1 else 2e-5
+        for s in (0, 1, S // 2, S - 1):
+            y = (Aref[s] @ W.astype(np.float64).T).astype(np.float32)
+            pos = pos0 + s
+            assert rel_err(Q[s], orc.rope(y[:nq * hd], nq, hd, pos, theta)) < qt
+            assert rel_err(kc[:, pos].reshape(-1), orc.rope(y[nq * hd:(nq + nkv) * hd], nkv, hd, pos, theta)) < kt
+            assert rel_err(vc[:, pos].reshape(-1), y[(nq + nkv) * hd:]) < kt
+
+
+def test_gemm_qkv_rope_append_refuses_before_launch(vsl, dev, H):
+    """Capacity and dtype errors come back as codes with nothing written."""
+    S, K, nq, nkv, hd, cap = 64, 512, 4, 4, 64, 80
+    N = (nq + 2 * nkv) * hd
+    A = dev.put(np.zeros((S, K), np.float16))
+    W = dev.put(np.zeros((N, K), np.float16))
+    t = dev.put(np.zeros((cap, hd // 2), np.float32))
+    q = dev.empty((S, nq * hd), np.float16)
+    K0 = np.full((nkv, cap, hd), 3.0, np.float16)
+    kc = dev.put(K0)
+    qkv = dev.empty((S, N), np.float32)
+    args = lambda pos0, qdt, kvdt: (dev.p(A), dev.p(W), S, K, 0, nq, nkv, hd, pos0, dev.p(t), dev.p(t), dev.p(q), qdt,
+                                    dev.p(kc), dev.p(kc), kvdt, cap, dev.p(qkv), None, 0, None)
+    assert H.vsl_gemm_f16_qkv_rope_append(*args(cap - S + 1, 1, 1)) == vsl.VSL_E_CAPACITY
+    assert H.vsl_gemm_f16_qkv_rope_append(*args(0, 0, 1)) == vsl.VSL_E_UNSUPPORTED
+    assert H.vsl_gemm_f16_qkv_rope_append(*args(0, 1, 5)) == vsl.VSL_E_UNSUPPORTED
+    assert np.array_equal(dev.get(kc), K0)
+
+
+@pytest.mark.parametrize("M,N,K,ax2,odt,gam", [
+    (512, 4096, 4096, True, 2, True),    # O projection of a 512-row chunk + FFN norm (split planes)
+    (512, 4096, 14336, True, 2, True),   # down projection + next layer's attention norm
+    (300, 4096, 4096, False, 1, True),   # ragged rows, fp16 out
+    (512, 2048, 8192, False, 0, False),  # d = 2048, K split 8, fp32 out, no gains
+    (256, 8192, 4096, False, 2, True),   # d = 8192 (eight float4 per thread)
+])
+def test_gemm_resid_rmsnorm(vsl, orc, dev, H, M, N, K, ax2, odt, gam):
+    """Residual projection + the next RMSNorm through one entry point. With the workspace the split-K
+    partials are summed and added to x, and the rows normalized, by one launch: x equals the unfused
+    residual GEMM's exactly (same partials, same order) and the fp64 reference to fp32 rounding; the
+    norm matches the oracle's RMSNorm of the updated x. Without the workspace the entry runs the
+    unsplit residual GEMM and vsl_rmsnorm."""
+    rng = np.random.default_rng(M + N + K + odt)
+    Ad, Aref = _act(rng, M, K, ax2)
+    B = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    x0 = rng.normal(0, 1, (M, N)).astype(np.float32)
+    g = rng.normal(1, 0.1, N).astype(np.float32) if gam else None
+    need = H.vsl_gemm_f16_ws_bytes(M, N, K, 2)
+    assert need > 0
+    ws = dev.empty((need // 4,), np.float32)
+    dA, dB = dev.put(Ad), dev.put(B)
+    dg = dev.put(g) if gam else None
+    aflag = 0x100 if ax2 else 0
+    planes = 2 if odt == 2 else 1
+    res = {}
+    for mode in ("fused", "unfused", "unsplit"):
+        x = dev.put(x0)
+        xn = dev.empty((planes, M, N), np.float32 if odt == 0 else np.float16)
+        if mode == "unfused":
+            ok(vsl, H.vsl_gemm_f16_ws(dev.p(dA), dev.p(dB), M, N, K, dev.p(x), 2 | aflag, dev.p(ws), need, None))
+        else:
+            ok(vsl, H.vsl_gemm_f16_resid_rmsnorm(dev.p(dA), dev.p(dB), M, N, K, aflag, dev.p(x),
+                                                 dev.p(dg) if gam else None, 1e-5, dev.p(xn), odt,
+                                                 dev.p(ws) if mode == "fused" else None,
+                                                 need if mode == "fused" else 0, None))
+        res[mode] = (dev.get(x).astype(np.float32), dev.get(xn).astype(np.float64))
+    assert np.array_equal(res["fused"][0], res["unfused"][0])
+    rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, 24)]))
+    ref = x0[rows].astype(np.float64) + Aref[rows] @ B.astype(np.float64).T
+    gg = g if gam else np.ones(N, np.float32)
+    for mode in ("fused", "unsplit"):
+        x, o = res[mode]
+        assert rel_err(x[rows], ref) < 1e-5
+        nref = np.stack([orc.rmsnorm(x[r], gg, 1e-5) for r in rows]).astype(np.float64)
+        if odt == 0:
+            assert rel_err(o[0][rows], nref) < 2e-6
+        elif odt == 1:
+            assert rel_err(o[0][rows], nref) < 2.0 ** -11
+        else:
+            assert rel_err(o[0][rows] + o[1][rows], nref) < 2e-6
+            hi16 = o[0][rows].astype(np.float16)
+            assert np.all(np.abs(o[1][rows]) <= 0.5 * np.spacing(np.abs(hi16)).astype(np.float64))
+
+
+def test_gemm_resid_rmsnorm_bad_arguments(vsl, dev, H):
+    A = dev.put(np.zeros((8, 512), np.float16))
+    x = dev.put(np.zeros((8, 1024), np.float32))
+    xn = dev.empty((8, 1024), np.float16)
+    assert H.vsl_gemm_f16_resid_rmsnorm(dev.p(A), dev.p(A), 8, 1024, 512, 0, dev.p(x), None, 1e-5, dev.p(xn), 7,
+                                        None, 0, None) == vsl.VSL_E_UNSUPPORTED
+    assert H.vsl_gemm_f16_resid_rmsnorm(dev.p(A), dev.p(A), 8, 1024, 512, 0x200, dev.p(x), None, 1e-5, dev.p(xn), 1,
+                                        None, 0, None) == vsl.VSL_E_INVALID
+    assert H.vsl_gemm_f16_resid_rmsnorm(dev.p(A), None, 8, 1024, 512, 0, dev.p(x), None, 1e-5, dev.p(xn), 1,
+                                        None, 0, None) == vsl.VSL_E_INVALID

@@ -20,6 +20,7 @@ LIB_DIR = os.path.join(_HERE, "lib")
 HIP_LIB = os.path.join(LIB_DIR, "libvsl_hip.so")
 ENGINE_LIB = os.path.join(LIB_DIR, "libvsl_engine.so")
 
+VSL_OK, VSL_E_INVALID, VSL_E_HIP, VSL_E_OOM, VSL_E_UNSUPPORTED, VSL_E_CAPACITY = 0, -100, -101, -102, -103, -104
 VSL_DT_F32, VSL_DT_F16, VSL_DT_F16X2 = 0, 1, 2
 VSL_WF_F32, VSL_WF_F16, VSL_WF_Q4_0, VSL_WF_Q4_1, VSL_WF_Q8_0 = 0, 1, 2, 3, 4
 VSL_QL_REFERENCE, VSL_QL_GGML = 0, 1
@@ -150,6 +151,9 @@ _HIP_SIGS = {
     "vsl_ctrl_reset": (_I32, [_P, _U32, _U32, _U32, _U32, _P]),
     "vsl_gemm_f16": (_I32, [_P, _P, _U32, _U32, _U32, _P, _I32, _P]),
     "vsl_rope_split_append": (_I32, [_P, _U32, _U32, _U32, _U32, _U32, _P, _P, _P, _I32, _P, _P, _I32, _U32, _P]),
+    "vsl_gemm_f16_qkv_rope_append": (_I32, [_P, _P, _U32, _U32, _I32, _U32, _U32, _U32, _U32, _P, _P, _P, _I32, _P,
+                                             _P, _I32, _U32, _P, _P, _U64, _P]),
+    "vsl_gemm_f16_resid_rmsnorm": (_I32, [_P, _P, _U32, _U32, _U32, _I32, _P, _P, _F32, _P, _I32, _P, _U64, _P]),
     "vsl_attn_prefill": (_I32, [_P, _I32, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _F32, _P, _I32, _P]),
     "vsl_graph_begin": (_I32, [_P]),
     "vsl_graph_end": (_I32, [_P, ctypes.POINTER(_P)]),

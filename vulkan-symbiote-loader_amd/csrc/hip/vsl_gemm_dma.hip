@@ -382,12 +382,17 @@ uint32_t vsl_gemm_splitk_plan(uint32_t M, uint32_t N, uint32_t K, int epi, uint3
     return 0;
 }
 
+void vsl_gemm_splitk_partials(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
+                              uint32_t K, bool ax2, float* ws) {
+    const uint32_t tiles = dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
+    launch_splitk<DmaMid>(tiles * ksplit, static_cast<hipStream_t>(stream), static_cast<const vsl_half*>(A),
+                          static_cast<const vsl_half*>(B), M, N, K, ws, ksplit, ax2);
+}
+
 int vsl_gemm_splitk_launch(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
                            uint32_t K, void* C, int epi, bool ax2, float* ws) {
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const uint32_t tiles = dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
-    launch_splitk<DmaMid>(tiles * ksplit, s, static_cast<const vsl_half*>(A), static_cast<const vsl_half*>(B), M, N,
-                          K, ws, ksplit, ax2);
+    vsl_gemm_splitk_partials(ksplit, stream, A, B, M, N, K, ax2, ws);
     const uint64_t MN = (uint64_t)M * N;
     const uint32_t rblocks = (uint32_t)((MN / 4 + 255) / 256);
     switch (epi) {

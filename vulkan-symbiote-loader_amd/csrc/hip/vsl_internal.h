@@ -35,5 +35,8 @@ int vsl_gemm_dma_launch(int cfg, void* stream, const void* A, const void* B, uin
 // Split-K plan of the direct-to-LDS GEMM (k chunks of the 128 x 256 tiling, fp32 partials in a
 // workspace, an ordered reduction applying the epilogue): returns the split (0: none).
 uint32_t vsl_gemm_splitk_plan(uint32_t M, uint32_t N, uint32_t K, int epi, uint32_t min_items, uint64_t* ws_bytes);
+// The k-chunk partials alone, ws[chunk][M][N] fp32, for a caller that sums them itself.
+void vsl_gemm_splitk_partials(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
+                              uint32_t K, bool ax2, float* ws);
 int vsl_gemm_splitk_launch(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
                            uint32_t K, void* C, int epi, bool ax2, float* ws);

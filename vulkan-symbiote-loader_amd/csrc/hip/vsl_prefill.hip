@@ -300,6 +300,116 @@ __global__ void k_rope_split(const float* __restrict__ qkv, uint32_t S, uint32_t
     }
 }
 
+// The same over four consecutive columns (two rotation pairs) per thread, with the projection given
+// as KS fp32 k-chunk partials ws[KS][S][W] summed in chunk order (KS = 1: the finished projection):
+// 16-byte loads of each partial, 8-byte loads of the rotation tables, 8-byte q and fp16 cache stores
+// (16-byte fp32 cache stores). Needs hd % 4 == 0; a quad then never straddles a head or the q/k/v
+// boundaries.
+template <class KT, bool QX2, int KS>
+__global__ __launch_bounds__(256) void k_rope_split4(const float* __restrict__ ws, uint32_t S, uint32_t n_q,
+                                                     uint32_t n_kv, uint32_t hd, uint32_t pos0,
+                                                     const float* __restrict__ rc, const float* __restrict__ rs,
+                                                     vsl_half* __restrict__ q_out, void* __restrict__ kc,
+                                                     void* __restrict__ vc, uint32_t cap) {
+    const uint32_t width = (n_q + 2 * n_kv) * hd, quads = width / 4;
+    const uint64_t e = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (uint64_t)S * quads) return;
+    const uint32_t s = (uint32_t)(e / quads), col = (uint32_t)(e % quads) * 4;
+    const uint64_t MN = (uint64_t)S * width;
+    const size_t off = (size_t)s * width + col;
+    float4v v = *reinterpret_cast<const float4v*>(ws + off);
+#pragma unroll
+    for (int k = 1; k < KS; ++k) v += *reinterpret_cast<const float4v*>(ws + k * MN + off);
+    const uint32_t pos = pos0 + s, qw = n_q * hd, kw = n_kv * hd;
+    if (col < qw + kw) {
+        const size_t j = (size_t)pos * (hd >> 1) + ((col % hd) >> 1);
+        const float2 c = *reinterpret_cast<const float2*>(rc + j);
+        const float2 sn = *reinterpret_cast<const float2*>(rs + j);
+        v = float4v{v[0] * c.x - v[1] * sn.x, v[0] * sn.x + v[1] * c.x, v[2] * c.y - v[3] * sn.y,
+                    v[2] * sn.y + v[3] * c.y};
+    }
+    if (col < qw) {
+        const size_t o = (size_t)s * qw + col;
+        if constexpr (QX2) {
+            vsl_half h0, h1, h2, h3, l0, l1, l2, l3;
+            split_f16(v[0], h0, l0);
+            split_f16(v[1], h1, l1);
+            split_f16(v[2], h2, l2);
+            split_f16(v[3], h3, l3);
+            *reinterpret_cast<half4*>(q_out + o) = half4{h0, h1, h2, h3};
+            *reinterpret_cast<half4*>(q_out + (size_t)S * qw + o) = half4{l0, l1, l2, l3};
+        } else {
+            *reinterpret_cast<half4*>(q_out + o) = half4{(vsl_half)v[0], (vsl_half)v[1], (vsl_half)v[2], (vsl_half)v[3]};
+        }
+    } else {
+        typedef typename KT::T T;
+        const bool is_k = col < qw + kw;
+        const uint32_t cc = col - (is_k ? qw : qw + kw);
+        T* dst = static_cast<T*>(is_k ? kc : vc) + ((size_t)(cc / hd) * cap + pos) * hd + cc % hd;
+        if constexpr (sizeof(T) == 2)
+            *reinterpret_cast<half4*>(dst) = half4{(vsl_half)v[0], (vsl_half)v[1], (vsl_half)v[2], (vsl_half)v[3]};
+        else
+            *reinterpret_cast<float4v*>(dst) = v;
+    }
+}
+
+// Residual projection given as KS fp32 k-chunk partials ws[KS][rows][d]: x += their sum (chunks in
+// order, then added to x), followed by the next RMSNorm of the updated rows, out = x / sqrt(mean(x^2)
+// + eps) * gamma (fp16, split or fp32). One 256-thread block per row, NV float4 per thread
+// (d = 1024 NV): every partial, x and gamma requested before the first is used, x written once, the
+// row's sum of squares by DPP within each wave and four floats of LDS across the waves.
+template <typename OT, bool X2, int NV, int KS>
+__global__ __launch_bounds__(256) void k_splitk_resid_rmsnorm(const float* __restrict__ ws, uint32_t rows,
+                                                              float* __restrict__ x, const float* __restrict__ gamma,
+                                                              float eps, OT* __restrict__ out) {
+    constexpr uint32_t d = 1024 * NV;
+    __shared__ float red[4];
+    const uint32_t t = threadIdx.x;
+    const size_t base = (size_t)blockIdx.x * d;
+    const uint64_t MN = (uint64_t)rows * d;
+    float4v v[NV], g[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) v[j] = *reinterpret_cast<const float4v*>(ws + base + (j * 256 + t) * 4);
+#pragma unroll
+    for (int k = 1; k < KS; ++k)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) v[j] += *reinterpret_cast<const float4v*>(ws + k * MN + base + (j * 256 + t) * 4);
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+        g[j] = gamma ? *reinterpret_cast<const float4v*>(gamma + (j * 256 + t) * 4) : float4v{1.f, 1.f, 1.f, 1.f};
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        float4v* xp = reinterpret_cast<float4v*>(x + base + (j * 256 + t) * 4);
+        v[j] = *xp + v[j];
+        *xp = v[j];
+        ss += v[j][0] * v[j][0] + v[j][1] * v[j][1] + v[j][2] * v[j][2] + v[j][3] * v[j][3];
+    }
+    ss = wave_sum_dpp(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)d + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const size_t o = base + (j * 256 + t) * 4;
+        const float4v y = float4v{v[j][0] * inv * g[j][0], v[j][1] * inv * g[j][1], v[j][2] * inv * g[j][2],
+                                  v[j][3] * inv * g[j][3]};
+        if constexpr (X2) {
+            vsl_half h0, h1, h2, h3, l0, l1, l2, l3;
+            split_f16(y[0], h0, l0);
+            split_f16(y[1], h1, l1);
+            split_f16(y[2], h2, l2);
+            split_f16(y[3], h3, l3);
+            *reinterpret_cast<half4*>(out + o) = half4{h0, h1, h2, h3};
+            *reinterpret_cast<half4*>(out + MN + o) = half4{l0, l1, l2, l3};
+        } else if constexpr (sizeof(OT) == 2) {
+            *reinterpret_cast<half4*>(out + o) = half4{(vsl_half)y[0], (vsl_half)y[1], (vsl_half)y[2], (vsl_half)y[3]};
+        } else {
+            *reinterpret_cast<float4v*>(out + o) = y;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // causal flash attention (prefill), fp16 in / fp16 out, fp32 softmax statistics
 // ---------------------------------------------------------------------------------------------
@@ -567,6 +677,18 @@ static uint32_t gemm_tiles(uint32_t M, uint32_t N) {
 
 constexpr uint32_t kDmaMinTiles = 192;
 
+// The K split launch_gemm takes for a shape and workspace (0: unsplit kernels).
+static uint32_t splitk_choice(uint32_t M, uint32_t N, uint32_t K, int epi, const float* ws, uint64_t ws_bytes) {
+    for (int cfg = 0; cfg < 2; ++cfg)
+        if (vsl_gemm_dma_tiles(cfg, M, N, K, epi) >= kDmaMinTiles) return 0;
+    if (!ws) return 0;
+    uint64_t need = 0;
+    const uint32_t ks = vsl_gemm_splitk_plan(M, N, K, epi, kDmaMinTiles, &need);
+    return ks && need <= ws_bytes ? ks : 0;
+}
+
+static bool aligned_to(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
 // Tile configuration by occupancy: the largest tiles that still give every CU a tile.
 template <int EPI>
 static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N, uint32_t K,
@@ -580,14 +702,10 @@ static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint
                        ? VSL_OK
                        : vsl_invalid("vsl_gemm_f16: shape %ux%ux%u does not fit the direct-to-LDS tiles", M, N, K);
     // otherwise, with a workspace, split K over enough blocks
-    if (ws) {
-        uint64_t need = 0;
-        const uint32_t ks = vsl_gemm_splitk_plan(M, N, K, EPI, kDmaMinTiles, &need);
-        if (ks && need <= ws_bytes) {
-            if (vsl_gemm_splitk_launch(ks, s, a, b, M, N, K, C, EPI, ax2, ws))
-                return vsl_invalid("vsl_gemm_f16: split-K epilogue %d", EPI);
-            return VSL_OK;
-        }
+    if (const uint32_t ks = splitk_choice(M, N, K, EPI, ws, ws_bytes)) {
+        if (vsl_gemm_splitk_launch(ks, s, a, b, M, N, K, C, EPI, ax2, ws))
+            return vsl_invalid("vsl_gemm_f16: split-K epilogue %d", EPI);
+        return VSL_OK;
     }
     const uint32_t tb = gemm_tiles<GemmBig, EPI>(M, N), tm = gemm_tiles<GemmMid, EPI>(M, N);
     const uint32_t ts = gemm_tiles<GemmSmall, EPI>(M, N);
@@ -645,31 +763,157 @@ extern "C" uint64_t vsl_gemm_f16_ws_bytes(uint32_t M, uint32_t N, uint32_t K, in
     return vsl_gemm_splitk_plan(M, N, K, epi, kDmaMinTiles, &need) ? need : 0;
 }
 
+// RoPE + Q/K/V split of KS partials (KS = 1: the finished projection), four columns per thread.
+template <int KS>
+static void launch_rope_split4(hipStream_t s, const float* ws, uint32_t S, uint32_t n_q, uint32_t n_kv, uint32_t hd,
+                               uint32_t pos0, const float* rc, const float* rsn, vsl_half* qo, bool qx2, void* kc,
+                               void* vc, bool kv32, uint32_t cap) {
+    const uint64_t quads = (uint64_t)S * (n_q + 2 * n_kv) * hd / 4;
+    const uint32_t grid = (uint32_t)((quads + 255) / 256);
+    if (!kv32) {
+        if (qx2) k_rope_split4<WF16, true, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap);
+        else k_rope_split4<WF16, false, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap);
+    } else {
+        if (qx2) k_rope_split4<WF32, true, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap);
+        else k_rope_split4<WF32, false, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap);
+    }
+}
+
+// Arguments of the RoPE + split step; VSL_OK or the error code (nothing launched on error).
+static int check_rope_split(const char* fn, const void* qkv, uint32_t S, uint32_t hd, uint32_t pos0,
+                            const float* rope_cos, const float* rope_sin, const void* q_out, int q_dtype,
+                            const void* kcache, const void* vcache, int kv_dtype, uint32_t cap) {
+    if (!qkv || !rope_cos || !rope_sin || !q_out || !kcache || !vcache) return vsl_invalid("%s: null pointer", fn);
+    if ((uint64_t)pos0 + S > cap) {
+        vsl_set_error("%s: positions %u..%u exceed capacity %u", fn, pos0, pos0 + S - 1, cap);
+        return VSL_E_CAPACITY;
+    }
+    if (hd % 2) return vsl_invalid("%s: odd head_dim", fn);
+    if (q_dtype != VSL_DT_F16 && q_dtype != VSL_DT_F16X2) return vsl_unsupported("%s: q dtype %d", fn, q_dtype);
+    if (kv_dtype != VSL_DT_F16 && kv_dtype != VSL_DT_F32) return vsl_unsupported("%s: kv dtype %d", fn, kv_dtype);
+    return VSL_OK;
+}
+
+// The four-column kernel's layout needs: hd % 4, 16-byte partials, 8-byte tables and q, caches
+// aligned to four elements.
+static bool rope_split4_fits(const void* ws, uint32_t hd, const float* rc, const float* rsn, const void* q,
+                             const void* kc, const void* vc, bool kv32) {
+    const uintptr_t ca = kv32 ? 16 : 8;
+    return hd % 4 == 0 && aligned_to(ws, 16) && aligned_to(rc, 8) && aligned_to(rsn, 8) && aligned_to(q, 8) &&
+           aligned_to(kc, ca) && aligned_to(vc, ca);
+}
+
 extern "C" int vsl_rope_split_append(const float* qkv, uint32_t S, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t pos0,
                                      const float* rope_cos, const float* rope_sin, void* q_out, int q_dtype,
                                      void* kcache, void* vcache, int kv_dtype, uint32_t cap, void* stream) {
-    if (!qkv || !rope_cos || !rope_sin || !q_out || !kcache || !vcache) return vsl_invalid("vsl_rope_split_append: null pointer");
+    if (const int rc = check_rope_split("vsl_rope_split_append", qkv, S, hd, pos0, rope_cos, rope_sin, q_out, q_dtype,
+                                        kcache, vcache, kv_dtype, cap))
+        return rc;
     if (S == 0) return VSL_OK;
-    if ((uint64_t)pos0 + S > cap) {
-        vsl_set_error("vsl_rope_split_append: positions %u..%u exceed capacity %u", pos0, pos0 + S - 1, cap);
-        return VSL_E_CAPACITY;
-    }
-    if (hd % 2) return vsl_invalid("vsl_rope_split_append: odd head_dim");
-    if (q_dtype != VSL_DT_F16 && q_dtype != VSL_DT_F16X2) return vsl_unsupported("vsl_rope_split_append: q dtype %d", q_dtype);
-    const uint64_t total = (uint64_t)S * (n_q + 2 * n_kv) * hd / 2;
-    const uint32_t grid = (uint32_t)std::min<uint64_t>((total + 255) / 256, 65536);
     hipStream_t s = static_cast<hipStream_t>(stream);
     vsl_half* qo = static_cast<vsl_half*>(q_out);
-    const bool x2 = q_dtype == VSL_DT_F16X2;
-    if (kv_dtype == VSL_DT_F16) {
+    const bool x2 = q_dtype == VSL_DT_F16X2, kv32 = kv_dtype == VSL_DT_F32;
+    if (rope_split4_fits(qkv, hd, rope_cos, rope_sin, q_out, kcache, vcache, kv32)) {
+        launch_rope_split4<1>(s, qkv, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap);
+        HIP_TRY(hipGetLastError());
+        return VSL_OK;
+    }
+    const uint64_t total = (uint64_t)S * (n_q + 2 * n_kv) * hd / 2;
+    const uint32_t grid = (uint32_t)std::min<uint64_t>((total + 255) / 256, 65536);
+    if (!kv32) {
         if (x2) k_rope_split<WF16, true><<<grid, 256, 0, s>>>(qkv, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, kcache, vcache, cap);
         else k_rope_split<WF16, false><<<grid, 256, 0, s>>>(qkv, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, kcache, vcache, cap);
-    } else if (kv_dtype == VSL_DT_F32) {
+    } else {
         if (x2) k_rope_split<WF32, true><<<grid, 256, 0, s>>>(qkv, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, kcache, vcache, cap);
         else k_rope_split<WF32, false><<<grid, 256, 0, s>>>(qkv, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, kcache, vcache, cap);
-    } else {
-        return vsl_unsupported("vsl_rope_split_append: kv dtype %d", kv_dtype);
     }
+    HIP_TRY(hipGetLastError());
+    return VSL_OK;
+}
+
+extern "C" int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uint32_t S, uint32_t K, int a_flags,
+                                            uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t pos0,
+                                            const float* rope_cos, const float* rope_sin, void* q_out, int q_dtype,
+                                            void* kcache, void* vcache, int kv_dtype, uint32_t cap, float* qkv,
+                                            void* workspace, uint64_t ws_bytes, void* stream) {
+    const char* fn = "vsl_gemm_f16_qkv_rope_append";
+    if (!A || !Wqkv) return vsl_invalid("%s: null pointer", fn);
+    if (a_flags & ~VSL_GEMM_A_X2) return vsl_invalid("%s: flags 0x%x", fn, a_flags);
+    if (const int rc = check_rope_split(fn, qkv, S, hd, pos0, rope_cos, rope_sin, q_out, q_dtype, kcache, vcache,
+                                        kv_dtype, cap))
+        return rc;
+    if (workspace && !aligned_to(workspace, 16)) return vsl_invalid("%s: workspace must be 16-byte aligned", fn);
+    if (S == 0) return VSL_OK;
+    const uint32_t N = (n_q + 2 * n_kv) * hd;
+    float* ws = static_cast<float*>(workspace);
+    const bool x2 = q_dtype == VSL_DT_F16X2, kv32 = kv_dtype == VSL_DT_F32;
+    const uint32_t ks = splitk_choice(S, N, K, VSL_EPI_STORE_F32, ws, ws ? ws_bytes : 0);
+    if (ks && rope_split4_fits(ws, hd, rope_cos, rope_sin, q_out, kcache, vcache, kv32)) {
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        vsl_half* qo = static_cast<vsl_half*>(q_out);
+        vsl_gemm_splitk_partials(ks, stream, A, Wqkv, S, N, K, (a_flags & VSL_GEMM_A_X2) != 0, ws);
+        switch (ks) {
+            case 2: launch_rope_split4<2>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
+            case 4: launch_rope_split4<4>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
+            default: launch_rope_split4<8>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
+        }
+        HIP_TRY(hipGetLastError());
+        return VSL_OK;
+    }
+    if (const int rc = gemm_f16(A, Wqkv, S, N, K, qkv, VSL_EPI_STORE_F32 | a_flags, ws, ws ? ws_bytes : 0, stream))
+        return rc;
+    return vsl_rope_split_append(qkv, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, q_out, q_dtype, kcache, vcache,
+                                 kv_dtype, cap, stream);
+}
+
+template <typename OT, bool X2, int NV>
+static void launch_resid_rmsnorm_nv(hipStream_t s, uint32_t ks, const float* ws, uint32_t rows, float* x,
+                                    const float* gamma, float eps, OT* out) {
+    switch (ks) {
+        case 2: k_splitk_resid_rmsnorm<OT, X2, NV, 2><<<rows, 256, 0, s>>>(ws, rows, x, gamma, eps, out); break;
+        case 4: k_splitk_resid_rmsnorm<OT, X2, NV, 4><<<rows, 256, 0, s>>>(ws, rows, x, gamma, eps, out); break;
+        default: k_splitk_resid_rmsnorm<OT, X2, NV, 8><<<rows, 256, 0, s>>>(ws, rows, x, gamma, eps, out); break;
+    }
+}
+
+template <typename OT, bool X2>
+static void launch_resid_rmsnorm(hipStream_t s, uint32_t ks, const float* ws, uint32_t rows, uint32_t d, float* x,
+                                 const float* gamma, float eps, OT* out) {
+    switch (d / 1024) {
+        case 1: launch_resid_rmsnorm_nv<OT, X2, 1>(s, ks, ws, rows, x, gamma, eps, out); break;
+        case 2: launch_resid_rmsnorm_nv<OT, X2, 2>(s, ks, ws, rows, x, gamma, eps, out); break;
+        case 4: launch_resid_rmsnorm_nv<OT, X2, 4>(s, ks, ws, rows, x, gamma, eps, out); break;
+        default: launch_resid_rmsnorm_nv<OT, X2, 8>(s, ks, ws, rows, x, gamma, eps, out); break;
+    }
+}
+
+extern "C" int vsl_gemm_f16_resid_rmsnorm(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K,
+                                          int a_flags, float* x, const float* gamma, float eps, void* xn,
+                                          int xn_dtype, void* workspace, uint64_t ws_bytes, void* stream) {
+    const char* fn = "vsl_gemm_f16_resid_rmsnorm";
+    if (!A || !B || !x || !xn || N == 0) return vsl_invalid("%s: bad arguments", fn);
+    if (a_flags & ~VSL_GEMM_A_X2) return vsl_invalid("%s: flags 0x%x", fn, a_flags);
+    if (xn_dtype != VSL_DT_F16 && xn_dtype != VSL_DT_F16X2 && xn_dtype != VSL_DT_F32)
+        return vsl_unsupported("%s: dtype %d", fn, xn_dtype);
+    if (workspace && !aligned_to(workspace, 16)) return vsl_invalid("%s: workspace must be 16-byte aligned", fn);
+    if (M == 0) return VSL_OK;
+    float* ws = static_cast<float*>(workspace);
+    const uint32_t ks = splitk_choice(M, N, K, VSL_EPI_RESID, ws, ws ? ws_bytes : 0);
+    const uint32_t nv = N / 1024;
+    const bool fused = ks && N % 1024 == 0 && (nv == 1 || nv == 2 || nv == 4 || nv == 8) && ks * nv <= 32 &&
+                       aligned_to(x, 16) && aligned_to(gamma, 16) && aligned_to(xn, xn_dtype == VSL_DT_F32 ? 16 : 8);
+    if (!fused) {
+        if (const int rc = gemm_f16(A, B, M, N, K, x, VSL_EPI_RESID | a_flags, ws, ws ? ws_bytes : 0, stream)) return rc;
+        return vsl_rmsnorm(x, gamma, M, N, eps, xn, xn_dtype, stream);
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    vsl_gemm_splitk_partials(ks, stream, A, B, M, N, K, (a_flags & VSL_GEMM_A_X2) != 0, ws);
+    if (xn_dtype == VSL_DT_F16)
+        launch_resid_rmsnorm<vsl_half, false>(s, ks, ws, M, N, x, gamma, eps, static_cast<vsl_half*>(xn));
+    else if (xn_dtype == VSL_DT_F16X2)
+        launch_resid_rmsnorm<vsl_half, true>(s, ks, ws, M, N, x, gamma, eps, static_cast<vsl_half*>(xn));
+    else
+        launch_resid_rmsnorm<float, false>(s, ks, ws, M, N, x, gamma, eps, static_cast<float*>(xn));
     HIP_TRY(hipGetLastError());
     return VSL_OK;
 }

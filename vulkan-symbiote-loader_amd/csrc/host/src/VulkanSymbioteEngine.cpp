@@ -642,22 +642,21 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
     const uint32_t sp = options_.prefill_split;
     const int n1 = (sp & 1) ? VSL_DT_F16X2 : VSL_DT_F16, qdt = (sp & 2) ? VSL_DT_F16X2 : VSL_DT_F16;
     const int odt = (sp & 4) ? VSL_DT_F16X2 : VSL_DT_F16, n2 = (sp & 8) ? VSL_DT_F16X2 : VSL_DT_F16;
-    const int g_qkv = VSL_EPI_STORE_F32 | ((sp & 1) ? VSL_GEMM_A_X2 : 0);
-    const int g_o = VSL_EPI_RESID | ((sp & 4) ? VSL_GEMM_A_X2 : 0);
+    const int a_qkv = (sp & 1) ? VSL_GEMM_A_X2 : 0, a_o = (sp & 4) ? VSL_GEMM_A_X2 : 0;
     const int g_gu = VSL_EPI_SWIGLU | ((sp & 8) ? VSL_GEMM_A_X2 : 0) | ((sp & 16) ? VSL_GEMM_C_X2 : 0);
-    const int g_dn = VSL_EPI_RESID | ((sp & 16) ? VSL_GEMM_A_X2 : 0);
+    const int a_dn = (sp & 16) ? VSL_GEMM_A_X2 : 0;
     uint32_t last_rows = 0;
     for (uint32_t c0 = 0; c0 < n_prompt; c0 += chunk_) {
         const uint32_t S = std::min(chunk_, n_prompt - c0);
         last_rows = S;
         check(vsl_embed(embed_, edt_, V, d, prompt_dev_ + c0, S, px_, stream_), "vsl_embed");
+        // every later layer's attention norm comes with the previous layer's down projection
+        check(vsl_rmsnorm(px_, layers_[0].attn_norm, S, d, eps, pxn_, n1, stream_), "vsl_rmsnorm");
         for (uint32_t l = 0; l < c.num_layers; ++l) {
             const Layer& y = layers_[l];
-            check(vsl_rmsnorm(px_, y.attn_norm, S, d, eps, pxn_, n1, stream_), "vsl_rmsnorm");
-            check(vsl_gemm_f16_ws(pxn_, y.wqkv, S, (nq + 2 * nkv) * hd, d, pqkv_, g_qkv, gws_, gws_bytes_, stream_),
-                  "gemm qkv");
-            check(vsl_rope_split_append(pqkv_, S, nq, nkv, hd, c0, rope_cos_, rope_sin_, pq_, qdt, y.kc, y.vc, kvdt_,
-                                        cap_, stream_), "vsl_rope_split_append");
+            check(vsl_gemm_f16_qkv_rope_append(pxn_, y.wqkv, S, d, a_qkv, nq, nkv, hd, c0, rope_cos_, rope_sin_, pq_,
+                                               qdt, y.kc, y.vc, kvdt_, cap_, pqkv_, gws_, gws_bytes_, stream_),
+                  "qkv + rope");
             if (config_.use_sparse_attention)
                 check(vsl_attn_prefill_window(pq_, qdt, y.kc, y.vc, S, c0, nq, nkv, hd, cap_, scale, pattn_, odt,
                                               config_.sparse_window_size, config_.sparse_global_tokens,
@@ -666,10 +665,17 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
             else
                 check(vsl_attn_prefill(pq_, qdt, y.kc, y.vc, S, c0, nq, nkv, hd, cap_, scale, pattn_, odt, stream_),
                       "vsl_attn_prefill");
-            check(vsl_gemm_f16_ws(pattn_, y.wo, S, d, nq * hd, px_, g_o, gws_, gws_bytes_, stream_), "gemm o");
-            check(vsl_rmsnorm(px_, y.ffn_norm, S, d, eps, pxn_, n2, stream_), "vsl_rmsnorm");
+            check(vsl_gemm_f16_resid_rmsnorm(pattn_, y.wo, S, d, nq * hd, a_o, px_, y.ffn_norm, eps, pxn_, n2, gws_,
+                                             gws_bytes_, stream_),
+                  "o + ffn norm");
             check(vsl_gemm_f16(pxn_, y.wgu, S, F, d, ph_, g_gu, stream_), "gemm gate/up");
-            check(vsl_gemm_f16_ws(ph_, y.wdown, S, d, F, px_, g_dn, gws_, gws_bytes_, stream_), "gemm down");
+            if (l + 1 < c.num_layers)
+                check(vsl_gemm_f16_resid_rmsnorm(ph_, y.wdown, S, d, F, a_dn, px_, layers_[l + 1].attn_norm, eps, pxn_,
+                                                 n1, gws_, gws_bytes_, stream_),
+                      "down + attention norm");
+            else
+                check(vsl_gemm_f16_ws(ph_, y.wdown, S, d, F, px_, VSL_EPI_RESID | a_dn, gws_, gws_bytes_, stream_),
+                      "gemm down");
         }
     }
     check(vsl_copy_d2d(x_, px_ + (size_t)(last_rows - 1) * d, (size_t)d * 4, stream_), "last row");
