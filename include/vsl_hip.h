@@ -194,7 +194,9 @@ int vsl_qkv_rope_append(const float* x, const float* gamma, float eps, const voi
 
 /* Flash-decode attention (attention.comp:116-189 semantics: softmax(q.k*scale) over positions
  * 0..ctrl->pos, GQA kv_head = head*n_kv/n_q): split-KV over `nsplit` chunks with online softmax,
- * then a combine launch.  Workspace: part_o [n_q][nsplit][hd] f32, part_ml [n_q][nsplit][2] f32. */
+ * then a combine launch.  Workspace: part_o [n_q][nsplit][hd] f32, part_ml [n_q][nsplit][2] f32.
+ * fp16 caches of head_dim 128 with more than 8192 positions of capacity run the scores on the
+ * matrix cores (the same results to fp32 rounding; faster from about 2K attended positions). */
 int vsl_attn_decode(const float* q, const void* kcache, const void* vcache, int kv_dtype, uint32_t n_q,
                     uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* part_o,
                     float* part_ml, float* out, vsl_ctrl* ctrl, void* stream);

@@ -179,6 +179,34 @@ def test_attn_decode(vsl, orc, dev, H, kvdt, hd, nq, nkv, length, nsplit):
     assert rel_err(dev.get(out), ref) < 2e-5
 
 
+@pytest.mark.parametrize("nq", [32, 8, 16, 64])
+@pytest.mark.parametrize("length", [1, 5, 17, 300, 1025, 9000, 16384])
+@pytest.mark.parametrize("nsplit", [32, 1, 7, 100])
+def test_attn_decode_long_cache(vsl, orc, dev, H, nq, length, nsplit):
+    """fp16 caches of head_dim 128 above 8192 positions of capacity run the matrix-core kernel (scores
+    from hi + lo fp16 planes of q on MFMA, 16-position tiles per wave): against the oracle for GQA
+    groups of 4, 1, 2 and 8 heads, lengths from one position to the full cache, the split counts of
+    the short-cache test."""
+    if nsplit != 32 and nq != 32:
+        pytest.skip("split sweep runs on the 8B head layout")
+    if length == 16384 and nsplit == 1:
+        pytest.skip("one block over the whole cache: covered at 9000 positions")
+    nkv, hd, cap = 8, 128, 16384
+    rng = np.random.default_rng(length * 7 + nq + nsplit)
+    K = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16)
+    V = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16)
+    q = rng.normal(0, 1, nq * hd).astype(np.float32)
+    scale = 1.0 / math.sqrt(hd)
+    po = dev.empty((nq * nsplit * hd,), np.float32)
+    pml = dev.empty((nq * nsplit * 2,), np.float32)
+    out = dev.empty((nq * hd,), np.float32)
+    c = ctrl_buf(vsl, dev, H, length - 1, cap=cap)
+    ok(vsl, H.vsl_attn_decode(dev.p(dev.put(q)), dev.p(dev.put(K)), dev.p(dev.put(V)), 1, nq, nkv, hd, cap, scale,
+                              nsplit, dev.p(po), dev.p(pml), dev.p(out), dev.p(c), None))
+    ref = orc.attention_decode(q, K.astype(np.float32), V.astype(np.float32), nq, nkv, hd, cap, length, scale)
+    assert rel_err(dev.get(out), ref) < 2e-5
+
+
 @pytest.mark.parametrize("kvdt,hd,nq,nkv", [(1, 128, 32, 8), (0, 64, 4, 4)])
 @pytest.mark.parametrize("length,window,n_glob,thr", [
     (300, 64, 4, 100),    # windowed: globals 0..3 and keys 235..299

@@ -822,6 +822,220 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_decode(const float* __restr
     }
 }
 
+// Flash-decode on the matrix cores, for fp16 caches with head_dim 128 and G <= 8 query heads per KV
+// head. Block (split s, KV head h) of WAVES waves; a wave owns 16-position tiles: block tile j holds
+// positions [(j * nsplit + s) * 16 WAVES, + 16 WAVES), wave w the w-th 16 of them. Per tile:
+//  - scores S = Q K^T by v_mfma_f32_16x16x32_f16 over the four 32-dim k-steps, twice: A = the G query
+//    rows (zero-padded to 16) as the hi and the lo fp16 planes of q * scale * log2(e), so the products
+//    are those of the fp32 q; B = the tile's K rows, lane l holding position l % 16, dims
+//    32 ks + 8 (l / 16) .. + 7 (its own 16-byte loads). D holds head 4 (l / 16) + i, position l % 16
+//    in register i of lane l, so each head's 16 scores lie on one 16-lane row;
+//  - the online softmax of each head on its row (DPP maximum, exp2): the running maximum is the same
+//    in every lane of the row, the running sum is kept per lane and summed over the row at the end;
+//  - the probabilities and each head's rescale factor go through the wave's 1 KB of LDS to every
+//    lane, and lane l accumulates head dims 2l and 2l + 1 of every head from its 4-byte V loads (a
+//    256-byte cache row per load instruction), fp32 FMAs on the fp16 values.
+// Against k_attn_decode (16 lanes per position, 8 dims per lane) a wave handles 16 positions per tile
+// instead of 4 and drops the per-head lane-group sums. Tiles are requested two ahead in registers as
+// there; positions at or past the length load position 0 and get probability 0. The output is
+// k_attn_decode's: per head of the split, (m, l) and the unnormalised sum, merged by k_attn_combine.
+template <int G, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void k_attn_decode_mfma(const float* __restrict__ q,
+                                                                 const vsl_half* __restrict__ kcache,
+                                                                 const vsl_half* __restrict__ vcache, uint32_t cap,
+                                                                 float scale, uint32_t nsplit,
+                                                                 float* __restrict__ part_o,
+                                                                 float* __restrict__ part_ml, vsl_ctrl* ctrl) {
+    constexpr int HD = 128, KS = HD / 32, TP = 16;  // k-steps, positions per wave tile
+    constexpr uint32_t TB = TP * WAVES;             // positions per block tile
+    constexpr int NR = (G + 3) / 4;                 // 16-lane rows holding heads (four per row)
+    static_assert(G >= 1 && G <= 8, "GQA group of 1..8 heads");
+    __shared__ __attribute__((aligned(16))) float s_p[WAVES][TP][8];  // probabilities [position][head]
+    __shared__ __attribute__((aligned(16))) float s_c[WAVES][8];      // rescale factor per head
+    __shared__ float s_ml[WAVES][G][2];
+    __shared__ float s_acc[WAVES][G][HD];
+
+    const uint32_t kvh = blockIdx.y, split = blockIdx.x;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t col = lane & 15, rg = lane >> 4;  // MFMA column (tile position / A row), row group
+    const uint32_t h0 = kvh * G;
+    const vsl_half* Kb = kcache + (size_t)kvh * cap * HD;
+    const vsl_half* Vb = vcache + (size_t)kvh * cap * HD;
+
+    struct Tile {
+        uint4 k[KS];
+        uint32_t v[TP];
+    };
+    auto tile_pos = [&](uint32_t j) { return (j * nsplit + split) * TB + wave * TP; };
+    // positions at or past `limit` read position 0 instead (in bounds)
+    auto issue = [&](Tile& b, uint32_t j, uint32_t limit) {
+        const uint32_t p0 = tile_pos(j);
+        const uint32_t t = p0 + col < limit ? p0 + col : 0;
+        const vsl_half* kp = Kb + (size_t)t * HD + rg * 8;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) b.k[ks] = load16<false>(kp + 32 * ks);
+#pragma unroll
+        for (int i = 0; i < TP; ++i) {
+            const uint32_t tv = p0 + i < limit ? p0 + i : 0;
+            b.v[i] = *reinterpret_cast<const uint32_t*>(Vb + (size_t)tv * HD + 2 * lane);
+        }
+    };
+
+    // A operands (lane l: query row l % 16, dims 32 ks + 8 (l / 16) .. + 7), requested with the first
+    // two tiles before the control block is read
+    float4 qa[KS][2];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        if (col < (uint32_t)G) {
+            const float* qp = q + (size_t)(h0 + col) * HD + 32 * ks + 8 * rg;
+            qa[ks][0] = *reinterpret_cast<const float4*>(qp);
+            qa[ks][1] = *reinterpret_cast<const float4*>(qp + 4);
+        } else {
+            qa[ks][0] = qa[ks][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    Tile ta, tb;
+    issue(ta, 0, cap);
+    issue(tb, 1, cap);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t done = ctrl->done;
+    const uint32_t pos = ctrl->pos;
+    const uint32_t n_att = pos < cap ? pos + 1 : cap;  // pos >= cap only with done set
+
+    half8 qh[KS], ql[KS];
+    const float f = scale * kLog2e;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const float x[8] = {qa[ks][0].x * f, qa[ks][0].y * f, qa[ks][0].z * f, qa[ks][0].w * f,
+                            qa[ks][1].x * f, qa[ks][1].y * f, qa[ks][1].z * f, qa[ks][1].w * f};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            vsl_half hi, lo;
+            split_f16(x[e], hi, lo);
+            qh[ks][e] = hi;
+            ql[ks][e] = lo;
+        }
+    }
+    float m[4], ls[4], acc[G][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        m[i] = -INFINITY;
+        ls[i] = 0.f;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
+
+    auto consume = [&](const Tile& b, uint32_t j) {
+        float4v s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const half8 kk = __builtin_bit_cast(half8, b.k[ks]);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[ks], kk, s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[ks], kk, s, 0, 0, 0);
+        }
+        const bool valid = tile_pos(j) + col < n_att;
+        float pr[4], corr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x = valid ? s[i] : -INFINITY;
+            const float mn = fmaxf(m[i], row_max16_dpp(x));
+            // mn = -inf: no valid key in this row yet (everything is still 0)
+            corr[i] = mn == -INFINITY ? 1.f : fast_exp2(m[i] - mn);
+            pr[i] = valid ? fast_exp2(x - mn) : 0.f;
+            ls[i] = fmaf(ls[i], corr[i], pr[i]);
+            m[i] = mn;
+        }
+        if (rg < (uint32_t)NR) {
+            *reinterpret_cast<float4*>(&s_p[wave][col][4 * rg]) = make_float4(pr[0], pr[1], pr[2], pr[3]);
+            if (col == 0) *reinterpret_cast<float4*>(&s_c[wave][4 * rg]) = make_float4(corr[0], corr[1], corr[2], corr[3]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        float c[8];
+        *reinterpret_cast<float4*>(c) = *reinterpret_cast<const float4*>(&s_c[wave][0]);
+        if constexpr (G > 4) *reinterpret_cast<float4*>(c + 4) = *reinterpret_cast<const float4*>(&s_c[wave][4]);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            acc[g][0] *= c[g];
+            acc[g][1] *= c[g];
+        }
+#pragma unroll
+        for (int i = 0; i < TP; ++i) {
+            float pp[8];
+            *reinterpret_cast<float4*>(pp) = *reinterpret_cast<const float4*>(&s_p[wave][i][0]);
+            if constexpr (G > 4) *reinterpret_cast<float4*>(pp + 4) = *reinterpret_cast<const float4*>(&s_p[wave][i][4]);
+            const half2v vv = __builtin_bit_cast(half2v, b.v[i]);
+            const float v0 = (float)vv[0], v1 = (float)vv[1];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                acc[g][0] = fmaf(pp[g], v0, acc[g][0]);
+                acc[g][1] = fmaf(pp[g], v1, acc[g][1]);
+            }
+        }
+        // every lane has read this tile's values before the next tile's stores
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    };
+
+    const uint32_t total = (n_att + TB - 1) / TB;  // block tiles holding positions < n_att
+    const uint32_t mine = total > split ? (total - 1 - split) / nsplit + 1 : 0;
+    // pairs with a single loop exit; the last pair (peeled) is consumed without refills so that no
+    // load is outstanding past it (tiles past the block's own are masked: positions >= n_att)
+    const uint32_t n_pairs = mine ? (mine + 1) / 2 : 1;
+    for (uint32_t pp = 0; pp + 1 < n_pairs; ++pp) {
+        consume(ta, 2 * pp);
+        issue(ta, 2 * pp + 2, n_att);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(tb, 2 * pp + 1);
+        issue(tb, 2 * pp + 3, n_att);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    consume(ta, 2 * n_pairs - 2);
+    consume(tb, 2 * n_pairs - 1);
+
+    // the wave's totals: sums over each row, maxima already row-uniform
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ls[i] = group_sum_dpp<16>(ls[i]);
+    if (col == 0 && rg < (uint32_t)NR) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t g = 4 * rg + i;
+            if (g < (uint32_t)G) {
+                s_ml[wave][g][0] = m[i];
+                s_ml[wave][g][1] = ls[i];
+            }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) *reinterpret_cast<float2*>(&s_acc[wave][g][2 * lane]) = make_float2(acc[g][0], acc[g][1]);
+    lds_barrier();
+    for (uint32_t e = threadIdx.x; e < (uint32_t)(G * HD); e += WAVES * 64) {
+        const uint32_t g = e / HD, dd = e % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) M = fmaxf(M, s_ml[w][g][0]);
+        float L = 0.f, A = 0.f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                const float fw = exp2f(s_ml[w][g][0] - M);
+                L += s_ml[w][g][1] * fw;
+                A += s_acc[w][g][dd] * fw;
+            }
+        }
+        const size_t pidx = (size_t)(h0 + g) * nsplit + split;
+        if (!done) {
+            part_o[pidx * HD + dd] = A;
+            if (dd == 0) {
+                part_ml[pidx * 2 + 0] = M;
+                part_ml[pidx * 2 + 1] = L;
+            }
+        }
+    }
+}
+
 // Combines the nsplit partials of every query head: out = sum_s A_s 2^(m_s-M) / sum_s l_s 2^(m_s-M).
 // One block per head. Up to kFastSplits splits, every partial is requested at once (before the
 // control block is read) and held in registers; larger split counts loop over the splits.
@@ -927,6 +1141,13 @@ struct AttnWindow {
 // workload against 4 x 2, 8 x 1 and 8 x 2 at 1K and 8K context: more positions per block lengthen
 // the per-block latency chain more than they save in block count).
 constexpr int kAttnWaves = 4, kAttnP = 1;
+// Caches of more than kAttnMfmaMinCap positions (fp16, head_dim 128, dense) take k_attn_decode_mfma
+// with 4 waves per block. Attention kernel alone at 32 splits, 8B shapes: 600 / 2000 / 8200 / 16000 /
+// 32000 positions 5.25 / 6.11 / 11.60 / 16.63 / 28.86 us for k_attn_decode and 6.05 / 6.09 / 9.51 /
+// 14.05 / 22.42 us for k_attn_decode_mfma: the launch is captured before the length is known, so
+// the capacity picks the kernel.
+constexpr uint32_t kAttnMfmaMinCap = 8192;
+constexpr int kAttnMfmaWaves = 4;
 
 template <class KT, int HD, int G, bool WIN, int WAVES, int P>
 void launch_attn_shape(dim3 grid, hipStream_t s, const float* q, const void* kc, const void* vc, uint32_t n_q,
@@ -940,6 +1161,13 @@ template <class KT, int HD, int G>
 void launch_attn_w(dim3 grid, hipStream_t s, const float* q, const void* kc, const void* vc, uint32_t n_q,
                    uint32_t n_kv, uint32_t cap, float scale, uint32_t nsplit, float* po, float* pml, vsl_ctrl* ctrl,
                    const AttnWindow& w) {
+    if constexpr (HD == 128 && G <= 8 && sizeof(typename KT::T) == 2) {
+        if (!w.on && cap > kAttnMfmaMinCap) {
+            k_attn_decode_mfma<G, kAttnMfmaWaves><<<grid, kAttnMfmaWaves * 64, 0, s>>>(
+                q, static_cast<const vsl_half*>(kc), static_cast<const vsl_half*>(vc), cap, scale, nsplit, po, pml, ctrl);
+            return;
+        }
+    }
     if (w.on)
         launch_attn_shape<KT, HD, G, true, kAttnWaves, kAttnP>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml,
                                                                ctrl, w);

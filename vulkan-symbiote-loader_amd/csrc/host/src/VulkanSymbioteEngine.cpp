@@ -276,7 +276,7 @@ void VulkanSymbioteEngine::init_device(const ModelConfig& cfg, bool fp16_weights
     if (cfg.hidden_size % 8 || cfg.intermediate_size % 8) throw std::runtime_error("hidden/ffn sizes must be multiples of 8");
     cap_ = options_.kv_capacity ? options_.kv_capacity : std::min<uint32_t>(cfg.max_position_embeddings ? cfg.max_position_embeddings : 4096, 4096);
     if (cap_ == 0) throw std::runtime_error("KV capacity must be positive");
-    nsplit_ = options_.attn_splits ? options_.attn_splits : (cap_ <= 8192 ? 32u : 64u);
+    nsplit_ = options_.attn_splits ? options_.attn_splits : 32u;
     int ndev = 0;
     check(vsl_device_count(&ndev), "vsl_device_count");
     if (ndev <= options_.device) throw std::runtime_error("no HIP device " + std::to_string(options_.device));

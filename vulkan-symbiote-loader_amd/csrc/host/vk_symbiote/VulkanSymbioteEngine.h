@@ -65,7 +65,7 @@ struct EngineOptions {
     uint32_t kv_capacity = 0;     // 0 = min(max_position_embeddings, 4096)
     bool use_graph = true;        // capture each decode step once, replay it
     uint32_t prefill_chunk = 2048;
-    uint32_t attn_splits = 0;     // 0 = chosen from the capacity
+    uint32_t attn_splits = 0;     // 0 = 32 splits
     bool batched_prefill = true;  // fp16 models: MFMA prefill (else token by token)
     // Which prefill activations are carried as hi/lo fp16 pairs (two MFMAs per tile, ~22-bit
     // inputs) instead of one rounded fp16 value: bit 0 QKV GEMM input, bit 1 attention (q and the
