@@ -475,18 +475,20 @@ __global__ __launch_bounds__(kFinishThreads) void k_argmax_finish(const float* _
 }
 
 // Upper bound on a decode GEMV's grid: blocks-per-CU x the current device's CU count, by default the
-// blocks that keep 16 waves per CU (one resident round); VSL_GEMV_BLOCKS_PER_CU overrides it and 0
-// removes the bound. A bounded grid strides over the row groups, staging the activation vector once
-// per block instead of once per few groups.
-uint32_t gemv_grid_cap(int waves) {
+// blocks that keep 16 waves per CU (one resident round), 8 for the QKV GEMV (measured on the 8B
+// step at 8 / 12 / 16 / 24 / 32 waves per CU and no bound: QKV 10.08 / 10.69 / 10.64 / 10.67 /
+// 10.67 / 10.65 us, the other GEMVs best or level at 16); VSL_GEMV_BLOCKS_PER_CU overrides it for
+// every GEMV and 0 removes the bound. A bounded grid strides over the row groups, staging the
+// activation vector once per block instead of once per few groups.
+uint32_t gemv_grid_cap(int waves, int epi) {
     static int per_cu_env = -2;
     if (per_cu_env == -2) {
         const char* e = getenv("VSL_GEMV_BLOCKS_PER_CU");
         per_cu_env = e ? atoi(e) : -1;
         if (e && per_cu_env < 0) per_cu_env = 0;
     }
-    // default: 16 resident waves per CU
-    const int per_cu = per_cu_env >= 0 ? per_cu_env : (waves >= 16 ? 1 : 16 / waves);
+    const int resident = epi == EPI_QKV ? 8 : 16;  // default waves per CU
+    const int per_cu = per_cu_env >= 0 ? per_cu_env : (waves >= resident ? 1 : resident / waves);
     if (per_cu == 0) return 0xFFFFFFFFu;
     static int cus[64] = {0};
     int dev = 0;
@@ -505,7 +507,7 @@ uint32_t gemv_blocks(uint32_t N, uint32_t max_blocks) {
     const uint32_t groups = (N + RG - 1) / RG;
     uint32_t blocks = (groups + WAVES - 1) / WAVES;
     if (blocks > max_blocks) blocks = max_blocks;
-    const uint32_t cap = gemv_grid_cap(WAVES);
+    const uint32_t cap = gemv_grid_cap(WAVES, EPI);
     if (blocks > cap) blocks = cap;
     return blocks == 0 ? 1 : blocks;
 }
