@@ -1,7 +1,8 @@
 // vsl_gemm_dma.hip -- prefill GEMM with direct-to-LDS loads: C[M][N] = A[M][K] * B[N][K]^T on
 // v_mfma_f32_32x32x16_f16, for the shapes whose tiles fill the chip.
 //
-// Pipeline: BK = 32 per stage, four LDS stage buffers (separate __shared__ arrays). Stage s + 3 is
+// Pipeline: BK = 32 (64 for the split 128 x 256 tile) per stage, up to four LDS stage buffers
+// (separate __shared__ arrays). Stage s + 3 is
 // requested with global_load_lds_dwordx4 (64 lanes x 16 bytes straight into LDS, no register
 // staging and no ds_write) while stage s is computed; before computing stage s a wave waits for
 // its own loads of that stage (s_waitcnt vmcnt with the two younger stages still in flight) and
@@ -302,15 +303,17 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
     }
 }
 
-template <int BM, int BN, int TWGM = 2, int TWGN = 2>
+template <int BM, int BN, int TWGM = 2, int TWGN = 2, int TBK = 32>
 struct DmaPair {  // the one-plane and the split-A configuration of a block tile
     using One = DmaCfg<BM, BN, 32, 1>;
-    using Two = DmaCfg<BM, BN, 32, 2, TWGM, TWGN>;
+    using Two = DmaCfg<BM, BN, TBK, 2, TWGM, TWGN>;
 };
 // The split-A tiles run eight waves (two per SIMD, 128 accumulators each): 4 x 2 waves of 64 x 128 for
-// 256 x 256, 2 x 4 waves of 64 x 64 for 128 x 256 (the one-plane tiles keep 2 x 2 waves of 128 x 128)
+// 256 x 256, 2 x 4 waves of 64 x 64 for 128 x 256 (the one-plane tiles keep 2 x 2 waves of 128 x 128).
+// The split 128 x 256 tile takes BK = 64 (two 64 KB stages, half the barriers): the K-split partials
+// of a 512-row chunk, O 37.8 -> 36.6 us, down 109.9 -> 104.5 us, QKV level.
 using DmaBig = DmaPair<256, 256, 4, 2>;
-using DmaMid = DmaPair<128, 256, 2, 4>;
+using DmaMid = DmaPair<128, 256, 2, 4, 64>;
 
 template <class G, int EPI>
 uint32_t dma_tiles(uint32_t M, uint32_t N) {
