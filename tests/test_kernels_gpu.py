@@ -842,3 +842,46 @@ def test_gemm_resid_rmsnorm_bad_arguments(vsl, dev, H):
                                         None, 0, None) == vsl.VSL_E_INVALID
     assert H.vsl_gemm_f16_resid_rmsnorm(dev.p(A), None, 8, 1024, 512, 0, dev.p(x), None, 1e-5, dev.p(xn), 1,
                                         None, 0, None) == vsl.VSL_E_INVALID
+
+
+def test_fused_prefill_entries_misaligned_outputs(vsl, orc, dev, H):
+    """Output buffers that are not 8-byte aligned take the unfused kernels (scalar RoPE split, residual
+    GEMM + row RMSNorm); their results agree with the aligned fused path: residual rows exactly,
+    normalized rows and q / k / v to fp32 rounding."""
+    rng = np.random.default_rng(99)
+    S, K, nq, nkv, hd, pos0, cap = 512, 4096, 32, 8, 128, 3, 1024
+    N = (nq + 2 * nkv) * hd
+    Ad, _ = _act(rng, S, K, True)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    cs, sn = rope_tables(cap, hd, 500000.0)
+    need = max(H.vsl_gemm_f16_ws_bytes(S, N, K, 0), H.vsl_gemm_f16_ws_bytes(S, 4096, K, 2))
+    ws = dev.empty((need // 4,), np.float32)
+    dA, dW, dcs, dsn = dev.put(Ad), dev.put(W), dev.put(cs), dev.put(sn)
+    qkv = dev.empty((S, N), np.float32)
+    res = []
+    for off in (0, 2):  # byte offset of q_out: 0 (fused path) or 2 (scalar fallback)
+        qbuf = dev.empty((2 * S * nq * hd + 8,), np.float16)
+        kc, vc = dev.empty((nkv, cap, hd), np.float16), dev.empty((nkv, cap, hd), np.float16)
+        ok(vsl, H.vsl_gemm_f16_qkv_rope_append(dev.p(dA), dev.p(dW), S, K, 0x100, nq, nkv, hd, pos0, dev.p(dcs),
+                                               dev.p(dsn), dev.p(qbuf) + off, 2, dev.p(kc), dev.p(vc), 1, cap,
+                                               dev.p(qkv), dev.p(ws), need, None))
+        q = dev.get(qbuf).view(np.uint8)[off:off + 2 * S * nq * hd * 2].view(np.float16).astype(np.float64)
+        res.append((q[:S * nq * hd] + q[S * nq * hd:], dev.get(kc).astype(np.float64), dev.get(vc).astype(np.float64)))
+    assert rel_err(res[1][0], res[0][0]) < 1e-6  # q as hi + lo carries the fp32 value
+    for a, b in zip(res[0][1:], res[1][1:]):
+        assert rel_err(b, a) < 2.0 ** -10  # fp16 caches: a last-bit fp32 difference can flip a rounding
+    # residual + RMSNorm into a misaligned fp16 output
+    B = rng.normal(0, 0.02, (4096, K)).astype(np.float16)
+    x0 = rng.normal(0, 1, (S, 4096)).astype(np.float32)
+    g = rng.normal(1, 0.1, 4096).astype(np.float32)
+    dB, dg = dev.put(B), dev.put(g)
+    out = []
+    for off in (0, 2):
+        x = dev.put(x0)
+        xbuf = dev.empty((S * 4096 + 8,), np.float16)
+        ok(vsl, H.vsl_gemm_f16_resid_rmsnorm(dev.p(dA), dev.p(dB), S, 4096, K, 0x100, dev.p(x), dev.p(dg), 1e-5,
+                                             dev.p(xbuf) + off, 1, dev.p(ws), need, None))
+        xn = dev.get(xbuf).view(np.uint8)[off:off + S * 4096 * 2].view(np.float16).astype(np.float64)
+        out.append((dev.get(x), xn))
+    assert np.array_equal(out[0][0], out[1][0])
+    assert rel_err(out[1][1], out[0][1]) < 2.0 ** -10
