@@ -416,11 +416,12 @@ __global__ __launch_bounds__(256) void k_splitk_resid_rmsnorm(const float* __res
 // Causal flash attention for one chunk of S prompt rows at positions pos0.. (their K/V already in
 // the cache). Block = the G query heads of one KV head x 32 query rows, one wave per head: each
 // 64-position K/V tile is copied once for all G heads straight from the cache into LDS
-// (global_load_lds, two tile buffers, the next tile requested before the current one is computed),
-// both row-major with the chunk swizzle of ksw. Per tile each wave computes S^T = K Q^T (two
-// 32-position fragments), the online softmax of its 32 query rows (each lane owns one row's
-// statistics with its partner lane l^32), and O^T += V^T P^T, whose V^T operand is gathered from
-// the row-major V tile (eight 2-byte reads per fragment, spread over the banks by the swizzle).
+// (global_load_lds, three tile buffers, each tile requested two tiles ahead), both row-major with the
+// chunk swizzle of ksw. Per tile each wave computes S^T = K Q^T (two 32-position fragments), the
+// online softmax of its 32 query rows (each lane owns one row's statistics with its partner lane
+// l^32), and O^T += V^T P^T, whose V^T operand comes from the row-major V tile through LDS
+// transpose reads. The next tile's S^T is issued on the matrix cores while the current tile's
+// probabilities are computed on the VALU.
 constexpr int kAttnTile = 64;  // KV positions per tile
 
 template <int HD>
@@ -441,8 +442,8 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     constexpr int NCH = TK * CPR / NT;          // chunks per thread per tile (K and V each)
     constexpr int QP = QX2 ? 2 : 1;             // q planes; with split q the probabilities are split too
     static_assert(NCH >= 1 && TK * CPR % NT == 0, "tile does not divide over the block");
-    __shared__ __attribute__((aligned(16))) vsl_half Ks[2][TK * HD];
-    __shared__ __attribute__((aligned(16))) vsl_half Vs[2][TK * HD];
+    __shared__ __attribute__((aligned(16))) vsl_half Ks[3][TK * HD];
+    __shared__ __attribute__((aligned(16))) vsl_half Vs[3][TK * HD];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n_qb = gridDim.x;
     const uint32_t qb = n_qb - 1 - blockIdx.x;  // the longest (latest) query blocks start first
@@ -518,9 +519,8 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     // it by more than kLazy (log2 units) in some lane of the wave, so every probability stays below
     // 2^kLazy and most tiles skip the rescale. The quotient O / l does not depend on m.
     constexpr float kLazy = 8.f;
-    auto compute = [&](int buf, uint32_t t) {
-        // S^T[kv][q] = sum_d K[kv][d] Q[q][d] for the tile's two 32-position halves
-        float16v st[2];
+    // S^T[kv][q] = sum_d K[kv][d] Q[q][d] for the two 32-position halves of the tile in `buf`
+    auto qk = [&](int buf, float16v (&st)[2]) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -534,27 +534,35 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
 #pragma unroll
                 for (int p = 0; p < QP; ++p) st[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[c], qf[p][c], st[kb], 0, 0, 0);
         }
-        // causal (and window) mask, only on tiles that reach past the block's first row
-        const bool full = !WIN && t * TK + TK - 1 <= p_first;
+    };
+    // scaled scores of tile t with the causal (and window) mask, applied only on tiles that reach past
+    // the block's first row; returns the tile maximum of this lane's row
+    auto mask_max = [&](float16v (&st)[2], uint32_t t) {
         float bm = -INFINITY;
+        if (!WIN && t * TK + TK - 1 <= p_first) {  // wave-uniform: no row of the block is cut by this tile
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                float sc = st[kb][v] * sl2;
-                if (!full) {
+                for (int v = 0; v < 16; ++v) {
+                    st[kb][v] *= sl2;
+                    bm = fmaxf(bm, st[kb][v]);
+                }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
                     const uint32_t kvp = t * TK + kb * 32 + d_row(v, lane);
                     const bool seen = WIN ? kvp <= my_pos && (kvp >= my_lo || kvp < n_glob) : kvp <= my_pos;
-                    sc = seen ? sc : -INFINITY;
+                    st[kb][v] = seen ? st[kb][v] * sl2 : -INFINITY;
+                    bm = fmaxf(bm, st[kb][v]);
                 }
-                st[kb][v] = sc;
-                bm = fmaxf(bm, sc);
-            }
-        {
-            float ba, bb;
-            lane_pair<32>(bm, ba, bb);
-            bm = fmaxf(ba, bb);
         }
+        float ba, bb;
+        lane_pair<32>(bm, ba, bb);
+        return fmaxf(ba, bb);
+    };
+    auto rescale = [&](float bm) {
         const bool raise = bm > m + kLazy;  // m = -inf: any finite tile maximum raises it
         if (__builtin_amdgcn_ballot_w64(raise)) {
             const float mn = raise ? bm : m;
@@ -566,8 +574,11 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
 #pragma unroll
                 for (int v = 0; v < 16; ++v) o[tt][v] *= corr;
         }
+    };
+    // probabilities 2^(score - m) as the P^T operand (split into hi / lo planes with a split q);
+    // returns their sum over the tile for this lane's row
+    auto probs = [&](const float16v (&st)[2], half8 (&pf)[QP][2][2]) {
         float ps = 0.f;
-        half8 pf[QP][2][2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -583,18 +594,17 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
                     pf[0][kb][v >> 3][v & 7] = (vsl_half)pv;
                 }
             }
-        {
-            float pa, pb;
-            lane_pair<32>(ps, pa, pb);
-            ps = pa + pb;
-        }
-        l += ps;
-        // O^T[dim][q] += sum_kv V^T[dim][kv] P^T[kv][q]; P^T slots v = 0..7 / 8..15 of each half are
-        // the kv rows (v/4)*8 + (l/32)*4 + v%4, which the V^T operand reads to match: lane l needs
-        // V[r0 + j][dim] and V[r0 + 8 + j][dim] (j = 0..3) for dim = 32 tt + l%32, r0 = 32 kb + 16 hi
-        // + 4 (l/32). ds_read_b64_tr_b16 gives lane i of a 16-lane group element i%4 of the 8-byte
-        // row addressed by lane 4j + i/4 of the group as its value j, so lane i addresses
-        // V[r0 + i/4][d0 + 4 (i%4) .. +3] with d0 the group's first dim: value j is V[r0 + j][d0 + i].
+        float pa, pb;
+        lane_pair<32>(ps, pa, pb);
+        return pa + pb;
+    };
+    // O^T[dim][q] += sum_kv V^T[dim][kv] P^T[kv][q]; P^T slots v = 0..7 / 8..15 of each half are
+    // the kv rows (v/4)*8 + (l/32)*4 + v%4, which the V^T operand reads to match: lane l needs
+    // V[r0 + j][dim] and V[r0 + 8 + j][dim] (j = 0..3) for dim = 32 tt + l%32, r0 = 32 kb + 16 hi
+    // + 4 (l/32). ds_read_b64_tr_b16 gives lane i of a 16-lane group element i%4 of the 8-byte
+    // row addressed by lane 4j + i/4 of the group as its value j, so lane i addresses
+    // V[r0 + i/4][d0 + 4 (i%4) .. +3] with d0 the group's first dim: value j is V[r0 + j][d0 + i].
+    auto pv = [&](int buf, const half8 (&pf)[QP][2][2]) {
         const vsl_half* Vt = Vs[buf];
         const int gi = lane & 15, gdim = ((lane >> 4) & 1) * 16 + 4 * (gi & 3);
 #pragma unroll
@@ -615,17 +625,31 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
         }
     };
 
-    // Tile pipeline: tile t+1 is requested into the other buffer before tile t is computed; after
-    // it, each wave waits for its own copies and the block meets at a barrier (every copy of t+1 is
-    // in LDS, every wave has finished reading buffer t, which the next request overwrites). The
-    // request past the last tile re-copies it into the buffer that is not read again.
+    // Tile pipeline over three buffers. At the top of iteration t tiles t and t+1 are in LDS and the
+    // scores of tile t are in registers: tile t+2 is requested into the buffer tile t-1 used, tile
+    // t's scores are masked and its maximum taken (the lazy rescale is the one branch), then tile
+    // t+1's scores are issued on the matrix cores while the VALU turns tile t's scores into
+    // probabilities (independent work in one basic block, so the two overlap), then tile t's PV
+    // products; each wave waits for its own copies and the block meets at a barrier (every copy of
+    // t+2 is in LDS, every wave has finished reading buffer t, which iteration t+1 overwrites).
+    // Requests past the last tile re-copy it (finite values; scores computed from them are unused).
+    auto buf_of = [](uint32_t t) { return (int)(t % 3); };
     issue(0, phys(0));
+    issue(1, phys(n_vt > 1 ? 1 : 0));
     VSL_VMCNT_WAIT(0);
     __syncthreads();
+    float16v st[2];
+    qk(0, st);
     for (uint32_t t = 0; t < n_vt; ++t) {
-        const int buf = t & 1;
-        issue(buf ^ 1, phys(t + 1 < n_vt ? t + 1 : t));
-        compute(buf, phys(t));
+        issue(buf_of(t + 2), phys(t + 2 < n_vt ? t + 2 : n_vt - 1));
+        rescale(mask_max(st, phys(t)));
+        float16v sn[2];
+        qk(buf_of(t + 1), sn);
+        half8 pf[QP][2][2];
+        l += probs(st, pf);
+        pv(buf_of(t), pf);
+        st[0] = sn[0];
+        st[1] = sn[1];
         VSL_VMCNT_WAIT(0);
         __syncthreads();
     }
