@@ -155,11 +155,11 @@ def test_qkv_capacity_guard(vsl, dev, H):
 
 @pytest.mark.parametrize("kvdt,hd,nq,nkv", [(1, 128, 32, 8), (1, 64, 32, 8), (0, 64, 4, 4), (1, 128, 8, 8)])
 @pytest.mark.parametrize("length", [1, 5, 300, 1025])
-@pytest.mark.parametrize("nsplit", [32, 1, 7, 100])
+@pytest.mark.parametrize("nsplit", [32, 1, 7, 48, 100])
 def test_attn_decode(vsl, orc, dev, H, kvdt, hd, nq, nkv, length, nsplit):
     """Split-KV decode attention against the oracle: split counts 1 (a single block walks every
-    tile), 7 (ragged tile ownership), 32 (the engine's default) and 100 (more than the register
-    fast path of the combine holds)."""
+    tile), 7 (ragged tile ownership), 32 (the engine's default), 48 (the combine's 64-split register
+    path) and 100 (more than the combine's register paths hold)."""
     if nsplit != 32 and (kvdt, hd, nq, nkv) not in ((1, 128, 32, 8), (0, 64, 4, 4)):
         pytest.skip("split sweep runs on two head layouts")
     rng = np.random.default_rng(length * 3 + hd)

@@ -1039,98 +1039,99 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_decode_mfma(const float* __
 }
 
 // Combines the nsplit partials of every query head: out = sum_s A_s 2^(m_s-M) / sum_s l_s 2^(m_s-M).
-// One block per head. Up to kFastSplits splits, every partial is requested at once (before the
-// control block is read) and held in registers; larger split counts loop over the splits.
+// One block per head, one thread per head dim. With NS > 0 (nsplit <= NS <= 64) every partial is
+// requested at once (before the control block is read) and held in registers, and wave 0 alone
+// forms the split weights -- one split per lane, maximum and sum by DPP -- behind a single barrier;
+// NS = 0 loops over any split count.
 constexpr int kCombineThreads = 128;
 constexpr uint32_t kMaxSplits = 1024;
 constexpr int kFastSplits = 64;
-template <int HD, bool FAST>
+template <int HD, int NS>
 __global__ __launch_bounds__(kCombineThreads) void k_attn_combine(const float* __restrict__ part_o,
                                                                   const float* __restrict__ part_ml, uint32_t nsplit,
                                                                   float* __restrict__ out, const vsl_ctrl* ctrl) {
-    __shared__ float wts[kMaxSplits];
+    static_assert(NS == 0 || (NS % 4 == 0 && NS <= 64), "register path: up to 64 splits in wave 0");
+    __shared__ float wts[NS > 0 ? NS : kMaxSplits];
     __shared__ float red[kCombineThreads / 64];
     __shared__ float s_M, s_L;
     const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const size_t base = (size_t)h * nsplit;
     const uint32_t dd = tid < (uint32_t)HD ? tid : 0;
-    float o[FAST ? kFastSplits : 1];
-    float m0 = -INFINITY, l0 = 0.f;
-    if constexpr (FAST) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    uint32_t done;
+    if constexpr (NS > 0) {
+        float m0 = -INFINITY, l0 = 0.f;
         if (tid < nsplit) {
             m0 = part_ml[(base + tid) * 2];
             l0 = part_ml[(base + tid) * 2 + 1];
         }
+        float o[NS];
 #pragma unroll
-        for (int s = 0; s < kFastSplits; ++s) o[s] = part_o[(base + (s < (int)nsplit ? s : 0)) * HD + dd];
-    }
-    const uint32_t done = ctrl->done;  // gates the store only (no branch to sink the loads behind)
-    float mx = -INFINITY;
-    if constexpr (FAST) {
-        wts[tid] = m0;
-        mx = m0;
-    } else {
-        for (uint32_t s = tid; s < nsplit; s += kCombineThreads) {
-            const float m = part_ml[(base + s) * 2];
-            wts[s] = m;
-            mx = fmaxf(mx, m);
+        for (int s = 0; s < NS; ++s) o[s] = part_o[(base + (s < (int)nsplit ? s : 0)) * HD + dd];
+        done = ctrl->done;  // gates the store only (no branch to sink the loads behind)
+        if (wave == 0) {    // lanes past nsplit hold m = -inf and weight 0
+            const float M = wave_max_dpp(m0);
+            const float f = m0 == -INFINITY ? 0.f : exp2f(m0 - M);
+            if (tid < (uint32_t)NS) wts[tid] = f;
+            const float L = wave_sum_dpp(l0 * f);
+            if (lane == 0) s_L = L;
         }
-    }
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    if (tid == 0) {
-        float M = red[0];
-        for (int w = 1; w < kCombineThreads / 64; ++w) M = fmaxf(M, red[w]);
-        s_M = M;
-    }
-    __syncthreads();
-    const float M = s_M;
-    float lsum = 0.f;
-    if constexpr (FAST) {
-        const float f = (tid >= nsplit || m0 == -INFINITY) ? 0.f : exp2f(m0 - M);
-        wts[tid] = f;
-        lsum = l0 * f;
-    } else {
-        for (uint32_t s = tid; s < nsplit; s += kCombineThreads) {
-            const float m = wts[s];
-            const float f = m == -INFINITY ? 0.f : exp2f(m - M);
-            wts[s] = f;
-            lsum += part_ml[(base + s) * 2 + 1] * f;
-        }
-    }
-    lsum = wave_sum(lsum);
-    __syncthreads();
-    if (lane == 0) red[wave] = lsum;
-    __syncthreads();
-    if (tid == 0) {
-        float L = 0.f;
-        for (int w = 0; w < kCombineThreads / 64; ++w) L += red[w];
-        s_L = L;
-    }
-    __syncthreads();
-    const float inv = 1.0f / s_L;
-    if (tid >= (uint32_t)HD) return;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    if constexpr (FAST) {
+        __syncthreads();
 #pragma unroll
-        for (int s = 0; s < kFastSplits; s += 4) {
-            // splits past nsplit carry weight 0 (wts[s] was written for every s < kCombineThreads)
+        for (int s = 0; s < NS; s += 4) {
             a0 = fmaf(o[s], wts[s], a0);
             a1 = fmaf(o[s + 1], wts[s + 1], a1);
             a2 = fmaf(o[s + 2], wts[s + 2], a2);
             a3 = fmaf(o[s + 3], wts[s + 3], a3);
         }
     } else {
-        uint32_t s = 0;
-        for (; s + 4 <= nsplit; s += 4) {
-            a0 = fmaf(part_o[(base + s) * HD + dd], wts[s], a0);
-            a1 = fmaf(part_o[(base + s + 1) * HD + dd], wts[s + 1], a1);
-            a2 = fmaf(part_o[(base + s + 2) * HD + dd], wts[s + 2], a2);
-            a3 = fmaf(part_o[(base + s + 3) * HD + dd], wts[s + 3], a3);
+        done = ctrl->done;
+        float mx = -INFINITY;
+        for (uint32_t s = tid; s < nsplit; s += kCombineThreads) {
+            const float m = part_ml[(base + s) * 2];
+            wts[s] = m;
+            mx = fmaxf(mx, m);
         }
-        for (; s < nsplit; ++s) a0 = fmaf(part_o[(base + s) * HD + dd], wts[s], a0);
+        mx = wave_max(mx);
+        if (lane == 0) red[wave] = mx;
+        __syncthreads();
+        if (tid == 0) {
+            float M = red[0];
+            for (int w = 1; w < kCombineThreads / 64; ++w) M = fmaxf(M, red[w]);
+            s_M = M;
+        }
+        __syncthreads();
+        const float M = s_M;
+        float lsum = 0.f;
+        for (uint32_t s = tid; s < nsplit; s += kCombineThreads) {
+            const float m = wts[s];
+            const float f = m == -INFINITY ? 0.f : exp2f(m - M);
+            wts[s] = f;
+            lsum += part_ml[(base + s) * 2 + 1] * f;
+        }
+        lsum = wave_sum(lsum);
+        __syncthreads();
+        if (lane == 0) red[wave] = lsum;
+        __syncthreads();
+        if (tid == 0) {
+            float L = 0.f;
+            for (int w = 0; w < kCombineThreads / 64; ++w) L += red[w];
+            s_L = L;
+        }
+        __syncthreads();
+        if (tid < (uint32_t)HD) {
+            uint32_t s = 0;
+            for (; s + 4 <= nsplit; s += 4) {
+                a0 = fmaf(part_o[(base + s) * HD + dd], wts[s], a0);
+                a1 = fmaf(part_o[(base + s + 1) * HD + dd], wts[s + 1], a1);
+                a2 = fmaf(part_o[(base + s + 2) * HD + dd], wts[s + 2], a2);
+                a3 = fmaf(part_o[(base + s + 3) * HD + dd], wts[s + 3], a3);
+            }
+            for (; s < nsplit; ++s) a0 = fmaf(part_o[(base + s) * HD + dd], wts[s], a0);
+        }
     }
+    if (tid >= (uint32_t)HD) return;
+    const float inv = 1.0f / s_L;
     if (!done) out[(size_t)h * HD + dd] = ((a0 + a1) + (a2 + a3)) * inv;
 }
 
@@ -1190,10 +1191,12 @@ int launch_attn_g(uint32_t G, dim3 grid, hipStream_t s, const float* q, const vo
         default: return vsl_unsupported("vsl_attn_decode: GQA ratio %u (supported 1,2,4,8)", G);
     }
     HIP_TRY(hipGetLastError());
-    if (nsplit <= (uint32_t)kFastSplits)
-        k_attn_combine<HD, true><<<n_q, kCombineThreads, 0, s>>>(po, pml, nsplit, out, ctrl);
+    if (nsplit <= 32)
+        k_attn_combine<HD, 32><<<n_q, kCombineThreads, 0, s>>>(po, pml, nsplit, out, ctrl);
+    else if (nsplit <= (uint32_t)kFastSplits)
+        k_attn_combine<HD, kFastSplits><<<n_q, kCombineThreads, 0, s>>>(po, pml, nsplit, out, ctrl);
     else
-        k_attn_combine<HD, false><<<n_q, kCombineThreads, 0, s>>>(po, pml, nsplit, out, ctrl);
+        k_attn_combine<HD, 0><<<n_q, kCombineThreads, 0, s>>>(po, pml, nsplit, out, ctrl);
     HIP_TRY(hipGetLastError());
     return VSL_OK;
 }

@@ -108,6 +108,20 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     v += VSL_DPP_F(v, 0x143, 0xC);  // row_bcast:31 into rows 2 and 3
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// Wave-wide maximum by the same steps; lanes a broadcast step does not write keep their own value
+// (old operand = v), so any set of values, -inf included, reduces correctly.
+#define VSL_DPP_M(v, ctrl, row_mask) \
+    __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), (ctrl), (row_mask), 0xF, false))
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, VSL_DPP_M(v, 0xB1, 0xF));
+    v = fmaxf(v, VSL_DPP_M(v, 0x4E, 0xF));
+    v = fmaxf(v, VSL_DPP_M(v, 0x124, 0xF));
+    v = fmaxf(v, VSL_DPP_M(v, 0x128, 0xF));
+    v = fmaxf(v, VSL_DPP_M(v, 0x142, 0xA));
+    v = fmaxf(v, VSL_DPP_M(v, 0x143, 0xC));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+#undef VSL_DPP_M
 #undef VSL_DPP_F
 
 // Sum across aligned groups of W = 8 or 16 lanes with DPP row operations (VALU only, every lane of
