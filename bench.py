@@ -29,7 +29,7 @@ KV_CAPACITY = 4096
 # HBM bytes per launch of the dominant decode kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
 # passes summarised in profiles/llama8b_decode_prefill_rocprof.md (FETCH_SIZE scaled x1.9999 by a 1 GiB copy).
 # Re-measure with the commands listed there whenever the kernel changes.
-DOMINANT_TRAFFIC_BYTES = 235_280_000 + 115_000
+DOMINANT_TRAFFIC_BYTES = 235_290_000 + 115_000
 
 
 def load_package():
