@@ -83,6 +83,14 @@ int vsl_engine_close(vsl_engine* e);
  * number of generated tokens. */
 int vsl_engine_generate_ids(vsl_engine* e, const uint32_t* prompt, uint32_t n_prompt, uint32_t max_new,
                             const vsl_gen_params* params, uint32_t* out_tokens, float* out_logits, uint32_t* n_out);
+/* Teacher-forced generation (parity checks): as vsl_engine_generate_ids, but step t + 1 takes forced[t]
+ * as its input instead of the token sampled at step t (n_forced >= max_new - 1), and EOS does not stop
+ * the run.  out_tokens receives the sampled tokens, out_logits each step's logits, so that every step
+ * can be compared with another implementation fed the same token history.  No reference counterpart
+ * (the reference's generate always feeds back its own samples, VulkanSymbioteEngine.cpp:730-760). */
+int vsl_engine_generate_forced(vsl_engine* e, const uint32_t* prompt, uint32_t n_prompt, const uint32_t* forced,
+                               uint32_t n_forced, uint32_t max_new, const vsl_gen_params* params, uint32_t* out_tokens,
+                               float* out_logits, uint32_t* n_out);
 /* generate(prompt, max_tokens, temperature): text in, prompt + decode({id}) of each generated token out
  * (NUL-terminated), with the tokenizer of the model file (the byte fallback for synthetic engines) */
 int vsl_engine_generate_text(vsl_engine* e, const char* prompt, uint32_t max_tokens, float temperature, char* out,

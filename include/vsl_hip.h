@@ -46,10 +46,17 @@ enum { VSL_DT_F32 = 0, VSL_DT_F16 = 1, VSL_DT_F16X2 = 2 };
 
 /* Sampling modes (VulkanSymbioteEngine::sample_token, VulkanSymbioteEngine.cpp:1540-1553) */
 enum {
-    VSL_SAMPLE_GREEDY = 0,     /* greedy_sampling (:1794-1804): first index of the max            */
-    VSL_SAMPLE_REFERENCE = 1,  /* T>0 through member top_k_sampling (:1806-1855) == argmax          */
+    VSL_SAMPLE_GREEDY = 0,     /* greedy_sampling (:1794-1804): first index of the max logit        */
+    VSL_SAMPLE_REFERENCE = 1,  /* T>0 through member top_k_sampling (:1806-1855), which returns its
+                                  tokens[0]: the first index of the largest fp32 probability
+                                  exp(l/T - max)/sum (the logit argmax unless rounding merges
+                                  probabilities next to the maximum)                              */
     VSL_SAMPLE_TOPK_SEEDED = 2 /* Utils.cpp:140-172 top-k with a Philox4x32-10 uniform             */
 };
+/* Limits of the samplers that scan the logits in one block (modes REFERENCE and TOPK_SEEDED with
+ * T > 0): V <= VSL_MAX_SAMPLE_VOCAB, and for TOPK_SEEDED 1 <= top_k <= VSL_MAX_TOP_K (top_k > V means
+ * all of V).  Other requests return VSL_E_UNSUPPORTED; greedy has no limit. */
+enum { VSL_MAX_TOP_K = 64, VSL_MAX_SAMPLE_VOCAB = 65536 };
 
 const char* vsl_last_error(void);
 int vsl_device_count(int* n);
@@ -225,8 +232,9 @@ int vsl_norm_swiglu(const float* x, const float* gamma, float eps, const void* W
 
 /* Output stage (final norm + final_linear.comp + sample_token) for one position:
  *   f = RMSNorm(x, gamma) (gamma may be NULL: no final norm); logits = W f (fp32 [V]);
- *   greedy / reference mode: per-block argmax fused into the GEMV, reduced by a second launch;
- *   top-k mode: the GEMV writes logits and a sampling launch follows.
+ *   greedy: per-block argmax fused into the GEMV, reduced by a second launch;
+ *   reference and top-k modes (T > 0): the GEMV writes logits and a sampling launch follows
+ *   (limits: VSL_MAX_SAMPLE_VOCAB, VSL_MAX_TOP_K; otherwise VSL_E_UNSUPPORTED before any launch).
  *   The sampled token is written to tokens[ctrl->step]; then x <- embed[token] (the next step's
  *   embedding_lookup), ctrl->pos += 1, ctrl->step += 1, and done is set on max_steps / EOS.
  *   Workspace: ws_val/ws_idx >= vsl_lm_head_ws_blocks() entries. */
@@ -236,7 +244,7 @@ int vsl_lm_head_sample(const float* gamma, float eps, const void* W, int wdtype,
 uint32_t vsl_lm_head_ws_blocks(void);
 
 /* Sample one token from fp32 logits already in memory (no bookkeeping): the samplers alone,
- * exposed for the sampler parity tests.  out: one u32. */
+ * exposed for the sampler parity tests.  out: one u32.  Sampler limits as above. */
 int vsl_sample_logits(const float* logits, uint32_t V, vsl_sampler sampler, uint64_t step,
                       uint32_t* out, void* stream);
 

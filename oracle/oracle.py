@@ -184,6 +184,41 @@ class Model:
             raise RuntimeError(f"orc_teacher_forced -> {rc}")
         return out
 
+    def continuations(self, prompt, runs, kv_f16=False):
+        """Several generations from one processed prompt (the prompt's positions are computed once).
+        runs: list of dicts with n (tokens to generate) and optionally sampler, temperature, top_k, seed.
+        Each run restarts at position len(prompt); positions past it are overwritten before they are
+        read, so the runs are independent.  Returns [(tokens, logits)], logits [n][vocab]: the logits
+        each token was sampled from (as generate(..., logits=True))."""
+        L = lib()
+        V = self.config["vocab_size"]
+        n_max = max(r["n"] for r in runs)
+        st = L.orc_state_new(self.h, len(prompt) + n_max, int(kv_f16))
+        if not st:
+            raise MemoryError("oracle state")
+        try:
+            first = np.zeros(V, np.float32)
+            for i, t in enumerate(prompt):
+                rc = L.orc_forward(self.h, st, int(t), i, ptr(first) if i == len(prompt) - 1 else None)
+                if rc:
+                    raise RuntimeError(f"orc_forward -> {rc}")
+            out = []
+            for r in runs:
+                n = r["n"]
+                toks = np.zeros(n, np.uint32)
+                lg = np.zeros((n, V), np.float32)
+                cur = first.copy()
+                for t in range(n):
+                    lg[t] = cur
+                    toks[t] = sample(cur, r.get("sampler", SAMPLE_GREEDY), r.get("temperature", 0.0),
+                                     r.get("top_k", 40), r.get("seed", 0), t)
+                    if t + 1 < n and L.orc_forward(self.h, st, int(toks[t]), len(prompt) + t, ptr(cur)):
+                        raise RuntimeError("orc_forward failed")
+                out.append((toks, lg))
+            return out
+        finally:
+            L.orc_state_free(st)
+
     def decode_rate(self, prompt, max_seconds=20.0, max_tokens=64, kv_f16=True):
         """Time the oracle's token loop on the host: the prompt is processed first (untimed), then
         greedy decode steps run until max_seconds or max_tokens.  Returns (tokens, seconds)."""

@@ -1,6 +1,7 @@
 """End-to-end parity of the MI355X engine (VulkanSymbioteEngine token loop) against the oracle and
 the committed golden vectors, through the engine C ABI."""
 import os
+import subprocess
 
 import numpy as np
 import pytest
@@ -57,6 +58,23 @@ def test_tiny_stop_on_eos_capacity_and_text(vsl, orc, tiny_path):
         assert out == "hello world" + "".join(chr(t % 256) for t in ref)
 
 
+def test_integration_program_runs(vsl, orc, tiny_path, tmp_path):
+    """The C++ drop-in program (tests/cpp/integration_app.cpp: ConfigManager from the command line,
+    VulkanSymbioteEngine(path), generate(text, 8, 0.0), run_benchmark) on the tiny model: the text
+    equals the oracle's greedy continuation of the byte-fallback ids, the benchmark reports a rate."""
+    from test_cpp_api import compile_cpp
+    exe = compile_cpp(vsl, "integration_app.cpp", tmp_path / "integration_app")
+    r = subprocess.run([exe, "--model", str(tiny_path), "hello world"], capture_output=True, timeout=300)
+    assert r.returncode == 0, r.stderr.decode(errors="replace")
+    m = orc.Model(tiny_path)
+    ref = m.generate(np.array([ord(c) for c in "helloworld"], np.uint32), 8, stop_on_eos=True)
+    m.close()
+    want = b"generate: hello world" + bytes(int(t) % 256 for t in ref) + b"\n"
+    assert r.stdout.startswith(want), (r.stdout[:80], want)
+    bench = r.stdout[len(want):].decode().split()
+    assert bench[0] == "benchmark:" and float(bench[1]) > 0 and float(bench[2]) <= float(bench[3])
+
+
 def test_text_path_with_gguf_vocabulary(vsl, orc, tmp_path):
     """generate(text) with the model file's vocabulary (array and keyed layouts): the prompt encoded
     by the oracle's tokenizer, greedy ids from the oracle model (EOS 0/2 stops), and the output
@@ -85,9 +103,15 @@ def test_tiny_seeded_topk(vsl, orc, tiny_path):
             t = e.generate_ids(g["prompt"], 32, mode="topk", temperature=0.7, top_k=40, seed=seed)
             r = m.generate(g["prompt"], 32, sampler=orc.SAMPLE_TOPK_SEEDED, temperature=0.7, top_k=40, seed=seed)
             assert np.array_equal(t, r)
-        # reference mode (T > 0 through the member top_k_sampling) is the argmax
+        # reference mode (T > 0 through the member top_k_sampling): the first index of the largest
+        # softmax probability, which on these logits is the greedy token
         t = e.generate_ids(g["prompt"], 32, mode="reference", temperature=0.7)
-        assert np.array_equal(t, g["tokens"])
+        r = m.generate(g["prompt"], 32, sampler=orc.SAMPLE_REFERENCE, temperature=0.7)
+        assert np.array_equal(t, r) and np.array_equal(t, g["tokens"])
+        for k in (0, 65):  # outside the seeded sampler's 1..64
+            with pytest.raises(vsl.VslError):
+                e.generate_ids(g["prompt"], 4, mode="topk", temperature=0.7, top_k=k, seed=1)
+        assert len(e.generate_ids(g["prompt"], 4, mode="topk", temperature=0.7, top_k=64, seed=1)) == 4
 
 
 def _oracle_from_engine(orc, e, cfg):
@@ -113,14 +137,80 @@ def _oracle_from_engine(orc, e, cfg):
     return m
 
 
-def _parity(vsl, orc, cfg, n_prompt, n_new, batched, kv_capacity, seed=0):
-    with vsl.Engine(spec=cfg, seed=seed, kv_capacity=kv_capacity, batched_prefill=batched) as e:
-        prompt = orc.random_ids(n_prompt, cfg["vocab_size"], 1)
-        toks, lg = e.generate_ids(prompt, n_new, return_logits=True)
-        m = _oracle_from_engine(orc, e, cfg)
-    ref_toks, ref_lg = m.generate(prompt, n_new, kv_f16=True, logits=True)
+def _forced_parity(e, m, prompt, n_new, tol, runs=None):
+    """The oracle generates from the prompt (greedy unless `runs` says otherwise), then the engine is
+    teacher-forced with the oracle's tokens, so both compute every step on the same token history:
+    every step's logits within max-abs `tol`, and the engine's own pick at every step equal to the
+    oracle's (greedy identity, or the seeded sampler's pick).  A mismatch names its step with the
+    oracle's top1-top2 margin and the logit error there.  Returns the per-step oracle margins and
+    logit errors of each run."""
+    runs = runs or [dict(n=n_new)]
+    ref = m.continuations(prompt, runs, kv_f16=True)
+    report = []
+    for r, (rt, rl) in zip(runs, ref):
+        kw = dict(mode={0: "greedy", 1: "reference", 2: "topk"}[r.get("sampler", 0)],
+                  temperature=r.get("temperature", 0.0), top_k=r.get("top_k", 40), seed=r.get("seed", 0))
+        toks, lg = e.generate_ids(prompt, r["n"], return_logits=True, forced=rt[:-1], **kw)
+        assert len(toks) == r["n"]
+        srt = np.sort(rl, axis=1)
+        margins = srt[:, -1] - srt[:, -2]
+        err = np.max(np.abs(lg - rl), axis=1)
+        bad = [i for i in range(r["n"]) if toks[i] != rt[i]]
+        print(f"run {r}: max logit error {err.max():.5f}, smallest oracle margin {margins.min():.5f} "
+              f"(step {int(np.argmin(margins))})")
+        assert err.max() < tol, f"logits: step {int(np.argmax(err))} error {err.max():.5f} (tol {tol})"
+        assert not bad, (f"engine pick differs from the oracle's at steps {bad}: margins "
+                         f"{[round(float(margins[i]), 5) for i in bad]}, logit errors {[round(float(err[i]), 5) for i in bad]}")
+        report.append((margins, err))
+    return report
+
+
+def test_forced_history_feeds_the_given_tokens(vsl, orc, tiny_path):
+    """Teacher forcing itself: the engine forced with its own greedy tokens reproduces its free run bit
+    for bit; forced with another history, its logits equal the oracle's on that history (tiny fp32
+    model, 1e-4 relative)."""
+    g = np.load(GOLD)
+    with vsl.Engine(tiny_path, kv_capacity=64) as e:
+        toks, lg = e.generate_ids(g["prompt"], 32, return_logits=True)
+        t2, l2 = e.generate_ids(g["prompt"], 32, return_logits=True, forced=toks[:-1])
+        assert np.array_equal(t2, toks) and np.array_equal(l2, lg)
+        hist = np.random.default_rng(4).integers(0, 4096, 31).astype(np.uint32)
+        t3, l3 = e.generate_ids(g["prompt"], 32, return_logits=True, forced=hist)
+        with pytest.raises(vsl.VslError):
+            e.generate_ids(g["prompt"], 32, forced=hist[:20])  # fewer than max_new - 1 forced ids
+    m = orc.Model(tiny_path)
+    ref = m.teacher_forced(np.concatenate([g["prompt"], hist]), 32)
     m.close()
-    return prompt, toks, lg, ref_toks, ref_lg
+    scale = np.max(np.abs(ref))
+    assert np.max(np.abs(l3 - ref)) < 1e-4 * scale
+    assert np.array_equal(t3, np.argmax(ref, axis=1))
+
+
+def test_out_of_range_prompt_ids(vsl, orc, tiny_path):
+    """Prompt ids at or past the vocabulary read embedding row V - 1 (embedding_lookup.comp:32), in the
+    per-token prompt pass (tiny fp32) and in the MFMA prompt pass (1B fp16): tokens and logits equal
+    the oracle's, which clamps the same way, and equal a run with the ids replaced by V - 1."""
+    g = np.load(GOLD)
+    prompt = g["prompt"].copy()
+    prompt[[2, 9]] = [4096, 2**32 - 1]
+    m = orc.Model(tiny_path)
+    rt, rl = m.generate(prompt, 16, logits=True)
+    m.close()
+    with vsl.Engine(tiny_path, kv_capacity=64) as e:
+        toks, lg = e.generate_ids(prompt, 16, return_logits=True)
+        t2, l2 = e.generate_ids(np.minimum(prompt, 4095), 16, return_logits=True)
+    assert np.array_equal(toks, rt) and np.array_equal(toks, t2) and np.array_equal(lg, l2)
+    assert np.max(np.abs(lg - rl)) < 1e-4 * np.max(np.abs(rl))
+    cfg = vsl.LLAMA_1B
+    prompt = orc.random_ids(64, cfg["vocab_size"], 1)
+    prompt[[0, 40]] = [cfg["vocab_size"], cfg["vocab_size"] + 12345]
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=128, batched_prefill=True) as e:
+        m = _oracle_from_engine(orc, e, cfg)
+        _forced_parity(e, m, prompt, 8, 2e-2)
+        t1, l1 = e.generate_ids(prompt, 8, return_logits=True)
+        t2, l2 = e.generate_ids(np.minimum(prompt, cfg["vocab_size"] - 1), 8, return_logits=True)
+    m.close()
+    assert np.array_equal(t1, t2) and np.array_equal(l1, l2)
 
 
 def test_windowed_mode_tiny(vsl, orc, tiny_path):
@@ -148,52 +238,65 @@ def test_windowed_mode_tiny(vsl, orc, tiny_path):
 
 def test_windowed_mode_1b_batched_prefill(vsl, orc):
     """1B fp16 with the MFMA prefill crossing the threshold inside the prompt (window 16, 4 globals,
-    threshold 64, prompt 128): greedy 32 tokens identical to the oracle over the resident weights
-    with the same window, logits within max-abs 2e-2."""
+    threshold 64, prompt 128): 32 teacher-forced steps against the oracle over the resident weights
+    with the same window -- logits within max-abs 2e-2 at every step, greedy picks identical."""
     cfg = vsl.LLAMA_1B
     win = (16, 4, 64)
     with vsl.Engine(spec=cfg, seed=0, kv_capacity=512, batched_prefill=True, window=win) as e:
-        prompt = orc.random_ids(128, cfg["vocab_size"], 1)
-        toks, lg = e.generate_ids(prompt, 32, return_logits=True)
         m = _oracle_from_engine(orc, e, cfg)
-    m.set_window(*win)
-    rt, rl = m.generate(prompt, 32, kv_f16=True, logits=True)
+        m.set_window(*win)
+        _forced_parity(e, m, orc.random_ids(128, cfg["vocab_size"], 1), 32, 2e-2)
     m.close()
-    first, margins = _report(toks, rt, lg, rl)
-    n = min(len(toks), len(rt), first if first is not None else 32)
-    assert np.max(np.abs(lg[:n] - rl[:n])) < 2e-2, np.max(np.abs(lg[:n] - rl[:n]))
-    assert first is None, f"first mismatch at step {first}, oracle top1-top2 margin {margins[first]:.5f}"
-
-
-def _report(toks, ref_toks, lg, ref_lg):
-    n = min(len(toks), len(ref_toks))
-    first = next((i for i in range(n) if toks[i] != ref_toks[i]), None)
-    srt = np.sort(ref_lg, axis=1)
-    margins = srt[:, -1] - srt[:, -2]
-    return first, margins
 
 
 @pytest.mark.parametrize("batched", [False, True])
 def test_llama_1b_fp16_parity(vsl, orc, batched):
-    """1B-class fp16 (GQA 32/8, head_dim 64): prompt 128, greedy 32 tokens identical to the oracle;
-    logits of every step within max-abs 2e-2."""
+    """1B-class fp16 (GQA 32/8, head_dim 64): prompt 128, 32 teacher-forced steps against the oracle
+    over the resident weights -- logits within max-abs 2e-2 at every step, greedy picks identical --
+    for the per-token and the MFMA prompt pass."""
     cfg = vsl.LLAMA_1B
-    prompt, toks, lg, rt, rl = _parity(vsl, orc, cfg, 128, 32, batched, kv_capacity=512)
-    first, margins = _report(toks, rt, lg, rl)
-    n = min(len(toks), len(rt), first if first is not None else 32)
-    assert np.max(np.abs(lg[:n] - rl[:n])) < 2e-2, np.max(np.abs(lg[:n] - rl[:n]))
-    assert first is None, f"first mismatch at step {first}, oracle top1-top2 margin {margins[first]:.5f}"
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=512, batched_prefill=batched) as e:
+        m = _oracle_from_engine(orc, e, cfg)
+        _forced_parity(e, m, orc.random_ids(128, cfg["vocab_size"], 1), 32, 2e-2)
+    m.close()
 
 
 @pytest.mark.slow
-def test_llama_8b_fp16_parity_short(vsl, orc):
-    """8B-class fp16 (head_dim 128, theta 500000): MFMA prefill of 64 tokens, greedy 16 tokens."""
+@pytest.mark.timeout(900)
+def test_llama_8b_fp16_parity(vsl, orc):
+    """The 8B-class fp16 configuration as benchmarked (head_dim 128, theta 500000): the 512-token prompt
+    through the MFMA prompt pass (one 512-row chunk: K-split QKV / O / down projections with their fused
+    RoPE + cache append and residual + RMSNorm consumers, flash attention on hi/lo planes), then 32
+    teacher-forced decode steps against the oracle over the resident weights: logits within max-abs 2e-2
+    at every step and greedy picks identical at every step."""
     cfg = vsl.LLAMA_8B
-    prompt, toks, lg, rt, rl = _parity(vsl, orc, cfg, 64, 16, True, kv_capacity=256)
-    first, margins = _report(toks, rt, lg, rl)
-    n = min(len(toks), len(rt), first if first is not None else 16)
-    assert np.max(np.abs(lg[:n] - rl[:n])) < 2e-2, np.max(np.abs(lg[:n] - rl[:n]))
-    assert first is None, f"first mismatch at step {first}, oracle top1-top2 margin {margins[first]:.5f}"
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=1024, batched_prefill=True) as e:
+        m = _oracle_from_engine(orc, e, cfg)
+        _forced_parity(e, m, orc.random_ids(512, cfg["vocab_size"], 1), 32, 2e-2)
+    m.close()
+
+
+# A small model with the 8B attention geometry (head_dim 128, GQA 4, theta 500000) so that the oracle can
+# follow an 8192-token prompt: the chunked MFMA prompt pass (four 2048-row chunks), RoPE at positions
+# past 8K, and the matrix-core decode attention that caches above 8192 positions select.
+LONG_SMALL = dict(hidden_size=1024, num_layers=2, num_heads=8, num_kv_heads=2, intermediate_size=2816,
+                  vocab_size=32000, max_position_embeddings=32768, rope_theta=500000.0, rms_eps=1e-5, dtype=1)
+
+
+@pytest.mark.slow
+@pytest.mark.timeout(900)
+def test_long_context_oracle_small_model(vsl, orc):
+    """Long-context path against the oracle: 8192 prompt tokens in 2048-row chunks into a 32768-position
+    fp16 cache, then 32 teacher-forced greedy steps (logits within max-abs 2e-2, picks identical) and 32
+    teacher-forced T = 0.7 seeded top-k 40 steps (the engine's pick at every step equal to the oracle's
+    Utils.cpp:140-172 restatement with the same Philox uniform)."""
+    cfg = LONG_SMALL
+    prompt = np.random.default_rng(11).integers(0, cfg["vocab_size"], 8192).astype(np.uint32)
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=32768, batched_prefill=True, prefill_chunk=2048) as e:
+        m = _oracle_from_engine(orc, e, cfg)
+        _forced_parity(e, m, prompt, 32, 2e-2,
+                       runs=[dict(n=32), dict(n=32, sampler=orc.SAMPLE_TOPK_SEEDED, temperature=0.7, top_k=40, seed=7)])
+    m.close()
 
 
 def test_engine_stats_and_packs(vsl):
@@ -230,52 +333,30 @@ def test_engine_stats_and_packs(vsl):
 
 
 @pytest.mark.slow
+@pytest.mark.timeout(900)
 def test_llama_8b_long_context(vsl):
-    """Long-context 8B workload: an 8192-token prompt in 2048-row MFMA chunks into a 32768-position
-    fp16 KV cache, then greedy and T=0.7 seeded decode. The chunked prefill is checked against the
-    per-token path (the decode kernels the oracle pins at small sizes) on the same weights: every
-    step's logits within max-abs 2e-2 and greedy tokens identical up to the first step whose
-    reference top1-top2 margin is below 4e-2 (a near-tie either path may break either way);
-    seeded sampling is reproducible, seed-dependent and in range."""
+    """Long-context 8B workload at full size (too large for the oracle): an 8192-token prompt in 2048-row
+    MFMA chunks into a 32768-position fp16 KV cache against the per-token path (the decode kernels the
+    oracle pins) on the same weights, teacher-forced with the per-token path's greedy tokens: logits
+    within max-abs 2e-2 and picks identical at all 8 steps; seeded T = 0.7 sampling reproducible per
+    seed, seed-dependent and in range."""
     cfg = vsl.LLAMA_8B
     V = cfg["vocab_size"]
     prompt = np.random.default_rng(11).integers(0, V, 8192).astype(np.uint32)
     n_new = 8
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=32768, batched_prefill=False) as e:
+        rt, rl = e.generate_ids(prompt, n_new, return_logits=True)
     with vsl.Engine(spec=cfg, seed=0, kv_capacity=32768, batched_prefill=True) as e:
-        toks, lg = e.generate_ids(prompt, n_new, return_logits=True)
+        toks, lg = e.generate_ids(prompt, n_new, return_logits=True, forced=rt[:-1])
         s1 = e.generate_ids(prompt, 32, mode="topk", temperature=0.7, top_k=40, seed=7)
         s2 = e.generate_ids(prompt, 32, mode="topk", temperature=0.7, top_k=40, seed=7)
         s3 = e.generate_ids(prompt, 32, mode="topk", temperature=0.7, top_k=40, seed=8)
-    with vsl.Engine(spec=cfg, seed=0, kv_capacity=32768, batched_prefill=False) as e:
-        rt, rl = e.generate_ids(prompt, n_new, return_logits=True)
-    _assert_matches_tokenwise(toks, lg, rt, rl)
-    assert np.array_equal(s1, s2) and not np.array_equal(s1, s3)
-    assert len(s1) == 32 and int(s1.max()) < V and int(s3.max()) < V
-
-
-def _assert_matches_tokenwise(toks, lg, rt, rl):
-    """Greedy tokens identical up to the first step whose per-token reference top1-top2 margin is below
-    4e-2 (a near-tie either path may break either way); logits within max-abs 2e-2 up to and including
-    that step."""
-    n_new = len(rt)
     srt = np.sort(rl, axis=1)
     margins = srt[:, -1] - srt[:, -2]
-    tie = next((i for i in range(n_new) if margins[i] < 4e-2), n_new)
-    n = next((i for i in range(tie) if toks[i] != rt[i]), tie)
-    assert n == tie, f"greedy mismatch at step {n} (reference margin {margins[n]:.4f})"
-    last = min(tie + 1, n_new)
-    assert np.max(np.abs(lg[:last] - rl[:last])) < 2e-2, np.max(np.abs(lg[:last] - rl[:last]))
-
-
-def test_llama_8b_prefill_512_matches_tokenwise(vsl):
-    """The 8B-class 512-token prefill as one MFMA chunk -- QKV, O and down projections split over K,
-    their sums fused with RoPE + the Q/K/V split and with the residual add + the next RMSNorm --
-    against the per-token path (the decode kernels the oracle pins at small sizes) on the same
-    weights, 32 greedy tokens."""
-    cfg = vsl.LLAMA_8B
-    prompt = np.random.default_rng(5).integers(0, cfg["vocab_size"], 512).astype(np.uint32)
-    with vsl.Engine(spec=cfg, seed=0, kv_capacity=1024, batched_prefill=True) as e:
-        toks, lg = e.generate_ids(prompt, 32, return_logits=True)
-    with vsl.Engine(spec=cfg, seed=0, kv_capacity=1024, batched_prefill=False) as e:
-        rt, rl = e.generate_ids(prompt, 32, return_logits=True)
-    _assert_matches_tokenwise(toks, lg, rt, rl)
+    err = np.max(np.abs(lg - rl), axis=1)
+    print(f"max logit error {err.max():.5f}, smallest reference margin {margins.min():.5f}")
+    assert err.max() < 2e-2, err
+    bad = [i for i in range(n_new) if toks[i] != rt[i]]
+    assert not bad, f"picks differ at {bad}: margins {margins[bad]}, errors {err[bad]}"
+    assert np.array_equal(s1, s2) and not np.array_equal(s1, s3)
+    assert len(s1) == 32 and int(s1.max()) < V and int(s3.max()) < V

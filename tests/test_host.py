@@ -112,6 +112,56 @@ def test_product_gguf_error_codes(vsl, tmp_path):
     vsl.engine_lib().vsl_gguf_close(h)
 
 
+def _one_tensor_gguf(dims, raw_type, offset, payload):
+    """A reference-convention file with one tensor "t" whose offset field is given literally."""
+    out = bytearray(struct.pack("<IIQQ", 0x46554747, 3, 1, 0))
+    out += _gstr("t") + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+    out += struct.pack("<IQ", raw_type, offset)
+    start = len(out)
+    return bytes(out + payload), start
+
+
+def test_product_gguf_rejects_out_of_range_tensors(vsl, tmp_path):
+    """Tensor infos of an untrusted file that point outside it: an offset that puts the tensor's start
+    just below 2^64 (so that start + size wraps to a small number) and a size past the end of the file
+    read as -11 (no pointer outside the mapping is formed); a dimension product that overflows 64 bits,
+    or whose byte size would, is a tensor-info error (-4) at load."""
+    L = vsl.engine_lib()
+    out = np.zeros(64, np.float32)
+    # start + offset = 2^64 - 64; 32 F32 elements = 128 bytes, so start + offset + size wraps to 64
+    _, start = _one_tensor_gguf([32], 6, 0, b"")
+    data, _ = _one_tensor_gguf([32], 6, 2**64 - 64 - start, b"\0" * 256)
+    p = tmp_path / "wrap.gguf"
+    p.write_bytes(data)
+    rc, h = _gguf(vsl, p)
+    assert rc == 0
+    assert L.vsl_gguf_read_f32(h, b"t", out.ctypes.data_as(ctypes.c_void_p), 64) == -11
+    L.vsl_gguf_close(h)
+    # the tensor's bytes run past the end of the file by one byte
+    data, _ = _one_tensor_gguf([16], 6, 0, b"\0" * 63)
+    p = tmp_path / "short.gguf"
+    p.write_bytes(data)
+    rc, h = _gguf(vsl, p)
+    assert rc == 0
+    assert L.vsl_gguf_read_f32(h, b"t", out.ctypes.data_as(ctypes.c_void_p), 64) == -11
+    L.vsl_gguf_close(h)
+    # the same tensor with every byte present reads
+    data, _ = _one_tensor_gguf([16], 6, 0, np.arange(16, dtype=np.float32).tobytes())
+    p = tmp_path / "ok.gguf"
+    p.write_bytes(data)
+    rc, h = _gguf(vsl, p)
+    assert rc == 0
+    assert L.vsl_gguf_read_f32(h, b"t", out.ctypes.data_as(ctypes.c_void_p), 64) == 16
+    assert np.array_equal(out[:16], np.arange(16, dtype=np.float32))
+    L.vsl_gguf_close(h)
+    # 2^32 * 2^32 * 2 elements wrap to 0; 2^62 F32 elements are 2^64 bytes
+    for dims in ([2**32, 2**32, 2], [2**62]):
+        data, _ = _one_tensor_gguf(dims, 6, 0, b"\0" * 64)
+        p = tmp_path / "dims.gguf"
+        p.write_bytes(data)
+        assert _gguf(vsl, p)[0] == -4
+
+
 @pytest.mark.parametrize("convention", ["reference", "ggml"])
 @pytest.mark.parametrize("dtype", [0, 1])
 def test_writer_roundtrip_through_both_readers(vsl, orc, tmp_path, convention, dtype):

@@ -153,20 +153,31 @@ def test_qkv_capacity_guard(vsl, dev, H):
     assert ctrl[2] == 1 and ctrl[7] == 1
 
 
-@pytest.mark.parametrize("kvdt,hd,nq,nkv", [(1, 128, 32, 8), (1, 64, 32, 8), (0, 64, 4, 4), (1, 128, 8, 8)])
-@pytest.mark.parametrize("length", [1, 5, 300, 1025])
-@pytest.mark.parametrize("nsplit", [32, 1, 7, 48, 100])
-def test_attn_decode(vsl, orc, dev, H, kvdt, hd, nq, nkv, length, nsplit):
+_LAYOUTS = [(1, 128, 32, 8), (1, 64, 32, 8), (0, 64, 4, 4), (1, 128, 8, 8)]
+_LENGTHS = [1, 5, 300, 1025]
+# every head layout at the engine's 32 splits; the split sweep on two layouts
+_ATTN_CASES = ([(lay, n, 32) for lay in _LAYOUTS for n in _LENGTHS] +
+               [(lay, n, s) for lay in ((1, 128, 32, 8), (0, 64, 4, 4)) for n in _LENGTHS for s in (1, 7, 48, 100)])
+
+
+def _nan_past(cache, length):
+    """Cache rows at and past the attended length hold NaN: they are never written before they are
+    read by a later step, so the kernels must not let them reach the output."""
+    cache[:, length:] = np.nan
+    return cache
+
+
+@pytest.mark.parametrize("layout,length,nsplit", _ATTN_CASES)
+def test_attn_decode(vsl, orc, dev, H, layout, length, nsplit):
     """Split-KV decode attention against the oracle: split counts 1 (a single block walks every
     tile), 7 (ragged tile ownership), 32 (the engine's default), 48 (the combine's 64-split register
-    path) and 100 (more than the combine's register paths hold)."""
-    if nsplit != 32 and (kvdt, hd, nq, nkv) not in ((1, 128, 32, 8), (0, 64, 4, 4)):
-        pytest.skip("split sweep runs on two head layouts")
+    path) and 100 (more than the combine's register paths hold); cache rows past the length are NaN."""
+    kvdt, hd, nq, nkv = layout
     rng = np.random.default_rng(length * 3 + hd)
     cap = 2048
     kvnp = np.float16 if kvdt == 1 else np.float32
-    K = rng.normal(0, 1, (nkv, cap, hd)).astype(kvnp)
-    V = rng.normal(0, 1, (nkv, cap, hd)).astype(kvnp)
+    K = _nan_past(rng.normal(0, 1, (nkv, cap, hd)).astype(kvnp), length)
+    V = _nan_past(rng.normal(0, 1, (nkv, cap, hd)).astype(kvnp), length)
     q = rng.normal(0, 1, nq * hd).astype(np.float32)
     scale = 1.0 / math.sqrt(hd)
     po = dev.empty((nq * nsplit * hd,), np.float32)
@@ -176,25 +187,29 @@ def test_attn_decode(vsl, orc, dev, H, kvdt, hd, nq, nkv, length, nsplit):
     ok(vsl, H.vsl_attn_decode(dev.p(dev.put(q)), dev.p(dev.put(K)), dev.p(dev.put(V)), kvdt, nq, nkv, hd, cap, scale,
                               nsplit, dev.p(po), dev.p(pml), dev.p(out), dev.p(c), None))
     ref = orc.attention_decode(q, K.astype(np.float32), V.astype(np.float32), nq, nkv, hd, cap, length, scale)
-    assert rel_err(dev.get(out), ref) < 2e-5
+    got = dev.get(out)
+    assert np.all(np.isfinite(got))
+    assert rel_err(got, ref) < 2e-5
 
 
-@pytest.mark.parametrize("nq", [32, 8, 16, 64])
-@pytest.mark.parametrize("length", [1, 5, 17, 300, 1025, 9000, 16384])
-@pytest.mark.parametrize("nsplit", [32, 1, 7, 100])
+_LONG_LENGTHS = [1, 5, 17, 300, 1025, 9000, 16384]
+# GQA groups of 4, 1, 2 and 8 heads at 32 splits; the split sweep on the 8B layout (one block over
+# the whole 16384-position cache is left to the 9000-position case)
+_LONG_CASES = ([(nq, n, 32) for nq in (32, 8, 16, 64) for n in _LONG_LENGTHS] +
+               [(32, n, s) for s in (1, 7, 100) for n in _LONG_LENGTHS if not (n == 16384 and s == 1)])
+
+
+@pytest.mark.parametrize("nq,length,nsplit", _LONG_CASES)
 def test_attn_decode_long_cache(vsl, orc, dev, H, nq, length, nsplit):
     """fp16 caches of head_dim 128 above 8192 positions of capacity run the matrix-core kernel (scores
     from hi + lo fp16 planes of q on MFMA, 16-position tiles per wave): against the oracle for GQA
     groups of 4, 1, 2 and 8 heads, lengths from one position to the full cache, the split counts of
-    the short-cache test."""
-    if nsplit != 32 and nq != 32:
-        pytest.skip("split sweep runs on the 8B head layout")
-    if length == 16384 and nsplit == 1:
-        pytest.skip("one block over the whole cache: covered at 9000 positions")
+    the short-cache test; cache rows past the length are NaN (the kernel requests its first two tiles
+    before it knows the length)."""
     nkv, hd, cap = 8, 128, 16384
     rng = np.random.default_rng(length * 7 + nq + nsplit)
-    K = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16)
-    V = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16)
+    K = _nan_past(rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16), length)
+    V = _nan_past(rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16), length)
     q = rng.normal(0, 1, nq * hd).astype(np.float32)
     scale = 1.0 / math.sqrt(hd)
     po = dev.empty((nq * nsplit * hd,), np.float32)
@@ -204,7 +219,9 @@ def test_attn_decode_long_cache(vsl, orc, dev, H, nq, length, nsplit):
     ok(vsl, H.vsl_attn_decode(dev.p(dev.put(q)), dev.p(dev.put(K)), dev.p(dev.put(V)), 1, nq, nkv, hd, cap, scale,
                               nsplit, dev.p(po), dev.p(pml), dev.p(out), dev.p(c), None))
     ref = orc.attention_decode(q, K.astype(np.float32), V.astype(np.float32), nq, nkv, hd, cap, length, scale)
-    assert rel_err(dev.get(out), ref) < 2e-5
+    got = dev.get(out)
+    assert np.all(np.isfinite(got))
+    assert rel_err(got, ref) < 2e-5
 
 
 @pytest.mark.parametrize("kvdt,hd,nq,nkv", [(1, 128, 32, 8), (0, 64, 4, 4)])
@@ -231,7 +248,7 @@ def test_attn_decode_window(vsl, orc, dev, H, kvdt, hd, nq, nkv, length, window,
         hidden = slice(n_glob, p - window)
         K[:, hidden] = np.repeat(q.reshape(nq, hd)[::nq // nkv][:, None, :], p - window - n_glob, axis=1) * 4
         V[:, hidden] = 100.0
-    K, V = K.astype(kvnp), V.astype(kvnp)
+    K, V = _nan_past(K, length).astype(kvnp), _nan_past(V, length).astype(kvnp)
     scale = 1.0 / math.sqrt(hd)
     po = dev.empty((nq * nsplit * hd,), np.float32)
     pml = dev.empty((nq * nsplit * 2,), np.float32)
@@ -339,6 +356,81 @@ def test_sample_logits_greedy_ties_and_topk(vsl, orc, dev, H):
     for step in range(64):
         ok(vsl, H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 0.7, 40, 0, 99), step, dev.p(out), None))
         assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_TOPK_SEEDED, 0.7, 40, 99, step)
+
+
+def test_sample_logits_topk_limits(vsl, orc, dev, H):
+    """Seeded top-k at the largest supported k (64) against the oracle; k = 65 and k = 0 (which the
+    oracle would read as all of V) are refused with VSL_E_UNSUPPORTED, and so is a vocabulary above
+    65536, by vsl_sample_logits and by vsl_lm_head_sample before anything is launched; top_k above a
+    small V means all of V."""
+    out = dev.empty((1,), np.int32)
+    l = np.random.default_rng(21).normal(0, 1.0, 32000).astype(np.float32)
+    dl = dev.put(l)
+    for step in range(16):
+        ok(vsl, H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 1.5, 64, 0, 5), step, dev.p(out), None))
+        assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_TOPK_SEEDED, 1.5, 64, 5, step)
+    for k in (65, 0):
+        assert H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 0.7, k, 0, 5), 0, dev.p(out), None) == -103
+    big = dev.empty((70000,), np.float32)
+    assert H.vsl_sample_logits(dev.p(big), 70000, vsl.Sampler(1, 0.7, 40, 0, 5), 0, dev.p(out), None) == -103
+    ok(vsl, H.vsl_sample_logits(dev.p(big), 70000, vsl.Sampler(0, 0.0, 40, 0, 5), 0, dev.p(out), None))
+    small = np.random.default_rng(22).normal(0, 1.0, 40).astype(np.float32)
+    for step in range(8):
+        ok(vsl, H.vsl_sample_logits(dev.p(dev.put(small)), 40, vsl.Sampler(2, 0.9, 50, 0, 6), step, dev.p(out), None))
+        assert dev.get(out)[0] == orc.sample(small, orc.SAMPLE_TOPK_SEEDED, 0.9, 50, 6, step)
+    V, d = 4096, 256
+    nb = H.vsl_lm_head_ws_blocks()
+    ws_v, ws_i = dev.empty((nb,), np.float32), dev.empty((nb,), np.int32)
+    toks, logits = dev.empty((8,), np.int32), dev.empty((V,), np.float32)
+    W = dev.empty((V, d), np.float16)
+    x = dev.empty((d,), np.float32)
+    c = ctrl_buf(vsl, dev, H, 3, max_steps=4, cap=64)
+    before = dev.get(c).copy()
+    for k in (0, 65):
+        rc = H.vsl_lm_head_sample(None, 1e-5, dev.p(W), 1, V, d, dev.p(x), dev.p(W), 1, dev.p(logits),
+                                  vsl.Sampler(2, 0.7, k, 0, 1), dev.p(ws_v), dev.p(ws_i), dev.p(toks), dev.p(c), None)
+        assert rc == -103
+    assert np.array_equal(dev.get(c), before)  # nothing ran
+
+
+def test_sample_reference_mode_is_softmax_argmax(vsl, orc, dev, H):
+    """VSL_SAMPLE_REFERENCE restates the member top_k_sampling's tokens[0]: the first index of the
+    largest fp32 probability exp(l/T - max)/sum.  Where logits next to the maximum differ by less than
+    exp can resolve (here by ~1e-12 at 1e-6), their probabilities are equal and the lower index wins --
+    the logit argmax would pick the larger logit.  On ordinary logits it is the argmax.  Both against
+    the oracle's restatement; any NaN logit gives token 0 as in the reference's scan."""
+    out = dev.empty((1,), np.int32)
+    lg = np.full(32000, -5.0, np.float32)
+    top = np.float32(1e-6)
+    lg[3000] = top
+    lg[1200] = np.nextafter(np.nextafter(top, np.float32(0)), np.float32(0))  # two ulps below, lower index
+    for T in (0.7, 1.0, 1.3):
+        r = orc.sample(lg, orc.SAMPLE_REFERENCE, T)
+        assert r == 1200 and orc.sample(lg, orc.SAMPLE_GREEDY) == 3000
+        ok(vsl, H.vsl_sample_logits(dev.p(dev.put(lg)), 32000, vsl.Sampler(1, T, 40, 0, 0), 0, dev.p(out), None))
+        assert dev.get(out)[0] == r
+    ok(vsl, H.vsl_sample_logits(dev.p(dev.put(lg)), 32000, vsl.Sampler(0, 0.0, 40, 0, 0), 0, dev.p(out), None))
+    assert dev.get(out)[0] == 3000
+    rng = np.random.default_rng(23)
+    for i in range(8):
+        l = rng.normal(0, 2.0, 32000).astype(np.float32)
+        ok(vsl, H.vsl_sample_logits(dev.p(dev.put(l)), 32000, vsl.Sampler(1, 0.7, 40, 0, 0), 0, dev.p(out), None))
+        assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_REFERENCE, 0.7) == int(np.argmax(l))
+    l[17] = np.nan
+    ok(vsl, H.vsl_sample_logits(dev.p(dev.put(l)), 32000, vsl.Sampler(1, 0.7, 40, 0, 0), 0, dev.p(out), None))
+    assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_REFERENCE, 0.7) == 0
+
+
+def test_embed_clamps_out_of_range_ids(vsl, dev, H):
+    """embedding_lookup.comp:32: an id at or past the vocabulary reads row V - 1 (fp16 and fp32 tables)."""
+    V, d = 300, 64
+    for dt, npdt in ((1, np.float16), (0, np.float32)):
+        E = np.random.default_rng(24).normal(0, 1, (V, d)).astype(npdt)
+        ids = np.array([0, 5, V - 1, V, V + 7, 2**32 - 1], np.uint32)
+        o = dev.empty((len(ids), d), np.float32)
+        ok(vsl, H.vsl_embed(dev.p(dev.put(E)), dt, V, d, dev.p(dev.put(ids.view(np.int32))), len(ids), dev.p(o), None))
+        want = E[np.minimum(ids, V - 1)].astype(np.float32)
+        assert np.array_equal(dev.get(o), want)
 
 
 # ------------------------------------------------------------------------------------------

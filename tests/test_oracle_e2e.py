@@ -65,3 +65,17 @@ def test_oracle_token_id_clamp(orc, tiny_gguf):
     a = m.teacher_forced(np.array([5, 4095], np.uint32), 1)
     b = m.teacher_forced(np.array([5, 10**6], np.uint32), 1)
     assert np.array_equal(a, b)
+
+
+def test_oracle_continuations_match_generate(orc, tiny_gguf):
+    """continuations() (one processed prompt, several runs restarting at its end) gives each run exactly
+    what generate() gives from scratch: greedy and seeded top-k, tokens and logits, in either order."""
+    m = orc.Model(tiny_gguf)
+    prompt = orc.random_ids(16, 4096, 1)
+    runs = [dict(n=12, sampler=orc.SAMPLE_TOPK_SEEDED, temperature=0.7, top_k=40, seed=3), dict(n=9)]
+    got = m.continuations(prompt, runs)
+    t0, l0 = m.generate(prompt, 12, sampler=orc.SAMPLE_TOPK_SEEDED, temperature=0.7, top_k=40, seed=3, logits=True)
+    t1, l1 = m.generate(prompt, 9, logits=True)
+    assert np.array_equal(got[0][0], t0) and np.array_equal(got[0][1], l0)
+    assert np.array_equal(got[1][0], t1) and np.array_equal(got[1][1], l1)
+    assert np.array_equal(t1, np.load(GOLD)["tokens"][:9])

@@ -169,6 +169,8 @@ _ENGINE_SIGS = {
     "vsl_engine_close": (_I32, [_P]),
     "vsl_engine_generate_ids": (_I32, [_P, _P, _U32, _U32, ctypes.POINTER(GenParams), _P, _P,
                                        ctypes.POINTER(_U32)]),
+    "vsl_engine_generate_forced": (_I32, [_P, _P, _U32, _P, _U32, _U32, ctypes.POINTER(GenParams), _P, _P,
+                                          ctypes.POINTER(_U32)]),
     "vsl_engine_generate_text": (_I32, [_P, ctypes.c_char_p, _U32, _F32, ctypes.c_char_p, _U64,
                                         ctypes.POINTER(_U64)]),
     "vsl_engine_begin": (_I32, [_P, _P, _U32, _U32, ctypes.POINTER(GenParams)]),
@@ -382,7 +384,10 @@ class Engine:
         return {f: getattr(s, f) for f, _ in ModelSpec._fields_}
 
     def generate_ids(self, prompt, max_new, mode="greedy", temperature=0.0, top_k=40, seed=0, stop_on_eos=False,
-                     return_logits=False):
+                     return_logits=False, forced=None):
+        """Token ids in, generated ids out (and each step's logits with return_logits).  forced: a
+        token history of at least max_new - 1 ids; step t + 1 then takes forced[t] as its input
+        instead of its own sample (teacher forcing; EOS does not stop the run)."""
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
         p = GenParams(_MODES[mode] if isinstance(mode, str) else mode, temperature, top_k, int(bool(stop_on_eos)),
                       seed)
@@ -390,9 +395,16 @@ class Engine:
         V = self.config["vocab_size"]
         logits = np.zeros((max(max_new, 1), V), dtype=np.float32) if return_logits else None
         n = ctypes.c_uint32(0)
-        check(self._lib.vsl_engine_generate_ids(self._h, _ptr(prompt), len(prompt), max_new, ctypes.byref(p),
-                                                _ptr(out), _ptr(logits) if return_logits else None,
-                                                ctypes.byref(n)), self._lib)
+        if forced is not None:
+            f = np.ascontiguousarray(forced, dtype=np.uint32)
+            check(self._lib.vsl_engine_generate_forced(self._h, _ptr(prompt), len(prompt), _ptr(f), len(f), max_new,
+                                                       ctypes.byref(p), _ptr(out),
+                                                       _ptr(logits) if return_logits else None, ctypes.byref(n)),
+                  self._lib)
+        else:
+            check(self._lib.vsl_engine_generate_ids(self._h, _ptr(prompt), len(prompt), max_new, ctypes.byref(p),
+                                                    _ptr(out), _ptr(logits) if return_logits else None,
+                                                    ctypes.byref(n)), self._lib)
         toks = out[:n.value].copy()
         return (toks, logits[:n.value].copy()) if return_logits else toks
 

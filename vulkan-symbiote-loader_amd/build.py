@@ -39,18 +39,31 @@ def _run(cmd):
     return out
 
 
-def build(jobs=8, verbose=False):
+def _stale(obj, src, headers):
+    """True when obj is missing or older than its source or any header it may include."""
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(p) > t for p in [src, *headers])
+
+
+def build(jobs=8, verbose=False, incremental=False):
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIB, exist_ok=True)
     hip_srcs = sorted(f for f in os.listdir(HIP_DIR) if f.endswith(".hip"))
     host_srcs = sorted(f for f in os.listdir(os.path.join(HOST_DIR, "src")) if f.endswith(".cpp"))
+    inc_h = [os.path.join(INC, f) for f in os.listdir(INC) if f.endswith(".h")]
+    hip_h = inc_h + [os.path.join(HIP_DIR, f) for f in os.listdir(HIP_DIR) if f.endswith(".h")]
+    host_h = inc_h + [os.path.join(HOST_DIR, "vk_symbiote", f) for f in os.listdir(os.path.join(HOST_DIR, "vk_symbiote"))]
     jobs_list = []
     for f in hip_srcs:
-        o = os.path.join(OBJ, f + ".o")
-        jobs_list.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(HIP_DIR, f), "-o", o])
+        o, src = os.path.join(OBJ, f + ".o"), os.path.join(HIP_DIR, f)
+        if not incremental or _stale(o, src, hip_h):
+            jobs_list.append([HIPCC, *HIP_FLAGS, "-c", src, "-o", o])
     for f in host_srcs:
-        o = os.path.join(OBJ, f + ".o")
-        jobs_list.append([CXX, *HOST_FLAGS, "-c", os.path.join(HOST_DIR, "src", f), "-o", o])
+        o, src = os.path.join(OBJ, f + ".o"), os.path.join(HOST_DIR, "src", f)
+        if not incremental or _stale(o, src, host_h):
+            jobs_list.append([CXX, *HOST_FLAGS, "-c", src, "-o", o])
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         for out in ex.map(_run, jobs_list):
             if verbose and out.strip():
@@ -70,7 +83,8 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--incremental", action="store_true", help="recompile only objects older than their sources")
     a = ap.parse_args()
-    for p in build(a.jobs, a.verbose):
+    for p in build(a.jobs, a.verbose, a.incremental):
         print(p)
     sys.exit(0)

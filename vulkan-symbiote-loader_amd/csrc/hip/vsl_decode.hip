@@ -962,12 +962,16 @@ __global__ __launch_bounds__(WAVES * 64) void k_attn_decode_mfma(const float* __
             acc[g][0] *= c[g];
             acc[g][1] *= c[g];
         }
+        const uint32_t p0 = tile_pos(j);
 #pragma unroll
         for (int i = 0; i < TP; ++i) {
             float pp[8];
             *reinterpret_cast<float4*>(pp) = *reinterpret_cast<const float4*>(&s_p[wave][i][0]);
             if constexpr (G > 4) *reinterpret_cast<float4*>(pp + 4) = *reinterpret_cast<const float4*>(&s_p[wave][i][4]);
-            const half2v vv = __builtin_bit_cast(half2v, b.v[i]);
+            // the first two tiles were requested up to the capacity: cache rows past the length hold
+            // arbitrary bits (possibly Inf / NaN), and 0 * NaN would reach the sum
+            const uint32_t vbits = p0 + i < n_att ? b.v[i] : 0u;
+            const half2v vv = __builtin_bit_cast(half2v, vbits);
             const float v0 = (float)vv[0], v1 = (float)vv[1];
 #pragma unroll
             for (int g = 0; g < G; ++g) {
@@ -1206,7 +1210,8 @@ int launch_attn_g(uint32_t G, dim3 grid, hipStream_t s, const float* q, const vo
 // ---------------------------------------------------------------------------------------------
 constexpr int kSampBlock = 1024;
 constexpr int kSampPer = 64;  // values per thread: V <= 65536
-constexpr int kMaxTopK = 64;
+constexpr int kMaxTopK = VSL_MAX_TOP_K;
+static_assert(kSampBlock * kSampPer == VSL_MAX_SAMPLE_VOCAB, "one block scans every logit");
 
 __device__ __forceinline__ float sample_uniform(uint32_t k0, uint32_t k1, uint64_t step) {
     uint32_t c[4] = {(uint32_t)step, (uint32_t)(step >> 32), 0u, 0u};
@@ -1230,8 +1235,63 @@ __device__ uint32_t block_sample(const float* __restrict__ logits, uint32_t V, i
         const uint32_t i = tid + (uint32_t)j * kSampBlock;
         vals[j] = i < V ? logits[i] : -INFINITY;
     }
-    const bool greedy = (mode == VSL_SAMPLE_GREEDY || mode == VSL_SAMPLE_REFERENCE || temperature <= 0.f);
-    uint32_t k = greedy ? 1u : (top_k == 0 || top_k > V ? V : top_k);
+    const bool greedy = (mode == VSL_SAMPLE_GREEDY || temperature <= 0.f);
+    if (!greedy && mode == VSL_SAMPLE_REFERENCE) {
+        // sample_token(T > 0) -> member top_k_sampling (VulkanSymbioteEngine.cpp:1806-1855) -> tokens[0]:
+        // the first index of the largest fp32 probability exp(l/T - max) / sum.  That is the logit
+        // argmax except where exp and the division round neighbours of the maximum to the same
+        // probability; any NaN probability (a NaN or +inf logit) gives token 0, as there.
+        __shared__ float red[kSampBlock / 64];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < kSampPer; ++j) {
+            const uint32_t i = tid + (uint32_t)j * kSampBlock;
+            if (i < V) {
+                if (temperature != 1.0f) vals[j] = vals[j] / temperature;
+                mx = fmaxf(mx, vals[j]);
+            }
+        }
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, VSL_WAVE));
+        if (lane == 0) red[wave] = mx;
+        __syncthreads();
+        mx = red[0];
+        for (int w = 1; w < kSampBlock / 64; ++w) mx = fmaxf(mx, red[w]);
+        __syncthreads();
+        float part = 0.f;
+#pragma unroll
+        for (int j = 0; j < kSampPer; ++j) {
+            const uint32_t i = tid + (uint32_t)j * kSampBlock;
+            if (i < V) {
+                vals[j] = expf(vals[j] - mx);
+                part += vals[j];
+            }
+        }
+        for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o, VSL_WAVE);
+        if (lane == 0) red[wave] = part;
+        __syncthreads();
+        float sum = 0.f;
+        for (int w = 0; w < kSampBlock / 64; ++w) sum += red[w];
+        float bv = -INFINITY;
+        uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+        for (int j = 0; j < kSampPer; ++j) {
+            const uint32_t i = tid + (uint32_t)j * kSampBlock;
+            if (i < V) argmax_merge(bv, bi, vals[j] / sum, i);
+        }
+        wave_argmax(bv, bi);
+        if (lane == 0) { wv[wave] = bv; wi[wave] = bi; }
+        __syncthreads();
+        if (tid == 0) {
+            float v = wv[0];
+            uint32_t i = wi[0];
+            for (int w = 1; w < kSampBlock / 64; ++w) argmax_merge(v, i, wv[w], wi[w]);
+            s_tok = i == 0xFFFFFFFFu ? 0u : i;
+        }
+        __syncthreads();
+        return s_tok;
+    }
+    // top-k of at most kMaxTopK (the entry points reject larger k); k > V means all of V
+    uint32_t k = greedy ? 1u : (top_k > V ? V : top_k);
     if (k > (uint32_t)kMaxTopK) k = kMaxTopK;
     for (uint32_t it = 0; it < k; ++it) {
         float bv = -INFINITY;
@@ -1745,6 +1805,17 @@ extern "C" int vsl_norm_swiglu(const float* x, const float* gamma, float eps, co
 
 extern "C" uint32_t vsl_lm_head_ws_blocks(void) { return kMaxLmBlocks; }
 
+// Sampler arguments the kernels serve: a known mode, V <= 65536 wherever logits are scanned by one
+// block, and for seeded top-k 1 <= top_k <= 64 (top_k > V means all of V).
+static int check_sampler(const vsl_sampler& sp, uint32_t V, const char* who) {
+    if (sp.mode < VSL_SAMPLE_GREEDY || sp.mode > VSL_SAMPLE_TOPK_SEEDED) return vsl_invalid("%s: sampler mode %d", who, sp.mode);
+    if (sp.temperature <= 0.f || sp.mode == VSL_SAMPLE_GREEDY) return VSL_OK;  // greedy: no limits
+    if (V > (uint32_t)(kSampBlock * kSampPer)) return vsl_unsupported("%s: sampling supports V <= %d", who, kSampBlock * kSampPer);
+    if (sp.mode == VSL_SAMPLE_TOPK_SEEDED && (sp.top_k == 0 || sp.top_k > (uint32_t)kMaxTopK))
+        return vsl_unsupported("%s: seeded top-k supports 1 <= top_k <= %d (got %u)", who, kMaxTopK, sp.top_k);
+    return VSL_OK;
+}
+
 extern "C" int vsl_lm_head_sample(const float* gamma, float eps, const void* W, int wdtype, uint32_t V, uint32_t d,
                                   float* x, const void* embed, int embed_dtype, float* logits, vsl_sampler sampler,
                                   float* ws_val, uint32_t* ws_idx, uint32_t* tokens, vsl_ctrl* ctrl, void* stream) {
@@ -1754,8 +1825,8 @@ extern "C" int vsl_lm_head_sample(const float* gamma, float eps, const void* W, 
     if (embed_dtype != VSL_DT_F16 && embed_dtype != VSL_DT_F32) return vsl_unsupported("embed dtype %d", embed_dtype);
     if (wdtype != VSL_DT_F16 && wdtype != VSL_DT_F32) return vsl_unsupported("vsl_lm_head_sample: dtype %d", wdtype);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const bool fused = sampler.mode == VSL_SAMPLE_GREEDY || sampler.mode == VSL_SAMPLE_REFERENCE ||
-                       sampler.temperature <= 0.f;
+    if (int rc = check_sampler(sampler, V, "vsl_lm_head_sample")) return rc;
+    const bool fused = sampler.mode == VSL_SAMPLE_GREEDY || sampler.temperature <= 0.f;
     GemvArgs a{};
     a.W = W; a.N = V; a.K = d; a.x = x; a.gamma = gamma; a.eps = eps; a.y = logits;
     a.ws_val = ws_val; a.ws_idx = ws_idx; a.tokens = tokens; a.embed = embed; a.x_next = x;
@@ -1772,8 +1843,6 @@ extern "C" int vsl_lm_head_sample(const float* gamma, float eps, const void* W, 
         HIP_TRY(hipGetLastError());
         return VSL_OK;
     }
-    if (sampler.mode != VSL_SAMPLE_TOPK_SEEDED) return vsl_invalid("vsl_lm_head_sample: sampler mode %d", sampler.mode);
-    if (V > (uint32_t)(kSampBlock * kSampPer)) return vsl_unsupported("top-k sampling supports V <= %d", kSampBlock * kSampPer);
     // logits only (EPI_STORE with the norm prologue), then the sampling kernel
     int rc = wdtype == VSL_DT_F16 ? launch_gemv_k<WF16, 2, 4, EPI_STORE>(a, 1u << 20, s)
                                   : launch_gemv_k<WF32, 2, 4, EPI_STORE>(a, 1u << 20, s);
@@ -1792,8 +1861,7 @@ extern "C" int vsl_lm_head_sample(const float* gamma, float eps, const void* W, 
 extern "C" int vsl_sample_logits(const float* logits, uint32_t V, vsl_sampler sampler, uint64_t step, uint32_t* out,
                                  void* stream) {
     if (!logits || !out || V == 0) return vsl_invalid("vsl_sample_logits: bad arguments");
-    if (V > (uint32_t)(kSampBlock * kSampPer)) return vsl_unsupported("sampling supports V <= %d", kSampBlock * kSampPer);
-    if (sampler.mode < 0 || sampler.mode > 2) return vsl_invalid("vsl_sample_logits: mode %d", sampler.mode);
+    if (int rc = check_sampler(sampler, V, "vsl_sample_logits")) return rc;
     const uint64_t key = vsl_derive_key(sampler.seed, "sampler");
     k_sample_logits<<<1, kSampBlock, 0, static_cast<hipStream_t>(stream)>>>(
         logits, V, sampler.mode, sampler.temperature, sampler.top_k, (uint32_t)key, (uint32_t)(key >> 32), step, out);

@@ -283,7 +283,8 @@ std::vector<uint8_t> quantize_blocks(const float* x, uint64 n, int fmt, int layo
     return out;
 }
 
-GGUFLoader::GGUFLoader(const Path& file_path) : file_path_(file_path) {}
+GGUFLoader::GGUFLoader(const Path& file_path)
+    : file_path_(file_path), tensor_cache_(std::make_unique<TensorLRUCache>()) {}
 GGUFLoader::~GGUFLoader() { close(); }
 
 uint64 GGUFLoader::align_offset(uint64 offset, uint64 alignment) {
@@ -302,10 +303,10 @@ ExpectedVoid GGUFLoader::close() {
     metadata_order_.clear();
     tensors_.clear();
     tensor_order_.clear();
-    {
-        std::lock_guard<std::mutex> lk(cache_mu_);
-        cache_.clear();
-    }
+    if (tensor_cache_) tensor_cache_->clear();
+    vocabulary_.clear();
+    tokenizer_config_ = TokenizerConfig{};
+    shards_.clear();
     return ExpectedVoid();
 }
 
@@ -382,12 +383,18 @@ ExpectedVoid GGUFLoader::load() {
     }
     for (auto& kv : tensors_) {
         GGUFTensorInfo& t = kv.second;
+        // The file is untrusted: an element count whose byte size cannot be represented is a malformed
+        // tensor info (the largest element is 8 bytes, so counts stay below 2^60).
         uint64_t n = 1;
-        for (auto d : t.dimensions) n *= d;
-        t.data_offset = data_start_ + t.offset;
+        for (auto d : t.dimensions)
+            if (__builtin_mul_overflow(n, d, &n) || n >= (1ull << 60)) { close(); return kErrTensorInfo; }
+        // an offset that wraps past 2^64 saturates; tensor_bytes() then rejects it like any other
+        // range outside the mapping
+        if (__builtin_add_overflow(data_start_, t.offset, &t.data_offset)) t.data_offset = UINT64_MAX;
         t.data_size = convention_ == GGUFConvention::REFERENCE ? reference_type_size(static_cast<uint32_t>(t.data_type), n)
                                                                : ggml_type_size(static_cast<uint32_t>(t.data_type), n);
     }
+    parse_vocabulary();
     loaded_ = true;
     return ExpectedVoid();
 }
@@ -424,9 +431,10 @@ ModelConfig GGUFLoader::get_model_config() const {  // GGUFLoader.cpp:673-728
 
 std::vector<PackMetadata> GGUFLoader::generate_packs(const ModelConfig&) {  // GGUFLoader.cpp:730-751
     std::vector<PackMetadata> packs;
-    packs.reserve(tensors_.size());
-    for (const auto& name : tensor_order_) {
-        const GGUFTensorInfo& info = tensors_.at(name);
+    const std::vector<std::string> names = get_tensor_names();
+    packs.reserve(names.size());
+    for (const auto& name : names) {
+        const GGUFTensorInfo& info = *get_tensor(name);
         PackMetadata p;
         p.pack_id = std::hash<std::string>{}(name);
         p.tensor_name = name;
@@ -445,15 +453,33 @@ std::vector<PackMetadata> GGUFLoader::generate_packs(const ModelConfig&) {  // G
     return packs;
 }
 
-uint64 GGUFLoader::tensor_count() const { return header_.tensor_count; }
+uint64 GGUFLoader::tensor_count() const {
+    uint64 n = header_.tensor_count;
+    for (const auto& sh : shards_) n += sh->tensor_count();
+    return n;
+}
 uint64 GGUFLoader::metadata_count() const { return header_.metadata_kv_count; }
 
 const GGUFTensorInfo* GGUFLoader::get_tensor(const std::string& name) const {
     auto it = tensors_.find(name);
-    return it == tensors_.end() ? nullptr : &it->second;
+    if (it != tensors_.end()) return &it->second;
+    for (const auto& sh : shards_)
+        if (const GGUFTensorInfo* t = sh->get_tensor(name)) return t;
+    return nullptr;
+}
+
+const GGUFLoader* GGUFLoader::shard_of(const GGUFTensorInfo& t) const {
+    auto it = tensors_.find(t.name);
+    if (it != tensors_.end() && &it->second == &t) return nullptr;
+    for (const auto& sh : shards_) {
+        auto jt = sh->tensors_.find(t.name);
+        if (jt != sh->tensors_.end() && &jt->second == &t) return sh.get();
+    }
+    return nullptr;
 }
 
 int GGUFLoader::storage_dtype(const GGUFTensorInfo& t) const {
+    if (const GGUFLoader* sh = shard_of(t)) return sh->storage_dtype(t);
     const uint32_t id = static_cast<uint32_t>(t.data_type);
     if (convention_ == GGUFConvention::REFERENCE) {
         if (id == 6) return VSL_DT_F32;
@@ -466,6 +492,7 @@ int GGUFLoader::storage_dtype(const GGUFTensorInfo& t) const {
 }
 
 int GGUFLoader::weight_format(const GGUFTensorInfo& t) const {
+    if (const GGUFLoader* sh = shard_of(t)) return sh->weight_format(t);
     const uint32_t id = static_cast<uint32_t>(t.data_type);
     if (convention_ == GGUFConvention::REFERENCE) {
         switch (id) {
@@ -492,13 +519,22 @@ int GGUFLoader::block_layout() const {
     return convention_ == GGUFConvention::GGML ? VSL_QL_GGML : VSL_QL_REFERENCE;
 }
 
+int GGUFLoader::block_layout(const GGUFTensorInfo& t) const {
+    const GGUFLoader* sh = shard_of(t);
+    return sh ? sh->block_layout() : block_layout();
+}
+
 const uint8_t* GGUFLoader::tensor_bytes(const GGUFTensorInfo& t) const {
-    if (!map_ || t.data_offset + t.data_size > size_ || t.data_offset < data_start_) return nullptr;
+    if (const GGUFLoader* sh = shard_of(t)) return sh->tensor_bytes(t);
+    // written so that no sum can wrap: [data_offset, data_offset + data_size) inside the data section
+    if (!map_ || t.data_offset < data_start_ || t.data_offset > size_ || t.data_size > size_ - t.data_offset)
+        return nullptr;
     return map_ + t.data_offset;
 }
 
 Expected<std::vector<float>> GGUFLoader::read_tensor_data(const GGUFTensorInfo& t, bool fp16_to_fp32) {
     if (!loaded_) return -10;
+    if (const GGUFLoader* sh = shard_of(t)) return const_cast<GGUFLoader*>(sh)->read_tensor_data(t, fp16_to_fp32);
     const uint8_t* p = tensor_bytes(t);
     if (!p) return kErrRead;
     const int dt = storage_dtype(t);
@@ -531,19 +567,181 @@ Expected<std::vector<float>> GGUFLoader::read_tensor_data(const GGUFTensorInfo& 
 }
 
 Expected<std::vector<float>> GGUFLoader::read_tensor_cached(const std::string& name, bool fp16_to_fp32) {
-    {
-        std::lock_guard<std::mutex> lk(cache_mu_);
-        auto it = cache_.find(name);
-        if (it != cache_.end()) return it->second;
-    }
+    std::vector<float> hit;
+    if (tensor_cache_->get(name, hit)) return hit;
     const GGUFTensorInfo* t = get_tensor(name);
     if (!t) return kErrNotFound;
     auto r = read_tensor_data(*t, fp16_to_fp32);
-    if (r.has_value()) {
-        std::lock_guard<std::mutex> lk(cache_mu_);
-        cache_[name] = r.value();
-    }
+    if (r.has_value()) tensor_cache_->put(name, r.value());
     return r;
+}
+
+std::vector<Expected<std::vector<float>>> GGUFLoader::stream_tensors_parallel(const std::vector<std::string>& names,
+                                                                              uint32_t num_chunks) {
+    std::vector<Expected<std::vector<float>>> out(names.size(), Expected<std::vector<float>>(kErrNotFound));
+    const size_t nt = std::max<size_t>(1, std::min<size_t>(num_chunks ? num_chunks : 1, names.size()));
+    std::vector<std::thread> th;
+    th.reserve(nt);
+    for (size_t w = 0; w < nt; ++w)
+        th.emplace_back([&, w]() {
+            // chunk w: a contiguous range of the names; every slot is written by exactly one thread
+            for (size_t i = names.size() * w / nt; i < names.size() * (w + 1) / nt; ++i)
+                if (const GGUFTensorInfo* t = get_tensor(names[i])) out[i] = read_tensor_data(*t, true);
+        });
+    for (auto& t : th) t.join();
+    return out;
+}
+
+void GGUFLoader::clear_tensor_cache() { tensor_cache_->clear(); }
+size_t GGUFLoader::get_tensor_cache_size() const { return tensor_cache_->get_stats().current_memory_bytes; }
+TensorLRUCache::Stats GGUFLoader::get_cache_stats() const { return tensor_cache_->get_stats(); }
+void GGUFLoader::configure_cache(const TensorCacheConfig& config) { tensor_cache_ = std::make_unique<TensorLRUCache>(config); }
+
+ExpectedVoid GGUFLoader::add_shard(const Path& shard_path) {
+    if (!loaded_) return kErrInvalid;
+    auto sh = std::make_unique<GGUFLoader>(shard_path);
+    ExpectedVoid r = sh->load();
+    if (!r.has_value()) return r;
+    shards_.push_back(std::move(sh));
+    return ExpectedVoid();
+}
+
+// GGUFLoaderImpl::parse_vocabulary (GGUFLoader.cpp:982-1075): the tokenizer keys, then the token
+// strings of the "tokenizer.ggml.tokens" array with their scores and types where present.
+void GGUFLoader::parse_vocabulary() {
+    vocabulary_.clear();
+    tokenizer_config_ = TokenizerConfig{};
+    const GGUFMetadataKV* tokens = get_metadata("tokenizer.ggml.tokens");
+    if (!tokens) return;
+    if (auto* kv = get_metadata("tokenizer.ggml.model")) tokenizer_config_.model_type = kv->get_string();
+    if (auto* kv = get_metadata("tokenizer.ggml.bos_token_id")) tokenizer_config_.bos_token_id = kv->get_uint32();
+    if (auto* kv = get_metadata("tokenizer.ggml.eos_token_id")) tokenizer_config_.eos_token_id = kv->get_uint32();
+    if (auto* kv = get_metadata("tokenizer.ggml.padding_token_id")) tokenizer_config_.pad_token_id = kv->get_uint32();
+    if (auto* kv = get_metadata("tokenizer.ggml.unknown_token_id")) tokenizer_config_.unk_token_id = kv->get_uint32();
+    if (auto* kv = get_metadata("tokenizer.ggml.add_bos_token")) tokenizer_config_.add_bos_token = kv->get_bool();
+    if (auto* kv = get_metadata("tokenizer.ggml.add_eos_token")) tokenizer_config_.add_eos_token = kv->get_bool();
+    if (auto* kv = get_metadata("tokenizer.chat_template")) tokenizer_config_.chat_template = kv->get_string();
+    // array payload: element type (u32), count (u64), then the elements
+    auto array_view = [](const GGUFMetadataKV* kv, uint32_t want_type, uint64_t& count) -> const std::vector<uint8_t>* {
+        if (!kv || kv->value_type != GGUFValueType::ARRAY || kv->raw_value.size() < 12) return nullptr;
+        uint32_t et;
+        std::memcpy(&et, kv->raw_value.data(), 4);
+        std::memcpy(&count, kv->raw_value.data() + 4, 8);
+        return et == want_type ? &kv->raw_value : nullptr;
+    };
+    uint64_t n = 0;
+    const std::vector<uint8_t>* a = array_view(tokens, 8, n);
+    if (!a) return;
+    size_t off = 12;
+    for (uint64_t i = 0; i < n; ++i) {
+        uint64_t len;
+        if (a->size() - off < 8) break;
+        std::memcpy(&len, a->data() + off, 8);
+        off += 8;
+        if (len > a->size() - off) break;
+        VocabularyEntry e;
+        e.bytes.assign(a->data() + off, a->data() + off + len);
+        e.token.assign(reinterpret_cast<const char*>(a->data() + off), len);
+        vocabulary_.push_back(std::move(e));
+        off += len;
+    }
+    uint64_t ns = 0;
+    if (const std::vector<uint8_t>* sc = array_view(get_metadata("tokenizer.ggml.scores"), 6, ns))
+        for (uint64_t i = 0; i < ns && i < vocabulary_.size() && 12 + 4 * (i + 1) <= sc->size(); ++i)
+            std::memcpy(&vocabulary_[i].score, sc->data() + 12 + 4 * i, 4);
+    uint64_t ny = 0;
+    const GGUFMetadataKV* ty = get_metadata("tokenizer.ggml.token_type");
+    const std::vector<uint8_t>* tv = array_view(ty, 5, ny);  // INT32 in llama.cpp files
+    if (!tv) tv = array_view(ty, 4, ny);                     // UINT32
+    if (tv)
+        for (uint64_t i = 0; i < ny && i < vocabulary_.size() && 12 + 4 * (i + 1) <= tv->size(); ++i)
+            std::memcpy(&vocabulary_[i].token_type, tv->data() + 12 + 4 * i, 4);
+}
+
+// ------------------------------------------------------------------------------------------
+// TensorLRUCache
+// ------------------------------------------------------------------------------------------
+TensorLRUCache::TensorLRUCache(const TensorCacheConfig& config) : config_(config) {}
+
+bool TensorLRUCache::expired(const Entry& e) const {
+    return config_.ttl_seconds && std::chrono::steady_clock::now() - e.stored > std::chrono::seconds(config_.ttl_seconds);
+}
+
+void TensorLRUCache::drop(std::list<Entry>::iterator it, bool eviction) {
+    bytes_ -= it->data.size() * sizeof(float);
+    index_.erase(it->name);
+    lru_.erase(it);
+    if (eviction) ++stats_.evictions;
+}
+
+bool TensorLRUCache::get(const std::string& name, std::vector<float>& out) {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = index_.find(name);
+    if (it == index_.end() || expired(*it->second)) {
+        if (it != index_.end()) drop(it->second, true);
+        ++stats_.misses;
+        return false;
+    }
+    lru_.splice(lru_.begin(), lru_, it->second);
+    out = it->second->data;
+    ++stats_.hits;
+    return true;
+}
+
+void TensorLRUCache::put(const std::string& name, const std::vector<float>& data) {
+    const size_t cost = data.size() * sizeof(float);
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = index_.find(name);
+    if (it != index_.end()) drop(it->second, false);
+    if (cost > config_.max_memory_bytes || config_.max_entries == 0) return;  // never fits
+    while (!lru_.empty() && (lru_.size() + 1 > config_.max_entries || bytes_ + cost > config_.max_memory_bytes))
+        drop(std::prev(lru_.end()), true);
+    lru_.push_front(Entry{name, data, std::chrono::steady_clock::now()});
+    index_[name] = lru_.begin();
+    bytes_ += cost;
+}
+
+bool TensorLRUCache::contains(const std::string& name) const {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = index_.find(name);
+    return it != index_.end() && !expired(*it->second);
+}
+
+void TensorLRUCache::clear() {
+    std::lock_guard<std::mutex> lk(mu_);
+    lru_.clear();
+    index_.clear();
+    bytes_ = 0;
+}
+
+TensorLRUCache::Stats TensorLRUCache::get_stats() const {
+    std::lock_guard<std::mutex> lk(mu_);
+    Stats s = stats_;
+    s.current_entries = lru_.size();
+    s.current_memory_bytes = bytes_;
+    return s;
+}
+
+void TensorLRUCache::touch(const std::string& name) {
+    std::lock_guard<std::mutex> lk(mu_);
+    auto it = index_.find(name);
+    if (it == index_.end()) return;
+    it->second->stored = std::chrono::steady_clock::now();
+    lru_.splice(lru_.begin(), lru_, it->second);
+}
+
+size_t TensorLRUCache::remove_expired() {
+    std::lock_guard<std::mutex> lk(mu_);
+    size_t n = 0;
+    for (auto it = lru_.begin(); it != lru_.end();) {
+        auto nx = std::next(it);
+        if (expired(*it)) {
+            drop(it, true);
+            ++n;
+        }
+        it = nx;
+    }
+    return n;
 }
 
 std::vector<Expected<std::vector<float>>> GGUFLoader::read_tensors_parallel(const std::vector<std::string>& names,
@@ -562,7 +760,13 @@ std::vector<Expected<std::vector<float>>> GGUFLoader::read_tensors_parallel(cons
     return out;
 }
 
-std::vector<std::string> GGUFLoader::get_tensor_names() const { return tensor_order_; }
+std::vector<std::string> GGUFLoader::get_tensor_names() const {
+    std::vector<std::string> names = tensor_order_;
+    for (const auto& sh : shards_)
+        for (const auto& n : sh->get_tensor_names())
+            if (get_tensor(n) == sh->get_tensor(n)) names.push_back(n);  // not shadowed by an earlier file
+    return names;
+}
 std::vector<std::string> GGUFLoader::get_metadata_keys() const { return metadata_order_; }
 const GGUFMetadataKV* GGUFLoader::get_metadata(const std::string& key) const {
     auto it = metadata_.find(key);
@@ -587,6 +791,15 @@ void GGUFWriter::add_string(const std::string& key, const std::string& v) {
     uint64_t l = v.size();
     std::memcpy(kv.bytes.data(), &l, 8);
     std::memcpy(kv.bytes.data() + 8, v.data(), v.size());
+    kvs_.push_back(std::move(kv));
+}
+void GGUFWriter::add_bool(const std::string& key, bool v) { kvs_.push_back(KV{key, 7, {static_cast<uint8_t>(v ? 1 : 0)}}); }
+void GGUFWriter::add_array(const std::string& key, uint32_t elem_type, uint64_t count, const void* elems,
+                           uint64_t bytes) {
+    KV kv{key, 9, std::vector<uint8_t>(12 + bytes)};
+    std::memcpy(kv.bytes.data(), &elem_type, 4);
+    std::memcpy(kv.bytes.data() + 4, &count, 8);
+    if (bytes) std::memcpy(kv.bytes.data() + 12, elems, bytes);
     kvs_.push_back(std::move(kv));
 }
 void GGUFWriter::add_string_array(const std::string& key, const std::vector<std::string>& v) {

@@ -471,7 +471,7 @@ void VulkanSymbioteEngine::load_weights_from_gguf() {
     // form into a device staging slot and are expanded there by vsl_convert_weights.
     std::unique_ptr<vsl_arena, int (*)(vsl_arena*)> conv_arena(nullptr, vsl_arena_destroy);
     void* dstage[2] = {nullptr, nullptr};
-    auto upload_convert = [&](void* dst, const uint8_t* src, int fmt, uint64_t n, int dst_dt) {
+    auto upload_convert = [&](void* dst, const uint8_t* src, int fmt, int layout, uint64_t n, int dst_dt) {
         if (!conv_arena) {
             vsl_arena* a = nullptr;
             check(vsl_arena_create(options_.device, 2 * kStageBytes + (1u << 20), &a), "staging arena");
@@ -488,7 +488,7 @@ void VulkanSymbioteEngine::load_weights_from_gguf() {
             if (pending[slot]) check(vsl_event_sync(ev_[2 + slot]), "staging wait");
             std::memcpy(stage[slot], src + off, len);
             check(vsl_pack_upload(dstage[slot], stage[slot], len, upload_stream_, nullptr), "vsl_pack_upload");
-            check(vsl_convert_weights(dstage[slot], fmt, g.block_layout(), cnt, static_cast<char*>(dst) + e0 * es,
+            check(vsl_convert_weights(dstage[slot], fmt, layout, cnt, static_cast<char*>(dst) + e0 * es,
                                       dst_dt, upload_stream_),
                   "vsl_convert_weights");
             check(vsl_event_record(ev_[2 + slot], upload_stream_), "staging event");
@@ -514,7 +514,7 @@ void VulkanSymbioteEngine::load_weights_from_gguf() {
         if (fmt == (dt == VSL_DT_F16 ? VSL_WF_F16 : VSL_WF_F32))
             upload(dst, g.tensor_bytes(t), vsl_weight_bytes(fmt, elems));
         else
-            upload_convert(dst, g.tensor_bytes(t), fmt, elems, dt);
+            upload_convert(dst, g.tensor_bytes(t), fmt, g.block_layout(t), elems, dt);
         pack_manager_.register_pack(meta_of(name), dst, elems * (dt == VSL_DT_F16 ? 2 : 4), dt);
     };
     auto load_linear = [&](void* dst, const std::string& name, uint64_t elems) { load_weight(dst, name, elems, wdt_); };
@@ -601,8 +601,9 @@ vsl_graph* VulkanSymbioteEngine::step_graph(const SamplingParams& p) {
     const vsl_sampler s = to_vsl_sampler(p);
     uint32_t tbits;
     std::memcpy(&tbits, &s.temperature, 4);
+    // the temperature is baked into the captured launches of both sampling modes
     auto key = std::make_tuple(s.mode, s.mode == VSL_SAMPLE_TOPK_SEEDED ? s.top_k : 0u,
-                               s.mode == VSL_SAMPLE_TOPK_SEEDED ? tbits : 0u, s.mode == VSL_SAMPLE_TOPK_SEEDED ? s.seed : 0ull);
+                               s.mode != VSL_SAMPLE_GREEDY ? tbits : 0u, s.mode == VSL_SAMPLE_TOPK_SEEDED ? s.seed : 0ull);
     auto it = graphs_.find(key);
     if (it != graphs_.end()) return it->second;
     vsl_graph* g = nullptr;
@@ -695,6 +696,13 @@ int VulkanSymbioteEngine::begin_generation(const std::vector<uint32_t>& prompt, 
     const uint32_t n = static_cast<uint32_t>(prompt.size());
     if ((uint64_t)n + max_new - 1 > cap_) return kErrCapacity;
     if (params.mode < 0 || params.mode > 2) return kErrInvalid;
+    // the samplers' limits are checked before anything is enqueued (vsl_lm_head_sample would refuse
+    // the same request inside the prompt pass)
+    if (params.temperature > 0.0f && params.mode != VSL_SAMPLE_GREEDY) {
+        if (config_.vocab_size > VSL_MAX_SAMPLE_VOCAB) return VSL_E_UNSUPPORTED;
+        if (params.mode == VSL_SAMPLE_TOPK_SEEDED && (params.top_k == 0 || params.top_k > VSL_MAX_TOP_K))
+            return VSL_E_UNSUPPORTED;
+    }
     std::memcpy(host_tokens_, prompt.data(), (size_t)n * 4);
     check(vsl_copy_h2d(prompt_dev_, host_tokens_, (size_t)n * 4, stream_), "prompt upload");
     host_ctrl_->max_steps = max_new;
@@ -754,27 +762,45 @@ int VulkanSymbioteEngine::finish_generation(std::vector<uint32_t>& out_tokens) {
 
 int VulkanSymbioteEngine::generate_ids(const std::vector<uint32_t>& prompt, uint32_t max_new,
                                        const SamplingParams& params, std::vector<uint32_t>& out_tokens,
-                                       std::vector<float>* logits_out) {
+                                       std::vector<float>* logits_out, const std::vector<uint32_t>* forced) {
     out_tokens.clear();
     if (logits_out) logits_out->clear();
     if (max_new == 0) return prompt.empty() ? kErrInvalid : 0;
-    int rc = begin_generation(prompt, max_new, params);
+    if (forced && forced->size() + 1 < max_new) return kErrInvalid;
+    SamplingParams p = params;
+    if (forced) p.stop_on_eos = false;  // the forced history decides every step's input
+    int rc = begin_generation(prompt, max_new, p);
     if (rc < 0) return rc;
-    if (!logits_out) {
+    if (!logits_out && !forced) {
         decode_steps(max_new - 1);
         return finish_generation(out_tokens);
     }
-    // Logits requested (tests): copy the logits row after every sampled token.
-    const uint32_t V = config_.vocab_size;
-    logits_out->assign((size_t)max_new * V, 0.0f);
-    check(vsl_copy_d2h(logits_out->data(), logits_, (size_t)V * 4, stream_), "logits copy");
+    // Step by step: the logits row after every sampled token (when requested), and with a forced
+    // history the next step's input embedding replaced by the forced id (the sampled id stays in
+    // the output).  The forced ids sit in the prompt buffer after the prompt (n + max_new - 1 <= cap).
+    const uint32_t V = config_.vocab_size, n = static_cast<uint32_t>(prompt.size());
+    if (forced && max_new > 1) {
+        // staged after the prompt's ids in the pinned mirror: the prompt's own upload may still be
+        // in flight; the sync keeps finish_generation's reuse of the mirror behind this copy
+        std::memcpy(host_tokens_ + n, forced->data(), (size_t)(max_new - 1) * 4);
+        check(vsl_copy_h2d(prompt_dev_ + n, host_tokens_ + n, (size_t)(max_new - 1) * 4, stream_), "forced upload");
+        check(vsl_stream_sync(stream_), "sync");
+    }
+    if (logits_out) {
+        logits_out->assign((size_t)max_new * V, 0.0f);
+        check(vsl_copy_d2h(logits_out->data(), logits_, (size_t)V * 4, stream_), "logits copy");
+    }
     for (uint32_t t = 1; t < max_new; ++t) {
+        if (forced)
+            check(vsl_embed(embed_, edt_, V, config_.hidden_size, prompt_dev_ + n + (t - 1), 1, x_, stream_),
+                  "forced embedding");
         decode_steps(1);
-        check(vsl_copy_d2h(logits_out->data() + (size_t)t * V, logits_, (size_t)V * 4, stream_), "logits copy");
+        if (logits_out)
+            check(vsl_copy_d2h(logits_out->data() + (size_t)t * V, logits_, (size_t)V * 4, stream_), "logits copy");
     }
     check(vsl_stream_sync(stream_), "sync");
     rc = finish_generation(out_tokens);
-    if (rc >= 0) logits_out->resize((size_t)rc * V);
+    if (rc >= 0 && logits_out) logits_out->resize((size_t)rc * V);
     return rc;
 }
 

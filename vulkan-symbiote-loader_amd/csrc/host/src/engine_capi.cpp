@@ -126,9 +126,38 @@ extern "C" int vsl_engine_generate_ids(vsl_engine* e, const uint32_t* prompt, ui
         int rc = e->impl->generate_ids(ids, max_new, p, out, out_logits ? &logits : nullptr);
         if (rc < 0) {
             const char* why = rc == kErrCapacity ? "prompt + max_new exceeds the KV capacity"
-                              : rc == kErrInvalid ? "empty prompt or bad sampling mode" : "generation failed";
+                              : rc == kErrInvalid ? "empty prompt or bad sampling mode"
+                              : rc == VSL_E_UNSUPPORTED ? "sampler outside its limits (top_k 1..64, V <= 65536)"
+                                                        : "generation failed";
             return fail(rc, std::string("vsl_engine_generate_ids: ") + why);
         }
+        if (!out.empty()) std::memcpy(out_tokens, out.data(), out.size() * 4);
+        if (out_logits && !logits.empty()) std::memcpy(out_logits, logits.data(), logits.size() * 4);
+        if (n_out) *n_out = static_cast<uint32_t>(out.size());
+        return VSL_OK;
+    } catch (const std::exception& ex) {
+        return fail(VSL_E_HIP, ex.what());
+    }
+}
+
+extern "C" int vsl_engine_generate_forced(vsl_engine* e, const uint32_t* prompt, uint32_t n_prompt,
+                                          const uint32_t* forced, uint32_t n_forced, uint32_t max_new,
+                                          const vsl_gen_params* params, uint32_t* out_tokens, float* out_logits,
+                                          uint32_t* n_out) {
+    if (!e || !prompt || !params || (!out_tokens && max_new) || (!forced && n_forced))
+        return fail(VSL_E_INVALID, "vsl_engine_generate_forced: null argument");
+    if (max_new && n_forced + 1 < max_new)
+        return fail(VSL_E_INVALID, "vsl_engine_generate_forced: needs max_new - 1 forced ids");
+    try {
+        SamplingParams p;
+        p.mode = params->mode;
+        p.temperature = params->temperature;
+        p.top_k = params->top_k;
+        p.seed = params->seed;
+        std::vector<uint32_t> ids(prompt, prompt + n_prompt), hist(forced, forced + n_forced), out;
+        std::vector<float> logits;
+        int rc = e->impl->generate_ids(ids, max_new, p, out, out_logits ? &logits : nullptr, &hist);
+        if (rc < 0) return fail(rc, "vsl_engine_generate_forced: generation failed (capacity, prompt or sampler)");
         if (!out.empty()) std::memcpy(out_tokens, out.data(), out.size() * 4);
         if (out_logits && !logits.empty()) std::memcpy(out_logits, logits.data(), logits.size() * 4);
         if (n_out) *n_out = static_cast<uint32_t>(out.size());

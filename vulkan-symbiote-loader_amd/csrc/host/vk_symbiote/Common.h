@@ -10,9 +10,11 @@
 #include <cstdint>
 #include <filesystem>
 #include <new>
+#include <optional>
 #include <stdexcept>
 #include <string>
 #include <utility>
+#include <variant>
 #include <vector>
 
 namespace vk_symbiote {
@@ -61,72 +63,54 @@ struct InferenceParams {
     uint32 context_length = 2048;
 };
 
+// A value or an integer error code: the public interface of the reference's Expected<T>
+// (Common.h:88-193) -- construction from a value or from an int code, has_value(), explicit bool,
+// value() (throws std::runtime_error on an error) and error() (0 while a value is held).  Stored as
+// a std::variant of the value and a tagged code, so copies, moves and destruction are the variant's.
 template <typename T>
 class Expected {
-   private:
-    bool has_value_;
-    alignas(T) unsigned char storage_[sizeof(T)];
-    int error_code_;
+    struct Failure {
+        int code;
+    };
+    std::variant<T, Failure> state_;
+
+    [[noreturn]] void fail_access() const {
+        throw std::runtime_error("Expected::value() called on error state (code " + std::to_string(error()) + ")");
+    }
 
    public:
-    Expected() : has_value_(true), error_code_(0) { new (storage_) T(); }
-    Expected(const T& val) : has_value_(true), error_code_(0) { new (storage_) T(val); }
-    Expected(T&& val) : has_value_(true), error_code_(0) { new (storage_) T(std::move(val)); }
-    Expected(int err) : has_value_(false), error_code_(err) {}
-    ~Expected() {
-        if (has_value_) reinterpret_cast<T*>(storage_)->~T();
-    }
-    Expected(const Expected& o) : has_value_(o.has_value_), error_code_(o.error_code_) {
-        if (has_value_) new (storage_) T(*reinterpret_cast<const T*>(o.storage_));
-    }
-    Expected& operator=(const Expected& o) {
-        if (this != &o) {
-            if (has_value_) reinterpret_cast<T*>(storage_)->~T();
-            has_value_ = o.has_value_;
-            error_code_ = o.error_code_;
-            if (has_value_) new (storage_) T(*reinterpret_cast<const T*>(o.storage_));
-        }
-        return *this;
-    }
-    Expected(Expected&& o) noexcept : has_value_(o.has_value_), error_code_(o.error_code_) {
-        if (has_value_) new (storage_) T(std::move(*reinterpret_cast<T*>(o.storage_)));
-        o.has_value_ = false;
-    }
-    Expected& operator=(Expected&& o) noexcept {
-        if (this != &o) {
-            if (has_value_) reinterpret_cast<T*>(storage_)->~T();
-            has_value_ = o.has_value_;
-            error_code_ = o.error_code_;
-            if (has_value_) new (storage_) T(std::move(*reinterpret_cast<T*>(o.storage_)));
-            o.has_value_ = false;
-        }
-        return *this;
-    }
-    bool has_value() const noexcept { return has_value_; }
-    explicit operator bool() const noexcept { return has_value_; }
+    Expected() : state_(std::in_place_index<0>) {}
+    Expected(const T& val) : state_(std::in_place_index<0>, val) {}
+    Expected(T&& val) : state_(std::in_place_index<0>, std::move(val)) {}
+    Expected(int err) : state_(std::in_place_index<1>, Failure{err}) {}
+
+    bool has_value() const noexcept { return state_.index() == 0; }
+    explicit operator bool() const noexcept { return has_value(); }
     T& value() {
-        if (!has_value_) throw std::runtime_error("Expected::value() called on error state");
-        return *reinterpret_cast<T*>(storage_);
+        if (T* p = std::get_if<0>(&state_)) return *p;
+        fail_access();
     }
     const T& value() const {
-        if (!has_value_) throw std::runtime_error("Expected::value() called on error state");
-        return *reinterpret_cast<const T*>(storage_);
+        if (const T* p = std::get_if<0>(&state_)) return *p;
+        fail_access();
     }
-    int error() const noexcept { return error_code_; }
+    int error() const noexcept {
+        const Failure* f = std::get_if<1>(&state_);
+        return f ? f->code : 0;
+    }
 };
 
+// Success, or the error code it was constructed with (any int, 0 included, means failure).
 template <>
 class Expected<void> {
-   private:
-    int error_code_;
-    bool has_value_;
+    std::optional<int> failure_;
 
    public:
-    Expected() : error_code_(0), has_value_(true) {}
-    Expected(int err) : error_code_(err), has_value_(false) {}
-    bool has_value() const noexcept { return has_value_; }
-    explicit operator bool() const noexcept { return has_value_; }
-    int error() const noexcept { return error_code_; }
+    Expected() = default;
+    Expected(int err) : failure_(err) {}
+    bool has_value() const noexcept { return !failure_.has_value(); }
+    explicit operator bool() const noexcept { return has_value(); }
+    int error() const noexcept { return failure_.value_or(0); }
 };
 using ExpectedVoid = Expected<void>;
 

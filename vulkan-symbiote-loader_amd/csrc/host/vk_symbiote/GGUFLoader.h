@@ -17,7 +17,9 @@
 //    ids (which the reference cannot read at all).
 #pragma once
 
+#include <chrono>
 #include <cstdint>
+#include <list>
 #include <memory>
 #include <mutex>
 #include <string>
@@ -70,6 +72,83 @@ struct GGUFMetadataKV {
     std::vector<uint8_t> get_array_data() const;
 };
 
+// A vocabulary entry of the model file (GGUFLoader.h:110-116): token text and bytes from
+// "tokenizer.ggml.tokens", score from "tokenizer.ggml.scores", type from "tokenizer.ggml.token_type".
+struct VocabularyEntry {
+    std::string token;
+    std::vector<uint8_t> bytes;
+    float score = 0.0f;
+    uint32_t token_type = 0;
+    bool is_special = false;
+};
+
+// The tokenizer keys of the model file (GGUFLoader.h:119-132), read when the file has a vocabulary.
+struct TokenizerConfig {
+    std::string model_type = "gpt2";
+    bool add_bos_token = false;
+    bool add_eos_token = false;
+    uint32_t bos_token_id = 0;
+    uint32_t eos_token_id = 0;
+    uint32_t pad_token_id = 0;
+    uint32_t unk_token_id = 0;
+    std::string chat_template;
+    std::string pre_tokenizer;
+    bool add_space_prefix = true;
+    bool remove_extra_whitespaces = false;
+    std::vector<std::pair<std::string, uint32_t>> added_tokens;
+};
+
+// Bounds of the host-side tensor cache behind read_tensor_cached (GGUFLoader.h:135-140).
+// enable_compression is accepted and ignored (nothing is compressed here).
+struct TensorCacheConfig {
+    size_t max_entries = 256;
+    size_t max_memory_bytes = 4ULL * 1024 * 1024 * 1024;
+    uint64_t ttl_seconds = 300;
+    bool enable_compression = true;
+};
+
+// Least-recently-used cache of converted tensors (the role of the reference's TensorLRUCache,
+// GGUFLoader.h:150-204): bounded by entry count and bytes, entries older than the TTL dropped on
+// access.  Thread-safe.
+class TensorLRUCache {
+   public:
+    struct Stats {
+        size_t hits = 0;
+        size_t misses = 0;
+        size_t evictions = 0;
+        size_t current_entries = 0;
+        size_t current_memory_bytes = 0;
+        double hit_rate() const {
+            const size_t total = hits + misses;
+            return total ? static_cast<double>(hits) / static_cast<double>(total) : 0.0;
+        }
+    };
+    explicit TensorLRUCache(const TensorCacheConfig& config = TensorCacheConfig{});
+    bool get(const std::string& name, std::vector<float>& out);
+    void put(const std::string& name, const std::vector<float>& data);
+    bool contains(const std::string& name) const;
+    void clear();
+    Stats get_stats() const;
+    void touch(const std::string& name);
+    size_t remove_expired();
+    const TensorCacheConfig& config() const { return config_; }
+
+   private:
+    struct Entry {
+        std::string name;
+        std::vector<float> data;
+        std::chrono::steady_clock::time_point stored;
+    };
+    TensorCacheConfig config_;
+    mutable std::mutex mu_;
+    std::list<Entry> lru_;  // front = most recently used
+    std::unordered_map<std::string, std::list<Entry>::iterator> index_;
+    size_t bytes_ = 0;
+    Stats stats_;
+    bool expired(const Entry& e) const;
+    void drop(std::list<Entry>::iterator it, bool eviction);
+};
+
 class GGUFLoader {
    public:
     explicit GGUFLoader(const Path& file_path);
@@ -92,6 +171,31 @@ class GGUFLoader {
     std::vector<Expected<std::vector<float>>> read_tensors_parallel(const std::vector<std::string>& tensor_names,
                                                                     bool fp16_to_fp32 = true);
 
+    // Reads every named tensor as read_tensor_data does, spread over num_chunks threads; one result
+    // per name in the given order (-30 for a name that is not in the model).  The reference routes this
+    // through StreamingTensorReader and drops names it cannot find (GGUFLoader.cpp:1446-1494).
+    std::vector<Expected<std::vector<float>>> stream_tensors_parallel(const std::vector<std::string>& tensor_names,
+                                                                      uint32_t num_chunks = 4);
+
+    // Vocabulary and tokenizer keys of the file (empty / defaults when it has no "tokenizer.ggml.tokens"
+    // array), parsed at load as GGUFLoaderImpl::parse_vocabulary does (GGUFLoader.cpp:982-1075).
+    const std::vector<VocabularyEntry>& get_vocabulary() const { return vocabulary_; }
+    const TokenizerConfig& get_tokenizer_config() const { return tokenizer_config_; }
+
+    // The cache behind read_tensor_cached (GGUFLoader.cpp:1504-1518).
+    void clear_tensor_cache();
+    size_t get_tensor_cache_size() const;  // bytes held
+    TensorLRUCache::Stats get_cache_stats() const;
+    void configure_cache(const TensorCacheConfig& config);  // replaces the cache (entries dropped)
+
+    // Multi-file models: the tensors of another GGUF file join this model's (get_tensor, the tensor
+    // names and counts, generate_packs, read_tensor_data, the engine's upload); each file keeps its own
+    // tensor-type convention.  Metadata stays this file's.  A name already present is not replaced.
+    // Returns the shard's load error, or -60 when this loader is not loaded.  (The reference only logs
+    // the path and reports success, GGUFLoader.cpp:1520-1529.)
+    ExpectedVoid add_shard(const Path& shard_path);
+    bool is_sharded() const { return !shards_.empty(); }
+
     std::vector<std::string> get_tensor_names() const;
     std::vector<std::string> get_metadata_keys() const;
     const GGUFMetadataKV* get_metadata(const std::string& key) const;
@@ -112,6 +216,8 @@ class GGUFLoader {
     int weight_format(const GGUFTensorInfo& t) const;
     // VSL_QL_REFERENCE or VSL_QL_GGML: block layout of this file's quantized tensors
     int block_layout() const;
+    // the block layout of the file (this one or a shard) holding `t`
+    int block_layout(const GGUFTensorInfo& t) const;
 
    private:
     Path file_path_;
@@ -126,8 +232,14 @@ class GGUFLoader {
     std::vector<std::string> metadata_order_;
     std::unordered_map<std::string, GGUFTensorInfo> tensors_;
     std::vector<std::string> tensor_order_;
-    std::unordered_map<std::string, std::vector<float>> cache_;
-    std::mutex cache_mu_;
+    std::unique_ptr<TensorLRUCache> tensor_cache_;
+    std::vector<VocabularyEntry> vocabulary_;
+    TokenizerConfig tokenizer_config_;
+    std::vector<std::unique_ptr<GGUFLoader>> shards_;
+
+    void parse_vocabulary();
+    // the shard whose tensor table holds `t` (nullptr: this file's, or unknown)
+    const GGUFLoader* shard_of(const GGUFTensorInfo& t) const;
 };
 
 // IEEE binary16 <-> binary32 (every case exact / round to nearest even; the reference's
@@ -153,6 +265,10 @@ class GGUFWriter {
     void add_f32(const std::string& key, float v);
     void add_string(const std::string& key, const std::string& v);
     void add_string_array(const std::string& key, const std::vector<std::string>& v);
+    void add_bool(const std::string& key, bool v);
+    // an array of fixed-size elements: elem_type is the GGUF metadata type id (e.g. 6 FLOAT32, 5 INT32),
+    // elems `count` values of `bytes` bytes in total
+    void add_array(const std::string& key, uint32_t elem_type, uint64_t count, const void* elems, uint64_t bytes);
     // data: raw bytes in the storage type (is_f16 ? binary16 : binary32); dims ne0-first
     void add_tensor(const std::string& name, const std::vector<uint64_t>& dims, bool is_f16, const void* data,
                     uint64_t bytes);

@@ -134,9 +134,13 @@ class VulkanSymbioteEngine {
 
     // Token-id entry point.  Returns the number of generated tokens (<0 on error).
     // logits_out (optional) receives one vocab-sized row per generated token: the logits that
-    // token was sampled from.
+    // token was sampled from.  forced (optional, >= max_new - 1 ids) teacher-forces the history:
+    // step t + 1 takes forced[t] as its input instead of the token sampled at step t (the sampled
+    // tokens are still returned, and EOS does not stop the run), so every step's logits can be
+    // compared with another implementation's on the same token history.
     int generate_ids(const std::vector<uint32_t>& prompt, uint32_t max_new, const SamplingParams& params,
-                     std::vector<uint32_t>& out_tokens, std::vector<float>* logits_out = nullptr);
+                     std::vector<uint32_t>& out_tokens, std::vector<float>* logits_out = nullptr,
+                     const std::vector<uint32_t>* forced = nullptr);
 
     const ModelConfig& config() const noexcept { return config_; }
     ModelConfig& config() noexcept { return config_; }
