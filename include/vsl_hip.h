@@ -208,6 +208,17 @@ int vsl_attn_decode(const float* q, const void* kcache, const void* vcache, int 
                     uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* part_o,
                     float* part_ml, float* out, vsl_ctrl* ctrl, void* stream);
 
+/* vsl_attn_decode with no workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The split partials go to a static device array of the library (2 MiB + 32 KiB per GPU,
+ * held until the process ends): n_q * nsplit <= 4096 and head_dim <= 128, else VSL_E_CAPACITY before
+ * anything is launched.  Allocates nothing.  Every call on one GPU shares that array, so calls that
+ * overlap on one GPU (concurrent streams, threads) race; calls ordered on one stream do not.  Results
+ * are those of vsl_attn_decode bit for bit. */
+int vsl_attn_decode_noalloc(const float* q, const void* kcache, const void* vcache, int kv_dtype, uint32_t n_q,
+                            uint32_t n_kv, uint32_t hd, uint32_t cap, float scale, uint32_t nsplit, float* out,
+                            vsl_ctrl* ctrl, void* stream);
+
 /* Windowed long-context mode (the reference's use_sparse_attention, Common.h:70-75, switched on
  * above `seq_len > 8192` at VulkanSymbioteEngine.cpp:788; sparse_attention.comp:77-100 sliding
  * window + global tokens).  With p = ctrl->pos: while p + 1 <= threshold the query attends to every

@@ -143,6 +143,7 @@ _HIP_SIGS = {
     "vsl_qkv_rope_append": (_I32, [_P, _P, _F32, _P, _I32, _U32, _U32, _U32, _U32, _P, _P, _P, _P, _I32, _U32, _P,
                                    _P, _P]),
     "vsl_attn_decode": (_I32, [_P, _P, _P, _I32, _U32, _U32, _U32, _U32, _F32, _U32, _P, _P, _P, _P, _P]),
+    "vsl_attn_decode_noalloc": (_I32, [_P, _P, _P, _I32, _U32, _U32, _U32, _U32, _F32, _U32, _P, _P, _P]),
     "vsl_gemv_residual": (_I32, [_P, _I32, _U32, _U32, _P, _P, _P, _P]),
     "vsl_norm_swiglu": (_I32, [_P, _P, _F32, _P, _I32, _U32, _U32, _P, _P, _P]),
     "vsl_lm_head_sample": (_I32, [_P, _F32, _P, _I32, _U32, _U32, _P, _P, _I32, _P, Sampler, _P, _P, _P, _P, _P]),

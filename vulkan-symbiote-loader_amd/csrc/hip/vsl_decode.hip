@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 #include "vsl_device.h"
@@ -1777,6 +1778,56 @@ extern "C" int vsl_attn_decode_window(const float* q, const void* kcache, const 
         return vsl_invalid("vsl_attn_decode_window: window %u + global %u too large", window, n_global);
     return attn_decode(q, kcache, vcache, kv_dtype, n_q, n_kv, hd, cap, scale, nsplit, part_o, part_ml, out, ctrl,
                        AttnWindow{true, window, n_global, threshold}, stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// vsl_attn_decode without a caller workspace: the split partials live in a static device array.
+// ---------------------------------------------------------------------------------------------
+// Up to kScratchPairs (query head, split) pairs of partials: an fp32 output row of up to
+// kScratchHd dims each, then the (m, l) pairs.  2 MiB + 32 KiB per GPU, held until the process ends.
+constexpr uint32_t kScratchPairs = 4096, kScratchHd = 128;
+constexpr size_t kScratchFloats = (size_t)kScratchPairs * (kScratchHd + 2);
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+// The array's address on the current device, looked up once per device (each GPU holds its own copy;
+// the array's name in host code is not a device address).  nullptr after a failed lookup.
+static float* scratch_on_current_device() {
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static float* addr[kMaxDevices] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        vsl_set_error("vsl_attn_decode_noalloc: no current device (or device id >= %d)", kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            vsl_set_error("vsl_attn_decode_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                          hipGetErrorString(e));
+            return nullptr;
+        }
+        addr[dev] = static_cast<float*>(p);
+    }
+    return addr[dev];
+}
+
+extern "C" int vsl_attn_decode_noalloc(const float* q, const void* kcache, const void* vcache, int kv_dtype,
+                                       uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale,
+                                       uint32_t nsplit, float* out, vsl_ctrl* ctrl, void* stream) {
+    if ((uint64_t)n_q * nsplit > kScratchPairs || hd > kScratchHd)
+        return vsl_capacity("vsl_attn_decode_noalloc: n_q * nsplit = %llu (max %u) and head_dim %u (max %u) "
+                            "exceed the static partials buffer",
+                            (unsigned long long)n_q * nsplit, kScratchPairs, hd, kScratchHd);
+    float* base = scratch_on_current_device();
+    if (!base) return VSL_E_HIP;
+    // same layout as a caller workspace: part_o [n_q][nsplit][hd], then part_ml [n_q][nsplit][2]
+    float* part_o = base;
+    float* part_ml = base + (size_t)kScratchPairs * kScratchHd;
+    return attn_decode(q, kcache, vcache, kv_dtype, n_q, n_kv, hd, cap, scale, nsplit, part_o, part_ml, out, ctrl,
+                       AttnWindow{false, 0, 0, 0}, stream);
 }
 
 extern "C" int vsl_gemv_residual(const void* W, int wdtype, uint32_t N, uint32_t K, const float* x, float* resid,

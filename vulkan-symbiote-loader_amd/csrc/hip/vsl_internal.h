@@ -28,6 +28,12 @@ static inline int vsl_unsupported(const char* fmt, A... a) {
     return VSL_E_UNSUPPORTED;
 }
 
+template <typename... A>
+static inline int vsl_capacity(const char* fmt, A... a) {
+    vsl_set_error(fmt, a...);
+    return VSL_E_CAPACITY;
+}
+
 // Direct-to-LDS prefill GEMM (vsl_gemm_dma.hip). cfg 0: 256 x 256 tiles, cfg 1: 128 x 256.
 uint32_t vsl_gemm_dma_tiles(int cfg, uint32_t M, uint32_t N, uint32_t K, int epi);
 int vsl_gemm_dma_launch(int cfg, void* stream, const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K,
