@@ -7,6 +7,10 @@ Workload: 32 layers, d_model 4096, 32 query / 8 KV heads (head_dim 128), SwiGLU 
 cache fp16 with capacity 4096; prompt of 512 uniform-random token ids (prefill timed on its own),
 then greedy decode.  A step is one decode token; K steps are timed between two synchronisations.
 
+The same run also measures, as extra keys of the one JSON line: the configured 512-step decode
+(positions 513..1024), the 1B-class model (prompt 128, greedy decode 256), the fp16 GEMV sweep and the
+long-context workload (8192-token prompt in 2048-token chunks, KV capacity 32768); --quick skips them.
+
 Prints one JSON line.  --gpus N with N > 1 exits: this build targets one GPU.
 """
 import argparse
@@ -26,10 +30,51 @@ CFG = dict(hidden_size=4096, num_layers=32, num_heads=32, num_kv_heads=8, interm
            max_position_embeddings=32768, rope_theta=500000.0, rms_eps=1e-5, dtype=1)
 KV_CAPACITY = 4096
 
-# HBM bytes per launch of the dominant decode kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
-# passes summarised in profiles/llama8b_decode_prefill_rocprof.md (FETCH_SIZE scaled x1.9999 by a 1 GiB copy).
-# Re-measure with the commands listed there whenever the kernel changes.
-DOMINANT_TRAFFIC_BYTES = 235_290_000 + 115_000
+LLAMA_1B = dict(hidden_size=2048, num_layers=16, num_heads=32, num_kv_heads=8, intermediate_size=8192,
+                vocab_size=32000, max_position_embeddings=4096, rope_theta=10000.0, rms_eps=1e-5, dtype=1)
+
+# The rocprofv3 summary whose FETCH_SIZE / WRITE_SIZE columns give the dominant decode kernel's HBM
+# traffic per launch (counters scaled by a copy kernel of known size, as the file states).
+PROFILE = os.path.join(ROOT, "profiles", "llama8b_decode_prefill_rocprof.md")
+DOMINANT_KERNEL_ROW = "`k_gemv_dec<WF16, 2, 4, 2, WF32, 4, 4>`"
+
+
+def profiled_traffic(path=PROFILE, row=DOMINANT_KERNEL_ROW):
+    """HBM bytes per launch (FETCH + WRITE, MB = 1e6 bytes) of the dominant decode kernel, read from
+    the kernel table of the committed profile summary; None when the row is missing."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("| " + row):
+                    cols = [c.strip() for c in line.strip().strip("|").split("|")]
+                    return int(round((float(cols[5]) + float(cols[6])) * 1e6))
+    except (OSError, ValueError, IndexError):
+        return None
+    return None
+
+
+def host_facts():
+    """CPU model, sockets / NUMA nodes of the host, and the CPUs and memory nodes this process may use."""
+    import subprocess
+    facts = {"cpus_allowed": len(os.sched_getaffinity(0)), "nproc": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k in ("Model name", "Socket(s)", "NUMA node(s)", "Thread(s) per core", "Core(s) per socket"):
+                facts[k.lower().replace("(s)", "s").replace(" ", "_")] = v
+    except Exception:
+        pass
+    try:
+        with open("/proc/self/status") as f:
+            for line in f:
+                if line.startswith(("Cpus_allowed_list", "Mems_allowed_list")):
+                    k, _, v = line.partition(":")
+                    facts[k.strip().lower()] = v.strip()
+    except OSError:
+        pass
+    return facts
 
 
 def load_package():
@@ -68,8 +113,8 @@ def prefill_flops(c, S):
 
 def cpu_baseline(eng, cfg, prompt, seconds):
     """The oracle (CPU restatement of the reference's token loop) on this host, timed on a bounded
-    sample: the engine's resident weights copied to host memory, a short prompt, then greedy decode
-    steps for about `seconds`."""
+    sample of the same workload: the engine's resident weights copied to host memory, the bench's
+    prompt processed (untimed), then greedy decode steps from the next position for about `seconds`."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
     d, L, nq, nkv, F, V = (cfg["hidden_size"], cfg["num_layers"], cfg["num_heads"], cfg["num_kv_heads"],
@@ -89,21 +134,29 @@ def cpu_baseline(eng, cfg, prompt, seconds):
     for n in ["output_norm.weight"] + [f"blk.{l}.{s}.weight" for l in range(L) for s in ("attn_norm", "ffn_norm")]:
         m.set_tensor(n, eng.read_tensor(n, d * 4))
     threads = orc.num_threads()
+    t0 = time.perf_counter()
     n, secs = m.decode_rate(prompt, max_seconds=seconds, max_tokens=4096)
+    wall = time.perf_counter() - t0
     m.close()
     return {"value": n / secs, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"oracle greedy decode of {n} tokens after a {len(prompt)}-token prompt on the same 8B "
-                      f"weights ({secs:.1f} s, {threads} threads, fp16 weights / fp32 math)"}
+            "sample": f"oracle greedy decode of {n} tokens at positions {len(prompt) + 1}..{len(prompt) + n} after "
+                      f"the bench's {len(prompt)}-token prompt (processed untimed, {wall - secs:.1f} s) on the same "
+                      f"8B weights ({secs:.1f} s timed, {threads} OpenMP threads, fp16 weights / fp32 math)",
+            "host": host_facts()}
 
 
-def run_sweep(a):
-    """GEMV sweep: W [N,K] fp16 ~N(0,0.02), X [K,B] fp16 ~N(0,1), fp32 accumulate, fp16 Y."""
-    import ctypes
+def gpus_or_exit(a):
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (use --gpus 1)",
               file=sys.stderr)
         sys.exit(2)
-    vsl = load_package()
+
+
+def sweep_leg(vsl):
+    """GEMV sweep: W [N,K] fp16 ~N(0,0.02), X [K,B] fp16 ~N(0,1), fp32 accumulate, fp16 Y; W rotated
+    over >= 512 MB of distinct copies so the 256 MB MALL cannot serve it.  Returns the per-shape rows and
+    geometric means (all shapes, and per B)."""
+    import ctypes
     H = vsl.hip()
     P = ctypes.c_void_p
     arena = P()
@@ -149,85 +202,134 @@ def run_sweep(a):
             rows.append({"N": N, "K": K, "B": B, "us": round(us, 2), "gbps": round(nbytes / us / 1e3, 1),
                          "hbm_frac": round(nbytes / us / 1e3 / (PEAK_HBM / 1e9), 4),
                          "tflops": round(2 * N * K * B / us / 1e6, 2)})
+    vsl.check(H.vsl_event_destroy(e0))
+    vsl.check(H.vsl_event_destroy(e1))
     vsl.check(H.vsl_arena_destroy(arena))
-    geo = float(np.exp(np.mean([np.log(r["gbps"]) for r in rows])))
+    geo = lambda rs: round(float(np.exp(np.mean([np.log(r["gbps"]) for r in rs]))), 1)
+    return {"geomean_gbps": geo(rows), "geomean_hbm_frac": round(geo(rows) / (PEAK_HBM / 1e9), 4),
+            "geomean_gbps_by_B": {str(B): geo([r for r in rows if r["B"] == B]) for B in (1, 4, 16)},
+            "shapes": rows}
+
+
+def run_sweep(a):
+    gpus_or_exit(a)
+    sw = sweep_leg(load_package())
     out = {"metric": "GEMV sweep HBM GB/s (geometric mean over 12 shapes), fp16 W/X/Y, fp32 accumulate",
-           "value": round(geo, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f16",
+           "value": sw["geomean_gbps"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f16",
            "data": "synthetic: W ~N(0,0.02), X ~N(0,1) fp16 (Philox on device); W rotated over >= 512 MB",
            "config": {"workload": "GEMV / skinny-GEMM sweep y = W X, (N,K) in {(4096,4096),(14336,4096),"
-                                  "(4096,14336),(32000,4096)}, B in {1,4,16}"},
-           "shapes": rows}
+                                  "(4096,14336),(32000,4096)}, B in {1,4,16}"}}
+    out.update(sw)
     print(json.dumps(out), flush=True)
+
+
+def timed_decode(eng, prompt, steps, **kw):
+    """One generation: the prompt pass, then exactly `steps` decode steps between two synchronisations.
+    Returns (decode seconds, the engine's stats of the generation)."""
+    eng.begin(prompt, steps + 1, **kw)
+    eng.sync()
+    t0 = time.perf_counter()
+    issued = eng.decode(steps)
+    eng.sync()
+    dt = time.perf_counter() - t0
+    toks = eng.finish()
+    assert issued == steps and len(toks) == steps + 1, (issued, len(toks))
+    return dt, eng.last_stats()
+
+
+def decode_rates(cfg, n_prompt, steps, secs):
+    """tok/s and algorithmic HBM rate of `steps` decode steps after an n_prompt-token prompt (step i
+    processes position n_prompt + i - 1 and attends n_prompt + i positions)."""
+    total = sum(decode_bytes(cfg, n_prompt + i) for i in range(1, steps + 1))
+    return {"tok_s": round(steps / secs, 2), "ms_per_step": round(secs * 1e3 / steps, 4),
+            "hbm_gbps": round(total / secs / 1e9, 1), "hbm_frac": round(total / secs / PEAK_HBM, 4),
+            "bytes_per_token": int(total / steps)}
+
+
+def long_leg(vsl, steps, eager):
+    """Long-context workload: 8B-class fp16, prompt 8192 prefilled in 2048-row chunks, KV capacity 32768,
+    greedy decode, the same decode with T=0.7 top-k 40 seeded sampling, and with the windowed mode at
+    the reference's parameters (window 512, 16 global tokens, from sequence length 8193 on)."""
+    n_prompt, cap, chunk = 8192, 32768, 2048
+    prompt = np.random.default_rng(1).integers(0, CFG["vocab_size"], n_prompt).astype(np.uint32)
+    eng = vsl.Engine(spec=CFG, seed=0, kv_capacity=cap, prefill_chunk=chunk, use_graph=not eager)
+    try:
+        eng.begin(prompt, 3)  # warmup: capture, caches
+        eng.decode(2)
+        eng.finish()
+        dec_s, st = timed_decode(eng, prompt, steps)
+        samp_s, _ = timed_decode(eng, prompt, steps, mode="topk", temperature=0.7, top_k=40, seed=7)
+    finally:
+        eng.close()
+    pre_s = st["prefill_ms"] / 1e3
+    pre_flops = prefill_flops(CFG, n_prompt)
+    out = {"workload": f"8B-class fp16 bs=1: prompt {n_prompt} prefilled in {chunk}-token chunks, KV cap {cap}, "
+                       f"decode {steps} greedy, then {steps} with T=0.7 top-k 40 seeded sampling",
+           "decode": decode_rates(CFG, n_prompt, steps, dec_s),
+           "sampled_tok_s": round(steps / samp_s, 2),
+           "prefill_tok_s": round(n_prompt / pre_s, 1), "prefill_ms": round(st["prefill_ms"], 3),
+           "prefill_tflops": round(pre_flops / pre_s / 1e12, 1),
+           "prefill_mfma_frac": round(pre_flops / pre_s / PEAK_F16, 4)}
+    win = (512, 16, 8192)
+    eng = vsl.Engine(spec=CFG, seed=0, kv_capacity=cap, prefill_chunk=chunk, use_graph=not eager, window=win)
+    try:
+        eng.begin(prompt, 3)
+        eng.decode(2)
+        eng.finish()
+        win_s, _ = timed_decode(eng, prompt, steps)
+    finally:
+        eng.close()
+    n_att = win[1] + win[0] + 1
+    win_bytes = sum(decode_bytes(CFG, n_prompt + i if n_prompt + i <= win[2] else n_att) for i in range(1, steps + 1))
+    out["window"] = {"sparse_window": win[0], "sparse_global": win[1], "sparse_threshold": win[2],
+                     "decode_tok_s": round(steps / win_s, 2), "hbm_gbps": round(win_bytes / win_s / 1e9, 1),
+                     "hbm_frac": round(win_bytes / win_s / PEAK_HBM, 4)}
+    return out
 
 
 def run_long(a):
-    """Long-context workload: 8B-class fp16, prompt 8192 (2048-row chunks), KV capacity 32768."""
-    if a.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (use --gpus 1)",
-              file=sys.stderr)
-        sys.exit(2)
+    gpus_or_exit(a)
     steps = a.steps if a.steps != 512 else 128
-    n_prompt, cap, chunk = 8192, 32768, 2048
-    vsl = load_package()
-    eng = vsl.Engine(spec=CFG, seed=0, kv_capacity=cap, prefill_chunk=chunk, use_graph=not a.eager)
-    prompt = np.random.default_rng(1).integers(0, CFG["vocab_size"], n_prompt).astype(np.uint32)
-    eng.begin(prompt, 3)  # warmup: capture, caches
-    eng.decode(2)
-    eng.finish()
-
-    def timed(**kw):
-        eng.begin(prompt, steps + 1, **kw)
-        eng.sync()
-        t0 = time.perf_counter()
-        issued = eng.decode(steps)
-        eng.sync()
-        dt = time.perf_counter() - t0
-        toks = eng.finish()
-        assert issued == steps and len(toks) == steps + 1, (issued, len(toks))
-        return dt, eng.last_stats()
-
-    dec_s, st = timed()
-    samp_s, st2 = timed(mode="topk", temperature=0.7, top_k=40, seed=7)
-    total_bytes = sum(decode_bytes(CFG, n_prompt + i) for i in range(1, steps + 1))
-    pre_s = st["prefill_ms"] / 1e3
-    pre_flops = prefill_flops(CFG, n_prompt)
+    lg = long_leg(load_package(), steps, a.eager)
     out = {
         "metric": "decode tok/s + HBM GB/s (% peak), 8B fp16 bs=1, long context; prefill tok/s",
-        "value": round(steps / dec_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": 2,
-        "ms_per_step": round(dec_s * 1e3 / steps, 4), "higher_is_better": True, "scaling": "weak",
+        "value": lg["decode"]["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": 2,
+        "ms_per_step": lg["decode"]["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f16",
         "data": "synthetic: random-init N(0,0.02) fp16 weights (Philox on device), uniform-random prompt ids",
-        "config": {"workload": f"8B-class Llama decoder fp16 bs=1, long context: prompt {n_prompt} prefilled in "
-                               f"{chunk}-token chunks, KV cap {cap}, greedy decode {steps}; then T=0.7 top-k 40 "
-                               f"seeded decode {steps}",
-                   "global_batch": 1, "seq_len": n_prompt + steps, "parallelism": "single-gpu"},
-        "decode_hbm_gbps": round(total_bytes / dec_s / 1e9, 1),
-        "decode_hbm_frac": round(total_bytes / dec_s / PEAK_HBM, 4),
-        "decode_bytes_per_token": int(total_bytes / steps),
-        "sampled_tok_s": round(steps / samp_s, 2),
-        "prefill_tok_s": round(n_prompt / pre_s, 1),
-        "prefill_ms": round(st["prefill_ms"], 3),
-        "prefill_tflops": round(pre_flops / pre_s / 1e12, 1),
-        "prefill_mfma_frac": round(pre_flops / pre_s / PEAK_F16, 4),
+        "config": {"workload": lg["workload"], "global_batch": 1, "seq_len": 8192 + steps,
+                   "parallelism": "single-gpu"},
         "decode_launch": "eager" if a.eager else "hipGraph replay",
     }
-    eng.close()
-    # the same decode with the windowed long-context mode at the reference's parameters (window 512,
-    # 16 global tokens, from sequence length 8193 on): every decode step attends 529 positions
-    win = (512, 16, 8192)
-    eng = vsl.Engine(spec=CFG, seed=0, kv_capacity=cap, prefill_chunk=chunk, use_graph=not a.eager, window=win)
-    eng.begin(prompt, 3)
-    eng.decode(2)
-    eng.finish()
-    win_s, _ = timed()
-    eng.close()
-    n_att = win[1] + win[0] + 1
-    win_bytes = sum(decode_bytes(CFG, n_prompt + i if n_prompt + i <= win[2] else n_att) for i in range(1, steps + 1))
-    out["window_decode_tok_s"] = round(steps / win_s, 2)
-    out["window_decode_hbm_gbps"] = round(win_bytes / win_s / 1e9, 1)
-    out["window_decode_hbm_frac"] = round(win_bytes / win_s / PEAK_HBM, 4)
-    out["window"] = {"sparse_window": win[0], "sparse_global": win[1], "sparse_threshold": win[2]}
+    out.update(lg)
     print(json.dumps(out), flush=True)
+
+
+def llama_1b_leg(vsl, eager, prefill_runs=5):
+    """1B-class fp16 (16 layers, d 2048, 32/8 heads, FFN 8192, V 32000): prompt 128, greedy decode 256."""
+    n_prompt, steps = 128, 256
+    prompt = np.random.default_rng(2).integers(0, LLAMA_1B["vocab_size"], n_prompt).astype(np.uint32)
+    eng = vsl.Engine(spec=LLAMA_1B, seed=0, kv_capacity=1024, use_graph=not eager)
+    try:
+        eng.begin(prompt, 9)
+        eng.decode(8)
+        eng.finish()
+        dec_s, st = timed_decode(eng, prompt, steps)
+        pre = [st["prefill_ms"]]
+        for _ in range(prefill_runs - 1):
+            eng.begin(prompt, 1)
+            eng.finish()
+            pre.append(eng.last_stats()["prefill_ms"])
+    finally:
+        eng.close()
+    pre_ms = float(np.median(pre))
+    pre_flops = prefill_flops(LLAMA_1B, n_prompt)
+    return {"workload": f"1B-class Llama decoder fp16 bs=1 (16L, d2048, 32/8 heads, FFN 8192, V32000): prompt "
+                        f"{n_prompt}, greedy decode {steps}",
+            "decode": decode_rates(LLAMA_1B, n_prompt, steps, dec_s),
+            "prefill_ms": round(pre_ms, 3), "prefill_tok_s": round(n_prompt / (pre_ms / 1e3), 1),
+            "prefill_tflops": round(pre_flops / (pre_ms / 1e3) / 1e12, 1),
+            "prefill_mfma_frac": round(pre_flops / (pre_ms / 1e3) / PEAK_F16, 4)}
 
 
 def main():
@@ -238,7 +340,11 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--prefill-runs", type=int, default=5, help="prompt passes timed; the median is reported")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--attn-splits", type=int, default=0,
+                    help="decode attention split count of the 8B engine (0: the engine's choice)")
+    ap.add_argument("--quick", action="store_true",
+                    help="the headline decode / prefill only (no 512-step decode, 1B, sweep or long-context legs)")
     ap.add_argument("--no-kernel-timing", action="store_true")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="after the run, copy this many MB device-to-device once (a kernel of known traffic "
@@ -261,17 +367,14 @@ def main():
     if a.sweep:
         run_sweep(a)
         return
-    if a.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {a.gpus} is not supported (use --gpus 1)",
-              file=sys.stderr)
-        sys.exit(2)
+    gpus_or_exit(a)
     if a.prompt + a.steps > KV_CAPACITY:
         print("bench.py: prompt + steps exceed the KV capacity", file=sys.stderr)
         sys.exit(2)
 
     vsl = load_package()
     t_init = time.perf_counter()
-    eng = vsl.Engine(spec=CFG, seed=0, kv_capacity=KV_CAPACITY, use_graph=not a.eager)
+    eng = vsl.Engine(spec=CFG, seed=0, kv_capacity=KV_CAPACITY, use_graph=not a.eager, attn_splits=a.attn_splits)
     init_s = time.perf_counter() - t_init
     prompt = np.random.default_rng(1).integers(0, CFG["vocab_size"], a.prompt).astype(np.uint32)
 
@@ -357,19 +460,36 @@ def main():
         dom = ops["norm_gateup_swiglu"]
         achieved = dom["bytes"] / (dom["avg_us"] * 1e-6)
         out["roofline"] = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
-                           "frac": round(achieved / PEAK_HBM, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
+                           "frac": round(achieved / PEAK_HBM, 4), "traffic": profiled_traffic(),
                            "algorithmic_bytes": dom["bytes"],
                            "kernel": "k_gemv_dec<EPI_SWIGLU> (ffn norm + [Wgate;Wup] GEMV + SwiGLU)",
-                           "traffic_source": "profiles/llama8b_decode_prefill_rocprof.md"}
+                           "traffic_source": os.path.relpath(PROFILE, ROOT) + " (FETCH_SIZE + WRITE_SIZE columns "
+                                             "of the kernel's row, read at run time)"}
         out["decode_ops"] = ops
+
+    # the configured decode length: 512 greedy steps after the 512-token prompt (positions 513..1024)
+    if not a.quick and a.prompt + 512 <= KV_CAPACITY:
+        secs, _ = timed_decode(eng, prompt, 512)
+        out["decode_512"] = dict(decode_rates(CFG, a.prompt, 512, secs),
+                                 workload=f"prompt {a.prompt}, greedy decode 512 (positions {a.prompt + 1}.."
+                                          f"{a.prompt + 512}), KV cap {KV_CAPACITY}")
 
     if not a.no_cpu_baseline:
         try:
-            out["cpu_baseline"] = cpu_baseline(eng, CFG, prompt[:8], a.cpu_seconds)
+            out["cpu_baseline"] = cpu_baseline(eng, CFG, prompt, a.cpu_seconds)
         except Exception as ex:  # reported, never fatal to the GPU measurement
             out["cpu_baseline"] = {"value": None, "unit": "tok/s", "cores": None, "kind": "port",
                                    "sample": f"failed: {ex}"}
     eng.close()
+    if not a.quick:
+        # the other configurations, each in its own engine after the 8B one is released
+        for key, leg in (("llama_1b", lambda: llama_1b_leg(vsl, a.eager)),
+                         ("gemv_sweep", lambda: sweep_leg(vsl)),
+                         ("long_context", lambda: long_leg(vsl, 128, a.eager))):
+            try:
+                out[key] = leg()
+            except Exception as ex:  # reported, never fatal to the headline measurement
+                out[key] = {"failed": str(ex)}
     if a.copy_calibration_mb:
         import ctypes
         H = vsl.hip()

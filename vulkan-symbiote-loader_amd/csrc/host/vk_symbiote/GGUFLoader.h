@@ -126,6 +126,8 @@ class TensorLRUCache {
     explicit TensorLRUCache(const TensorCacheConfig& config = TensorCacheConfig{});
     bool get(const std::string& name, std::vector<float>& out);
     void put(const std::string& name, const std::vector<float>& data);
+    // the reference's signature (the tensor info is not needed to cache the values)
+    void put(const std::string& name, const std::vector<float>& data, const GGUFTensorInfo&) { put(name, data); }
     bool contains(const std::string& name) const;
     void clear();
     Stats get_stats() const;
