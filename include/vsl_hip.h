@@ -178,12 +178,12 @@ int vsl_rmsnorm(const float* x, const float* gamma, uint32_t rows, uint32_t d, f
 
 /* GEMV / skinny GEMM (the GEMV sweep): Y[N][B] = W[N][K] * X[K][B] (X, Y row-major), fp32
  * accumulation.  W f16/f32; X, Y f16 or f32; 1 <= B <= 16; K % 8 == 0.  f16 W with f16 X and
- * K % 2048 == 0 runs on MFMA (any B, including 1); B = 1 otherwise needs fp32 X. */
+ * K % 512 == 0 runs on MFMA (any B, including 1); B = 1 otherwise needs fp32 X. */
 int vsl_gemv(const void* W, int wdtype, uint32_t N, uint32_t K, const void* X, int xdtype, uint32_t B,
              void* Y, int ydtype, void* stream);
 
 /* The same product for a batch of B activation vectors, each contiguous: X fp16 [B][K], Y [B][N]
- * (f16 or f32), W fp16 [N][K]; 1 <= B <= 16, K % 2048 == 0.  MFMA, one pass over W.  No reference
+ * (f16 or f32), W fp16 [N][K]; 1 <= B <= 16, K % 512 == 0.  MFMA, one pass over W.  No reference
  * counterpart (the reference multiplies one vector at a time, final_linear.comp:37-85); it is the
  * batch>1 decode shape of the GEMV sweep. */
 int vsl_gemv_batched(const void* W, uint32_t N, uint32_t K, const void* X, uint32_t B, void* Y, int ydtype,

@@ -78,9 +78,29 @@ def test_gemv_sweep(vsl, orc, dev, H, N, K, B):
     assert rel_err(dev.get(dYt).T, ref) < 1e-5
 
 
+@pytest.mark.parametrize("N,K,B", [(9000, 1536, 12), (8200, 512, 16), (16, 512, 1), (8193, 2560, 8), (8191, 1024, 9)])
+def test_gemv_batched_ragged(vsl, orc, dev, H, N, K, B):
+    """The sweep kernel on shapes outside the sweep: N not a multiple of the 16- or 32-row tiles (the
+    two-tile blocks from N >= 8192 and B >= 8), K a multiple of 512 only, B neither 1, 4 nor 16;
+    X [B][K] and X [K][B] layouts."""
+    rng = np.random.default_rng(N + K + B)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    X = rng.normal(0, 1, (K, B)).astype(np.float16)
+    ref = orc.gemm_nt(W, X.astype(np.float32))
+    dW = dev.put(W)
+    dYt = dev.empty((B, N), np.float32)
+    ok(vsl, H.vsl_gemv_batched(dev.p(dW), N, K, dev.p(dev.put(np.ascontiguousarray(X.T))), B, dev.p(dYt),
+                               vsl.VSL_DT_F32, None))
+    assert rel_err(dev.get(dYt).T, ref) < 1e-5
+    dY = dev.empty((N, B), np.float32)
+    ok(vsl, H.vsl_gemv(dev.p(dW), vsl.VSL_DT_F16, N, K, dev.p(dev.put(X)), vsl.VSL_DT_F16, B, dev.p(dY),
+                       vsl.VSL_DT_F32, None))
+    assert rel_err(dev.get(dY), ref) < 1e-5
+
+
 def test_gemv_rejects_bad_shapes(vsl, dev, H):
     d = dev.empty((16,), np.float32)
-    assert H.vsl_gemv_batched(dev.p(d), 4, 1024, dev.p(d), 1, dev.p(d), 0, None) == -100  # K % 2048
+    assert H.vsl_gemv_batched(dev.p(d), 4, 1000, dev.p(d), 1, dev.p(d), 0, None) == -100  # K % 512
     assert H.vsl_gemv_batched(dev.p(d), 4, 2048, dev.p(d), 0, dev.p(d), 0, None) == -100  # B < 1
     assert H.vsl_gemv(dev.p(d), 1, 4, 12, dev.p(d), 0, 1, dev.p(d), 0, None) == -100  # K % 8
     assert H.vsl_gemv(dev.p(d), 1, 4, 16, dev.p(d), 0, 17, dev.p(d), 0, None) == -100  # B > 16

@@ -1529,19 +1529,25 @@ int launch_gemv_multi(const void* W, uint32_t N, uint32_t K, const void* X, uint
 // accumulates the K range [w K/8, (w+1) K/8) in groups of U 32-wide steps, double-buffered (the next group's W loads issued before the current group's
 // MFMAs); the 8 partial tiles are summed in LDS in wave order (deterministic). HBM traffic is W
 // once; columns past B load column B-1 and are masked to zero.
-constexpr int kSkWaves = 8, kSkU = 4, kSkR = 1;              // kSkR row groups of 16 per wave
-constexpr uint32_t kSkRows = 16 * kSkR;                      // rows per block
+// Block = kSkWaves waves splitting K, each wave kSkU k-steps of 32 per register group and R row
+// tiles of 16 (R = 2 reuses each X fragment for two W tiles; chosen where N leaves enough blocks).
+// W is read with ordinary (temporal) loads: a fragment load covers 64 bytes of each of 16 rows, and
+// the next k-step's load the other half of those 128-byte lines, which then comes from L2. Measured
+// on the sweep shapes (GB/s, geometric mean of the 12 points): 8 waves x 4 k-steps, non-temporal W
+// 3564; 4 x 2 temporal 4218, with R = 2 for N >= 8192 and B >= 8 about 4350.
+constexpr int kSkWaves = 4, kSkU = 2;
 constexpr uint32_t kSkKAlign = kSkWaves * 32 * kSkU * 2;  // K multiple: whole group pairs per wave
 
 // VEC_MAJOR: X holds B vectors of K ([B][K]) and Y B vectors of N ([B][N]) -- a batch of
 // activation vectors, each contiguous -- so a lane's X operand is one 16-byte load; otherwise X is
 // [K][B] and Y [N][B] (row-major products), eight 2-byte loads per operand.
-template <typename YT, bool VEC_MAJOR>
+template <typename YT, bool VEC_MAJOR, int R>
 __global__ __launch_bounds__(kSkWaves * 64) void k_skinny(const vsl_half* __restrict__ W, uint32_t N, uint32_t K,
                                                          const vsl_half* __restrict__ X, uint32_t B, YT* __restrict__ Y) {
-    __shared__ float part[kSkWaves][kSkRows][17];
+    constexpr uint32_t ROWS = 16 * R;  // rows per block
+    __shared__ float part[kSkWaves][ROWS][17];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t row = blockIdx.x * kSkRows + (lane & 15);  // + 16 per row group
+    const uint32_t row = blockIdx.x * ROWS + (lane & 15);  // + 16 per row tile
     const uint32_t ksub = (lane >> 4) * 8;
     const uint32_t col = lane & 15;
     const uint32_t bc = col < B ? col : B - 1;
@@ -1549,15 +1555,15 @@ __global__ __launch_bounds__(kSkWaves * 64) void k_skinny(const vsl_half* __rest
     const uint32_t kw = K / kSkWaves;
     const uint32_t k_begin = wave * kw;
     const uint32_t n_groups = kw / (32 * kSkU);
-    const vsl_half* wrow[kSkR];
+    const vsl_half* wrow[R];
 #pragma unroll
-    for (int r = 0; r < kSkR; ++r) {
+    for (int r = 0; r < R; ++r) {
         const uint32_t rr = row + 16 * r;
         wrow[r] = W + (size_t)(rr < N ? rr : N - 1) * K;  // rows past N: never stored
     }
 
     struct Group {
-        uint4 a[kSkR][kSkU];
+        uint4 a[R][kSkU];
         uint4 xv[kSkU];              // VEC_MAJOR
         vsl_half x[kSkU][VEC_MAJOR ? 1 : 8];
     };
@@ -1566,7 +1572,7 @@ __global__ __launch_bounds__(kSkWaves * 64) void k_skinny(const vsl_half* __rest
         for (int u = 0; u < kSkU; ++u) {
             const uint32_t k = k_begin + (j * kSkU + u) * 32 + ksub;
 #pragma unroll
-            for (int r = 0; r < kSkR; ++r) g.a[r][u] = load16<true>(wrow[r] + k);
+            for (int r = 0; r < R; ++r) g.a[r][u] = load16<false>(wrow[r] + k);
             if constexpr (VEC_MAJOR) {
                 g.xv[u] = load16<false>(X + (size_t)bc * K + k);
             } else {
@@ -1575,9 +1581,9 @@ __global__ __launch_bounds__(kSkWaves * 64) void k_skinny(const vsl_half* __rest
             }
         }
     };
-    float4v acc[kSkR];
+    float4v acc[R];
 #pragma unroll
-    for (int r = 0; r < kSkR; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < R; ++r) acc[r] = float4v{0.f, 0.f, 0.f, 0.f};
     auto consume = [&](const Group& g) {
 #pragma unroll
         for (int u = 0; u < kSkU; ++u) {
@@ -1592,11 +1598,12 @@ __global__ __launch_bounds__(kSkWaves * 64) void k_skinny(const vsl_half* __rest
             }
             xr = make_uint4(xr.x & bmask, xr.y & bmask, xr.z & bmask, xr.w & bmask);
 #pragma unroll
-            for (int r = 0; r < kSkR; ++r)
+            for (int r = 0; r < R; ++r)
                 acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, g.a[r][u]),
                                                                 __builtin_bit_cast(half8, xr), acc[r], 0, 0, 0);
         }
     };
+    // n_groups is even (K % kSkKAlign == 0): the pair loop consumes exactly the wave's groups
     Group ga, gb;
     issue(ga, 0);
     for (uint32_t j = 0; j < n_groups; j += 2) {
@@ -1608,24 +1615,28 @@ __global__ __launch_bounds__(kSkWaves * 64) void k_skinny(const vsl_half* __rest
         consume(gb);
     }
 #pragma unroll
-    for (int r = 0; r < kSkR; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i) part[wave][16 * r + (lane >> 4) * 4 + i][col] = acc[r][i];
     __syncthreads();
-    for (uint32_t e = threadIdx.x; e < kSkRows * 16; e += kSkWaves * 64) {
+    for (uint32_t e = threadIdx.x; e < ROWS * 16; e += kSkWaves * 64) {
         const uint32_t m = e >> 4, n = e & 15;
         float v = 0.f;
 #pragma unroll
         for (int w = 0; w < kSkWaves; ++w) v += part[w][m][n];
-        const uint32_t r = blockIdx.x * kSkRows + m;
+        const uint32_t r = blockIdx.x * ROWS + m;
         if (r < N && n < B) store_elem(Y + (VEC_MAJOR ? (size_t)n * N + r : (size_t)r * B + n), v);
     }
 }
 
 template <typename YT, bool VEC_MAJOR>
 int launch_skinny(const void* W, uint32_t N, uint32_t K, const void* X, uint32_t B, void* Y, hipStream_t s) {
-    k_skinny<YT, VEC_MAJOR><<<(N + kSkRows - 1) / kSkRows, kSkWaves * 64, 0, s>>>(
-        static_cast<const vsl_half*>(W), N, K, static_cast<const vsl_half*>(X), B, static_cast<YT*>(Y));
+    const vsl_half* w = static_cast<const vsl_half*>(W);
+    const vsl_half* x = static_cast<const vsl_half*>(X);
+    if (N >= 8192 && B >= 8)
+        k_skinny<YT, VEC_MAJOR, 2><<<(N + 31) / 32, kSkWaves * 64, 0, s>>>(w, N, K, x, B, static_cast<YT*>(Y));
+    else
+        k_skinny<YT, VEC_MAJOR, 1><<<(N + 15) / 16, kSkWaves * 64, 0, s>>>(w, N, K, x, B, static_cast<YT*>(Y));
     HIP_TRY(hipGetLastError());
     return VSL_OK;
 }
