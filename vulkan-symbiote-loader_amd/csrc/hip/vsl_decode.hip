@@ -33,6 +33,7 @@ struct GemvArgs {
     uint32_t N;  // output rows (EPI_SWIGLU: F, the weight holds 2F rows)
     uint32_t K;
     const float* x;
+    const vsl_half* xh;  // when set, the activation vector is fp16 (8-byte aligned) and x is unused
     const float* gamma;  // RMSNorm gains; nullptr = no norm prologue
     float eps;
     float* y;
@@ -76,13 +77,25 @@ struct XStage {
     // then count exactly the loads issued after them.
     // (the gains only when there is a norm; these loads all precede the first weight tile, so a
     // uniform branch here changes no wait of the weight pipeline)
-    __device__ __forceinline__ void load(const float* __restrict__ x, const float* __restrict__ gamma, uint32_t K) {
+    __device__ __forceinline__ void load(const float* __restrict__ x, const vsl_half* __restrict__ xh,
+                                         const float* __restrict__ gamma, uint32_t K) {
         const uint32_t tid = threadIdx.x;
+        if (xh) {  // fp16 activations (a uniform branch ahead of every weight load)
 #pragma unroll
-        for (int j = 0; j < XPT; ++j) {
-            const uint32_t i = (j * NT + tid) * 4;
-            const uint32_t ic = i < K ? i : 0;
-            xr[j] = *reinterpret_cast<const float4*>(x + ic);
+            for (int j = 0; j < XPT; ++j) {
+                const uint32_t i = (j * NT + tid) * 4;
+                const uint32_t ic = i < K ? i : 0;
+                const uint2 hv = *reinterpret_cast<const uint2*>(xh + ic);
+                const half2v a = __builtin_bit_cast(half2v, hv.x), b = __builtin_bit_cast(half2v, hv.y);
+                xr[j] = make_float4((float)a[0], (float)a[1], (float)b[0], (float)b[1]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < XPT; ++j) {
+                const uint32_t i = (j * NT + tid) * 4;
+                const uint32_t ic = i < K ? i : 0;
+                xr[j] = *reinterpret_cast<const float4*>(x + ic);
+            }
         }
         if (gamma) {
 #pragma unroll
@@ -381,7 +394,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
     // Prologue: activation and gain loads, then the first weight tile, then the control block; the
     // staging, the norm and the control-block latency all complete under the weight fetch.
     XStage<WAVES, XPT> st;
-    st.load(a.x, a.gamma, a.K);
+    st.load(a.x, a.xh, a.gamma, a.K);
     uint4 wa[R][U], wb[R][U];
     float pa[R], pb[R];
     issue_w(wa, 0);
@@ -1643,6 +1656,20 @@ int launch_skinny(const void* W, uint32_t N, uint32_t K, const void* X, uint32_t
 
 }  // namespace
 
+// One fp16 activation vector against fp16 W: the decode GEMV (whole rows per wave, two rows per tile,
+// the vector staged in LDS as fp32), which streams W faster than the MFMA sweep kernel at B = 1.
+static int gemv_one_f16x(const void* W, uint32_t N, uint32_t K, const void* X, void* Y, int ydtype, hipStream_t s) {
+    if (int rc = check_gemv_shape(N, K, "vsl_gemv (B = 1)")) return rc;
+    GemvArgs a{};
+    a.W = W;
+    a.N = N;
+    a.K = K;
+    a.xh = static_cast<const vsl_half*>(X);
+    a.y = static_cast<float*>(Y);
+    return ydtype == VSL_DT_F16 ? launch_gemv_k<WF16, 2, 4, EPI_STORE_F16>(a, 1u << 20, s)
+                                : launch_gemv_k<WF16, 2, 4, EPI_STORE>(a, 1u << 20, s);
+}
+
 // =============================================================================================
 // C ABI
 // =============================================================================================
@@ -1687,6 +1714,9 @@ extern "C" int vsl_gemv(const void* W, int wdtype, uint32_t N, uint32_t K, const
         (ydtype != VSL_DT_F16 && ydtype != VSL_DT_F32))
         return vsl_unsupported("vsl_gemv: dtype combination %d/%d/%d", wdtype, xdtype, ydtype);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (wdtype == VSL_DT_F16 && xdtype == VSL_DT_F16 && B == 1 && K % 8 == 0 && K <= kMaxK &&
+        (reinterpret_cast<uintptr_t>(X) & 7) == 0)
+        return gemv_one_f16x(W, N, K, X, Y, ydtype, s);
     if (wdtype == VSL_DT_F16 && xdtype == VSL_DT_F16 && K % kSkKAlign == 0)
         return ydtype == VSL_DT_F16 ? launch_skinny<vsl_half, false>(W, N, K, X, B, Y, s)
                                     : launch_skinny<float, false>(W, N, K, X, B, Y, s);
@@ -1725,6 +1755,7 @@ extern "C" int vsl_gemv_batched(const void* W, uint32_t N, uint32_t K, const voi
     if (K % kSkKAlign) return vsl_invalid("vsl_gemv_batched: K=%u must be a multiple of %u", K, kSkKAlign);
     if (ydtype != VSL_DT_F16 && ydtype != VSL_DT_F32) return vsl_unsupported("vsl_gemv_batched: Y dtype %d", ydtype);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (B == 1 && K <= kMaxK) return gemv_one_f16x(W, N, K, X, Y, ydtype, s);
     return ydtype == VSL_DT_F16 ? launch_skinny<vsl_half, true>(W, N, K, X, B, Y, s)
                                 : launch_skinny<float, true>(W, N, K, X, B, Y, s);
 }
