@@ -341,6 +341,8 @@ def main():
     ap.add_argument("--prefill-runs", type=int, default=5, help="prompt passes timed; the median is reported")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--llama-1b", action="store_true",
+                    help="the 1B-class workload alone (prompt 128, greedy decode 256): one JSON line")
     ap.add_argument("--attn-splits", type=int, default=0,
                     help="decode attention split count of the 8B engine (0: the engine's choice)")
     ap.add_argument("--quick", action="store_true",
@@ -366,6 +368,16 @@ def main():
         return
     if a.sweep:
         run_sweep(a)
+        return
+    if a.llama_1b:
+        gpus_or_exit(a)
+        lg = llama_1b_leg(load_package(), a.eager)
+        out = {"metric": "decode tok/s + HBM GB/s (% peak), 1B fp16 bs=1; prefill tok/s",
+               "value": lg["decode"]["tok_s"], "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+               "dtype": "f16", "data": "synthetic: random-init N(0,0.02) fp16 weights, uniform-random prompt ids",
+               "config": {"workload": lg["workload"]}}
+        out.update(lg)
+        print(json.dumps(out), flush=True)
         return
     gpus_or_exit(a)
     if a.prompt + a.steps > KV_CAPACITY:

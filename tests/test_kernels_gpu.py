@@ -530,6 +530,9 @@ def test_gemm_dma(vsl, orc, dev, H, M, N, K, epi, ax2, cx2):
     (512, 6144, 4096, 0, True),    # QKV: fp32 store
     (512, 4096, 4096, 1, False),   # fp16 store
     (300, 4096, 2048, 2, False),   # ragged M
+    (128, 2048, 8192, 2, True),    # 1B down projection of a 128-row prompt: 32 chunks of 256
+    (128, 3072, 2048, 0, True),    # 1B QKV: 16 chunks of 128 reach 192 items
+    (128, 2048, 2048, 2, False),   # 1B O projection: the widest split (16) short of 192 items
 ])
 def test_gemm_splitk(vsl, dev, H, M, N, K, epi, ax2):
     """Narrow shapes through vsl_gemm_f16_ws: split over K into a workspace, reduced in order with the
@@ -816,6 +819,7 @@ def _act(rng, M, K, ax2):
     (512, 4096, 32, 8, 128, 100, False, False, 1),  # later chunk, fp16 q
     (300, 4096, 32, 8, 128, 7, True, True, 0),     # ragged rows (K split 4), fp32 cache
     (256, 4096, 32, 8, 64, 0, False, True, 1),     # head_dim 64 (K split 8)
+    (128, 2048, 32, 8, 64, 0, True, True, 1),      # 1B 128-row prompt: K split 16 (runtime-count sum)
 ])
 def test_gemm_qkv_rope_append(vsl, orc, dev, H, S, K, nq, nkv, hd, pos0, ax2, qx2, kvdt):
     """QKV projection + RoPE + Q/K/V split through one entry point. With the workspace the split-K
@@ -895,6 +899,8 @@ def test_gemm_qkv_rope_append_refuses_before_launch(vsl, dev, H):
     (300, 4096, 4096, False, 1, True),   # ragged rows, fp16 out
     (512, 2048, 8192, False, 0, False),  # d = 2048, K split 8, fp32 out, no gains
     (256, 8192, 4096, False, 2, True),   # d = 8192 (eight float4 per thread)
+    (128, 2048, 8192, True, 2, True),    # 1B down projection of a 128-row prompt: K split 32
+    (128, 2048, 2048, False, 1, True),   # 1B O projection: K split 16
 ])
 def test_gemm_resid_rmsnorm(vsl, orc, dev, H, M, N, K, ax2, odt, gam):
     """Residual projection + the next RMSNorm through one entry point. With the workspace the split-K

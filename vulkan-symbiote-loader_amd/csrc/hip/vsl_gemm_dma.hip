@@ -376,21 +376,28 @@ uint32_t vsl_gemm_dma_tiles(int cfg, uint32_t M, uint32_t N, uint32_t K, int epi
 }
 
 // Split-K plan for shapes whose tiles leave CUs idle: the 128 x 256 tiling with the smallest split
-// in {2, 4, 8} that gives >= min_items work items and >= 512 of K (whole 128-wide stage groups) per
-// chunk. Returns the split (0: none) and the fp32 workspace bytes it needs.
+// in {2, 4, 8} that gives >= min_items work items and >= 512 of K per chunk; else (few rows, e.g. a
+// 128-token prompt) the smallest split up to 32 with >= 128 of K per chunk that reaches min_items, or
+// failing that the largest such split when it gives at least 64 items. Chunks are whole 128-wide
+// stage groups. Returns the split (0: none) and the fp32 workspace bytes it needs.
 uint32_t vsl_gemm_splitk_plan(uint32_t M, uint32_t N, uint32_t K, int epi, uint32_t min_items, uint64_t* ws_bytes) {
     if (ws_bytes) *ws_bytes = 0;
     if (epi == VSL_EPI_SWIGLU || N % 4) return 0;
     const uint32_t tiles = dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
     if (!tiles || ((uint64_t)M * K * 2) >> 32 || ((uint64_t)N * K * 2) >> 32) return 0;
-    for (uint32_t ks : {2u, 4u, 8u}) {
-        if (K % (ks * kKAlign) || K / ks < 512) continue;
-        if (tiles * ks >= min_items) {
-            if (ws_bytes) *ws_bytes = (uint64_t)ks * M * N * 4;
-            return ks;
-        }
+    auto take = [&](uint32_t ks) {
+        if (ws_bytes) *ws_bytes = (uint64_t)ks * M * N * 4;
+        return ks;
+    };
+    for (uint32_t ks : {2u, 4u, 8u})
+        if (K % (ks * kKAlign) == 0 && K / ks >= 512 && tiles * ks >= min_items) return take(ks);
+    uint32_t widest = 0;
+    for (uint32_t ks : {2u, 4u, 8u, 16u, 32u}) {
+        if (K % (ks * kKAlign) || K / ks < 128) continue;
+        if (tiles * ks >= min_items) return take(ks);
+        widest = ks;
     }
-    return 0;
+    return widest && tiles * widest >= 64 ? take(widest) : 0;
 }
 
 void vsl_gemm_splitk_partials(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,

@@ -304,13 +304,13 @@ __global__ void k_rope_split(const float* __restrict__ qkv, uint32_t S, uint32_t
 // as KS fp32 k-chunk partials ws[KS][S][W] summed in chunk order (KS = 1: the finished projection):
 // 16-byte loads of each partial, 8-byte loads of the rotation tables, 8-byte q and fp16 cache stores
 // (16-byte fp32 cache stores). Needs hd % 4 == 0; a quad then never straddles a head or the q/k/v
-// boundaries.
+// boundaries. KS = 0: the partial count is ks_rt, summed in the same order by a loop.
 template <class KT, bool QX2, int KS>
 __global__ __launch_bounds__(256) void k_rope_split4(const float* __restrict__ ws, uint32_t S, uint32_t n_q,
                                                      uint32_t n_kv, uint32_t hd, uint32_t pos0,
                                                      const float* __restrict__ rc, const float* __restrict__ rs,
                                                      vsl_half* __restrict__ q_out, void* __restrict__ kc,
-                                                     void* __restrict__ vc, uint32_t cap) {
+                                                     void* __restrict__ vc, uint32_t cap, uint32_t ks_rt) {
     const uint32_t width = (n_q + 2 * n_kv) * hd, quads = width / 4;
     const uint64_t e = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= (uint64_t)S * quads) return;
@@ -318,8 +318,12 @@ __global__ __launch_bounds__(256) void k_rope_split4(const float* __restrict__ w
     const uint64_t MN = (uint64_t)S * width;
     const size_t off = (size_t)s * width + col;
     float4v v = *reinterpret_cast<const float4v*>(ws + off);
+    if constexpr (KS > 0) {
 #pragma unroll
-    for (int k = 1; k < KS; ++k) v += *reinterpret_cast<const float4v*>(ws + k * MN + off);
+        for (int k = 1; k < KS; ++k) v += *reinterpret_cast<const float4v*>(ws + k * MN + off);
+    } else {
+        for (uint32_t k = 1; k < ks_rt; ++k) v += *reinterpret_cast<const float4v*>(ws + k * MN + off);
+    }
     const uint32_t pos = pos0 + s, qw = n_q * hd, kw = n_kv * hd;
     if (col < qw + kw) {
         const size_t j = (size_t)pos * (hd >> 1) + ((col % hd) >> 1);
@@ -357,11 +361,12 @@ __global__ __launch_bounds__(256) void k_rope_split4(const float* __restrict__ w
 // order, then added to x), followed by the next RMSNorm of the updated rows, out = x / sqrt(mean(x^2)
 // + eps) * gamma (fp16, split or fp32). One 256-thread block per row, NV float4 per thread
 // (d = 1024 NV): every partial, x and gamma requested before the first is used, x written once, the
-// row's sum of squares by DPP within each wave and four floats of LDS across the waves.
+// row's sum of squares by DPP within each wave and four floats of LDS across the waves. KS = 0: the
+// partial count is ks_rt, summed in the same order by a loop (many partials: no register copy of each).
 template <typename OT, bool X2, int NV, int KS>
 __global__ __launch_bounds__(256) void k_splitk_resid_rmsnorm(const float* __restrict__ ws, uint32_t rows,
                                                               float* __restrict__ x, const float* __restrict__ gamma,
-                                                              float eps, OT* __restrict__ out) {
+                                                              float eps, OT* __restrict__ out, uint32_t ks_rt) {
     constexpr uint32_t d = 1024 * NV;
     __shared__ float red[4];
     const uint32_t t = threadIdx.x;
@@ -370,10 +375,16 @@ __global__ __launch_bounds__(256) void k_splitk_resid_rmsnorm(const float* __res
     float4v v[NV], g[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) v[j] = *reinterpret_cast<const float4v*>(ws + base + (j * 256 + t) * 4);
+    if constexpr (KS > 0) {
 #pragma unroll
-    for (int k = 1; k < KS; ++k)
+        for (int k = 1; k < KS; ++k)
 #pragma unroll
-        for (int j = 0; j < NV; ++j) v[j] += *reinterpret_cast<const float4v*>(ws + k * MN + base + (j * 256 + t) * 4);
+            for (int j = 0; j < NV; ++j) v[j] += *reinterpret_cast<const float4v*>(ws + k * MN + base + (j * 256 + t) * 4);
+    } else {
+        for (uint32_t k = 1; k < ks_rt; ++k)
+#pragma unroll
+            for (int j = 0; j < NV; ++j) v[j] += *reinterpret_cast<const float4v*>(ws + k * MN + base + (j * 256 + t) * 4);
+    }
 #pragma unroll
     for (int j = 0; j < NV; ++j)
         g[j] = gamma ? *reinterpret_cast<const float4v*>(gamma + (j * 256 + t) * 4) : float4v{1.f, 1.f, 1.f, 1.f};
@@ -791,15 +802,15 @@ extern "C" uint64_t vsl_gemm_f16_ws_bytes(uint32_t M, uint32_t N, uint32_t K, in
 template <int KS>
 static void launch_rope_split4(hipStream_t s, const float* ws, uint32_t S, uint32_t n_q, uint32_t n_kv, uint32_t hd,
                                uint32_t pos0, const float* rc, const float* rsn, vsl_half* qo, bool qx2, void* kc,
-                               void* vc, bool kv32, uint32_t cap) {
+                               void* vc, bool kv32, uint32_t cap, uint32_t ks_rt = KS) {
     const uint64_t quads = (uint64_t)S * (n_q + 2 * n_kv) * hd / 4;
     const uint32_t grid = (uint32_t)((quads + 255) / 256);
     if (!kv32) {
-        if (qx2) k_rope_split4<WF16, true, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap);
-        else k_rope_split4<WF16, false, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap);
+        if (qx2) k_rope_split4<WF16, true, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap, ks_rt);
+        else k_rope_split4<WF16, false, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap, ks_rt);
     } else {
-        if (qx2) k_rope_split4<WF32, true, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap);
-        else k_rope_split4<WF32, false, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap);
+        if (qx2) k_rope_split4<WF32, true, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap, ks_rt);
+        else k_rope_split4<WF32, false, KS><<<grid, 256, 0, s>>>(ws, S, n_q, n_kv, hd, pos0, rc, rsn, qo, kc, vc, cap, ks_rt);
     }
 }
 
@@ -879,7 +890,8 @@ extern "C" int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uin
         switch (ks) {
             case 2: launch_rope_split4<2>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
             case 4: launch_rope_split4<4>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
-            default: launch_rope_split4<8>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
+            case 8: launch_rope_split4<8>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
+            default: launch_rope_split4<0>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap, ks); break;
         }
         HIP_TRY(hipGetLastError());
         return VSL_OK;
@@ -894,9 +906,10 @@ template <typename OT, bool X2, int NV>
 static void launch_resid_rmsnorm_nv(hipStream_t s, uint32_t ks, const float* ws, uint32_t rows, float* x,
                                     const float* gamma, float eps, OT* out) {
     switch (ks) {
-        case 2: k_splitk_resid_rmsnorm<OT, X2, NV, 2><<<rows, 256, 0, s>>>(ws, rows, x, gamma, eps, out); break;
-        case 4: k_splitk_resid_rmsnorm<OT, X2, NV, 4><<<rows, 256, 0, s>>>(ws, rows, x, gamma, eps, out); break;
-        default: k_splitk_resid_rmsnorm<OT, X2, NV, 8><<<rows, 256, 0, s>>>(ws, rows, x, gamma, eps, out); break;
+        case 2: k_splitk_resid_rmsnorm<OT, X2, NV, 2><<<rows, 256, 0, s>>>(ws, rows, x, gamma, eps, out, ks); break;
+        case 4: k_splitk_resid_rmsnorm<OT, X2, NV, 4><<<rows, 256, 0, s>>>(ws, rows, x, gamma, eps, out, ks); break;
+        case 8: k_splitk_resid_rmsnorm<OT, X2, NV, 8><<<rows, 256, 0, s>>>(ws, rows, x, gamma, eps, out, ks); break;
+        default: k_splitk_resid_rmsnorm<OT, X2, NV, 0><<<rows, 256, 0, s>>>(ws, rows, x, gamma, eps, out, ks); break;
     }
 }
 
