@@ -937,7 +937,9 @@ extern "C" int vsl_gemm_f16_resid_rmsnorm(const void* A, const void* B, uint32_t
     float* ws = static_cast<float*>(workspace);
     const uint32_t ks = splitk_choice(M, N, K, VSL_EPI_RESID, ws, ws ? ws_bytes : 0);
     const uint32_t nv = N / 1024;
-    const bool fused = ks && N % 1024 == 0 && (nv == 1 || nv == 2 || nv == 4 || nv == 8) && ks * nv <= 32 &&
+    // (the unrolled sums hold up to 32 float4 of partials per thread; more than 8 partials take the
+    // loop of the runtime-count variant)
+    const bool fused = ks && N % 1024 == 0 && (nv == 1 || nv == 2 || nv == 4 || nv == 8) && (ks > 8 || ks * nv <= 32) &&
                        aligned_to(x, 16) && aligned_to(gamma, 16) && aligned_to(xn, xn_dtype == VSL_DT_F32 ? 16 : 8);
     if (!fused) {
         if (const int rc = gemm_f16(A, B, M, N, K, x, VSL_EPI_RESID | a_flags, ws, ws ? ws_bytes : 0, stream)) return rc;
