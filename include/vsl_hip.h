@@ -53,10 +53,9 @@ enum {
                                   probabilities next to the maximum)                              */
     VSL_SAMPLE_TOPK_SEEDED = 2 /* Utils.cpp:140-172 top-k with a Philox4x32-10 uniform             */
 };
-/* Limits of the samplers that scan the logits in one block (modes REFERENCE and TOPK_SEEDED with
- * T > 0): V <= VSL_MAX_SAMPLE_VOCAB, and for TOPK_SEEDED 1 <= top_k <= VSL_MAX_TOP_K (top_k > V means
- * all of V).  Other requests return VSL_E_UNSUPPORTED; greedy has no limit. */
-enum { VSL_MAX_TOP_K = 64, VSL_MAX_SAMPLE_VOCAB = 65536 };
+/* Limit of the seeded top-k sampler (TOPK_SEEDED with T > 0): 1 <= top_k <= VSL_MAX_TOP_K (top_k > V
+ * means all of V); other k return VSL_E_UNSUPPORTED.  No sampler limits V. */
+enum { VSL_MAX_TOP_K = 64 };
 
 const char* vsl_last_error(void);
 int vsl_device_count(int* n);
@@ -245,7 +244,7 @@ int vsl_norm_swiglu(const float* x, const float* gamma, float eps, const void* W
  *   f = RMSNorm(x, gamma) (gamma may be NULL: no final norm); logits = W f (fp32 [V]);
  *   greedy: per-block argmax fused into the GEMV, reduced by a second launch;
  *   reference and top-k modes (T > 0): the GEMV writes logits and a sampling launch follows
- *   (limits: VSL_MAX_SAMPLE_VOCAB, VSL_MAX_TOP_K; otherwise VSL_E_UNSUPPORTED before any launch).
+ *   (top-k limit VSL_MAX_TOP_K; otherwise VSL_E_UNSUPPORTED before any launch).
  *   The sampled token is written to tokens[ctrl->step]; then x <- embed[token] (the next step's
  *   embedding_lookup), ctrl->pos += 1, ctrl->step += 1, and done is set on max_steps / EOS.
  *   Workspace: ws_val/ws_idx >= vsl_lm_head_ws_blocks() entries. */

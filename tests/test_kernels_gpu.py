@@ -380,9 +380,9 @@ def test_sample_logits_greedy_ties_and_topk(vsl, orc, dev, H):
 
 def test_sample_logits_topk_limits(vsl, orc, dev, H):
     """Seeded top-k at the largest supported k (64) against the oracle; k = 65 and k = 0 (which the
-    oracle would read as all of V) are refused with VSL_E_UNSUPPORTED, and so is a vocabulary above
-    65536, by vsl_sample_logits and by vsl_lm_head_sample before anything is launched; top_k above a
-    small V means all of V."""
+    oracle would read as all of V) are refused with VSL_E_UNSUPPORTED by vsl_sample_logits and by
+    vsl_lm_head_sample before anything is launched; top_k above a small V means all of V; every mode
+    serves a 128256-entry vocabulary."""
     out = dev.empty((1,), np.int32)
     l = np.random.default_rng(21).normal(0, 1.0, 32000).astype(np.float32)
     dl = dev.put(l)
@@ -391,9 +391,12 @@ def test_sample_logits_topk_limits(vsl, orc, dev, H):
         assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_TOPK_SEEDED, 1.5, 64, 5, step)
     for k in (65, 0):
         assert H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 0.7, k, 0, 5), 0, dev.p(out), None) == -103
-    big = dev.empty((70000,), np.float32)
-    assert H.vsl_sample_logits(dev.p(big), 70000, vsl.Sampler(1, 0.7, 40, 0, 5), 0, dev.p(out), None) == -103
-    ok(vsl, H.vsl_sample_logits(dev.p(big), 70000, vsl.Sampler(0, 0.0, 40, 0, 5), 0, dev.p(out), None))
+    big = np.random.default_rng(23).normal(0, 2.0, 128256).astype(np.float32)
+    dbig = dev.put(big)
+    for mode, T in ((0, 0.0), (1, 0.7), (2, 0.7)):
+        for step in range(4):
+            ok(vsl, H.vsl_sample_logits(dev.p(dbig), big.size, vsl.Sampler(mode, T, 40, 0, 5), step, dev.p(out), None))
+            assert dev.get(out)[0] == orc.sample(big, mode, T, 40, 5, step), (mode, step)
     small = np.random.default_rng(22).normal(0, 1.0, 40).astype(np.float32)
     for step in range(8):
         ok(vsl, H.vsl_sample_logits(dev.p(dev.put(small)), 40, vsl.Sampler(2, 0.9, 50, 0, 6), step, dev.p(out), None))
@@ -411,6 +414,74 @@ def test_sample_logits_topk_limits(vsl, orc, dev, H):
                                   vsl.Sampler(2, 0.7, k, 0, 1), dev.p(ws_v), dev.p(ws_i), dev.p(toks), dev.p(c), None)
         assert rc == -103
     assert np.array_equal(dev.get(c), before)  # nothing ran
+
+
+def _topk_cases():
+    """Logit vectors that take each selection route of the seeded top-k kernel: few elements above
+    the threshold (normal logits), ties everywhere (all equal, small integers, +0 and -0), mostly
+    -inf, a small V, and large values packed into 30 of the 1024 threads' index classes so that more
+    than 1024 elements pass the threshold."""
+    rng = np.random.default_rng(31)
+    cases = {"normal": rng.normal(0, 1.3, 32000), "equal": np.zeros(32000),
+             "integers": rng.integers(0, 3, 32000), "small": rng.normal(0, 1.0, 37)}
+    z = rng.normal(0, 1.0, 5000)
+    z[::3] = -0.0
+    z[1::3] = 0.0
+    cases["signed_zero"] = z
+    inf = np.full(32000, -np.inf)
+    inf[[5, 700, 20000, 31999]] = [1.0, 2.0, 2.0, 0.5]
+    cases["mostly_neg_inf"] = inf
+    packed = rng.normal(0, 1.0, 65536)
+    packed[np.arange(65536) % 1024 < 30] += 50.0
+    cases["packed_classes"] = packed
+    return {n: v.astype(np.float32) for n, v in cases.items()}
+
+
+@pytest.mark.parametrize("name", list(_topk_cases()))
+def test_sample_topk_selection_routes(vsl, orc, dev, H, name):
+    """Seeded top-k against the oracle on every selection route, k in {1, 40, 64}."""
+    l = _topk_cases()[name]
+    out = dev.empty((1,), np.int32)
+    dl = dev.put(l)
+    for k in (1, 40, 64):
+        for step in range(6):
+            ok(vsl, H.vsl_sample_logits(dev.p(dl), l.size, vsl.Sampler(2, 0.8, k, 0, 3), step, dev.p(out), None))
+            assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_TOPK_SEEDED, 0.8, k, 3, step), (name, k, step)
+
+
+def test_sample_topk_nan_logits(vsl, orc, dev, H):
+    """NaN logits (where the reference's comparator has no order) rank below every number, lower
+    index first.  With at least k numbers the draw equals the oracle's on the vector with the NaNs
+    replaced by -inf (same k candidates, same weights); with fewer, a NaN weight reaches the sum and
+    the walk returns the first candidate."""
+    out = dev.empty((1,), np.int32)
+    l = np.random.default_rng(51).normal(0, 1.0, 32000).astype(np.float32)
+    l[::2] = np.nan
+    masked = np.where(np.isnan(l), -np.inf, l).astype(np.float32)
+    for step in range(8):
+        ok(vsl, H.vsl_sample_logits(dev.p(dev.put(l)), l.size, vsl.Sampler(2, 0.7, 40, 0, 8), step, dev.p(out), None))
+        assert dev.get(out)[0] == orc.sample(masked, orc.SAMPLE_TOPK_SEEDED, 0.7, 40, 8, step)
+    few = np.full(5000, np.nan, np.float32)
+    few[[9, 3]] = [1.0, 1.0]
+    for step in range(4):
+        ok(vsl, H.vsl_sample_logits(dev.p(dev.put(few)), few.size, vsl.Sampler(2, 0.7, 40, 0, 8), step, dev.p(out), None))
+        assert dev.get(out)[0] == 3
+
+
+def test_sample_greedy_any_vocabulary(vsl, orc, dev, H):
+    """Greedy over V above 65536 scans every logit; a NaN first logit gives token 0 (greedy_sampling
+    starts from logits[0] and a NaN is never beaten), other NaNs never win."""
+    out = dev.empty((1,), np.int32)
+    l = np.random.default_rng(41).normal(0, 1.0, 70000).astype(np.float32)
+    l[69000] = 9.0
+    ok(vsl, H.vsl_sample_logits(dev.p(dev.put(l)), 70000, vsl.Sampler(0, 0.0, 40, 0, 0), 0, dev.p(out), None))
+    assert dev.get(out)[0] == 69000 == orc.sample(l, orc.SAMPLE_GREEDY)
+    l[123] = np.nan
+    ok(vsl, H.vsl_sample_logits(dev.p(dev.put(l)), 70000, vsl.Sampler(2, 0.0, 40, 0, 0), 0, dev.p(out), None))
+    assert dev.get(out)[0] == 69000 == orc.sample(l, orc.SAMPLE_GREEDY)
+    l[0] = np.nan
+    ok(vsl, H.vsl_sample_logits(dev.p(dev.put(l)), 70000, vsl.Sampler(0, 0.0, 40, 0, 0), 0, dev.p(out), None))
+    assert dev.get(out)[0] == 0 == orc.sample(l, orc.SAMPLE_GREEDY)
 
 
 def test_sample_reference_mode_is_softmax_argmax(vsl, orc, dev, H):

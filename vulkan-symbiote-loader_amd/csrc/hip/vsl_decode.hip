@@ -1223,9 +1223,9 @@ int launch_attn_g(uint32_t G, dim3 grid, hipStream_t s, const float* q, const vo
 // samplers on logits in memory (top-k seeded, greedy) -- one block
 // ---------------------------------------------------------------------------------------------
 constexpr int kSampBlock = 1024;
-constexpr int kSampPer = 64;  // values per thread: V <= 65536
 constexpr int kMaxTopK = VSL_MAX_TOP_K;
-static_assert(kSampBlock * kSampPer == VSL_MAX_SAMPLE_VOCAB, "one block scans every logit");
+constexpr int kTauPerWave = 8;  // per-wave maxima entering the threshold: 16 waves x 8 = 128 keys
+static_assert(kSampBlock / 64 * kTauPerWave == 2 * VSL_WAVE && kMaxTopK <= VSL_WAVE, "threshold sort holds two keys per lane");
 
 __device__ __forceinline__ float sample_uniform(uint32_t k0, uint32_t k1, uint64_t step) {
     uint32_t c[4] = {(uint32_t)step, (uint32_t)(step >> 32), 0u, 0u};
@@ -1233,65 +1233,130 @@ __device__ __forceinline__ float sample_uniform(uint32_t k0, uint32_t k1, uint64
     return (float)(c[0] >> 8) * (1.0f / 16777216.0f);
 }
 
-// Returns the sampled token in thread 0 (valid for all threads through LDS).
-__device__ uint32_t block_sample(const float* __restrict__ logits, uint32_t V, int mode, float temperature,
+// Top-k order as a single unsigned key, larger = earlier: the high word orders the floats by value
+// (-0 as +0, every NaN below -inf, where the reference's comparator has no order), the low word is
+// the inverted index so that equal values put the lower index first.  No two elements share a key.
+__device__ __forceinline__ uint32_t value_key(float v) {
+    if (v != v) return 0u;
+    uint32_t b = __float_as_uint(v);
+    if (b == 0x80000000u) b = 0u;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+    if (k == 0u) return __uint_as_float(0x7FC00000u);
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+__device__ __forceinline__ uint64_t rank_key(uint32_t vkey, uint32_t i) { return ((uint64_t)vkey << 32) | (uint32_t)~i; }
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, m, VSL_WAVE), hi = __shfl_xor((uint32_t)(v >> 32), m, VSL_WAVE);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Bitonic sort, descending, one key per thread of the first N threads: thread r ends holding the key
+// of rank r.  Partners closer than a wave exchange through shuffles; farther ones through buf (N
+// keys of LDS), so N > 64 needs every thread of the block, N = 64 one whole wave.
+template <int N>
+__device__ __forceinline__ uint64_t bitonic_desc(uint64_t x, uint32_t t, uint64_t* buf) {
+#pragma unroll
+    for (uint32_t size = 2; size <= (uint32_t)N; size <<= 1) {
+#pragma unroll
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            uint64_t y;
+            if (stride >= (uint32_t)VSL_WAVE) {
+                buf[t] = x;
+                __syncthreads();
+                y = buf[t ^ stride];
+                __syncthreads();
+            } else {
+                y = shfl_xor_u64(x, (int)stride);
+            }
+            const bool ascending_run = (t & size) != 0, lower = (t & stride) == 0;
+            const uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
+            x = lower != ascending_run ? hi : lo;
+        }
+    }
+    return x;
+}
+
+// Bitonic sort, descending, of 64 * M keys held by one wave, M per lane (key r of the sequence in
+// register r / 64 of lane r % 64): rank r ends in the same place.  No LDS, no barriers.
+template <int M>
+__device__ __forceinline__ void wave_bitonic_desc(uint64_t (&x)[M], uint32_t lane) {
+#pragma unroll
+    for (uint32_t size = 2; size <= (uint32_t)(VSL_WAVE * M); size <<= 1) {
+#pragma unroll
+        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride >= (uint32_t)VSL_WAVE) {
+                const int rs = (int)(stride / VSL_WAVE);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    if (m & rs) continue;
+                    const bool ascending_run = (((uint32_t)m * VSL_WAVE + lane) & size) != 0;
+                    const uint64_t a = x[m], b = x[m | rs];
+                    const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+                    x[m] = ascending_run ? lo : hi;
+                    x[m | rs] = ascending_run ? hi : lo;
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const uint64_t y = shfl_xor_u64(x[m], (int)stride);
+                    const bool ascending_run = (((uint32_t)m * VSL_WAVE + lane) & size) != 0;
+                    const bool lower = (lane & stride) == 0;
+                    const uint64_t hi = x[m] > y ? x[m] : y, lo = x[m] > y ? y : x[m];
+                    x[m] = lower != ascending_run ? hi : lo;
+                }
+            }
+        }
+    }
+}
+
+// Calls f(v, base) for every batch of this thread's logits: v[j] is logit base + tid + j * kSampBlock
+// (0 past V); the batch's loads are all issued before f runs.  One block streams at about 0.2
+// cycles per logit whether or not the next batch is prefetched (the CU's outstanding misses bound
+// it), so there is no prefetch.
+constexpr int kSampBatch = 16;
+template <class F>
+__device__ __forceinline__ void for_each_logit_batch(const float* __restrict__ logits, uint32_t V, uint32_t tid, F&& f) {
+    for (uint32_t base = 0; base < V; base += kSampBlock * kSampBatch) {
+        float v[kSampBatch];
+#pragma unroll
+        for (int j = 0; j < kSampBatch; ++j) {
+            const uint32_t i = base + tid + (uint32_t)j * kSampBlock;
+            v[j] = i < V ? logits[i] : 0.f;
+        }
+        f(v, base);
+    }
+}
+
+// Calls f(value, index) for every logit of this thread, in increasing index order.
+template <class F>
+__device__ __forceinline__ void for_each_logit(const float* __restrict__ logits, uint32_t V, uint32_t tid, F&& f) {
+    for_each_logit_batch(logits, V, tid, [&](const float (&v)[kSampBatch], uint32_t base) {
+#pragma unroll
+        for (int j = 0; j < kSampBatch; ++j) {
+            const uint32_t i = base + tid + (uint32_t)j * kSampBlock;
+            if (i < V) f(v[j], i);
+        }
+    });
+}
+
+// Returns the sampled token (valid in every thread through LDS).  Every mode streams the logits
+// from memory once per pass (the first pass brings them into the cache); nothing is held per
+// element in registers.
+__device__ __forceinline__ uint32_t block_sample(const float* __restrict__ logits, uint32_t V, int mode, float temperature,
                                  uint32_t top_k, uint32_t k0, uint32_t k1, uint64_t step) {
     __shared__ float wv[kSampBlock / 64];
     __shared__ uint32_t wi[kSampBlock / 64];
-    __shared__ float cand_v[kMaxTopK];
-    __shared__ uint32_t cand_i[kMaxTopK];
+    __shared__ uint64_t s_sort[kSampBlock];
+    __shared__ uint64_t s_cand[kSampBlock];
+    __shared__ uint64_t s_top[kMaxTopK];
+    __shared__ uint64_t s_best[kSampBlock / 64];
+    __shared__ uint64_t s_tau;
+    __shared__ uint32_t s_count;
     __shared__ uint32_t s_tok;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float vals[kSampPer];
-    uint64_t taken = 0;
-#pragma unroll
-    for (int j = 0; j < kSampPer; ++j) {
-        const uint32_t i = tid + (uint32_t)j * kSampBlock;
-        vals[j] = i < V ? logits[i] : -INFINITY;
-    }
-    const bool greedy = (mode == VSL_SAMPLE_GREEDY || temperature <= 0.f);
-    if (!greedy && mode == VSL_SAMPLE_REFERENCE) {
-        // sample_token(T > 0) -> member top_k_sampling (VulkanSymbioteEngine.cpp:1806-1855) -> tokens[0]:
-        // the first index of the largest fp32 probability exp(l/T - max) / sum.  That is the logit
-        // argmax except where exp and the division round neighbours of the maximum to the same
-        // probability; any NaN probability (a NaN or +inf logit) gives token 0, as there.
-        __shared__ float red[kSampBlock / 64];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < kSampPer; ++j) {
-            const uint32_t i = tid + (uint32_t)j * kSampBlock;
-            if (i < V) {
-                if (temperature != 1.0f) vals[j] = vals[j] / temperature;
-                mx = fmaxf(mx, vals[j]);
-            }
-        }
-        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, VSL_WAVE));
-        if (lane == 0) red[wave] = mx;
-        __syncthreads();
-        mx = red[0];
-        for (int w = 1; w < kSampBlock / 64; ++w) mx = fmaxf(mx, red[w]);
-        __syncthreads();
-        float part = 0.f;
-#pragma unroll
-        for (int j = 0; j < kSampPer; ++j) {
-            const uint32_t i = tid + (uint32_t)j * kSampBlock;
-            if (i < V) {
-                vals[j] = expf(vals[j] - mx);
-                part += vals[j];
-            }
-        }
-        for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o, VSL_WAVE);
-        if (lane == 0) red[wave] = part;
-        __syncthreads();
-        float sum = 0.f;
-        for (int w = 0; w < kSampBlock / 64; ++w) sum += red[w];
-        float bv = -INFINITY;
-        uint32_t bi = 0xFFFFFFFFu;
-#pragma unroll
-        for (int j = 0; j < kSampPer; ++j) {
-            const uint32_t i = tid + (uint32_t)j * kSampBlock;
-            if (i < V) argmax_merge(bv, bi, vals[j] / sum, i);
-        }
+    auto block_argmax = [&](float bv, uint32_t bi) -> uint32_t {  // first index of the max; none -> 0
         wave_argmax(bv, bi);
         if (lane == 0) { wv[wave] = bv; wi[wave] = bi; }
         __syncthreads();
@@ -1303,52 +1368,141 @@ __device__ uint32_t block_sample(const float* __restrict__ logits, uint32_t V, i
         }
         __syncthreads();
         return s_tok;
-    }
-    // top-k of at most kMaxTopK (the entry points reject larger k); k > V means all of V
-    uint32_t k = greedy ? 1u : (top_k > V ? V : top_k);
-    if (k > (uint32_t)kMaxTopK) k = kMaxTopK;
-    for (uint32_t it = 0; it < k; ++it) {
+    };
+    if (mode == VSL_SAMPLE_GREEDY || temperature <= 0.f) {
+        // greedy_sampling (VulkanSymbioteEngine.cpp:1794-1804): the first index of the largest logit,
+        // over any V; a NaN first logit is never beaten, other NaNs never win.
         float bv = -INFINITY;
         uint32_t bi = 0xFFFFFFFFu;
-#pragma unroll
-        for (int j = 0; j < kSampPer; ++j) {
-            const uint32_t i = tid + (uint32_t)j * kSampBlock;
-            if (i < V && !((taken >> j) & 1ull)) argmax_merge(bv, bi, vals[j], i);
-        }
-        wave_argmax(bv, bi);
-        if (lane == 0) { wv[wave] = bv; wi[wave] = bi; }
-        __syncthreads();
-        if (tid == 0) {
-            float v = wv[0];
-            uint32_t i = wi[0];
-            for (int w = 1; w < kSampBlock / 64; ++w) argmax_merge(v, i, wv[w], wi[w]);
-            if (i == 0xFFFFFFFFu) { i = 0u; v = logits[0]; }
-            cand_v[it] = v;
-            cand_i[it] = i;
-        }
-        __syncthreads();
-        const uint32_t sel = cand_i[it];
-        if (sel % kSampBlock == tid) taken |= 1ull << (sel / kSampBlock);
+        for_each_logit(logits, V, tid, [&](float l, uint32_t i) { argmax_merge(bv, bi, l, i); });
+        const uint32_t tok = block_argmax(bv, bi);
+        const float l0 = logits[0];
+        return l0 != l0 ? 0u : tok;
     }
-    if (tid == 0) {
-        if (greedy) {
-            s_tok = cand_i[0];
-        } else {
-            // Utils.cpp:151-171 over the k candidates in descending order (ties: lower id first)
-            const float mx = cand_v[0];
-            float w[kMaxTopK];
-            float sum = 0.f;
-            for (uint32_t i = 0; i < k; ++i) { w[i] = expf((cand_v[i] - mx) / temperature); sum += w[i]; }
-            for (uint32_t i = 0; i < k; ++i) w[i] /= sum;
-            const float r = sample_uniform(k0, k1, step);
-            float cum = 0.f;
-            uint32_t pick = cand_i[0];
-            for (uint32_t i = 0; i < k; ++i) {
-                cum += w[i];
-                if (r < cum) { pick = cand_i[i]; break; }
-            }
-            s_tok = pick;
+    if (mode == VSL_SAMPLE_REFERENCE) {
+        // sample_token(T > 0) -> member top_k_sampling (VulkanSymbioteEngine.cpp:1806-1855) -> tokens[0]:
+        // the first index of the largest fp32 probability exp(l/T - max) / sum.  That is the logit
+        // argmax except where exp and the division round neighbours of the maximum to the same
+        // probability; any NaN probability (a NaN or +inf logit) gives token 0, as there.
+        __shared__ float red[kSampBlock / 64];
+        auto scaled = [&](float l) { return temperature != 1.0f ? l / temperature : l; };
+        float mx = -INFINITY;
+        for_each_logit(logits, V, tid, [&](float l, uint32_t) { mx = fmaxf(mx, scaled(l)); });
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, VSL_WAVE));
+        if (lane == 0) red[wave] = mx;
+        __syncthreads();
+        mx = red[0];
+        for (int w = 1; w < kSampBlock / 64; ++w) mx = fmaxf(mx, red[w]);
+        __syncthreads();
+        float part = 0.f;
+        for_each_logit(logits, V, tid, [&](float l, uint32_t) { part += expf(scaled(l) - mx); });
+        for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o, VSL_WAVE);
+        if (lane == 0) red[wave] = part;
+        __syncthreads();
+        float sum = 0.f;
+        for (int w = 0; w < kSampBlock / 64; ++w) sum += red[w];
+        float bv = -INFINITY;
+        uint32_t bi = 0xFFFFFFFFu;
+        for_each_logit(logits, V, tid, [&](float l, uint32_t i) { argmax_merge(bv, bi, expf(scaled(l) - mx) / sum, i); });
+        return block_argmax(bv, bi);
+    }
+    // Seeded top-k (Utils.cpp:151-171): the k first elements in rank-key order, exactly.  Every one
+    // of them is >= tau whenever k distinct elements are >= tau; tau is the k-th largest of the
+    // union of each wave's kTauPerWave largest per-thread maxima, so the elements >= tau -- about
+    // k of them for ordinary logits -- hold the k and are sorted.  More than kSampBlock such
+    // elements (many equal logits) take k rounds of "largest key below the last" instead.
+    uint32_t k = top_k > V ? V : top_k;
+    if (k > (uint32_t)kMaxTopK) k = kMaxTopK;
+    float bf = -INFINITY;  // per-thread maximum, first index among equals; NaNs skipped
+    uint32_t bi = 0xFFFFFFFFu;
+    for_each_logit(logits, V, tid, [&](float l, uint32_t i) {
+        if (l > bf || (bi == 0xFFFFFFFFu && l == l)) { bf = l; bi = i; }
+    });
+    uint64_t wm[1] = {bi == 0xFFFFFFFFu ? 0ull : rank_key(value_key(bf), bi)};  // 0 ranks below every element
+    wave_bitonic_desc<1>(wm, lane);
+    if (lane < (uint32_t)kTauPerWave) s_sort[wave * kTauPerWave + lane] = wm[0];
+    if (tid == 0) s_count = 0;
+    __syncthreads();
+    if (wave == 0) {
+        uint64_t u[2] = {s_sort[lane], s_sort[VSL_WAVE + lane]};
+        wave_bitonic_desc<2>(u, lane);
+        if (lane == k - 1) s_tau = u[0];  // k <= 64; tau = 0 when fewer than k threads hold a number
+    }
+    __syncthreads();
+    const uint64_t tau = s_tau;
+    const uint32_t tk = (uint32_t)(tau >> 32), ti = ~(uint32_t)tau;
+    const float tf = key_value(tk);
+    for_each_logit(logits, V, tid, [&](float l, uint32_t i) {
+        // rank_key(value_key(l), i) >= tau in float compares (tk == 0: tau is a NaN or the sentinel)
+        if (tk == 0u ? (l == l || i <= ti) : (l > tf || (l == tf && i <= ti))) {
+            const uint32_t slot = atomicAdd(&s_count, 1u);
+            if (slot < (uint32_t)kSampBlock) s_cand[slot] = rank_key(value_key(l), i);
         }
+    });
+    __syncthreads();
+    const uint32_t total = s_count;
+    if (total <= (uint32_t)VSL_WAVE) {
+        if (wave == 0) {
+            uint64_t x[1] = {lane < total ? s_cand[lane] : 0ull};
+            wave_bitonic_desc<1>(x, lane);
+            if (lane < k) s_top[lane] = x[0];
+        }
+    } else if (total <= 2u * VSL_WAVE) {
+        if (wave == 0) {
+            uint64_t x[2] = {s_cand[lane], VSL_WAVE + lane < total ? s_cand[VSL_WAVE + lane] : 0ull};
+            wave_bitonic_desc<2>(x, lane);
+            if (lane < k) s_top[lane] = x[0];
+        }
+    } else if (total <= (uint32_t)kSampBlock) {
+        uint64_t x = tid < total ? s_cand[tid] : 0ull;
+        x = bitonic_desc<kSampBlock>(x, tid, s_sort);
+        if (tid < k) s_top[tid] = x;
+    } else {
+        uint64_t prev = ~0ull;
+        for (uint32_t it = 0; it < k; ++it) {
+            uint64_t best = 0;
+            for_each_logit(logits, V, tid, [&](float l, uint32_t i) {
+                const uint64_t e = rank_key(value_key(l), i);
+                if (e < prev && e > best) best = e;
+            });
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                const uint64_t y = shfl_xor_u64(best, o);
+                best = y > best ? y : best;
+            }
+            if (lane == 0) s_best[wave] = best;
+            __syncthreads();
+            prev = s_best[0];
+            for (int w = 1; w < kSampBlock / 64; ++w) prev = s_best[w] > prev ? s_best[w] : prev;
+            if (tid == 0) s_top[it] = prev;
+            __syncthreads();
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // weights exp((l_i - max) / T) / sum in rank order: the sum and the cumulative walk in the
+        // reference's sequential order (every lane of the wave computes the same sums)
+        const uint64_t t = lane < k ? s_top[lane] : 0ull;
+        const float mx = key_value((uint32_t)(s_top[0] >> 32));
+        const float e = lane < k ? expf((key_value((uint32_t)(t >> 32)) - mx) / temperature) : 0.f;
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < kMaxTopK; ++i)
+            if ((uint32_t)i < k) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), i));
+        const int wi_bits = __float_as_int(e / sum);
+        const float r = sample_uniform(k0, k1, step);
+        float cum = 0.f;
+        int pick = 0;
+        bool found = false;
+#pragma unroll
+        for (int i = 0; i < kMaxTopK; ++i) {
+            if ((uint32_t)i < k && !found) {
+                cum += __int_as_float(__builtin_amdgcn_readlane(wi_bits, i));
+                if (r < cum) { pick = i; found = true; }
+            }
+        }
+        const uint32_t tok = ~(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)t, pick);
+        if (lane == 0) s_tok = tok;
     }
     __syncthreads();
     return s_tok;
@@ -1898,12 +2052,11 @@ extern "C" int vsl_norm_swiglu(const float* x, const float* gamma, float eps, co
 
 extern "C" uint32_t vsl_lm_head_ws_blocks(void) { return kMaxLmBlocks; }
 
-// Sampler arguments the kernels serve: a known mode, V <= 65536 wherever logits are scanned by one
-// block, and for seeded top-k 1 <= top_k <= 64 (top_k > V means all of V).
+// Sampler arguments the kernels serve: a known mode, and for seeded top-k 1 <= top_k <= 64 (top_k > V
+// means all of V).
 static int check_sampler(const vsl_sampler& sp, uint32_t V, const char* who) {
     if (sp.mode < VSL_SAMPLE_GREEDY || sp.mode > VSL_SAMPLE_TOPK_SEEDED) return vsl_invalid("%s: sampler mode %d", who, sp.mode);
     if (sp.temperature <= 0.f || sp.mode == VSL_SAMPLE_GREEDY) return VSL_OK;  // greedy: no limits
-    if (V > (uint32_t)(kSampBlock * kSampPer)) return vsl_unsupported("%s: sampling supports V <= %d", who, kSampBlock * kSampPer);
     if (sp.mode == VSL_SAMPLE_TOPK_SEEDED && (sp.top_k == 0 || sp.top_k > (uint32_t)kMaxTopK))
         return vsl_unsupported("%s: seeded top-k supports 1 <= top_k <= %d (got %u)", who, kMaxTopK, sp.top_k);
     return VSL_OK;

@@ -698,11 +698,9 @@ int VulkanSymbioteEngine::begin_generation(const std::vector<uint32_t>& prompt, 
     if (params.mode < 0 || params.mode > 2) return kErrInvalid;
     // the samplers' limits are checked before anything is enqueued (vsl_lm_head_sample would refuse
     // the same request inside the prompt pass)
-    if (params.temperature > 0.0f && params.mode != VSL_SAMPLE_GREEDY) {
-        if (config_.vocab_size > VSL_MAX_SAMPLE_VOCAB) return VSL_E_UNSUPPORTED;
-        if (params.mode == VSL_SAMPLE_TOPK_SEEDED && (params.top_k == 0 || params.top_k > VSL_MAX_TOP_K))
-            return VSL_E_UNSUPPORTED;
-    }
+    if (params.temperature > 0.0f && params.mode == VSL_SAMPLE_TOPK_SEEDED &&
+        (params.top_k == 0 || params.top_k > VSL_MAX_TOP_K))
+        return VSL_E_UNSUPPORTED;
     std::memcpy(host_tokens_, prompt.data(), (size_t)n * 4);
     check(vsl_copy_h2d(prompt_dev_, host_tokens_, (size_t)n * 4, stream_), "prompt upload");
     host_ctrl_->max_steps = max_new;
