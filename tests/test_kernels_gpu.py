@@ -98,6 +98,28 @@ def test_gemv_batched_ragged(vsl, orc, dev, H, N, K, B):
     assert rel_err(dev.get(dY), ref) < 1e-5
 
 
+@pytest.mark.parametrize("N,K,B,ydt", [(1, 1024, 2, 0), (37, 2048, 3, 0), (4099, 3072, 5, 0), (1000, 8192, 8, 0),
+                                       (515, 1024, 7, 1), (3001, 4096, 4, 1), (4100, 6144, 6, 0), (300, 9216, 8, 0)])
+def test_gemv_batched_rows(vsl, orc, dev, H, N, K, B, ydt):
+    """The row-streaming kernel of the batched product (2 <= B <= 8, X [B][K] up to 128 KB in LDS,
+    K % 1024 == 0): one row, odd row counts (a wave's second row past N), every B from 2 to 8, X at
+    the 128 KB limit (B = 8, K = 8192); fp32 and fp16 Y.  B = 8 with K = 9216 is past the limit and
+    takes the MFMA kernel."""
+    rng = np.random.default_rng(N * 7 + K + B)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    X = rng.normal(0, 1, (B, K)).astype(np.float16)
+    ref = orc.gemm_nt(W, np.ascontiguousarray(X.T).astype(np.float32))  # [N][B]
+    if ydt == 0:
+        dY = dev.empty((B, N), np.float32)
+        ok(vsl, H.vsl_gemv_batched(dev.p(dev.put(W)), N, K, dev.p(dev.put(X)), B, dev.p(dY), vsl.VSL_DT_F32, None))
+        assert rel_err(dev.get(dY).T, ref) < 1e-5
+    else:
+        dY = dev.empty((B, N), np.float16)
+        ok(vsl, H.vsl_gemv_batched(dev.p(dev.put(W)), N, K, dev.p(dev.put(X)), B, dev.p(dY), vsl.VSL_DT_F16, None))
+        y = dev.get(dY).astype(np.float32).T
+        assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -11 + 1e-4 * np.max(np.abs(ref)))
+
+
 def test_gemv_rejects_bad_shapes(vsl, dev, H):
     d = dev.empty((16,), np.float32)
     assert H.vsl_gemv_batched(dev.p(d), 4, 1000, dev.p(d), 1, dev.p(d), 0, None) == -100  # K % 512

@@ -1808,6 +1808,145 @@ int launch_skinny(const void* W, uint32_t N, uint32_t K, const void* X, uint32_t
     return VSL_OK;
 }
 
+// Small-batch GEMV (2 <= B <= 8, X fp16 [B][K] staged once per block in LDS): whole rows per wave as
+// in the decode GEMV, every weight load a 1 KB-contiguous run of one row (64 lanes x 16 bytes), two
+// tiles of R rows in flight per wave; each 16-byte weight chunk meets the same 8 elements of every
+// vector through v_dot2_f32_f16 (two fp16 products -- exact in fp32 -- added to an fp32 accumulator),
+// and the R rows of a wave share every activation read. One 16-wave block per CU; per-lane partial
+// sums reduced by DPP at the end of each row group.
+constexpr int kRowsWaves = 16;
+constexpr uint32_t kRowsLdsBytes = 128u << 10;  // X of at most B * K * 2 bytes
+
+__device__ __forceinline__ float dot8(uint4 w, uint4 x, float acc) {
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, w.x), __builtin_bit_cast(half2v, x.x), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, w.y), __builtin_bit_cast(half2v, x.y), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, w.z), __builtin_bit_cast(half2v, x.z), acc, false);
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, w.w), __builtin_bit_cast(half2v, x.w), acc, false);
+}
+
+// K % 1024 == 0 (an even number of 512-wide tiles: the tile pairs below never load past a row). A
+// wave requests its first group's first two tiles before the block stages X, and the next group's
+// first two tiles before it reduces and stores the current group, so the weight stream never waits
+// on the staging or the reductions.
+template <int B, int R, class YT>
+__global__ __launch_bounds__(kRowsWaves * 64) void k_gemv_rows(const vsl_half* __restrict__ W, uint32_t N, uint32_t K,
+                                                             const vsl_half* __restrict__ X, YT* __restrict__ Y) {
+    extern __shared__ uint4 xrows[];  // X [B][K], 8 halfs per entry
+    constexpr uint32_t NT = kRowsWaves * 64;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t kq = K / 8, tiles = K / 512;
+    const uint32_t groups = (N + R - 1) / R, gstride = gridDim.x * kRowsWaves;
+    const vsl_half* wr[R];
+    auto set_rows = [&](uint32_t g) {  // rows past N (and groups past the last) read row N - 1
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = g * R + r;
+            wr[r] = W + (size_t)(row < N ? row : N - 1) * K + lane * 8;
+        }
+    };
+    uint4 ta[R], tb[R];
+    auto load = [&](uint4 (&t)[R], uint32_t tile) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) t[r] = load16<true>(wr[r] + (size_t)tile * 512);
+    };
+    uint32_t g = blockIdx.x * kRowsWaves + wave;
+    set_rows(g);
+    load(ta, 0);
+    load(tb, 1);
+    for (uint32_t i = tid; i < (uint32_t)B * kq; i += NT) xrows[i] = load16<false>(X + (size_t)i * 8);
+    __syncthreads();
+    for (; g < groups; g += gstride) {
+        float acc[R][B];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int b = 0; b < B; ++b) acc[r][b] = 0.f;
+        auto use = [&](const uint4 (&t)[R], uint32_t tile) {
+            // one address register per tile, each vector's (uniform) offset added in the loop: left to
+            // itself the compiler keeps a strength-reduced address per vector and buffer live
+            uint32_t off = (tile * 64 + lane) * 16;
+            asm volatile("" : "+v"(off));
+            const char* xb = reinterpret_cast<const char*>(xrows) + off;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const uint4 xv = *reinterpret_cast<const uint4*>(xb + (size_t)b * kq * 16);
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r][b] = dot8(t[r], xv, acc[r][b]);
+            }
+        };
+        for (uint32_t t = 0; t + 2 < tiles; t += 2) {
+            use(ta, t);
+            load(ta, t + 2);
+            use(tb, t + 1);
+            load(tb, t + 3);
+        }
+        const uint32_t g0 = g;
+        set_rows(g + gstride);  // the next group (its tiles are requested even past the last group)
+        use(ta, tiles - 2);
+        load(ta, 0);
+        use(tb, tiles - 1);
+        load(tb, 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const float v = wave_sum_dpp(acc[r][b]);
+                const uint32_t row = g0 * R + r;
+                if (lane == 0 && row < N) Y[(size_t)b * N + row] = (YT)v;
+            }
+    }
+}
+
+template <int B, int R, class YT>
+int launch_rows_br(const vsl_half* w, uint32_t N, uint32_t K, const vsl_half* x, YT* y, hipStream_t s) {
+    const size_t lds = (size_t)B * K * 2;
+    static bool attr = false;
+    if (!attr) {
+        HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemv_rows<B, R, YT>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRowsLdsBytes));
+        attr = true;
+    }
+    uint32_t blocks = ((N + R - 1) / R + kRowsWaves - 1) / kRowsWaves;
+    const uint32_t cap = gemv_grid_cap(kRowsWaves, EPI_STORE);
+    if (blocks > cap) blocks = cap;
+    k_gemv_rows<B, R, YT><<<blocks, kRowsWaves * 64, lds, s>>>(w, N, K, x, y);
+    HIP_TRY(hipGetLastError());
+    return VSL_OK;
+}
+
+// One row per wave (sweep B = 4, interleaved runs: geometric mean 5053-5075 GB/s, against 4560 with
+// two rows per wave sharing each activation read from 8192 rows on -- 14336 rows in pairs leave the
+// 4096 waves one or two groups each -- and 4110 for the MFMA kernel).
+template <int B, class YT>
+int launch_rows_b(const vsl_half* w, uint32_t N, uint32_t K, const vsl_half* x, YT* y, hipStream_t s) {
+    return launch_rows_br<B, 1>(w, N, K, x, y, s);
+}
+
+// Whether k_gemv_rows serves a batched product: 2 <= B <= 8, X (B * K * 2 bytes) fits the block's
+// LDS, K % 1024 == 0 and X 16-byte aligned.  At B = 16 the 16 activation reads and 64 dot2 per 1 KB
+// of weights bound it at 1.1-1.8 TB/s on the sweep shapes, against 3.5-3.9 for the MFMA kernel.
+bool rows_fits(uint32_t B, uint32_t K, const void* X) {
+    return B >= 2 && B <= 8 && (uint64_t)B * K * 2 <= kRowsLdsBytes && K % 1024 == 0 &&
+           (reinterpret_cast<uintptr_t>(X) & 15) == 0;
+}
+
+template <class YT>
+int launch_rows(const void* W, uint32_t N, uint32_t K, const void* X, uint32_t B, void* Y, hipStream_t s) {
+    const vsl_half* w = static_cast<const vsl_half*>(W);
+    const vsl_half* x = static_cast<const vsl_half*>(X);
+    YT* y = static_cast<YT*>(Y);
+    switch (B) {
+        case 2: return launch_rows_b<2>(w, N, K, x, y, s);
+        case 3: return launch_rows_b<3>(w, N, K, x, y, s);
+        case 4: return launch_rows_b<4>(w, N, K, x, y, s);
+        case 5: return launch_rows_b<5>(w, N, K, x, y, s);
+        case 6: return launch_rows_b<6>(w, N, K, x, y, s);
+        case 7: return launch_rows_b<7>(w, N, K, x, y, s);
+        case 8: return launch_rows_b<8>(w, N, K, x, y, s);
+        default: return vsl_invalid("k_gemv_rows: B=%u", B);
+    }
+}
+
 }  // namespace
 
 // One fp16 activation vector against fp16 W: the decode GEMV (whole rows per wave, two rows per tile,
@@ -1910,6 +2049,8 @@ extern "C" int vsl_gemv_batched(const void* W, uint32_t N, uint32_t K, const voi
     if (ydtype != VSL_DT_F16 && ydtype != VSL_DT_F32) return vsl_unsupported("vsl_gemv_batched: Y dtype %d", ydtype);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (B == 1 && K <= kMaxK) return gemv_one_f16x(W, N, K, X, Y, ydtype, s);
+    if (rows_fits(B, K, X))
+        return ydtype == VSL_DT_F16 ? launch_rows<vsl_half>(W, N, K, X, B, Y, s) : launch_rows<float>(W, N, K, X, B, Y, s);
     return ydtype == VSL_DT_F16 ? launch_skinny<vsl_half, true>(W, N, K, X, B, Y, s)
                                 : launch_skinny<float, true>(W, N, K, X, B, Y, s);
 }
