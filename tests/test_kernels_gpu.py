@@ -309,10 +309,12 @@ def test_attn_decode_window(vsl, orc, dev, H, kvdt, hd, nq, nkv, length, window,
     (128, 32, 8, 200, 0, 100, 70, 60, False),     # globals over two tiles; a block straddles the threshold
     (128, 32, 8, 160, 300, 32, 0, 0, True),       # every row windowed, no globals, split q / out
     (64, 8, 8, 96, 0, 512, 16, 8192, False),      # threshold not reached: dense
+    (128, 32, 8, 192, 1000, 512, 16, 900, True),  # every row windowed, tiles wholly inside every window
+    (64, 8, 8, 160, 700, 256, 128, 600, False),   # two whole global tiles, then the windows
 ])
 def test_attn_prefill_window(vsl, orc, dev, H, hd, nq, nkv, S, pos0, window, n_glob, thr, x2):
     rng = np.random.default_rng(hd + S + pos0 + window)
-    cap = 512
+    cap = max(512, -(-(pos0 + S) // 512) * 512)
     Q = rng.normal(0, 1, (S, nq * hd)).astype(np.float32)
     K = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16)
     V = rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16)

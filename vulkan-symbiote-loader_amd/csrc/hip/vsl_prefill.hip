@@ -483,6 +483,9 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     auto phys = [&](uint32_t vt) { return vt < n_gt ? vt : vt - n_gt + t_lo; };
     // this lane's row: keys below my_lo (and not global) are masked
     const uint32_t my_lo = (WIN && my_pos + 1 > thr && my_pos > win) ? my_pos - win : 0;
+    // the largest window start of the block's rows (the last row's: starts grow with the position)
+    const uint32_t p_last = pos0 + last_s;
+    const uint32_t lo_max = (WIN && p_last + 1 > thr && p_last > win) ? p_last - win : 0;
     const vsl_half* Kb = kc + (size_t)kvh * cap * HD;
     const vsl_half* Vb = vc + (size_t)kvh * cap * HD;
 
@@ -550,7 +553,9 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     // the block's first row; returns the tile maximum of this lane's row
     auto mask_max = [&](float16v (&st)[2], uint32_t t) {
         float bm = -INFINITY;
-        if (!WIN && t * TK + TK - 1 <= p_first) {  // wave-uniform: no row of the block is cut by this tile
+        // wave-uniform: every key of the tile is visible to every row of the block (at or below the
+        // first row, and inside every row's window or among the global keys)
+        if (t * TK + TK - 1 <= p_first && (!WIN || t * TK >= lo_max || t * TK + TK - 1 < n_glob)) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
