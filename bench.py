@@ -152,10 +152,13 @@ def gpus_or_exit(a):
         sys.exit(2)
 
 
-def sweep_leg(vsl):
+def sweep_leg(vsl, graph=True):
     """GEMV sweep: W [N,K] fp16 ~N(0,0.02), X [K,B] fp16 ~N(0,1), fp32 accumulate, fp16 Y; W rotated
-    over >= 512 MB of distinct copies so the 256 MB MALL cannot serve it.  Returns the per-shape rows and
-    geometric means (all shapes, and per B)."""
+    over >= 512 MB of distinct copies so the 256 MB MALL cannot serve it.  Each point times >= 64
+    launches back to back: captured in one hipGraph and replayed (graph=True, as the decode step runs
+    its kernels; a Python loop of launches cannot issue a 5 us kernel as fast as the GPU retires it),
+    or launched one by one (graph=False: what rocprofv3's kernel trace follows).  Returns the per-shape
+    rows and geometric means (all shapes, and per B)."""
     import ctypes
     H = vsl.hip()
     P = ctypes.c_void_p
@@ -176,9 +179,10 @@ def sweep_leg(vsl):
     xbuf = alloc(14336 * 16 * 2)
     vsl.check(H.vsl_fill_normal(xbuf, vsl.VSL_DT_F16, 14336 * 16, 2, b"sweep.X", 0.0, 1.0, None))
     ybuf = alloc(32000 * 16 * 2)
-    e0, e1 = P(), P()
+    e0, e1, stream = P(), P(), P()
     vsl.check(H.vsl_event_create(ctypes.byref(e0)))
     vsl.check(H.vsl_event_create(ctypes.byref(e1)))
+    vsl.check(H.vsl_stream_create(ctypes.byref(stream)))
     rows = []
     for (N, K) in [(4096, 4096), (14336, 4096), (4096, 14336), (32000, 4096)]:
         wsz = N * K * 2
@@ -186,15 +190,28 @@ def sweep_leg(vsl):
         ptrs = [P(wbuf.value + (i * wsz) % (wtotal - wsz)) for i in range(copies)]
         for B in (1, 4, 16):
             # X as B contiguous K-vectors (vsl_gemv_batched); Y [B][N] fp16
-            args = lambda w: (w, N, K, xbuf, B, ybuf, vsl.VSL_DT_F16, None)
+            args = lambda w: (w, N, K, xbuf, B, ybuf, vsl.VSL_DT_F16, stream)
             for w in ptrs[:2]:
                 vsl.check(H.vsl_gemv_batched(*args(w)))
             reps = max(copies * 4, 64)
-            vsl.check(H.vsl_event_record(e0, None))
-            for i in range(reps):
-                vsl.check(H.vsl_gemv_batched(*args(ptrs[i % copies])))
-            vsl.check(H.vsl_event_record(e1, None))
+            g = P()
+            if graph:
+                vsl.check(H.vsl_graph_begin(stream))
+                for i in range(reps):
+                    vsl.check(H.vsl_gemv_batched(*args(ptrs[i % copies])))
+                vsl.check(H.vsl_graph_end(stream, ctypes.byref(g)))
+                vsl.check(H.vsl_graph_launch(g, stream))  # one untimed replay
+            vsl.check(H.vsl_stream_sync(stream))
+            vsl.check(H.vsl_event_record(e0, stream))
+            if graph:
+                vsl.check(H.vsl_graph_launch(g, stream))
+            else:
+                for i in range(reps):
+                    vsl.check(H.vsl_gemv_batched(*args(ptrs[i % copies])))
+            vsl.check(H.vsl_event_record(e1, stream))
             vsl.check(H.vsl_event_sync(e1))
+            if graph:
+                vsl.check(H.vsl_graph_destroy(g))
             ms = ctypes.c_float()
             vsl.check(H.vsl_event_elapsed_ms(e0, e1, ctypes.byref(ms)))
             us = ms.value * 1e3 / reps
@@ -204,6 +221,7 @@ def sweep_leg(vsl):
                          "tflops": round(2 * N * K * B / us / 1e6, 2)})
     vsl.check(H.vsl_event_destroy(e0))
     vsl.check(H.vsl_event_destroy(e1))
+    vsl.check(H.vsl_stream_destroy(stream))
     vsl.check(H.vsl_arena_destroy(arena))
     geo = lambda rs: round(float(np.exp(np.mean([np.log(r["gbps"]) for r in rs]))), 1)
     return {"geomean_gbps": geo(rows), "geomean_hbm_frac": round(geo(rows) / (PEAK_HBM / 1e9), 4),
@@ -213,7 +231,7 @@ def sweep_leg(vsl):
 
 def run_sweep(a):
     gpus_or_exit(a)
-    sw = sweep_leg(load_package())
+    sw = sweep_leg(load_package(), graph=not a.eager)
     out = {"metric": "GEMV sweep HBM GB/s (geometric mean over 12 shapes), fp16 W/X/Y, fp32 accumulate",
            "value": sw["geomean_gbps"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True, "dtype": "f16",
            "data": "synthetic: W ~N(0,0.02), X ~N(0,1) fp16 (Philox on device); W rotated over >= 512 MB",
@@ -352,8 +370,9 @@ def main():
                     help="after the run, copy this many MB device-to-device once (a kernel of known traffic "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--eager", action="store_true",
-                    help="launch each decode step's kernels directly instead of replaying the captured hipGraph "
-                         "(same kernels; used under rocprofv3, whose graph-launch interception crashes here)")
+                    help="launch each decode step's kernels (and each GEMV sweep launch) directly instead of "
+                         "replaying a captured hipGraph (same kernels; used under rocprofv3, whose graph-launch "
+                         "interception crashes here)")
     ap.add_argument("--sweep", action="store_true",
                     help="the standalone fp16 GEMV / skinny-GEMM sweep instead: Y = W X for (N, K) in "
                          "{(4096,4096), (14336,4096), (4096,14336), (32000,4096)} and B in {1, 4, 16}, W rotated "
@@ -496,7 +515,7 @@ def main():
     if not a.quick:
         # the other configurations, each in its own engine after the 8B one is released
         for key, leg in (("llama_1b", lambda: llama_1b_leg(vsl, a.eager)),
-                         ("gemv_sweep", lambda: sweep_leg(vsl)),
+                         ("gemv_sweep", lambda: sweep_leg(vsl, graph=not a.eager)),
                          ("long_context", lambda: long_leg(vsl, 128, a.eager))):
             try:
                 out[key] = leg()
