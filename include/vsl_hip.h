@@ -41,8 +41,14 @@ enum {
 
 /* VSL_DT_F16X2 -- split activations for the prefill MFMA path: an fp32 value v is held as two
  * binary16 planes, hi = fp16(v) and lo = fp16(v - hi) (hi plane first, then the lo plane of the
- * same shape), so that hi + lo carries ~22 significant bits through fp16 MFMA. */
-enum { VSL_DT_F32 = 0, VSL_DT_F16 = 1, VSL_DT_F16X2 = 2 };
+ * same shape), so that hi + lo carries ~22 significant bits through fp16 MFMA.
+ * VSL_DT_F16F8 -- the same hi plane followed by a plane of one byte per value: the fp8 e4m3 (OCP)
+ * rounding of (v - hi) * 2^12 (clamped to +-448), so that hi + lo8 * 2^-12 carries ~15 significant
+ * bits for |v| <= 224 (larger values keep part of their remainder); the GEMM multiplies the lo plane
+ * on the fp8 matrix cores.  Within every 32 consecutive
+ * columns of a row (rows a multiple of 32 columns wide) the byte of column k sits at position k
+ * with bits 3 and 4 exchanged. */
+enum { VSL_DT_F32 = 0, VSL_DT_F16 = 1, VSL_DT_F16X2 = 2, VSL_DT_F16F8 = 3 };
 
 /* Sampling modes (VulkanSymbioteEngine::sample_token, VulkanSymbioteEngine.cpp:1540-1553) */
 enum {
@@ -170,8 +176,9 @@ typedef struct vsl_sampler {
 int vsl_embed(const void* table, int dtype, uint32_t vocab, uint32_t d, const uint32_t* ids_dev,
               uint32_t n, float* out, void* stream);
 
-/* rms_norm.comp:24-34 over `rows` rows: y = x / sqrt(mean(x^2)+eps) * gamma; out fp32, fp16 or
- * VSL_DT_F16X2 (two planes of rows*d halfs) */
+/* rms_norm.comp:24-34 over `rows` rows: y = x / sqrt(mean(x^2)+eps) * gamma; out fp32, fp16,
+ * VSL_DT_F16X2 (two planes of rows*d halfs) or VSL_DT_F16F8 (rows*d halfs, then rows*d bytes;
+ * d % 32 == 0) */
 int vsl_rmsnorm(const float* x, const float* gamma, uint32_t rows, uint32_t d, float eps, void* out,
                 int out_dtype, void* stream);
 
@@ -271,9 +278,12 @@ int vsl_ctrl_reset(vsl_ctrl* ctrl, uint32_t pos, uint32_t max_steps, uint32_t st
  *   VSL_EPI_STORE_F32 (C f32), VSL_EPI_STORE_F16 (C f16), VSL_EPI_RESID (C f32 +=),
  *   VSL_EPI_SWIGLU (B = [Wgate; Wup], N = F: C f16 = silu(A Wg^T) * (A Wu^T)).
  * Flags or'ed into `epilogue`: VSL_GEMM_A_X2 (A is VSL_DT_F16X2: two MFMAs per tile, hi and lo),
- * VSL_GEMM_C_X2 (SwiGLU output written as VSL_DT_F16X2). */
+ * VSL_GEMM_C_X2 (SwiGLU output written as VSL_DT_F16X2), VSL_GEMM_A_F8 (A is VSL_DT_F16F8: the hi
+ * plane on fp16 MFMA, the lo plane on fp8 MFMA against B rounded to e4m3 as B * 2^6, into the same
+ * fp32 accumulators), VSL_GEMM_C_F8 (SwiGLU output written as VSL_DT_F16F8).  The F8 forms need
+ * N % 256 == 0 (N % 128 == 0 for SwiGLU) and K % 128 == 0, else VSL_E_UNSUPPORTED. */
 enum { VSL_EPI_STORE_F32 = 0, VSL_EPI_STORE_F16 = 1, VSL_EPI_RESID = 2, VSL_EPI_SWIGLU = 3 };
-enum { VSL_GEMM_A_X2 = 0x100, VSL_GEMM_C_X2 = 0x200 };
+enum { VSL_GEMM_A_X2 = 0x100, VSL_GEMM_C_X2 = 0x200, VSL_GEMM_A_F8 = 0x400, VSL_GEMM_C_F8 = 0x800 };
 int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
                  void* stream);
 /* The same with an fp32 workspace (16-byte aligned): shapes whose output tiles would leave CUs idle
@@ -294,8 +304,8 @@ int vsl_rope_split_append(const float* qkv, uint32_t S, uint32_t n_q, uint32_t n
 
 /* The attention stage's entry for S prompt rows (forward_layer_with_weights,
  * VulkanSymbioteEngine.cpp:777-806, normed -> attention_with_weights): the QKV projection of A
- * [S][K] against Wqkv [(n_q+2 n_kv) hd][K] followed by vsl_rope_split_append.  `a_flags` is 0 or
- * VSL_GEMM_A_X2.  When the shape splits over K (workspace as for vsl_gemm_f16_ws), the partials are
+ * [S][K] against Wqkv [(n_q+2 n_kv) hd][K] followed by vsl_rope_split_append.  `a_flags` is 0,
+ * VSL_GEMM_A_X2 or VSL_GEMM_A_F8.  When the shape splits over K (workspace as for vsl_gemm_f16_ws), the partials are
  * summed, rotated and stored by one launch and qkv is not touched; otherwise qkv (f32 [S][(n_q+2 n_kv)
  * hd]) receives the projection first.  Checks (capacity, dtypes) happen before anything is launched. */
 int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uint32_t S, uint32_t K, int a_flags,
@@ -307,7 +317,7 @@ int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uint32_t S, ui
 /* A residual projection and the RMSNorm that starts the next stage (forward_layer_with_weights,
  * VulkanSymbioteEngine.cpp:777-806: the attention output feeds the FFN's norm, the FFN output the
  * next layer's attention norm): x [M][N] f32 += A [M][K] B [N][K]^T, then xn = rmsnorm(x) * gamma as
- * vsl_rmsnorm (xn_dtype F16, F16X2 or F32).  When the shape splits over K, one launch sums the
+ * vsl_rmsnorm (xn_dtype F16, F16X2, F16F8 or F32; `a_flags` as for the QKV entry).  When the shape splits over K, one launch sums the
  * partials in order, adds them to x and normalizes the rows; otherwise the residual GEMM is followed
  * by vsl_rmsnorm. */
 int vsl_gemm_f16_resid_rmsnorm(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, int a_flags,

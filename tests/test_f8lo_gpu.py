@@ -1,0 +1,228 @@
+"""The VSL_DT_F16F8 activation form on the GPU: producers (row RMSNorm, the fused residual + RMSNorm,
+the SwiGLU epilogue) against the fp64 value they encode, and the GEMM's fp8 lo path against the
+product it is defined to compute -- hi B^T + lo B8^T with lo the e4m3 plane's value and B8 the e4m3
+rounding of B * 2^6 -- in float64 (vsl_testlib.f8lo_product), through the big / mid tiles, the K
+split, and the forced direct-to-LDS path for shapes that would otherwise take another kernel."""
+import numpy as np
+import pytest
+
+import vsl_testlib as T
+
+pytestmark = pytest.mark.gpu
+
+F8_VALUE_REL = 2.0 ** -16   # |hi + lo8 2^-12 - v| / |v| for normal lo (e4m3 rounds to 2^-4 of lo <= 2^-12 v)
+F8_VALUE_ABS = 2.0 ** -22   # e4m3 subnormal spacing 2^-9, times 2^-12, halved
+
+
+@pytest.fixture(scope="module")
+def _dev():
+    return T.Dev()
+
+
+@pytest.fixture
+def dev(_dev):
+    yield _dev
+    _dev.release()
+
+
+@pytest.fixture(scope="module")
+def H(vsl):
+    return vsl.hip()
+
+
+def ok(vsl, rc):
+    vsl.check(rc)
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(1e-30, np.max(np.abs(b))))
+
+
+def f8_buffer(dev, a):
+    """Device VSL_DT_F16F8 copy of fp32 rows a: the hi plane, then the byte plane. Returns (buffer,
+    hi, value)."""
+    hi, plane, val = T.f16f8_split(a)
+    buf = dev.put(np.concatenate([hi.reshape(-1).view(np.uint8), plane.reshape(-1)]))
+    return buf, hi, val
+
+
+def f8_read(dev, buf, M, N):
+    """(hi, value) of a device VSL_DT_F16F8 buffer of M x N."""
+    flat = dev.get(buf).reshape(-1).view(np.uint8)
+    hi = flat[:2 * M * N].view(np.float16).reshape(M, N)
+    plane = flat[2 * M * N:3 * M * N].reshape(M, N)
+    return hi, T.f16f8_value(hi, plane)
+
+
+def assert_f8_encodes(hi, val, ref):
+    """hi is the binary16 rounding of the encoded value's fp32 source and hi + lo8 2^-12 carries it
+    to e4m3's precision: within 2^-16 relative plus the subnormal floor, element by element."""
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(val - ref)
+    assert np.all(err <= F8_VALUE_REL * np.abs(ref) + F8_VALUE_ABS + 4e-7 * np.abs(ref)), float(np.max(err))
+    assert np.all(np.abs(hi.astype(np.float64) - ref) <= np.spacing(np.abs(hi)).astype(np.float64))
+
+
+@pytest.mark.parametrize("d", [256, 2048, 4096, 8192, 1056])
+@pytest.mark.parametrize("rows", [1, 6])
+def test_rmsnorm_f16f8(vsl, orc, dev, H, d, rows):
+    """Row RMSNorm into the F16F8 form: the one-row-per-wave kernel (256 .. 8192) and the block-per-row
+    kernel (1056); every element's hi + lo8 2^-12 is the oracle's RMSNorm to e4m3 precision of the
+    remainder (a byte in the wrong position of the plane misses that by ~2^-12)."""
+    rng = np.random.default_rng(d + rows)
+    x = rng.normal(0, 2, (rows, d)).astype(np.float32)
+    g = rng.normal(1, 0.1, d).astype(np.float32)
+    out = dev.empty((3 * rows * d,), np.uint8)
+    ok(vsl, H.vsl_rmsnorm(dev.p(dev.put(x)), dev.p(dev.put(g)), rows, d, 1e-5, dev.p(out), vsl.VSL_DT_F16F8, None))
+    hi, val = f8_read(dev, out, rows, d)
+    ref = np.stack([orc.rmsnorm(x[r], g, 1e-5) for r in range(rows)]).astype(np.float64)
+    assert_f8_encodes(hi, val, ref)
+
+
+def test_rmsnorm_f16f8_needs_whole_blocks(vsl, dev, H):
+    x = dev.put(np.ones((2, 1000), np.float32))
+    out = dev.empty((6000,), np.uint8)
+    assert H.vsl_rmsnorm(dev.p(x), None, 2, 1000, 1e-5, dev.p(out), vsl.VSL_DT_F16F8, None) == vsl.VSL_E_INVALID
+
+
+@pytest.mark.parametrize("M,N,K,epi,cmode", [
+    (512, 14336, 2048, 3, "f8"),    # SwiGLU, 256 x 256 tiles, F16F8 output
+    (512, 14336, 2048, 3, "x2"),    # F16F8 in, hi/lo fp16 out
+    (777, 4096, 2048, 3, "f16"),    # ragged M on 128 x 256 tiles, fp16 out
+    (777, 4096, 2048, 3, "f8"),
+    (2048, 6144, 4096, 0, None),    # fp32 store, 256 x 256
+    (2048, 4096, 1024, 2, None),    # residual add, 128 x 256 (16 x 16 tiles)
+    (1536, 8192, 256, 1, None),     # fp16 store, two 128-column stage groups
+])
+def test_gemm_f8lo_tiles(vsl, dev, H, M, N, K, epi, cmode):
+    rng = np.random.default_rng(M + N + K + epi)
+    nb = 2 * N if epi == 3 else N
+    A = rng.normal(0, 1, (M, K)).astype(np.float32)
+    B = rng.normal(0, 0.02, (nb, K)).astype(np.float16)
+    dA, hi, val = f8_buffer(dev, A)
+    lo = val - hi.astype(np.float64)
+    flags = vsl.GEMM_A_F8 | {"f8": vsl.GEMM_C_F8, "x2": vsl.GEMM_C_X2, "f16": 0, None: 0}[cmode]
+    if epi == 3:
+        C = dev.empty((4 * M * N,), np.uint8)
+    elif epi == 1:
+        C = dev.empty((M, N), np.float16)
+    else:
+        C0 = rng.normal(0, 1, (M, N)).astype(np.float32) if epi == 2 else np.zeros((M, N), np.float32)
+        C = dev.put(C0)
+    ok(vsl, H.vsl_gemm_f16(dev.p(dA), dev.p(dev.put(B)), M, N, K, dev.p(C), epi | flags, None))
+    rows = np.unique(np.concatenate([[0, M - 1, M // 2], rng.integers(0, M, 40)]))
+    prod = T.f8lo_product(hi[rows], lo[rows], B)
+    exact = A[rows].astype(np.float64) @ B.astype(np.float64).T
+    if epi == 3:
+        g, u = prod[:, :N], prod[:, N:]
+        ref = g / (1.0 + np.exp(-g)) * u
+        flat = dev.get(C).reshape(-1).view(np.uint8)
+        if cmode == "f8":
+            hi_o = flat[:2 * M * N].view(np.float16).reshape(M, N)
+            got = T.f16f8_value(hi_o[rows], flat[2 * M * N:3 * M * N].reshape(M, N)[rows])
+            assert rel_err(got, ref) < 2.0 ** -15  # the output form itself carries 2^-16 of each value
+            assert rel_err(hi_o[rows], ref) < 2.0 ** -11
+        elif cmode == "x2":
+            o = flat[:4 * M * N].view(np.float16).reshape(2, M, N).astype(np.float64)
+            got = o[0, rows] + o[1, rows]
+            assert rel_err(got, ref) < 2e-6
+        else:
+            got = flat[:2 * M * N].view(np.float16).reshape(M, N)[rows].astype(np.float64)
+            assert rel_err(got, ref) < 2.0 ** -10
+        ge, ue = exact[:, :N], exact[:, N:]
+        assert rel_err(got, ge / (1.0 + np.exp(-ge)) * ue) < (2.0 ** -10 if cmode == "f16" else 2.0 ** -12)
+    else:
+        out = dev.get(C).astype(np.float64)[rows]
+        if epi == 1:
+            assert rel_err(out, prod) < 2.0 ** -10
+        else:
+            base = C0[rows] if epi == 2 else 0.0
+            assert rel_err(out - base, prod) < 5e-6
+            # ~15-bit inputs: far closer to the fp32-input product than one fp16 rounding (2^-11)
+            assert rel_err(out - base, exact) < 2.0 ** -13
+
+
+@pytest.mark.parametrize("M,N,K,epi", [
+    (512, 4096, 14336, 2),   # 8B down projection of a 512-row chunk
+    (512, 6144, 4096, 0),    # 8B QKV
+    (128, 2048, 8192, 2),    # 1B down projection of a 128-row prompt: 32 chunks
+    (300, 4096, 2048, 1),    # ragged M, fp16 store
+])
+def test_gemm_f8lo_splitk(vsl, dev, H, M, N, K, epi):
+    """Narrow shapes split over K with an F16F8 A: the partials come from the fp8 lo path of the
+    128 x 256 tiles; without the workspace the forced direct-to-LDS tiles give the same result (to
+    fp32 rounding of the accumulation order)."""
+    rng = np.random.default_rng(3 * M + N + K + epi)
+    A = rng.normal(0, 1, (M, K)).astype(np.float32)
+    B = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    dA, hi, val = f8_buffer(dev, A)
+    flags = epi | vsl.GEMM_A_F8
+    need = H.vsl_gemm_f16_ws_bytes(M, N, K, flags)
+    assert need > 0
+    ws = dev.empty((need // 4 + 4,), np.float32)
+    C0 = rng.normal(0, 1, (M, N)).astype(np.float32) if epi == 2 else np.zeros((M, N), np.float32)
+    rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, 40)]))
+    ref = T.f8lo_product(hi[rows], val[rows] - hi[rows].astype(np.float64), B)
+    for with_ws in (True, False):
+        C = dev.empty((M, N), np.float16) if epi == 1 else dev.put(C0)
+        if with_ws:
+            ok(vsl, H.vsl_gemm_f16_ws(dev.p(dA), dev.p(dev.put(B)), M, N, K, dev.p(C), flags, dev.p(ws), need, None))
+        else:
+            ok(vsl, H.vsl_gemm_f16(dev.p(dA), dev.p(dev.put(B)), M, N, K, dev.p(C), flags, None))
+        out = dev.get(C).astype(np.float64)[rows]
+        if epi == 1:
+            assert rel_err(out, ref) < 2.0 ** -10
+        else:
+            assert rel_err(out - (C0[rows] if epi == 2 else 0.0), ref) < 5e-6
+
+
+def test_gemm_f8lo_forms_refused(vsl, dev, H):
+    A = dev.put(np.zeros((3 * 64 * 4096,), np.uint8))
+    B = dev.put(np.zeros((4096, 4096), np.float16))
+    C = dev.put(np.zeros((64, 4096), np.float32))
+    # N a multiple of 128 (what every form needs) but not of the 256-wide tile; N not even that
+    assert H.vsl_gemm_f16(dev.p(A), dev.p(B), 64, 3968, 4096, dev.p(C), vsl.GEMM_A_F8, None) == vsl.VSL_E_UNSUPPORTED
+    assert H.vsl_gemm_f16(dev.p(A), dev.p(B), 64, 4000, 4096, dev.p(C), vsl.GEMM_A_F8, None) == vsl.VSL_E_INVALID
+    # two A forms at once, an F8 output on a non-SwiGLU epilogue
+    assert H.vsl_gemm_f16(dev.p(A), dev.p(B), 64, 4096, 4096, dev.p(C), vsl.GEMM_A_F8 | vsl.GEMM_A_X2,
+                          None) == vsl.VSL_E_INVALID
+    assert H.vsl_gemm_f16(dev.p(A), dev.p(B), 64, 4096, 4096, dev.p(C), vsl.GEMM_C_F8, None) == vsl.VSL_E_INVALID
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 4096, 14336), (300, 2048, 8192)])
+def test_resid_rmsnorm_f8lo(vsl, orc, dev, H, M, N, K):
+    """The down projection's entry with an F16F8 input and an F16F8 normalized output: the fused launch
+    (K split) leaves x exactly as the unfused residual GEMM does, and both it and the unsplit path
+    encode the oracle's RMSNorm of the updated rows."""
+    rng = np.random.default_rng(M + N + K + 5)
+    A = rng.normal(0, 1, (M, K)).astype(np.float32)
+    B = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    x0 = rng.normal(0, 1, (M, N)).astype(np.float32)
+    g = rng.normal(1, 0.1, N).astype(np.float32)
+    dA, hi, val = f8_buffer(dev, A)
+    dB, dg = dev.put(B), dev.put(g)
+    need = H.vsl_gemm_f16_ws_bytes(M, N, K, 2 | vsl.GEMM_A_F8)
+    ws = dev.empty((need // 4 + 4,), np.float32)
+    res = {}
+    for mode in ("fused", "unfused", "unsplit"):
+        x = dev.put(x0)
+        xn = dev.empty((3 * M * N,), np.uint8)
+        if mode == "unfused":
+            ok(vsl, H.vsl_gemm_f16_ws(dev.p(dA), dev.p(dB), M, N, K, dev.p(x), 2 | vsl.GEMM_A_F8, dev.p(ws), need,
+                                      None))
+        else:
+            ok(vsl, H.vsl_gemm_f16_resid_rmsnorm(dev.p(dA), dev.p(dB), M, N, K, vsl.GEMM_A_F8, dev.p(x), dev.p(dg),
+                                                 1e-5, dev.p(xn), vsl.VSL_DT_F16F8,
+                                                 dev.p(ws) if mode == "fused" else None,
+                                                 need if mode == "fused" else 0, None))
+        res[mode] = (dev.get(x).astype(np.float32), f8_read(dev, xn, M, N))
+    assert np.array_equal(res["fused"][0], res["unfused"][0])
+    rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, 24)]))
+    ref = x0[rows].astype(np.float64) + T.f8lo_product(hi[rows], val[rows] - hi[rows].astype(np.float64), B)
+    for mode in ("fused", "unsplit"):
+        x, (hn, vn) = res[mode]
+        assert rel_err(x[rows], ref) < 1e-5
+        nref = np.stack([orc.rmsnorm(x[r], g, 1e-5) for r in rows]).astype(np.float64)
+        assert_f8_encodes(hn[rows], vn[rows], nref)

@@ -81,3 +81,60 @@ class Dev:
 
     def sync(self):
         self.torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------------------------------
+# fp8 e4m3 (OCP) and the VSL_DT_F16F8 activation form, in numpy: the values the GEMM's fp8 lo path is
+# defined to multiply (the lo plane, and B rounded to e4m3 as B * 2^6)
+# ------------------------------------------------------------------------------------------
+def e4m3_table():
+    """Value of every byte code (NaN for 0x7f / 0xff)."""
+    c = np.arange(256)
+    e, m, s = (c >> 3) & 15, c & 7, np.where(c >> 7, -1.0, 1.0)
+    v = np.where(e > 0, np.ldexp(1.0 + m / 8.0, e - 7), np.ldexp(m / 8.0, -6)) * s
+    v[0x7F] = v[0xFF] = np.nan
+    return v
+
+
+def e4m3_encode(x):
+    """Codes of the nearest e4m3 values (ties to the even code, magnitudes above 448 saturate, the sign
+    of a zero result kept)."""
+    x = np.asarray(x, np.float64)
+    pos = e4m3_table()[:127]                  # codes 0..126, increasing
+    a = np.minimum(np.abs(x), 448.0)
+    i = np.clip(np.searchsorted(pos, a), 1, 126)
+    lo, hi = pos[i - 1], pos[i]
+    take_hi = (a - lo > hi - a) | ((a - lo == hi - a) & (i % 2 == 0))
+    code = np.where(take_hi, i, i - 1).astype(np.uint8)
+    return np.where(np.signbit(x), code | 0x80, code).astype(np.uint8)
+
+
+def lo8_perm(K):
+    """Position of column k inside its row of the lo8 plane (bits 3 and 4 of k exchanged)."""
+    k = np.arange(K)
+    return (k & ~24) | ((k & 8) << 1) | ((k & 16) >> 1)
+
+
+def f16f8_split(a):
+    """VSL_DT_F16F8 planes of fp32 rows a [M][K]: (hi fp16 [M][K], lo8 bytes [M][K] in the plane's
+    order, the value hi + lo8 * 2^-12 as float64)."""
+    a = np.asarray(a, np.float32)
+    hi = a.astype(np.float16)
+    lo = (a - hi.astype(np.float32)).astype(np.float64) * 4096.0
+    codes = e4m3_encode(lo)
+    val = hi.astype(np.float64) + e4m3_table()[codes] / 4096.0
+    plane = np.empty_like(codes)
+    plane[:, lo8_perm(a.shape[1])] = codes
+    return hi, plane, val
+
+
+def f16f8_value(hi, plane):
+    """hi + lo8 * 2^-12 of stored planes (plane in its stored order)."""
+    codes = plane[:, lo8_perm(plane.shape[1])]
+    return hi.astype(np.float64) + e4m3_table()[codes] / 4096.0
+
+
+def f8lo_product(hi, lo_val, B):
+    """What a GEMM with an F16F8 A computes: hi B^T + lo B8^T, B8 = e4m3(B * 2^6) / 2^6 (float64)."""
+    B8 = e4m3_table()[e4m3_encode(B.astype(np.float64) * 64.0)] / 64.0
+    return hi.astype(np.float64) @ B.astype(np.float64).T + lo_val @ B8.T

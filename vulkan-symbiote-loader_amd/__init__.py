@@ -21,10 +21,10 @@ HIP_LIB = os.path.join(LIB_DIR, "libvsl_hip.so")
 ENGINE_LIB = os.path.join(LIB_DIR, "libvsl_engine.so")
 
 VSL_OK, VSL_E_INVALID, VSL_E_HIP, VSL_E_OOM, VSL_E_UNSUPPORTED, VSL_E_CAPACITY = 0, -100, -101, -102, -103, -104
-VSL_DT_F32, VSL_DT_F16, VSL_DT_F16X2 = 0, 1, 2
+VSL_DT_F32, VSL_DT_F16, VSL_DT_F16X2, VSL_DT_F16F8 = 0, 1, 2, 3
 VSL_WF_F32, VSL_WF_F16, VSL_WF_Q4_0, VSL_WF_Q4_1, VSL_WF_Q8_0 = 0, 1, 2, 3, 4
 VSL_QL_REFERENCE, VSL_QL_GGML = 0, 1
-GEMM_A_X2, GEMM_C_X2 = 0x100, 0x200
+GEMM_A_X2, GEMM_C_X2, GEMM_A_F8, GEMM_C_F8 = 0x100, 0x200, 0x400, 0x800
 SAMPLE_GREEDY, SAMPLE_REFERENCE, SAMPLE_TOPK_SEEDED = 0, 1, 2
 EPI_STORE_F32, EPI_STORE_F16, EPI_RESID, EPI_SWIGLU = 0, 1, 2, 3
 _MODES = {"greedy": SAMPLE_GREEDY, "reference": SAMPLE_REFERENCE, "topk": SAMPLE_TOPK_SEEDED}
@@ -59,7 +59,7 @@ class EngineOptions(ctypes.Structure):
                 ("batched_prefill", ctypes.c_uint32), ("prefill_split", ctypes.c_uint32),
                 ("dequant_f32", ctypes.c_uint32), ("sparse_attention", ctypes.c_uint32),
                 ("sparse_window", ctypes.c_uint32), ("sparse_global", ctypes.c_uint32),
-                ("sparse_threshold", ctypes.c_uint32)]
+                ("sparse_threshold", ctypes.c_uint32), ("prefill_lo8", ctypes.c_uint32)]
 
 
 class GenParams(ctypes.Structure):
@@ -338,9 +338,10 @@ class Engine:
 
     def __init__(self, gguf_path=None, spec=None, seed=0, device=0, kv_capacity=0, use_graph=True,
                  prefill_chunk=0, attn_splits=0, batched_prefill=True, init_std=0.02, prefill_split=None,
-                 dequant_f32=False, window=None):
+                 dequant_f32=False, window=None, prefill_lo8=None):
         """window: None (dense attention) or (sparse_window, sparse_global, sparse_threshold) for the
-        windowed long-context mode; (512, 16, 8192) are the reference's values."""
+        windowed long-context mode; (512, 16, 8192) are the reference's values. prefill_split /
+        prefill_lo8: None keeps vsl_engine_default_options' stage masks."""
         self._lib = engine_lib()
         opt = EngineOptions()
         self._lib.vsl_engine_default_options(ctypes.byref(opt))
@@ -348,6 +349,8 @@ class Engine:
         opt.prefill_chunk, opt.attn_splits, opt.batched_prefill = prefill_chunk, attn_splits, int(bool(batched_prefill))
         if prefill_split is not None:
             opt.prefill_split = prefill_split
+        if prefill_lo8 is not None:
+            opt.prefill_lo8 = prefill_lo8
         opt.dequant_f32 = int(bool(dequant_f32))
         if window is not None:
             opt.sparse_attention = 1

@@ -1538,7 +1538,8 @@ __global__ void k_embed(const void* table, uint32_t vocab, uint32_t d, const uin
     for (uint32_t i = threadIdx.x; i < d; i += blockDim.x) out[(size_t)t * d + i] = to_f32(e[i]);
 }
 
-template <typename OT, bool X2>
+// OM: output form, 0 plain (OT), 1 VSL_DT_F16X2, 2 VSL_DT_F16F8 (d % 32 == 0).
+template <typename OT, int OM>
 __global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float* x, const float* gamma, uint32_t rows, uint32_t d,
                                                          float eps, OT* out) {
     __shared__ float red[kWaves];
@@ -1553,11 +1554,17 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float* x, const f
     const float inv = 1.0f / sqrtf(tot / (float)d + eps);
     for (uint32_t i = threadIdx.x; i < d; i += kBlock) {
         const float v = xr[i] * inv * (gamma ? gamma[i] : 1.0f);
-        if constexpr (X2) {
+        if constexpr (OM == 1) {
             vsl_half hi, lo;
             split_f16(v, hi, lo);
             out[(size_t)blockIdx.x * d + i] = hi;
             out[(size_t)rows * d + (size_t)blockIdx.x * d + i] = lo;
+        } else if constexpr (OM == 2) {
+            vsl_half hi;
+            uint32_t lo8;
+            split_f16_f8(v, hi, lo8);
+            out[(size_t)blockIdx.x * d + i] = hi;
+            reinterpret_cast<uint8_t*>(out + (size_t)rows * d)[(size_t)blockIdx.x * d + lo8_pos(i)] = (uint8_t)lo8;
         } else {
             store_elem(out + (size_t)blockIdx.x * d + i, v);
         }
@@ -1567,7 +1574,7 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm_rows(const float* x, const f
 // One row per wave, held in registers: NV float4 per lane (d = 256 NV), 16-byte loads of x and the
 // gains, the sum of squares by DPP, 8-byte (fp16 / split) or 16-byte (fp32) stores. No LDS, no
 // barrier: one memory round trip per row.
-template <typename OT, bool X2, int NV>
+template <typename OT, int OM, int NV>
 __global__ __launch_bounds__(kBlock) void k_rmsnorm_wave(const float* __restrict__ x, const float* __restrict__ gamma,
                                                          uint32_t rows, float eps, OT* __restrict__ out) {
     constexpr uint32_t d = 256 * NV;
@@ -1590,7 +1597,7 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm_wave(const float* __restrict
         const size_t o = (size_t)row * d + (j * 64 + lane) * 4;
         const float4 y = make_float4(v[j].x * inv * g[j].x, v[j].y * inv * g[j].y, v[j].z * inv * g[j].z,
                                      v[j].w * inv * g[j].w);
-        if constexpr (X2) {
+        if constexpr (OM == 1) {
             vsl_half h0, h1, h2, h3, l0, l1, l2, l3;
             split_f16(y.x, h0, l0);
             split_f16(y.y, h1, l1);
@@ -1598,6 +1605,14 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm_wave(const float* __restrict
             split_f16(y.w, h3, l3);
             *reinterpret_cast<half4*>(out + o) = half4{h0, h1, h2, h3};
             *reinterpret_cast<half4*>(out + (size_t)rows * d + o) = half4{l0, l1, l2, l3};
+        } else if constexpr (OM == 2) {
+            half4 h;
+            uint32_t lo8;
+            split4_f16_f8(y.x, y.y, y.z, y.w, h, lo8);
+            *reinterpret_cast<half4*>(out + o) = h;
+            const uint32_t c = (j * 64 + lane) * 4;
+            *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(out + (size_t)rows * d) + (size_t)row * d +
+                                         lo8_pos(c)) = lo8;
         } else if constexpr (sizeof(OT) == 2) {
             *reinterpret_cast<half4*>(out + o) = half4{(vsl_half)y.x, (vsl_half)y.y, (vsl_half)y.z, (vsl_half)y.w};
         } else {
@@ -1606,7 +1621,7 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm_wave(const float* __restrict
     }
 }
 
-template <typename OT, bool X2>
+template <typename OT, int X2>
 void launch_rmsnorm(const float* x, const float* gamma, uint32_t rows, uint32_t d, float eps, OT* out, hipStream_t s) {
     const uint32_t wb = (rows + kWaves - 1) / kWaves;
     switch (d) {
@@ -1986,12 +2001,15 @@ extern "C" int vsl_rmsnorm(const float* x, const float* gamma, uint32_t rows, ui
     if (!x || !out || d == 0) return vsl_invalid("vsl_rmsnorm: bad arguments");
     if (rows == 0) return VSL_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (out_dtype == VSL_DT_F16F8 && d % 32) return vsl_invalid("vsl_rmsnorm: F16F8 needs d %% 32 == 0 (d = %u)", d);
     if (out_dtype == VSL_DT_F16)
-        launch_rmsnorm<vsl_half, false>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out), s);
+        launch_rmsnorm<vsl_half, 0>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out), s);
     else if (out_dtype == VSL_DT_F16X2)
-        launch_rmsnorm<vsl_half, true>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out), s);
+        launch_rmsnorm<vsl_half, 1>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out), s);
+    else if (out_dtype == VSL_DT_F16F8)
+        launch_rmsnorm<vsl_half, 2>(x, gamma, rows, d, eps, static_cast<vsl_half*>(out), s);
     else if (out_dtype == VSL_DT_F32)
-        launch_rmsnorm<float, false>(x, gamma, rows, d, eps, static_cast<float*>(out), s);
+        launch_rmsnorm<float, 0>(x, gamma, rows, d, eps, static_cast<float*>(out), s);
     else
         return vsl_unsupported("vsl_rmsnorm: dtype %d", out_dtype);
     HIP_TRY(hipGetLastError());

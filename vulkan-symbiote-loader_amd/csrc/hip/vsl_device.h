@@ -74,6 +74,42 @@ __device__ __forceinline__ void split_f16(float v, vsl_half& hi, vsl_half& lo) {
     lo = (vsl_half)(v - (float)hi);
 }
 
+// hi / lo8 split of an fp32 value (VSL_DT_F16F8): hi = fp16(v) as in split_f16, and the remainder
+// v - hi (exact in fp32) times 2^12 rounded to the nearest fp8 e4m3 value (OCP, largest finite 448;
+// the product is clamped to +-448 first, since the conversion turns larger values into NaN). The
+// value carried is hi + e4m3 * 2^-12: about 15 significant bits, against 11 for hi alone.
+constexpr float kLo8Scale = 4096.f;
+__device__ __forceinline__ uint32_t lo8_code(float lo) {
+    const float s = fminf(fmaxf(lo * kLo8Scale, -448.f), 448.f);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(s, 0.f, 0, false) & 0xFFu;
+}
+// Four values at once, packed little-endian (the first value in the low byte).
+__device__ __forceinline__ uint32_t lo8_code4(float a, float b, float c, float d) {
+    auto cl = [](float v) { return fminf(fmaxf(v * kLo8Scale, -448.f), 448.f); };
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(cl(a), cl(b), 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(cl(c), cl(d), r, true);
+    return (uint32_t)r;
+}
+__device__ __forceinline__ void split_f16_f8(float v, vsl_half& hi, uint32_t& lo8) {
+    hi = (vsl_half)v;
+    asm volatile("" : "+v"(hi));
+    lo8 = lo8_code(v - (float)hi);
+}
+// Four consecutive values: hi as four halfs, the four lo8 codes packed (first value in the low byte).
+__device__ __forceinline__ void split4_f16_f8(float a, float b, float c, float d, half4& h, uint32_t& lo8) {
+    vsl_half h0 = (vsl_half)a, h1 = (vsl_half)b, h2 = (vsl_half)c, h3 = (vsl_half)d;
+    asm volatile("" : "+v"(h0), "+v"(h1), "+v"(h2), "+v"(h3));
+    h = half4{h0, h1, h2, h3};
+    lo8 = lo8_code4(a - (float)h0, b - (float)h1, c - (float)h2, d - (float)h3);
+}
+// Byte position of column k within its row of the lo8 plane: bits 3 and 4 of k exchanged, so that
+// the 16 bytes one lane feeds to v_mfma_scale_f32_32x32x64_f8f6f4 from a 32-column block (columns
+// 16t + 8g + e, t = 0, 1, e = 0..7, for lane group g) are contiguous. Groups of four columns
+// starting at a multiple of 4 stay contiguous and in order.
+__device__ __host__ __forceinline__ constexpr uint32_t lo8_pos(uint32_t k) {
+    return (k & ~24u) | ((k & 8u) << 1) | ((k & 16u) >> 1);
+}
+
 // Unpack a 16-byte vector of weights into fp32 values.
 __device__ __forceinline__ void unpack(const uint4& v, WF16, float* out) {
     const half8 h = __builtin_bit_cast(half8, v);

@@ -26,6 +26,8 @@
 // instead of four).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "vsl_device.h"
 #include "vsl_internal.h"
 
@@ -33,19 +35,27 @@ namespace {
 
 constexpr uint32_t kKAlign = 128;  // K granularity: NBUF * BK for every configuration
 
-// Block tile BM x BN, BK halfs of K per stage, AP planes of A per stage (2: the hi and lo planes of
-// a split A share the stage's B tile), NBUF stage buffers (together at most 128 KB of LDS), WGM x WGN
-// waves of (BM / WGM) x (BN / WGN).
-template <int BM_, int BN_, int BK_, int AP_, int WGM_ = 2, int WGN_ = 2>
+constexpr int kA1 = kGemmA1, kAX2 = kGemmAX2, kAF8 = kGemmAF8;
+constexpr int kC1 = kGemmC1, kCX2 = kGemmCX2, kCF8 = kGemmCF8;
+
+// Block tile BM x BN, BK halfs of K per stage, AP fp16 planes of A per stage (2: the hi and lo planes
+// of a split A share the stage's B tile), L8: an fp8 lo plane of A after the B tile, NBUF stage
+// buffers (together at most 128 KB of LDS), WGM x WGN waves of (BM / WGM) x (BN / WGN).
+template <int BM_, int BN_, int BK_, int AP_, int WGM_ = 2, int WGN_ = 2, bool L8_ = false>
 struct DmaCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, AP = AP_, WGM = WGM_, WGN = WGN_;
+    static constexpr bool L8 = L8_;
     static constexpr int NT = 64 * WGM * WGN;
     static constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 32, FN = WN / 32;
     static constexpr int CPR = BK / 8;            // 16-byte chunks per tile row
+    static constexpr int CPR8 = BK / 16;          // 16-byte chunks per row of the fp8 lo tile
     static constexpr int ACH = BM * BK / 8 / NT;  // 16-byte chunks per thread per stage, per A plane
     static constexpr int BCH = BN * BK / 8 / NT;
+    static constexpr int LCH = L8 ? BM * BK / 16 / NT : 0;  // fp8 lo chunks per thread per stage
     static_assert(ACH * NT == BM * BK / 8 && BCH * NT == BN * BK / 8, "tile chunks do not divide over the threads");
-    static constexpr int STAGE = (AP * BM + BN) * BK;   // halfs per stage buffer
+    static_assert(!L8 || (LCH * NT == BM * BK / 16 && LCH >= 1), "fp8 lo chunks do not divide over the threads");
+    static constexpr int L8OFF = (AP * BM + BN) * BK;          // halfs before the fp8 lo tile
+    static constexpr int STAGE = L8OFF + (L8 ? BM * BK / 2 : 0);  // halfs per stage buffer
     static constexpr int NBUF = STAGE * 2 * 4 <= 128 * 1024 ? 4 : 2;
     static constexpr int KS = BK / 16;                  // MFMA k-steps per stage
     static_assert(STAGE * 2 * NBUF <= 128 * 1024, "stage buffers exceed 128 KB");
@@ -56,24 +66,51 @@ __device__ __forceinline__ int d_row(int v, int lane) { return (v >> 2) * 8 + (l
 // LDS chunk position (16-byte units) of logical chunk c of tile row r. A 256-byte LDS cycle serves
 // 16 lanes of a 16-byte read, i.e. 4 rows of 64 bytes (BK 32) or 2 rows of 128 bytes (BK 64); the
 // chunk index is xor-ed with the row's position among the 16 rows of a fragment read so that those
-// 16 reads fall in distinct bank groups.
+// 16 reads fall in distinct bank groups. The fp8 lo tile has rows of BK bytes: 8 rows of 32 bytes
+// (CPR 2) or 4 rows of 64 bytes (CPR 4) per cycle.
 template <int CPR>
 __device__ __forceinline__ int chunk_pos(int r, int c) {
-    if constexpr (CPR == 4) return r * 4 + (c ^ ((r >> 2) & 3));
+    if constexpr (CPR == 2) return r * 2 + (c ^ ((r >> 3) & 1));
+    else if constexpr (CPR == 4) return r * 4 + (c ^ ((r >> 2) & 3));
     else return r * 8 + (c ^ ((r >> 1) & 7));
+}
+
+typedef int int8v __attribute__((ext_vector_type(8)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+// Two fp16 values to two fp8 e4m3 bytes of v * 2^6 (round to nearest even), into the low or high
+// half of a dword. The weights (about N(0, 0.02)) then sit in e4m3's normal range.
+template <bool HI_WORD>
+__device__ __forceinline__ int w8_pack(int old, vsl_half a, vsl_half b) {
+    typedef short s2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 v = {a, b};
+    s2 o = __builtin_bit_cast(s2, old);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, v, 0.015625f, HI_WORD);
+    return __builtin_bit_cast(int, o);
 }
 
 // SK (split K): the block's work item is (k chunk, tile); it multiplies K / ksplit of K and stores
 // the fp32 partial tile to ws[chunk][M][N]; k_splitk_reduce sums the chunks in order and applies the
 // epilogue (SwiGLU is not split).
-template <class G, int EPI, bool AX2, bool CX2, bool SK>
+//
+// AM == kAF8: each k-step multiplies the hi plane on v_mfma_f32_32x32x16_f16; every 64 columns of K
+// the lo plane is multiplied on v_mfma_scale_f32_32x32x64_f8f6f4 against the same B fragments
+// converted to e4m3 (B * 2^6) in registers, with E8M0 scales 2^-12 and 2^-6, into the same
+// accumulators. Operand slot j of lane group g in that MFMA is column 16 (j / 8) + 8 g + j % 8 of
+// the 64: the B fragment of k-step t supplies slots 8t..8t+7, and the lo plane's byte order
+// (lo8_pos) puts the A slots of a 32-column block in one 16-byte chunk per lane group.
+template <class G, int EPI, int AM, int CM, bool SK>
 __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__ A, const vsl_half* __restrict__ B,
                                                        uint32_t M, uint32_t N, uint32_t K, void* __restrict__ C,
                                                        float* __restrict__ ws, uint32_t ksplit) {
     constexpr int BM = G::BM, BN = G::BN, BK = G::BK, WM = G::WM, WN = G::WN, FM = G::FM, FN = G::FN;
-    constexpr int ACH = G::ACH, BCH = G::BCH, STAGE = G::STAGE, CPR = G::CPR, NBUF = G::NBUF, KS = G::KS;
+    constexpr int ACH = G::ACH, BCH = G::BCH, LCH = G::LCH, STAGE = G::STAGE, CPR = G::CPR, CPR8 = G::CPR8;
+    constexpr int NBUF = G::NBUF, KS = G::KS;
     constexpr int AP = G::AP, NT = G::NT, WGN = G::WGN;
-    static_assert(AP == (AX2 ? 2 : 1), "configuration / plane count mismatch");
+    constexpr bool L8 = AM == kAF8;
+    static_assert(AP == (AM == kAX2 ? 2 : 1) && G::L8 == L8, "configuration / A mode mismatch");
+    static_assert(!L8 || BK == 32 || BK == 64, "the fp8 lo path takes 32 or 64 columns per stage");
     static_assert(EPI != VSL_EPI_SWIGLU || FN % 2 == 0, "SwiGLU waves pair gate and up fragments");
     __shared__ __attribute__((aligned(16))) vsl_half L0[STAGE];
     __shared__ __attribute__((aligned(16))) vsl_half L1[STAGE];
@@ -96,18 +133,21 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
     const uint32_t mt = t % n_m, nt = t / n_m;
     const uint32_t m0 = mt * BM, nout0 = nt * ncols;
     const uint32_t kspan = SK ? K / ksplit : K;  // K range of this block: [kc * kspan, (kc + 1) * kspan)
+    const size_t plane = (size_t)M * K;
+    // the fp8 lo plane follows the hi plane (bytes)
+    const vsl_half* A8 = reinterpret_cast<const vsl_half*>(reinterpret_cast<const uint8_t*>(A + plane) + (size_t)kc * kspan);
     A += (size_t)kc * kspan;
     B += (size_t)kc * kspan;
 
     // per-thread load sources (byte offsets without the stage's k0): load j of a stage covers
-    // chunk positions j*256 + tid; position P holds row P/CPR and the logical chunk whose swizzled
+    // chunk positions j*NT + tid; position P holds row P/CPR and the logical chunk whose swizzled
     // position is P%CPR (the xor is its own inverse).
     // Byte offsets fit in 32 bits: rows * K * 2 < 2^32 is checked by the launcher.
     auto unswz = [](int P, int& r, int& c) {
         r = P / CPR;
         c = chunk_pos<CPR>(r, P % CPR) - r * CPR;
     };
-    uint32_t a_off[ACH], b_off[BCH];
+    uint32_t a_off[ACH], b_off[BCH], l_off[LCH > 0 ? LCH : 1];
 #pragma unroll
     for (int j = 0; j < ACH; ++j) {
         int r, c;
@@ -124,8 +164,16 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
         else br = nout0 + r;
         b_off[j] = (br * K + c * 8) * 2;
     }
+    if constexpr (L8) {
+#pragma unroll
+        for (int j = 0; j < LCH; ++j) {
+            const int P = j * NT + tid, r = P / CPR8;
+            const int c = chunk_pos<CPR8>(r, P % CPR8) - r * CPR8;
+            const uint32_t gr = m0 + r < M ? m0 + r : M - 1;
+            l_off[j] = gr * K + c * 16;
+        }
+    }
     const uint32_t nst = kspan / BK;
-    const size_t plane = (size_t)M * K;
     // stages past the end re-load the last stage into a buffer that is not read again, keeping the
     // number of loads in flight the same at every wait
     auto issue = [&](vsl_half* L, uint32_t st) {
@@ -139,6 +187,11 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
         }
 #pragma unroll
         for (int j = 0; j < BCH; ++j) lds_load16(Bp, b_off[j], L + AP * BM * BK + (j * NT + wave * 64) * 8);
+        if constexpr (L8) {
+            const vsl_half* Lp = reinterpret_cast<const vsl_half*>(reinterpret_cast<const uint8_t*>(A8) + k0);
+#pragma unroll
+            for (int j = 0; j < LCH; ++j) lds_load16(Lp, l_off[j], L + G::L8OFF + (j * NT + wave * 64) * 8);
+        }
     };
 
     float16v acc[FM][FN];
@@ -181,16 +234,59 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
                 for (int j = 0; j < FN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[p][i], f.b[j], acc[i][j], 0, 0, 0);
     };
-    constexpr int kPerStage = AP * ACH + BCH;  // loads per thread per stage
+    // fp8 lo path: the A operand of the 64-column block (two 16-byte chunks per fragment) and the
+    // e4m3 copies of the B fragments of its four k-steps
+    int4v la[FM][2];
+    int8v w8[FN];
+    // the lo chunk of 32-column block q of this stage (lane group g = lane >> 5) into half h
+    auto lload = [&](const vsl_half* L, int q, int h) {
+        const uint8_t* L8p = reinterpret_cast<const uint8_t*>(L + G::L8OFF);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+            la[i][h] = *reinterpret_cast<const int4v*>(
+                L8p + chunk_pos<CPR8>(wm * WM + i * 32 + (lane & 31), 2 * q + (lane >> 5)) * 16);
+    };
+    // B fragments of k-step t (0..3 within the 64-column block) -> slots 8t..8t+7
+    auto wconv = [&](const Frags& f, int t) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            int d0 = w8[j][2 * t], d1 = w8[j][2 * t + 1];
+            d0 = w8_pack<false>(d0, f.b[j][0], f.b[j][1]);
+            d0 = w8_pack<true>(d0, f.b[j][2], f.b[j][3]);
+            d1 = w8_pack<false>(d1, f.b[j][4], f.b[j][5]);
+            d1 = w8_pack<true>(d1, f.b[j][6], f.b[j][7]);
+            w8[j][2 * t] = d0;
+            w8[j][2 * t + 1] = d1;
+        }
+    };
+    auto mfmas8 = [&]() {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int8v a8 = {la[i][0][0], la[i][0][1], la[i][0][2], la[i][0][3],
+                              la[i][1][0], la[i][1][1], la[i][1][2], la[i][1][3]};
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, w8[j], acc[i][j], 0, 0, 0, 127 - 12, 0,
+                                                                            127 - 6);
+        }
+    };
+    constexpr int kPerStage = AP * ACH + BCH + LCH;  // loads per thread per stage
     // Stage s in buffer Lc, k-steps 0..KS-1 alternating between the fragment sets f0 / f1; k-step
     // 0 was requested during the previous stage. Each k-step requests the next one's fragments and
     // then issues its MFMAs (the reads land meanwhile). Before the last k-step's MFMAs: wait for this
     // wave's reads (Lc is fully read) and for its loads of stage s+1, meet at the barrier (every
     // wave has read Lc, every load of stage s+1 is in LDS), request stage s+NBUF into Lc, and
     // request stage s+1's first k-step from Ln. The stage count is a multiple of NBUF
-    // (K % (NBUF * BK) == 0), so no step is ever skipped.
+    // (K % (NBUF * BK) == 0), so no step is ever skipped. PAR is the stage's parity: with BK = 32 an
+    // fp8 lo block spans an even stage and the odd stage after it.
     Frags f0, f1;
-    auto step = [&](vsl_half* Lc, const vsl_half* Ln, uint32_t s) {
+    auto step = [&](vsl_half* Lc, const vsl_half* Ln, uint32_t s, auto par) {
+        constexpr int PAR = decltype(par)::value;
+        if constexpr (L8) {
+            // lo chunks of this stage: before the barrier that lets Lc be overwritten
+#pragma unroll
+            for (int q = 0; q < BK / 32; ++q) lload(Lc, q, BK == 64 ? q : PAR);
+        }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             Frags& cur = (ks & 1) ? f1 : f0;
@@ -206,9 +302,16 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
             }
             __builtin_amdgcn_sched_barrier(0);
             mfmas(cur);
+            if constexpr (L8) {
+                const int t = BK == 64 ? ks : PAR * 2 + ks;  // k-step within the 64-column block
+                wconv(cur, t);
+                if (t == 3) mfmas8();
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
     issue(L0, 0);
     issue(L1, 1);
     if constexpr (NBUF == 4) {
@@ -220,15 +323,15 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
     fload(f0, L0, 0);
     if constexpr (NBUF == 4) {
         for (uint32_t s = 0; s < nst; s += 4) {
-            step(L0, L1, s);
-            step(L1, L2, s + 1);
-            step(L2, L3, s + 2);
-            step(L3, L0, s + 3);
+            step(L0, L1, s, P0{});
+            step(L1, L2, s + 1, P1{});
+            step(L2, L3, s + 2, P0{});
+            step(L3, L0, s + 3, P1{});
         }
     } else {
         for (uint32_t s = 0; s < nst; s += 2) {
-            step(L0, L1, s);
-            step(L1, L0, s + 1);
+            step(L0, L1, s, P0{});
+            step(L1, L0, s + 1, P1{});
         }
     }
     VSL_VMCNT_WAIT(0);  // the trailing loads land before the block's LDS is released
@@ -259,11 +362,17 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
                 for (int j = 0; j < FN / 2; ++j) {
                     const uint32_t col = nout0 + wn * (WN / 2) + j * 32 + (lane & 31);
                     const float h = silu(rd(acc[i][j], v)) * rd(acc[i][j + FN / 2], v);
-                    if constexpr (CX2) {
+                    if constexpr (CM == kCX2) {
                         vsl_half hi, lo;
                         split_f16(h, hi, lo);
                         Ch[(size_t)row * N + col] = hi;
                         Ch[(size_t)M * N + (size_t)row * N + col] = lo;
+                    } else if constexpr (CM == kCF8) {
+                        vsl_half hi;
+                        uint32_t lo8;
+                        split_f16_f8(h, hi, lo8);
+                        Ch[(size_t)row * N + col] = hi;
+                        reinterpret_cast<uint8_t*>(Ch + (size_t)M * N)[(size_t)row * N + lo8_pos(col)] = (uint8_t)lo8;
                     } else {
                         Ch[(size_t)row * N + col] = (vsl_half)h;
                     }
@@ -304,14 +413,16 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 }
 
 template <int BM, int BN, int TWGM = 2, int TWGN = 2, int TBK = 32>
-struct DmaPair {  // the one-plane and the split-A configuration of a block tile
+struct DmaPair {  // the one-plane, the split-A and the fp8-lo configuration of a block tile
     using One = DmaCfg<BM, BN, 32, 1>;
     using Two = DmaCfg<BM, BN, TBK, 2, TWGM, TWGN>;
+    using F8 = DmaCfg<BM, BN, TBK, 1, TWGM, TWGN, true>;
 };
 // The split-A tiles run eight waves (two per SIMD, 128 accumulators each): 4 x 2 waves of 64 x 128 for
 // 256 x 256, 2 x 4 waves of 64 x 64 for 128 x 256 (the one-plane tiles keep 2 x 2 waves of 128 x 128).
 // The split 128 x 256 tile takes BK = 64 (two 64 KB stages, half the barriers): the K-split partials
-// of a 512-row chunk, O 37.8 -> 36.6 us, down 109.9 -> 104.5 us, QKV level.
+// of a 512-row chunk, O 37.8 -> 36.6 us, down 109.9 -> 104.5 us, QKV level. The fp8-lo tiles use the
+// split-A wave layouts (a 40 KB stage for 256 x 256, 56 KB for 128 x 256).
 using DmaBig = DmaPair<256, 256, 4, 2>;
 using DmaMid = DmaPair<128, 256, 2, 4, 64>;
 
@@ -321,42 +432,58 @@ uint32_t dma_tiles(uint32_t M, uint32_t N) {
     return N % ncols ? 0u : ((M + G::BM - 1) / G::BM) * (N / ncols);
 }
 
+template <class G, int EPI, int AM>
+void launch_cm(uint32_t blocks, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N,
+               uint32_t K, void* C, int cm) {
+    if constexpr (EPI == VSL_EPI_SWIGLU) {
+        if (cm == kCX2) {
+            k_gemm_dma<G, EPI, AM, kCX2, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+            return;
+        }
+        if (cm == kCF8) {
+            k_gemm_dma<G, EPI, AM, kCF8, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+            return;
+        }
+    }
+    k_gemm_dma<G, EPI, AM, kC1, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+}
+
 template <class P, int EPI>
 void launch_cfg(uint32_t tiles, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N,
-                uint32_t K, void* C, bool ax2, bool cx2) {
+                uint32_t K, void* C, int am, int cm) {
     const uint32_t blocks = ((tiles + 7) / 8) * 8;  // whole XCD ranges
-    using One = typename P::One;
-    using Two = typename P::Two;
-    if (ax2 && cx2) k_gemm_dma<Two, EPI, true, true, false><<<blocks, Two::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
-    else if (ax2) k_gemm_dma<Two, EPI, true, false, false><<<blocks, Two::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
-    else if (cx2) k_gemm_dma<One, EPI, false, true, false><<<blocks, One::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
-    else k_gemm_dma<One, EPI, false, false, false><<<blocks, One::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+    if (am == kAX2) launch_cm<typename P::Two, EPI, kAX2>(blocks, s, a, b, M, N, K, C, cm);
+    else if (am == kAF8) launch_cm<typename P::F8, EPI, kAF8>(blocks, s, a, b, M, N, K, C, cm);
+    else launch_cm<typename P::One, EPI, kA1>(blocks, s, a, b, M, N, K, C, cm);
 }
 
 // split-K GEMM (partials, the epilogue's type only selects the reduce kernel)
 template <class P>
 void launch_splitk(uint32_t items, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N,
-                   uint32_t K, float* ws, uint32_t ksplit, bool ax2) {
+                   uint32_t K, float* ws, uint32_t ksplit, int am) {
     const uint32_t blocks = ((items + 7) / 8) * 8;
-    if (ax2)
-        k_gemm_dma<typename P::Two, VSL_EPI_STORE_F32, true, false, true><<<blocks, P::Two::NT, 0, s>>>(
+    if (am == kAX2)
+        k_gemm_dma<typename P::Two, VSL_EPI_STORE_F32, kAX2, kC1, true><<<blocks, P::Two::NT, 0, s>>>(
+            a, b, M, N, K, nullptr, ws, ksplit);
+    else if (am == kAF8)
+        k_gemm_dma<typename P::F8, VSL_EPI_STORE_F32, kAF8, kC1, true><<<blocks, P::F8::NT, 0, s>>>(
             a, b, M, N, K, nullptr, ws, ksplit);
     else
-        k_gemm_dma<typename P::One, VSL_EPI_STORE_F32, false, false, true><<<blocks, P::One::NT, 0, s>>>(
+        k_gemm_dma<typename P::One, VSL_EPI_STORE_F32, kA1, kC1, true><<<blocks, P::One::NT, 0, s>>>(
             a, b, M, N, K, nullptr, ws, ksplit);
 }
 
 template <int EPI>
 int launch_epi(int cfg, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N, uint32_t K,
-               void* C, bool ax2, bool cx2) {
+               void* C, int am, int cm) {
     if (cfg == 0) {
         const uint32_t t = dma_tiles<DmaBig::One, EPI>(M, N);
         if (!t) return -1;
-        launch_cfg<DmaBig, EPI>(t, s, a, b, M, N, K, C, ax2, cx2);
+        launch_cfg<DmaBig, EPI>(t, s, a, b, M, N, K, C, am, cm);
     } else {
         const uint32_t t = dma_tiles<DmaMid::One, EPI>(M, N);
         if (!t) return -1;
-        launch_cfg<DmaMid, EPI>(t, s, a, b, M, N, K, C, ax2, cx2);
+        launch_cfg<DmaMid, EPI>(t, s, a, b, M, N, K, C, am, cm);
     }
     return 0;
 }
@@ -401,16 +528,16 @@ uint32_t vsl_gemm_splitk_plan(uint32_t M, uint32_t N, uint32_t K, int epi, uint3
 }
 
 void vsl_gemm_splitk_partials(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
-                              uint32_t K, bool ax2, float* ws) {
+                              uint32_t K, int am, float* ws) {
     const uint32_t tiles = dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
     launch_splitk<DmaMid>(tiles * ksplit, static_cast<hipStream_t>(stream), static_cast<const vsl_half*>(A),
-                          static_cast<const vsl_half*>(B), M, N, K, ws, ksplit, ax2);
+                          static_cast<const vsl_half*>(B), M, N, K, ws, ksplit, am);
 }
 
 int vsl_gemm_splitk_launch(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
-                           uint32_t K, void* C, int epi, bool ax2, float* ws) {
+                           uint32_t K, void* C, int epi, int am, float* ws) {
     hipStream_t s = static_cast<hipStream_t>(stream);
-    vsl_gemm_splitk_partials(ksplit, stream, A, B, M, N, K, ax2, ws);
+    vsl_gemm_splitk_partials(ksplit, stream, A, B, M, N, K, am, ws);
     const uint64_t MN = (uint64_t)M * N;
     const uint32_t rblocks = (uint32_t)((MN / 4 + 255) / 256);
     switch (epi) {
@@ -424,7 +551,7 @@ int vsl_gemm_splitk_launch(uint32_t ksplit, void* stream, const void* A, const v
 
 // Launches the direct-to-LDS GEMM; returns 0, or -1 when the shape does not fit `cfg`.
 int vsl_gemm_dma_launch(int cfg, void* stream, const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K,
-                        void* C, int epi, bool ax2, bool cx2) {
+                        void* C, int epi, int am, int cm) {
     if (K % kKAlign || K == 0) return -1;
     const uint64_t brows = epi == VSL_EPI_SWIGLU ? 2ull * N : N;
     if (((uint64_t)M * K * 2) >> 32 || (brows * K * 2) >> 32) return -1;  // 32-bit byte offsets
@@ -432,10 +559,10 @@ int vsl_gemm_dma_launch(int cfg, void* stream, const void* A, const void* B, uin
     const vsl_half* a = static_cast<const vsl_half*>(A);
     const vsl_half* b = static_cast<const vsl_half*>(B);
     switch (epi) {
-        case VSL_EPI_STORE_F32: return launch_epi<VSL_EPI_STORE_F32>(cfg, s, a, b, M, N, K, C, ax2, false);
-        case VSL_EPI_STORE_F16: return launch_epi<VSL_EPI_STORE_F16>(cfg, s, a, b, M, N, K, C, ax2, false);
-        case VSL_EPI_RESID: return launch_epi<VSL_EPI_RESID>(cfg, s, a, b, M, N, K, C, ax2, false);
-        case VSL_EPI_SWIGLU: return launch_epi<VSL_EPI_SWIGLU>(cfg, s, a, b, M, N, K, C, ax2, cx2);
+        case VSL_EPI_STORE_F32: return launch_epi<VSL_EPI_STORE_F32>(cfg, s, a, b, M, N, K, C, am, kC1);
+        case VSL_EPI_STORE_F16: return launch_epi<VSL_EPI_STORE_F16>(cfg, s, a, b, M, N, K, C, am, kC1);
+        case VSL_EPI_RESID: return launch_epi<VSL_EPI_RESID>(cfg, s, a, b, M, N, K, C, am, kC1);
+        case VSL_EPI_SWIGLU: return launch_epi<VSL_EPI_SWIGLU>(cfg, s, a, b, M, N, K, C, am, cm);
         default: return -1;
     }
 }

@@ -35,14 +35,18 @@ static inline int vsl_capacity(const char* fmt, A... a) {
 }
 
 // Direct-to-LDS prefill GEMM (vsl_gemm_dma.hip). cfg 0: 256 x 256 tiles, cfg 1: 128 x 256.
+// A operand forms: one fp16 plane, VSL_DT_F16X2 (hi/lo fp16 planes), VSL_DT_F16F8 (fp16 hi plane and
+// fp8 lo plane); SwiGLU output forms: fp16, VSL_DT_F16X2, VSL_DT_F16F8.
+enum { kGemmA1 = 0, kGemmAX2 = 1, kGemmAF8 = 2 };
+enum { kGemmC1 = 0, kGemmCX2 = 1, kGemmCF8 = 2 };
 uint32_t vsl_gemm_dma_tiles(int cfg, uint32_t M, uint32_t N, uint32_t K, int epi);
 int vsl_gemm_dma_launch(int cfg, void* stream, const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K,
-                        void* C, int epi, bool ax2, bool cx2);
+                        void* C, int epi, int am, int cm);
 // Split-K plan of the direct-to-LDS GEMM (k chunks of the 128 x 256 tiling, fp32 partials in a
 // workspace, an ordered reduction applying the epilogue): returns the split (0: none).
 uint32_t vsl_gemm_splitk_plan(uint32_t M, uint32_t N, uint32_t K, int epi, uint32_t min_items, uint64_t* ws_bytes);
 // The k-chunk partials alone, ws[chunk][M][N] fp32, for a caller that sums them itself.
 void vsl_gemm_splitk_partials(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
-                              uint32_t K, bool ax2, float* ws);
+                              uint32_t K, int am, float* ws);
 int vsl_gemm_splitk_launch(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
-                           uint32_t K, void* C, int epi, bool ax2, float* ws);
+                           uint32_t K, void* C, int epi, int am, float* ws);

@@ -359,11 +359,11 @@ __global__ __launch_bounds__(256) void k_rope_split4(const float* __restrict__ w
 
 // Residual projection given as KS fp32 k-chunk partials ws[KS][rows][d]: x += their sum (chunks in
 // order, then added to x), followed by the next RMSNorm of the updated rows, out = x / sqrt(mean(x^2)
-// + eps) * gamma (fp16, split or fp32). One 256-thread block per row, NV float4 per thread
+// + eps) * gamma (OM: 0 fp16 or fp32 as OT, 1 VSL_DT_F16X2, 2 VSL_DT_F16F8). One 256-thread block per row, NV float4 per thread
 // (d = 1024 NV): every partial, x and gamma requested before the first is used, x written once, the
 // row's sum of squares by DPP within each wave and four floats of LDS across the waves. KS = 0: the
 // partial count is ks_rt, summed in the same order by a loop (many partials: no register copy of each).
-template <typename OT, bool X2, int NV, int KS>
+template <typename OT, int OM, int NV, int KS>
 __global__ __launch_bounds__(256) void k_splitk_resid_rmsnorm(const float* __restrict__ ws, uint32_t rows,
                                                               float* __restrict__ x, const float* __restrict__ gamma,
                                                               float eps, OT* __restrict__ out, uint32_t ks_rt) {
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(256) void k_splitk_resid_rmsnorm(const float* __res
         const size_t o = base + (j * 256 + t) * 4;
         const float4v y = float4v{v[j][0] * inv * g[j][0], v[j][1] * inv * g[j][1], v[j][2] * inv * g[j][2],
                                   v[j][3] * inv * g[j][3]};
-        if constexpr (X2) {
+        if constexpr (OM == 1) {
             vsl_half h0, h1, h2, h3, l0, l1, l2, l3;
             split_f16(y[0], h0, l0);
             split_f16(y[1], h1, l1);
@@ -413,6 +413,12 @@ __global__ __launch_bounds__(256) void k_splitk_resid_rmsnorm(const float* __res
             split_f16(y[3], h3, l3);
             *reinterpret_cast<half4*>(out + o) = half4{h0, h1, h2, h3};
             *reinterpret_cast<half4*>(out + MN + o) = half4{l0, l1, l2, l3};
+        } else if constexpr (OM == 2) {
+            half4 h;
+            uint32_t lo8;
+            split4_f16_f8(y[0], y[1], y[2], y[3], h, lo8);
+            *reinterpret_cast<half4*>(out + o) = h;
+            *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(out + MN) + base + lo8_pos((j * 256 + t) * 4)) = lo8;
         } else if constexpr (sizeof(OT) == 2) {
             *reinterpret_cast<half4*>(out + o) = half4{(vsl_half)y[0], (vsl_half)y[1], (vsl_half)y[2], (vsl_half)y[3]};
         } else {
@@ -717,6 +723,11 @@ static uint32_t gemm_tiles(uint32_t M, uint32_t N) {
 
 constexpr uint32_t kDmaMinTiles = 192;
 
+// A operand form of a GEMM's flags (the caller has rejected A_X2 | A_F8 together)
+static int gemm_a_mode(int flags) {
+    return (flags & VSL_GEMM_A_X2) ? kGemmAX2 : (flags & VSL_GEMM_A_F8) ? kGemmAF8 : kGemmA1;
+}
+
 // The K split launch_gemm takes for a shape and workspace (0: unsplit kernels).
 static uint32_t splitk_choice(uint32_t M, uint32_t N, uint32_t K, int epi, const float* ws, uint64_t ws_bytes) {
     for (int cfg = 0; cfg < 2; ++cfg)
@@ -732,21 +743,31 @@ static bool aligned_to(const void* p, uintptr_t a) { return (reinterpret_cast<ui
 // Tile configuration by occupancy: the largest tiles that still give every CU a tile.
 template <int EPI>
 static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N, uint32_t K,
-                       void* C, bool ax2, bool cx2, float* ws, uint64_t ws_bytes) {
+                       void* C, int am, int cm, float* ws, uint64_t ws_bytes) {
     auto blocks = [](uint32_t tiles) { return ((tiles + 7) / 8) * 8; };  // whole XCD ranges (tile_of)
     // shapes whose 256 x 256 (else 128 x 256) tiles cover at least three quarters of the CUs take
     // the direct-to-LDS kernel
     for (int cfg = 0; cfg < 2; ++cfg)
         if (vsl_gemm_dma_tiles(cfg, M, N, K, EPI) >= kDmaMinTiles)
-            return vsl_gemm_dma_launch(cfg, s, a, b, M, N, K, C, EPI, ax2, cx2) == 0
+            return vsl_gemm_dma_launch(cfg, s, a, b, M, N, K, C, EPI, am, cm) == 0
                        ? VSL_OK
                        : vsl_invalid("vsl_gemm_f16: shape %ux%ux%u does not fit the direct-to-LDS tiles", M, N, K);
     // otherwise, with a workspace, split K over enough blocks
     if (const uint32_t ks = splitk_choice(M, N, K, EPI, ws, ws_bytes)) {
-        if (vsl_gemm_splitk_launch(ks, s, a, b, M, N, K, C, EPI, ax2, ws))
+        if (vsl_gemm_splitk_launch(ks, s, a, b, M, N, K, C, EPI, am, ws))
             return vsl_invalid("vsl_gemm_f16: split-K epilogue %d", EPI);
         return VSL_OK;
     }
+    // the fp8 lo forms exist in the direct-to-LDS kernel only: take its tiles even when they leave
+    // CUs idle
+    if (am == kGemmAF8 || cm == kGemmCF8) {
+        for (int cfg = 1; cfg >= 0; --cfg)
+            if (vsl_gemm_dma_tiles(cfg, M, N, K, EPI) && vsl_gemm_dma_launch(cfg, s, a, b, M, N, K, C, EPI, am, cm) == 0)
+                return VSL_OK;
+        return vsl_unsupported("vsl_gemm_f16: F16F8 operands need N %% 256 == 0 (128 for SwiGLU) and K %% 128 == 0 "
+                               "(shape %ux%ux%u)", M, N, K);
+    }
+    const bool ax2 = am == kGemmAX2, cx2 = cm == kGemmCX2;
     const uint32_t tb = gemm_tiles<GemmBig, EPI>(M, N), tm = gemm_tiles<GemmMid, EPI>(M, N);
     const uint32_t ts = gemm_tiles<GemmSmall, EPI>(M, N);
     if (tb >= 256) launch_gemm_cfg<GemmBig, EPI>(blocks(tb), s, a, b, M, N, K, C, ax2, cx2);
@@ -760,10 +781,14 @@ static int gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32
                     float* ws, uint64_t ws_bytes, void* stream) {
     if (!A || !B || !C) return vsl_invalid("vsl_gemm_f16: null pointer");
     if (M == 0) return VSL_OK;
-    const bool ax2 = (epilogue & VSL_GEMM_A_X2) != 0, cx2 = (epilogue & VSL_GEMM_C_X2) != 0;
     const int epi = epilogue & 0xFF;
-    if (epilogue & ~(0xFF | VSL_GEMM_A_X2 | VSL_GEMM_C_X2)) return vsl_invalid("vsl_gemm_f16: flags 0x%x", epilogue);
-    if (cx2 && epi != VSL_EPI_SWIGLU) return vsl_invalid("vsl_gemm_f16: VSL_GEMM_C_X2 needs VSL_EPI_SWIGLU");
+    if ((epilogue & ~(0xFF | VSL_GEMM_A_X2 | VSL_GEMM_C_X2 | VSL_GEMM_A_F8 | VSL_GEMM_C_F8)) ||
+        (epilogue & (VSL_GEMM_A_X2 | VSL_GEMM_A_F8)) == (VSL_GEMM_A_X2 | VSL_GEMM_A_F8) ||
+        (epilogue & (VSL_GEMM_C_X2 | VSL_GEMM_C_F8)) == (VSL_GEMM_C_X2 | VSL_GEMM_C_F8))
+        return vsl_invalid("vsl_gemm_f16: flags 0x%x", epilogue);
+    const int am = gemm_a_mode(epilogue);
+    const int cm = (epilogue & VSL_GEMM_C_X2) ? kGemmCX2 : (epilogue & VSL_GEMM_C_F8) ? kGemmCF8 : kGemmC1;
+    if (cm != kGemmC1 && epi != VSL_EPI_SWIGLU) return vsl_invalid("vsl_gemm_f16: C_X2 / C_F8 need VSL_EPI_SWIGLU");
     if (K % 32) return vsl_invalid("vsl_gemm_f16: K=%u must be a multiple of 32", K);
     const uint32_t ncols = epi == VSL_EPI_SWIGLU ? 64 : 128;
     if (N % ncols) return vsl_invalid("vsl_gemm_f16: N=%u must be a multiple of %u", N, ncols);
@@ -772,10 +797,10 @@ static int gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32
     const vsl_half* b = static_cast<const vsl_half*>(B);
     int rc;
     switch (epi) {
-        case VSL_EPI_STORE_F32: rc = launch_gemm<VSL_EPI_STORE_F32>(s, a, b, M, N, K, C, ax2, false, ws, ws_bytes); break;
-        case VSL_EPI_STORE_F16: rc = launch_gemm<VSL_EPI_STORE_F16>(s, a, b, M, N, K, C, ax2, false, ws, ws_bytes); break;
-        case VSL_EPI_RESID: rc = launch_gemm<VSL_EPI_RESID>(s, a, b, M, N, K, C, ax2, false, ws, ws_bytes); break;
-        case VSL_EPI_SWIGLU: rc = launch_gemm<VSL_EPI_SWIGLU>(s, a, b, M, N, K, C, ax2, cx2, ws, ws_bytes); break;
+        case VSL_EPI_STORE_F32: rc = launch_gemm<VSL_EPI_STORE_F32>(s, a, b, M, N, K, C, am, kGemmC1, ws, ws_bytes); break;
+        case VSL_EPI_STORE_F16: rc = launch_gemm<VSL_EPI_STORE_F16>(s, a, b, M, N, K, C, am, kGemmC1, ws, ws_bytes); break;
+        case VSL_EPI_RESID: rc = launch_gemm<VSL_EPI_RESID>(s, a, b, M, N, K, C, am, kGemmC1, ws, ws_bytes); break;
+        case VSL_EPI_SWIGLU: rc = launch_gemm<VSL_EPI_SWIGLU>(s, a, b, M, N, K, C, am, cm, ws, ws_bytes); break;
         default: return vsl_invalid("vsl_gemm_f16: epilogue %d", epi);
     }
     if (rc) return rc;
@@ -878,7 +903,8 @@ extern "C" int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uin
                                             void* workspace, uint64_t ws_bytes, void* stream) {
     const char* fn = "vsl_gemm_f16_qkv_rope_append";
     if (!A || !Wqkv) return vsl_invalid("%s: null pointer", fn);
-    if (a_flags & ~VSL_GEMM_A_X2) return vsl_invalid("%s: flags 0x%x", fn, a_flags);
+    if ((a_flags & ~(VSL_GEMM_A_X2 | VSL_GEMM_A_F8)) || a_flags == (VSL_GEMM_A_X2 | VSL_GEMM_A_F8))
+        return vsl_invalid("%s: flags 0x%x", fn, a_flags);
     if (const int rc = check_rope_split(fn, qkv, S, hd, pos0, rope_cos, rope_sin, q_out, q_dtype, kcache, vcache,
                                         kv_dtype, cap))
         return rc;
@@ -891,7 +917,7 @@ extern "C" int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uin
     if (ks && rope_split4_fits(ws, hd, rope_cos, rope_sin, q_out, kcache, vcache, kv32)) {
         hipStream_t s = static_cast<hipStream_t>(stream);
         vsl_half* qo = static_cast<vsl_half*>(q_out);
-        vsl_gemm_splitk_partials(ks, stream, A, Wqkv, S, N, K, (a_flags & VSL_GEMM_A_X2) != 0, ws);
+        vsl_gemm_splitk_partials(ks, stream, A, Wqkv, S, N, K, gemm_a_mode(a_flags), ws);
         switch (ks) {
             case 2: launch_rope_split4<2>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
             case 4: launch_rope_split4<4>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
@@ -907,7 +933,7 @@ extern "C" int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uin
                                  kv_dtype, cap, stream);
 }
 
-template <typename OT, bool X2, int NV>
+template <typename OT, int X2, int NV>
 static void launch_resid_rmsnorm_nv(hipStream_t s, uint32_t ks, const float* ws, uint32_t rows, float* x,
                                     const float* gamma, float eps, OT* out) {
     switch (ks) {
@@ -918,7 +944,7 @@ static void launch_resid_rmsnorm_nv(hipStream_t s, uint32_t ks, const float* ws,
     }
 }
 
-template <typename OT, bool X2>
+template <typename OT, int X2>
 static void launch_resid_rmsnorm(hipStream_t s, uint32_t ks, const float* ws, uint32_t rows, uint32_t d, float* x,
                                  const float* gamma, float eps, OT* out) {
     switch (d / 1024) {
@@ -934,9 +960,11 @@ extern "C" int vsl_gemm_f16_resid_rmsnorm(const void* A, const void* B, uint32_t
                                           int xn_dtype, void* workspace, uint64_t ws_bytes, void* stream) {
     const char* fn = "vsl_gemm_f16_resid_rmsnorm";
     if (!A || !B || !x || !xn || N == 0) return vsl_invalid("%s: bad arguments", fn);
-    if (a_flags & ~VSL_GEMM_A_X2) return vsl_invalid("%s: flags 0x%x", fn, a_flags);
-    if (xn_dtype != VSL_DT_F16 && xn_dtype != VSL_DT_F16X2 && xn_dtype != VSL_DT_F32)
+    if ((a_flags & ~(VSL_GEMM_A_X2 | VSL_GEMM_A_F8)) || a_flags == (VSL_GEMM_A_X2 | VSL_GEMM_A_F8))
+        return vsl_invalid("%s: flags 0x%x", fn, a_flags);
+    if (xn_dtype != VSL_DT_F16 && xn_dtype != VSL_DT_F16X2 && xn_dtype != VSL_DT_F16F8 && xn_dtype != VSL_DT_F32)
         return vsl_unsupported("%s: dtype %d", fn, xn_dtype);
+    if (xn_dtype == VSL_DT_F16F8 && N % 32) return vsl_invalid("%s: F16F8 needs N %% 32 == 0 (N = %u)", fn, N);
     if (workspace && !aligned_to(workspace, 16)) return vsl_invalid("%s: workspace must be 16-byte aligned", fn);
     if (M == 0) return VSL_OK;
     float* ws = static_cast<float*>(workspace);
@@ -951,13 +979,15 @@ extern "C" int vsl_gemm_f16_resid_rmsnorm(const void* A, const void* B, uint32_t
         return vsl_rmsnorm(x, gamma, M, N, eps, xn, xn_dtype, stream);
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
-    vsl_gemm_splitk_partials(ks, stream, A, B, M, N, K, (a_flags & VSL_GEMM_A_X2) != 0, ws);
+    vsl_gemm_splitk_partials(ks, stream, A, B, M, N, K, gemm_a_mode(a_flags), ws);
     if (xn_dtype == VSL_DT_F16)
-        launch_resid_rmsnorm<vsl_half, false>(s, ks, ws, M, N, x, gamma, eps, static_cast<vsl_half*>(xn));
+        launch_resid_rmsnorm<vsl_half, 0>(s, ks, ws, M, N, x, gamma, eps, static_cast<vsl_half*>(xn));
     else if (xn_dtype == VSL_DT_F16X2)
-        launch_resid_rmsnorm<vsl_half, true>(s, ks, ws, M, N, x, gamma, eps, static_cast<vsl_half*>(xn));
+        launch_resid_rmsnorm<vsl_half, 1>(s, ks, ws, M, N, x, gamma, eps, static_cast<vsl_half*>(xn));
+    else if (xn_dtype == VSL_DT_F16F8)
+        launch_resid_rmsnorm<vsl_half, 2>(s, ks, ws, M, N, x, gamma, eps, static_cast<vsl_half*>(xn));
     else
-        launch_resid_rmsnorm<float, false>(s, ks, ws, M, N, x, gamma, eps, static_cast<float*>(xn));
+        launch_resid_rmsnorm<float, 0>(s, ks, ws, M, N, x, gamma, eps, static_cast<float*>(xn));
     HIP_TRY(hipGetLastError());
     return VSL_OK;
 }

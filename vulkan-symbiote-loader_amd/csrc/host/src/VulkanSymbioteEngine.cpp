@@ -633,6 +633,17 @@ void VulkanSymbioteEngine::prefill_tokenwise(uint32_t n_prompt, const SamplingPa
           "vsl_lm_head_sample");
 }
 
+uint32_t VulkanSymbioteEngine::prefill_lo8_stages() const {
+    // VSL_GEMM_A_F8 / VSL_GEMM_C_F8 need N % 256 == 0 (128 for SwiGLU) and K % 128 == 0
+    const ModelConfig& c = config_;
+    const uint32_t d = c.hidden_size, F = c.intermediate_size;
+    const uint32_t wqkv = (c.num_attention_heads + 2 * c.num_key_value_heads) * c.head_dim;
+    uint32_t ok = 0;
+    if (d % 256 == 0 && wqkv % 256 == 0) ok |= 1u;    // QKV input: [Wq; Wk; Wv] against d
+    if (d % 256 == 0 && F % 256 == 0) ok |= 8u | 16u;  // gate/up (F outputs, K = d), down (d outputs, K = F)
+    return options_.prefill_lo8 & ok;
+}
+
 void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingParams& p) {
     // The prompt in chunks of chunk_ positions: fp16 MFMA GEMMs over all rows of the chunk, RoPE +
     // KV append, causal flash attention against every cached position, residual adds in fp32.
@@ -640,12 +651,16 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
     const uint32_t d = c.hidden_size, hd = c.head_dim, nq = c.num_attention_heads, nkv = c.num_key_value_heads,
                    F = c.intermediate_size, V = c.vocab_size;
     const float eps = c.rms_epsilon, scale = 1.0f / std::sqrt((float)hd);
-    const uint32_t sp = options_.prefill_split;
-    const int n1 = (sp & 1) ? VSL_DT_F16X2 : VSL_DT_F16, qdt = (sp & 2) ? VSL_DT_F16X2 : VSL_DT_F16;
-    const int odt = (sp & 4) ? VSL_DT_F16X2 : VSL_DT_F16, n2 = (sp & 8) ? VSL_DT_F16X2 : VSL_DT_F16;
-    const int a_qkv = (sp & 1) ? VSL_GEMM_A_X2 : 0, a_o = (sp & 4) ? VSL_GEMM_A_X2 : 0;
-    const int g_gu = VSL_EPI_SWIGLU | ((sp & 8) ? VSL_GEMM_A_X2 : 0) | ((sp & 16) ? VSL_GEMM_C_X2 : 0);
-    const int a_dn = (sp & 16) ? VSL_GEMM_A_X2 : 0;
+    const uint32_t sp = options_.prefill_split, l8 = prefill_lo8_stages();
+    // per stage: fp16 (one plane), hi/lo fp16 planes, or fp16 hi + fp8 lo
+    auto form = [&](uint32_t bit) { return (sp & bit) ? ((l8 & bit) ? VSL_DT_F16F8 : VSL_DT_F16X2) : VSL_DT_F16; };
+    auto aflag = [&](uint32_t bit) { return (sp & bit) ? ((l8 & bit) ? VSL_GEMM_A_F8 : VSL_GEMM_A_X2) : 0; };
+    const int n1 = form(1), qdt = (sp & 2) ? VSL_DT_F16X2 : VSL_DT_F16;
+    const int odt = (sp & 4) ? VSL_DT_F16X2 : VSL_DT_F16, n2 = form(8);
+    const int a_qkv = aflag(1), a_o = (sp & 4) ? VSL_GEMM_A_X2 : 0;
+    const int c_gu = (sp & 16) ? ((l8 & 16) ? VSL_GEMM_C_F8 : VSL_GEMM_C_X2) : 0;
+    const int g_gu = VSL_EPI_SWIGLU | aflag(8) | c_gu;
+    const int a_dn = aflag(16);
     uint32_t last_rows = 0;
     for (uint32_t c0 = 0; c0 < n_prompt; c0 += chunk_) {
         const uint32_t S = std::min(chunk_, n_prompt - c0);

@@ -30,6 +30,7 @@ extern "C" void vsl_engine_default_options(vsl_engine_options* o) {
     o->use_graph = 1;
     o->batched_prefill = 1;
     o->prefill_split = EngineOptions::kPrefillSplitAll;
+    o->prefill_lo8 = EngineOptions::kPrefillLo8Default;
     const EngineOptions d;
     o->sparse_window = d.sparse_window;
     o->sparse_global = d.sparse_global;
@@ -46,6 +47,7 @@ static EngineOptions to_options(const vsl_engine_options* o) {
     e.attn_splits = o->attn_splits;
     e.batched_prefill = o->batched_prefill != 0;
     e.prefill_split = o->prefill_split & EngineOptions::kPrefillSplitAll;
+    e.prefill_lo8 = o->prefill_lo8 & EngineOptions::kPrefillLo8Stages;
     e.dequant_f32 = o->dequant_f32 != 0;
     e.sparse_attention = o->sparse_attention != 0;
     e.sparse_window = o->sparse_window;
