@@ -1,8 +1,8 @@
 // vsl_gemm_dma.hip -- prefill GEMM with direct-to-LDS loads: C[M][N] = A[M][K] * B[N][K]^T on
 // v_mfma_f32_32x32x16_f16, for the shapes whose tiles fill the chip.
 //
-// Pipeline: BK = 32 (64 for the split 128 x 256 tile) per stage, up to four LDS stage buffers
-// (separate __shared__ arrays). Stage s + 3 is
+// Pipeline: BK = 32 (64 for the split 128 x 256 tile and the fp8-lo tiles) per stage, up to four LDS
+// stage buffers (separate __shared__ arrays). Stage s + 3 is
 // requested with global_load_lds_dwordx4 (64 lanes x 16 bytes straight into LDS, no register
 // staging and no ds_write) while stage s is computed; before computing stage s a wave waits for
 // its own loads of that stage (s_waitcnt vmcnt with the two younger stages still in flight) and
@@ -23,7 +23,8 @@
 // With a split A (VSL_DT_F16X2) a stage holds the hi and the lo A tiles and one B tile: both MFMAs
 // of a fragment pair read the same B fragment, and B crosses L2 once (the stage grows from 24 to
 // 32 KB for 128 x 256 and from 32 to 48 KB for 256 x 256, which then gets two stage buffers
-// instead of four).
+// instead of four). With an fp8 lo A (VSL_DT_F16F8) a stage holds the hi tile, the B tile and a
+// one-byte-per-element lo tile; the lo plane is multiplied on the fp8 matrix cores (see k_gemm_dma).
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -41,7 +42,7 @@ constexpr int kC1 = kGemmC1, kCX2 = kGemmCX2, kCF8 = kGemmCF8;
 // Block tile BM x BN, BK halfs of K per stage, AP fp16 planes of A per stage (2: the hi and lo planes
 // of a split A share the stage's B tile), L8: an fp8 lo plane of A after the B tile, NBUF stage
 // buffers (together at most 128 KB of LDS), WGM x WGN waves of (BM / WGM) x (BN / WGN).
-template <int BM_, int BN_, int BK_, int AP_, int WGM_ = 2, int WGN_ = 2, bool L8_ = false>
+template <int BM_, int BN_, int BK_, int AP_, int WGM_ = 2, int WGN_ = 2, bool L8_ = false, int NBUF_ = 0>
 struct DmaCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, AP = AP_, WGM = WGM_, WGN = WGN_;
     static constexpr bool L8 = L8_;
@@ -56,9 +57,10 @@ struct DmaCfg {
     static_assert(!L8 || (LCH * NT == BM * BK / 16 && LCH >= 1), "fp8 lo chunks do not divide over the threads");
     static constexpr int L8OFF = (AP * BM + BN) * BK;          // halfs before the fp8 lo tile
     static constexpr int STAGE = L8OFF + (L8 ? BM * BK / 2 : 0);  // halfs per stage buffer
-    static constexpr int NBUF = STAGE * 2 * 4 <= 128 * 1024 ? 4 : 2;
+    // four stage buffers where they fit in 128 KB, else two (NBUF_ overrides; 160 KB is all of the LDS)
+    static constexpr int NBUF = NBUF_ ? NBUF_ : (STAGE * 2 * 4 <= 128 * 1024 ? 4 : 2);
     static constexpr int KS = BK / 16;                  // MFMA k-steps per stage
-    static_assert(STAGE * 2 * NBUF <= 128 * 1024, "stage buffers exceed 128 KB");
+    static_assert(STAGE * 2 * NBUF <= 160 * 1024, "stage buffers exceed the LDS");
 };
 
 __device__ __forceinline__ int d_row(int v, int lane) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
@@ -282,11 +284,6 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
     Frags f0, f1;
     auto step = [&](vsl_half* Lc, const vsl_half* Ln, uint32_t s, auto par) {
         constexpr int PAR = decltype(par)::value;
-        if constexpr (L8) {
-            // lo chunks of this stage: before the barrier that lets Lc be overwritten
-#pragma unroll
-            for (int q = 0; q < BK / 32; ++q) lload(Lc, q, BK == 64 ? q : PAR);
-        }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             Frags& cur = (ks & 1) ? f1 : f0;
@@ -294,6 +291,12 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
             if (ks < KS - 1) {
                 fload(nxt, Lc, ks + 1);
             } else {
+                if constexpr (L8) {
+                    // lo chunks of this stage, read late (fewer live registers) but before the
+                    // barrier that lets Lc be overwritten
+#pragma unroll
+                    for (int q = 0; q < BK / 32; ++q) lload(Lc, q, BK == 64 ? q : PAR);
+                }
                 VSL_LGKM_WAIT0();
                 VSL_VMCNT_WAIT((NBUF - 2) * kPerStage);
                 __builtin_amdgcn_s_barrier();
@@ -412,18 +415,24 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
     }
 }
 
-template <int BM, int BN, int TWGM = 2, int TWGN = 2, int TBK = 32>
+template <int BM, int BN, int TWGM = 2, int TWGN = 2, int TBK = 32, int FWGM = TWGM, int FWGN = TWGN, int FNB = 0,
+          int FBK = TBK>
 struct DmaPair {  // the one-plane, the split-A and the fp8-lo configuration of a block tile
     using One = DmaCfg<BM, BN, 32, 1>;
     using Two = DmaCfg<BM, BN, TBK, 2, TWGM, TWGN>;
-    using F8 = DmaCfg<BM, BN, TBK, 1, TWGM, TWGN, true>;
+    using F8 = DmaCfg<BM, BN, FBK, 1, FWGM, FWGN, true, FNB>;
 };
 // The split-A tiles run eight waves (two per SIMD, 128 accumulators each): 4 x 2 waves of 64 x 128 for
 // 256 x 256, 2 x 4 waves of 64 x 64 for 128 x 256 (the one-plane tiles keep 2 x 2 waves of 128 x 128).
 // The split 128 x 256 tile takes BK = 64 (two 64 KB stages, half the barriers): the K-split partials
-// of a 512-row chunk, O 37.8 -> 36.6 us, down 109.9 -> 104.5 us, QKV level. The fp8-lo tiles use the
-// split-A wave layouts (a 40 KB stage for 256 x 256, 56 KB for 128 x 256).
-using DmaBig = DmaPair<256, 256, 4, 2>;
+// of a 512-row chunk, O 37.8 -> 36.6 us, down 109.9 -> 104.5 us, QKV level.
+// fp8-lo tiles: 256 x 256 as 2 x 2 waves of 128 x 128 with BK = 64 (two 80 KB stages, all of the
+// LDS; each row's 128-byte line of a stage comes in one load instruction instead of two 64-byte
+// halves): gate/up 2048 rows 754 -> 690 us, 512 rows 195 -> 185 us against 4 x 2 waves at BK = 32
+// (BK = 32 with 2 x 2 waves, or with four stage buffers: level; 4 x 2 waves at BK = 64 spill). The
+// 128 x 256 fp8-lo tile keeps 2 x 4 waves at BK = 64 (56 KB stages): down 512 rows 102 us against
+// 106-113 for 4 x 2, 2 x 2 and 1 x 4 waves.
+using DmaBig = DmaPair<256, 256, 4, 2, 32, 2, 2, 0, 64>;
 using DmaMid = DmaPair<128, 256, 2, 4, 64>;
 
 template <class G, int EPI>
