@@ -294,6 +294,11 @@ int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t 
 int vsl_gemm_f16_ws(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
                     void* workspace, uint64_t ws_bytes, void* stream);
 uint64_t vsl_gemm_f16_ws_bytes(uint32_t M, uint32_t N, uint32_t K, int epilogue);
+/* 1 when vsl_gemm_f16_ws (with vsl_gemm_f16_ws_bytes of workspace) runs this shape on the
+ * direct-to-LDS kernel -- the one with the F8 forms -- with enough tiles or K-split items to cover
+ * three quarters of the CUs; 0 when it would take the register-staged kernel instead (an F8 form
+ * then forces the direct-to-LDS tiles at lower occupancy, e.g. a 128-row SwiGLU on 64 tiles). */
+int vsl_gemm_f16_direct(uint32_t M, uint32_t N, uint32_t K, int epilogue);
 
 /* Q/K/V split of a prefill QKV GEMM output (f32 [S][(n_q+2 n_kv) hd]) with RoPE at positions
  * pos0..pos0+S-1: q -> q_out [S][n_q][hd] (q_dtype VSL_DT_F16 or VSL_DT_F16X2), k/v -> caches at

@@ -40,6 +40,21 @@ def test_c_abi_exports_every_declared_symbol(vsl):
     assert set(decl_hip) <= set(vsl._HIP_SIGS) and set(decl_eng) <= set(vsl._ENGINE_SIGS)
 
 
+def test_gemm_direct_query(vsl):
+    """vsl_gemm_f16_direct (host arithmetic only): whole 256 x 256 or 128 x 256 tiles covering >= 192
+    CUs, or a K split reaching 192 items, count as direct-to-LDS; a 128-row SwiGLU (64 tiles, no K split
+    for SwiGLU) does not; widths off the 256 / 128 grid never do."""
+    H = vsl.hip()
+    SW, F32, RES = 3, 0, 2
+    assert H.vsl_gemm_f16_direct(512, 14336, 4096, SW) == 1      # 8B gate/up, 2 x 112 tiles
+    assert H.vsl_gemm_f16_direct(128, 8192, 2048, SW) == 0       # 1B gate/up of a 128-row prompt
+    assert H.vsl_gemm_f16_direct(512, 8192, 2048, SW) == 1       # 1B gate/up of a 512-row chunk
+    assert H.vsl_gemm_f16_direct(512, 4096, 14336, RES) == 1     # 8B down: K split
+    assert H.vsl_gemm_f16_direct(128, 2048, 8192, RES | 0x400) == 1  # flags beyond the epilogue ignored
+    assert H.vsl_gemm_f16_direct(512, 4000, 4096, F32) == 0      # N off the tile grid
+    assert H.vsl_gemm_f16_direct(512, 4096, 4000, F32) == 0      # K not a multiple of 128
+
+
 def test_no_cpu_fallback_in_the_product(vsl):
     """The product libraries link HIP and nothing from the oracle."""
     for lib in (vsl.HIP_LIB, vsl.ENGINE_LIB):

@@ -107,6 +107,7 @@ _HIP_SIGS = {
     "vsl_weight_bytes": (_U64, [_I32, _U64]),
     "vsl_gemm_f16_ws": (_I32, [_P, _P, _U32, _U32, _U32, _P, _I32, _P, _U64, _P]),
     "vsl_gemm_f16_ws_bytes": (_U64, [_U32, _U32, _U32, _I32]),
+    "vsl_gemm_f16_direct": (_I32, [_U32, _U32, _U32, _I32]),
     "vsl_convert_weights": (_I32, [_P, _I32, _I32, _U64, _P, _I32, _P]),
     "vsl_attn_decode_window": (_I32, [_P, _P, _P, _I32, _U32, _U32, _U32, _U32, _F32, _U32, _P, _P, _P, _P,
                                       _U32, _U32, _U32, _P]),

@@ -820,6 +820,13 @@ extern "C" int vsl_gemm_f16_ws(const void* A, const void* B, uint32_t M, uint32_
     return gemm_f16(A, B, M, N, K, C, epilogue, static_cast<float*>(workspace), workspace ? ws_bytes : 0, stream);
 }
 
+extern "C" int vsl_gemm_f16_direct(uint32_t M, uint32_t N, uint32_t K, int epilogue) {
+    const int epi = epilogue & 0xFF;
+    for (int cfg = 0; cfg < 2; ++cfg)
+        if (vsl_gemm_dma_tiles(cfg, M, N, K, epi) >= kDmaMinTiles) return 1;
+    return vsl_gemm_splitk_plan(M, N, K, epi, kDmaMinTiles, nullptr) ? 1 : 0;
+}
+
 extern "C" uint64_t vsl_gemm_f16_ws_bytes(uint32_t M, uint32_t N, uint32_t K, int epilogue) {
     const int epi = epilogue & 0xFF;
     for (int cfg = 0; cfg < 2; ++cfg)

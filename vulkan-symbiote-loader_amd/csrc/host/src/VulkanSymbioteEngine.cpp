@@ -651,20 +651,27 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
     const uint32_t d = c.hidden_size, hd = c.head_dim, nq = c.num_attention_heads, nkv = c.num_key_value_heads,
                    F = c.intermediate_size, V = c.vocab_size;
     const float eps = c.rms_epsilon, scale = 1.0f / std::sqrt((float)hd);
-    const uint32_t sp = options_.prefill_split, l8 = prefill_lo8_stages();
-    // per stage: fp16 (one plane), hi/lo fp16 planes, or fp16 hi + fp8 lo
-    auto form = [&](uint32_t bit) { return (sp & bit) ? ((l8 & bit) ? VSL_DT_F16F8 : VSL_DT_F16X2) : VSL_DT_F16; };
-    auto aflag = [&](uint32_t bit) { return (sp & bit) ? ((l8 & bit) ? VSL_GEMM_A_F8 : VSL_GEMM_A_X2) : 0; };
-    const int n1 = form(1), qdt = (sp & 2) ? VSL_DT_F16X2 : VSL_DT_F16;
-    const int odt = (sp & 4) ? VSL_DT_F16X2 : VSL_DT_F16, n2 = form(8);
-    const int a_qkv = aflag(1), a_o = (sp & 4) ? VSL_GEMM_A_X2 : 0;
-    const int c_gu = (sp & 16) ? ((l8 & 16) ? VSL_GEMM_C_F8 : VSL_GEMM_C_X2) : 0;
-    const int g_gu = VSL_EPI_SWIGLU | aflag(8) | c_gu;
-    const int a_dn = aflag(16);
+    const uint32_t sp = options_.prefill_split, wqkv = (nq + 2 * nkv) * hd;
     uint32_t last_rows = 0;
     for (uint32_t c0 = 0; c0 < n_prompt; c0 += chunk_) {
         const uint32_t S = std::min(chunk_, n_prompt - c0);
         last_rows = S;
+        // fp8 lo stages of this chunk: those whose GEMMs run on the direct-to-LDS tiles at full
+        // occupancy anyway (the down input also needs the gate/up GEMM there, whose epilogue writes it)
+        uint32_t l8 = prefill_lo8_stages();
+        const bool gu_direct = vsl_gemm_f16_direct(S, F, d, VSL_EPI_SWIGLU) != 0;
+        if (!vsl_gemm_f16_direct(S, wqkv, d, VSL_EPI_STORE_F32)) l8 &= ~1u;
+        if (!gu_direct) l8 &= ~(8u | 16u);
+        if (!vsl_gemm_f16_direct(S, d, F, VSL_EPI_RESID)) l8 &= ~16u;
+        // per stage: fp16 (one plane), hi/lo fp16 planes, or fp16 hi + fp8 lo
+        auto form = [&](uint32_t bit) { return (sp & bit) ? ((l8 & bit) ? VSL_DT_F16F8 : VSL_DT_F16X2) : VSL_DT_F16; };
+        auto aflag = [&](uint32_t bit) { return (sp & bit) ? ((l8 & bit) ? VSL_GEMM_A_F8 : VSL_GEMM_A_X2) : 0; };
+        const int n1 = form(1), qdt = (sp & 2) ? VSL_DT_F16X2 : VSL_DT_F16;
+        const int odt = (sp & 4) ? VSL_DT_F16X2 : VSL_DT_F16, n2 = form(8);
+        const int a_qkv = aflag(1), a_o = (sp & 4) ? VSL_GEMM_A_X2 : 0;
+        const int c_gu = (sp & 16) ? ((l8 & 16) ? VSL_GEMM_C_F8 : VSL_GEMM_C_X2) : 0;
+        const int g_gu = VSL_EPI_SWIGLU | aflag(8) | c_gu;
+        const int a_dn = aflag(16);
         check(vsl_embed(embed_, edt_, V, d, prompt_dev_ + c0, S, px_, stream_), "vsl_embed");
         // every later layer's attention norm comes with the previous layer's down projection
         check(vsl_rmsnorm(px_, layers_[0].attn_norm, S, d, eps, pxn_, n1, stream_), "vsl_rmsnorm");
