@@ -191,7 +191,8 @@ int vsl_gemv(const void* W, int wdtype, uint32_t N, uint32_t K, const void* X, i
 /* The same product for a batch of B activation vectors, each contiguous: X fp16 [B][K], Y [B][N]
  * (f16 or f32), W fp16 [N][K]; 1 <= B <= 16, K % 512 == 0.  One pass over W: whole rows streamed
  * with fp16 dot products into fp32 for 2 <= B <= 8 when X (B * K * 2 bytes) is at most 128 KB, K %
- * 1024 == 0 and X is 16-byte aligned; MFMA otherwise.  No reference
+ * 1024 == 0 and X is 16-byte aligned; MFMA otherwise (W and X staged through LDS in whole-line runs
+ * when K % 1024 == 0 and X is 16-byte aligned, register fragments else).  No reference
  * counterpart (the reference multiplies one vector at a time, final_linear.comp:37-85); it is the
  * batch>1 decode shape of the GEMV sweep. */
 int vsl_gemv_batched(const void* W, uint32_t N, uint32_t K, const void* X, uint32_t B, void* Y, int ydtype,

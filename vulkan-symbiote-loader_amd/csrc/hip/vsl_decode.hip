@@ -1811,6 +1811,108 @@ __global__ __launch_bounds__(kSkWaves * 64) void k_skinny(const vsl_half* __rest
     }
 }
 
+// The same product with both operands staged through LDS (X [B][K], K % 1024 == 0): block = 16 rows x
+// 4 waves splitting K, each wave its own double-buffered LDS chunks of 128 columns -- the 16 W rows
+// and the 16 X vectors (vectors past B re-read vector B-1 and are masked). Every load instruction
+// (global_load_lds) moves 256-byte runs of four rows, whole 128-byte lines, where the register
+// fragment loads of k_skinny take 64 bytes of each of 16 rows; the fragments come from LDS, chunk q
+// of row r stored at position q ^ r so that the 16 rows of a fragment read fall in distinct banks.
+// Each wave waits only for its own copies (vmcnt): no block barrier until the partial tiles are summed
+// in wave order. 64 KB of LDS per block, two blocks per CU. Sweep at B = 16 (GB/s, geometric mean of
+// the four shapes): k_skinny 3690; chunks of 256 columns (one block per CU) 4160, 128 x 4 buffers 4155,
+// 128 x 2 buffers 4500, 64 x 2 4180, 64 x 4 4336, 128 x 2 with 8 waves 4187.
+constexpr int kSlWaves = 4;
+template <uint32_t CH_, int NB_>
+struct SlCfg {
+    static constexpr uint32_t CH = CH_;  // columns of K per LDS chunk
+    static constexpr int NB = NB_;       // chunk buffers per wave (NB - 1 in flight)
+    static constexpr uint32_t RUN = CH * 2;             // bytes of one row per chunk
+    static constexpr uint32_t LPR = RUN / 16;           // lanes per row in a load instruction
+    static constexpr uint32_t RPI = 64 / LPR;           // rows per load instruction
+    static constexpr uint32_t NLD = 16 / RPI;           // load instructions per operand and chunk
+    static constexpr uint32_t KALIGN = kSlWaves * CH * NB;
+    static_assert(LPR <= 64 && 16 % RPI == 0 && LPR >= 8, "rows of 128 .. 1024 bytes per chunk");
+    // position of logical 16-byte chunk q of row r: the 16 rows of a fragment read in distinct bank
+    // groups (a 256-byte LDS cycle holds one row of 256+ bytes, or two rows of 128)
+    static __device__ __forceinline__ uint32_t pos(uint32_t q, uint32_t r) {
+        return LPR >= 16 ? q ^ (r & 15) : q ^ ((r >> 1) & 7);
+    }
+};
+using SlDefault = SlCfg<128, 2>;
+constexpr uint32_t kSlKAlign = SlDefault::KALIGN;  // K multiple: whole buffer rounds per wave
+
+template <class C, typename YT>
+__global__ __launch_bounds__(kSlWaves * 64) void k_skinny_lds(const vsl_half* __restrict__ W, uint32_t N, uint32_t K,
+                                                             const vsl_half* __restrict__ X, uint32_t B,
+                                                             YT* __restrict__ Y) {
+    constexpr uint32_t CH = C::CH, REG = 16 * CH;  // halfs per operand region (16 rows / vectors)
+    constexpr int NB = C::NB;
+    __shared__ __attribute__((aligned(16))) vsl_half buf[kSlWaves][NB][2 * REG];  // [wave][buffer][W | X]
+    __shared__ float part[kSlWaves][16][17];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t row0 = blockIdx.x * 16;
+    const uint32_t kw = K / kSlWaves, k_begin = wave * kw, nch = kw / CH;
+    // load instruction j covers rows / vectors RPI j .. RPI j + RPI - 1 (LPR lanes each); lane position
+    // p of its row holds logical chunk p ^ (row & 15)
+    const uint32_t p = lane % C::LPR, rsub = lane / C::LPR;
+    uint32_t woff[C::NLD], xoff[C::NLD];
+#pragma unroll
+    for (int j = 0; j < (int)C::NLD; ++j) {
+        const uint32_t rr = C::RPI * j + rsub;
+        const uint32_t wrow = row0 + rr < N ? row0 + rr : N - 1;  // rows past N: never stored
+        const uint32_t xcol = rr < B ? rr : B - 1;                // vectors past B: masked
+        woff[j] = (wrow * K + k_begin + C::pos(p, rr) * 8) * 2;  // pos is its own inverse
+        xoff[j] = (xcol * K + k_begin + C::pos(p, rr) * 8) * 2;
+    }
+    auto issue = [&](uint32_t c, int bsel) {
+        const uint32_t cc = c < nch ? c : nch - 1;  // past the end: re-load the last chunk (never read)
+        vsl_half* L = buf[wave][bsel];
+#pragma unroll
+        for (int j = 0; j < (int)C::NLD; ++j) lds_load16(W + cc * CH, woff[j], L + j * 512);
+#pragma unroll
+        for (int j = 0; j < (int)C::NLD; ++j) lds_load16(X + cc * CH, xoff[j], L + REG + j * 512);
+    };
+    const uint32_t r = lane & 15, g = lane >> 4;
+    const uint32_t bmask = r < B ? 0xFFFFFFFFu : 0u;  // this lane's X fragment is vector r
+    float4v acc = float4v{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](int bsel) {
+        const vsl_half* L = buf[wave][bsel];
+#pragma unroll
+        for (int u = 0; u < (int)(CH / 32); ++u) {
+            const uint32_t pos = C::pos(4 * u + g, r) * 8;
+            const half8 a = *reinterpret_cast<const half8*>(L + r * CH + pos);
+            uint4 xv = __builtin_bit_cast(uint4, *reinterpret_cast<const half8*>(L + REG + r * CH + pos));
+            xv = make_uint4(xv.x & bmask, xv.y & bmask, xv.z & bmask, xv.w & bmask);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(half8, xv), acc, 0, 0, 0);
+        }
+    };
+    // chunk c in buffer c % NB; chunks c + 1 .. c + NB - 1 in flight while c is consumed; nch % NB == 0
+    constexpr int kPer = 2 * C::NLD;  // loads per chunk
+#pragma unroll
+    for (int b = 0; b < NB - 1; ++b) issue(b, b);
+    for (uint32_t c = 0; c < nch; c += NB) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            issue(c + b + NB - 1, (b + NB - 1) % NB);
+            VSL_VMCNT_WAIT((NB - 1) * kPer);
+            consume(b);
+            VSL_LGKM_WAIT0();  // buffer b fully read before it is refilled
+        }
+    }
+    VSL_VMCNT_WAIT(0);  // the trailing re-loads land before the LDS is released
+#pragma unroll
+    for (int i = 0; i < 4; ++i) part[wave][(lane >> 4) * 4 + i][r] = acc[i];
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < 16 * 16; e += kSlWaves * 64) {
+        const uint32_t m = e >> 4, n = e & 15;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kSlWaves; ++w) v += part[w][m][n];
+        const uint32_t row = row0 + m;
+        if (row < N && n < B) store_elem(Y + (size_t)n * N + row, v);
+    }
+}
+
 template <typename YT, bool VEC_MAJOR>
 int launch_skinny(const void* W, uint32_t N, uint32_t K, const void* X, uint32_t B, void* Y, hipStream_t s) {
     const vsl_half* w = static_cast<const vsl_half*>(W);
@@ -2069,6 +2171,17 @@ extern "C" int vsl_gemv_batched(const void* W, uint32_t N, uint32_t K, const voi
     if (B == 1 && K <= kMaxK) return gemv_one_f16x(W, N, K, X, Y, ydtype, s);
     if (rows_fits(B, K, X))
         return ydtype == VSL_DT_F16 ? launch_rows<vsl_half>(W, N, K, X, B, Y, s) : launch_rows<float>(W, N, K, X, B, Y, s);
+    if (K % kSlKAlign == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ((uint64_t)N * K * 2) >> 32 == 0 &&
+        ((uint64_t)B * K * 2) >> 32 == 0) {
+        if (ydtype == VSL_DT_F16)
+            k_skinny_lds<SlDefault, vsl_half><<<(N + 15) / 16, kSlWaves * 64, 0, s>>>(
+                static_cast<const vsl_half*>(W), N, K, static_cast<const vsl_half*>(X), B, static_cast<vsl_half*>(Y));
+        else
+            k_skinny_lds<SlDefault, float><<<(N + 15) / 16, kSlWaves * 64, 0, s>>>(
+                static_cast<const vsl_half*>(W), N, K, static_cast<const vsl_half*>(X), B, static_cast<float*>(Y));
+        HIP_TRY(hipGetLastError());
+        return VSL_OK;
+    }
     return ydtype == VSL_DT_F16 ? launch_skinny<vsl_half, true>(W, N, K, X, B, Y, s)
                                 : launch_skinny<float, true>(W, N, K, X, B, Y, s);
 }
