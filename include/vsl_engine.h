@@ -56,9 +56,10 @@ typedef struct vsl_engine_options {
     uint32_t sparse_global;     /* 16 */
     uint32_t sparse_threshold;  /* 8192 (the reference's seq_len > 8192, VulkanSymbioteEngine.cpp:788) */
     uint32_t prefill_lo8;       /* split stages whose lo part is fp8 (VSL_DT_F16F8, the lo plane on the fp8
-                                   matrix cores): bit 0 QKV input, bit 3 gate/up input, bit 4 down input;
+                                   matrix cores): bit 0 QKV input, bit 2 O input, bit 3 gate/up input,
+                                   bit 4 down input;
                                    taken where the shapes allow it (d, F and the QKV width multiples of
-                                   256), else the fp16 lo plane; vsl_engine_default_options sets 0x18 */
+                                   256), else the fp16 lo plane; vsl_engine_default_options sets 0x1C */
 } vsl_engine_options;
 
 typedef struct vsl_gen_params {

@@ -332,7 +332,7 @@ int vsl_gemm_f16_resid_rmsnorm(const void* A, const void* B, uint32_t M, uint32_
 
 /* Causal prefill attention for S queries at positions pos0..pos0+S-1 against cache positions
  * 0..pos0+s: q [S][n_q][hd] (q_dtype F16 or F16X2), caches f16 [n_kv][cap][hd],
- * out [S][n_q*hd] (out_dtype F16 or F16X2).  With F16X2 q the probabilities are split as well. */
+ * out [S][n_q*hd] (out_dtype F16, F16X2 or F16F8).  With F16X2 q the probabilities are split as well. */
 int vsl_attn_prefill(const void* q, int q_dtype, const void* kcache, const void* vcache, uint32_t S,
                      uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t hd, uint32_t cap, float scale,
                      void* out, int out_dtype, void* stream);

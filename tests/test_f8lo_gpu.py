@@ -226,3 +226,27 @@ def test_resid_rmsnorm_f8lo(vsl, orc, dev, H, M, N, K):
         assert rel_err(x[rows], ref) < 1e-5
         nref = np.stack([orc.rmsnorm(x[r], g, 1e-5) for r in rows]).astype(np.float64)
         assert_f8_encodes(hn[rows], vn[rows], nref)
+
+
+@pytest.mark.parametrize("hd,nq,nkv,S,pos0", [(128, 8, 2, 300, 0), (64, 4, 4, 97, 37), (128, 32, 8, 512, 0)])
+def test_attn_prefill_f16f8_output(vsl, dev, H, hd, nq, nkv, S, pos0):
+    """The prefill attention writing its output as F16F8: the same hi plane as the hi/lo fp16 output of
+    the same call, bit for bit, and hi + lo8 2^-12 within e4m3 precision of hi + lo (so every byte sits
+    at its lo8_pos position)."""
+    rng = np.random.default_rng(hd + nq + S + pos0)
+    cap = 1024
+    q = dev.put(rng.normal(0, 1, (2, S, nq * hd)).astype(np.float16) * np.array([1.0, 2.0 ** -11], np.float16)[:, None, None])
+    kc = dev.put(rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16))
+    vc = dev.put(rng.normal(0, 1, (nkv, cap, hd)).astype(np.float16))
+    scale = 1.0 / np.sqrt(hd)
+    out2 = dev.empty((2, S, nq * hd), np.float16)
+    ok(vsl, H.vsl_attn_prefill(dev.p(q), vsl.VSL_DT_F16X2, dev.p(kc), dev.p(vc), S, pos0, nq, nkv, hd, cap, scale,
+                               dev.p(out2), vsl.VSL_DT_F16X2, None))
+    out8 = dev.empty((3 * S * nq * hd,), np.uint8)
+    ok(vsl, H.vsl_attn_prefill(dev.p(q), vsl.VSL_DT_F16X2, dev.p(kc), dev.p(vc), S, pos0, nq, nkv, hd, cap, scale,
+                               dev.p(out8), vsl.VSL_DT_F16F8, None))
+    o2 = dev.get(out2)
+    hi8, val8 = f8_read(dev, out8, S, nq * hd)
+    assert np.array_equal(hi8.view(np.uint16), o2[0].view(np.uint16))
+    v2 = o2[0].astype(np.float64) + o2[1].astype(np.float64)
+    assert np.all(np.abs(val8 - v2) <= F8_VALUE_REL * np.abs(v2) + F8_VALUE_ABS)

@@ -15,6 +15,8 @@
 // Which physical k a slot holds is free as long as A and B agree.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include <cmath>
 
 #include "vsl_device.h"
@@ -447,7 +449,7 @@ __device__ __forceinline__ int ksw(int r, int c) {
     else return r * HD + ((c ^ ((r >> 1) & 7)) * 8);                      // 128-byte rows: row pairs
 }
 
-template <int HD, int G, bool QX2, bool OX2, bool WIN>
+template <int HD, int G, bool QX2, int OM, bool WIN>
 __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restrict__ q, const vsl_half* __restrict__ kc,
                                                          const vsl_half* __restrict__ vc, uint32_t S, uint32_t pos0,
                                                          uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
@@ -686,10 +688,20 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
 #pragma unroll
         for (int v0 = 0; v0 < 16; v0 += 4) {
             half4 hv, lv;
+            const int dim = t * 32 + d_row(v0, lane);
+            if constexpr (OM == 2) {
+                uint32_t lo8;
+                split4_f16_f8(o[t][v0] * inv, o[t][v0 + 1] * inv, o[t][v0 + 2] * inv, o[t][v0 + 3] * inv, hv, lo8);
+                *reinterpret_cast<half4*>(orow + dim) = hv;
+                // the lo8 plane (bytes) follows the hi plane; columns h HD + dim .. + 3 stay contiguous
+                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(out + qplane) + (size_t)my_s * qw +
+                                             lo8_pos(h * HD + dim)) = lo8;
+                continue;
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float val = o[t][v0 + i] * inv;
-                if constexpr (OX2) {
+                if constexpr (OM == 1) {
                     vsl_half hi, lo;
                     split_f16(val, hi, lo);
                     hv[i] = hi;
@@ -698,9 +710,8 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
                     hv[i] = (vsl_half)val;
                 }
             }
-            const int dim = t * 32 + d_row(v0, lane);
             *reinterpret_cast<half4*>(orow + dim) = hv;
-            if constexpr (OX2) *reinterpret_cast<half4*>(orow + qplane + dim) = lv;
+            if constexpr (OM == 1) *reinterpret_cast<half4*>(orow + qplane + dim) = lv;
         }
 }
 
@@ -1007,35 +1018,45 @@ struct PrefillWindow {
 template <int HD, int G, bool WIN>
 static void launch_attn_prefill_w(dim3 grid, hipStream_t s, const vsl_half* q, const vsl_half* k, const vsl_half* v,
                                   uint32_t S, uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
-                                  vsl_half* o, bool qx2, bool ox2, const PrefillWindow& w) {
+                                  vsl_half* o, bool qx2, int om, const PrefillWindow& w) {
     constexpr int NT = 64 * G;
-    if (qx2 && ox2)
-        k_attn_prefill<HD, G, true, true, WIN><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
-    else if (qx2)
-        k_attn_prefill<HD, G, true, false, WIN><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
-    else if (ox2)
-        k_attn_prefill<HD, G, false, true, WIN><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
-    else
-        k_attn_prefill<HD, G, false, false, WIN><<<grid, NT, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+    auto go = [&](auto qc, auto oc) {
+        k_attn_prefill<HD, G, decltype(qc)::value, decltype(oc)::value, WIN><<<grid, NT, 0, s>>>(
+            q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    using O0 = std::integral_constant<int, 0>;
+    using O1 = std::integral_constant<int, 1>;
+    using O2 = std::integral_constant<int, 2>;
+    if (qx2) {
+        if (om == 2) go(T{}, O2{});
+        else if (om == 1) go(T{}, O1{});
+        else go(T{}, O0{});
+    } else {
+        if (om == 2) go(F{}, O2{});
+        else if (om == 1) go(F{}, O1{});
+        else go(F{}, O0{});
+    }
 }
 
 template <int HD, int G>
 static void launch_attn_prefill_g(dim3 grid, hipStream_t s, const vsl_half* q, const vsl_half* k, const vsl_half* v,
                                   uint32_t S, uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
-                                  vsl_half* o, bool qx2, bool ox2, const PrefillWindow& w) {
-    if (w.on) launch_attn_prefill_w<HD, G, true>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w);
-    else launch_attn_prefill_w<HD, G, false>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w);
+                                  vsl_half* o, bool qx2, int om, const PrefillWindow& w) {
+    if (w.on) launch_attn_prefill_w<HD, G, true>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w);
+    else launch_attn_prefill_w<HD, G, false>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w);
 }
 
 template <int HD>
 static int launch_attn_prefill(dim3 grid, hipStream_t s, const vsl_half* q, const vsl_half* k, const vsl_half* v,
                                uint32_t S, uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
-                               vsl_half* o, bool qx2, bool ox2, const PrefillWindow& w) {
+                               vsl_half* o, bool qx2, int om, const PrefillWindow& w) {
     switch (n_q / n_kv) {
-        case 1: launch_attn_prefill_g<HD, 1>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w); break;
-        case 2: launch_attn_prefill_g<HD, 2>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w); break;
-        case 4: launch_attn_prefill_g<HD, 4>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w); break;
-        case 8: launch_attn_prefill_g<HD, 8>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, ox2, w); break;
+        case 1: launch_attn_prefill_g<HD, 1>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
+        case 2: launch_attn_prefill_g<HD, 2>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
+        case 4: launch_attn_prefill_g<HD, 4>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
+        case 8: launch_attn_prefill_g<HD, 8>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
         default: return vsl_unsupported("vsl_attn_prefill: GQA ratio %u (supported 1, 2, 4, 8)", n_q / n_kv);
     }
     return VSL_OK;
@@ -1051,20 +1072,24 @@ static int attn_prefill(const void* q, int q_dtype, const void* kcache, const vo
         vsl_set_error("vsl_attn_prefill: positions %u..%u exceed capacity %u", pos0, pos0 + S - 1, cap);
         return VSL_E_CAPACITY;
     }
-    if ((q_dtype != VSL_DT_F16 && q_dtype != VSL_DT_F16X2) || (out_dtype != VSL_DT_F16 && out_dtype != VSL_DT_F16X2))
+    if ((q_dtype != VSL_DT_F16 && q_dtype != VSL_DT_F16X2) ||
+        (out_dtype != VSL_DT_F16 && out_dtype != VSL_DT_F16X2 && out_dtype != VSL_DT_F16F8))
         return vsl_unsupported("vsl_attn_prefill: dtypes %d/%d", q_dtype, out_dtype);
+    if (out_dtype == VSL_DT_F16F8 && (n_q * hd) % 32)
+        return vsl_invalid("vsl_attn_prefill: F16F8 output needs n_q * head_dim %% 32 == 0");
     dim3 grid((S + 31) / 32, n_kv);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const bool qx2 = q_dtype == VSL_DT_F16X2, ox2 = out_dtype == VSL_DT_F16X2;
+    const bool qx2 = q_dtype == VSL_DT_F16X2;
+    const int om = out_dtype == VSL_DT_F16X2 ? 1 : out_dtype == VSL_DT_F16F8 ? 2 : 0;
     const vsl_half* qq = static_cast<const vsl_half*>(q);
     const vsl_half* kk = static_cast<const vsl_half*>(kcache);
     const vsl_half* vv = static_cast<const vsl_half*>(vcache);
     vsl_half* oo = static_cast<vsl_half*>(out);
     int rc;
     if (hd == 128)
-        rc = launch_attn_prefill<128>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, ox2, w);
+        rc = launch_attn_prefill<128>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, om, w);
     else if (hd == 64)
-        rc = launch_attn_prefill<64>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, ox2, w);
+        rc = launch_attn_prefill<64>(grid, s, qq, kk, vv, S, pos0, n_q, n_kv, cap, scale, oo, qx2, om, w);
     else
         return vsl_unsupported("vsl_attn_prefill: head_dim %u", hd);
     if (rc) return rc;

@@ -640,6 +640,7 @@ uint32_t VulkanSymbioteEngine::prefill_lo8_stages() const {
     const uint32_t wqkv = (c.num_attention_heads + 2 * c.num_key_value_heads) * c.head_dim;
     uint32_t ok = 0;
     if (d % 256 == 0 && wqkv % 256 == 0) ok |= 1u;    // QKV input: [Wq; Wk; Wv] against d
+    if (d % 256 == 0 && (c.num_attention_heads * c.head_dim) % 128 == 0) ok |= 4u;  // O input: d outputs
     if (d % 256 == 0 && F % 256 == 0) ok |= 8u | 16u;  // gate/up (F outputs, K = d), down (d outputs, K = F)
     return options_.prefill_lo8 & ok;
 }
@@ -663,12 +664,13 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
         if (!vsl_gemm_f16_direct(S, wqkv, d, VSL_EPI_STORE_F32)) l8 &= ~1u;
         if (!gu_direct) l8 &= ~(8u | 16u);
         if (!vsl_gemm_f16_direct(S, d, F, VSL_EPI_RESID)) l8 &= ~16u;
+        if (!vsl_gemm_f16_direct(S, d, nq * hd, VSL_EPI_RESID)) l8 &= ~4u;
         // per stage: fp16 (one plane), hi/lo fp16 planes, or fp16 hi + fp8 lo
         auto form = [&](uint32_t bit) { return (sp & bit) ? ((l8 & bit) ? VSL_DT_F16F8 : VSL_DT_F16X2) : VSL_DT_F16; };
         auto aflag = [&](uint32_t bit) { return (sp & bit) ? ((l8 & bit) ? VSL_GEMM_A_F8 : VSL_GEMM_A_X2) : 0; };
         const int n1 = form(1), qdt = (sp & 2) ? VSL_DT_F16X2 : VSL_DT_F16;
-        const int odt = (sp & 4) ? VSL_DT_F16X2 : VSL_DT_F16, n2 = form(8);
-        const int a_qkv = aflag(1), a_o = (sp & 4) ? VSL_GEMM_A_X2 : 0;
+        const int odt = form(4), n2 = form(8);
+        const int a_qkv = aflag(1), a_o = aflag(4);
         const int c_gu = (sp & 16) ? ((l8 & 16) ? VSL_GEMM_C_F8 : VSL_GEMM_C_X2) : 0;
         const int g_gu = VSL_EPI_SWIGLU | aflag(8) | c_gu;
         const int a_dn = aflag(16);

@@ -73,14 +73,15 @@ struct EngineOptions {
     uint32_t prefill_split = kPrefillSplitAll;
     // Which of the split stages carry their lo part as fp8 e4m3 (VSL_DT_F16F8: ~15-bit inputs, the
     // lo plane multiplied on the fp8 matrix cores) instead of a second fp16 plane: bit 0 QKV input,
-    // bit 3 gate/up input, bit 4 down input (the attention and O-projection inputs have no fp8 form).
+    // bit 2 O-projection input (the attention output), bit 3 gate/up input, bit 4 down input (the
+    // attention's own q / probabilities have no fp8 form).
     // Taken where the shapes allow it (model width and FFN size multiples of 256, the QKV width a
     // multiple of 256) and, per prompt chunk, where the stage's GEMMs run on the direct-to-LDS tiles
     // at full occupancy (vsl_gemm_f16_direct; e.g. not the 1B model's 128-row gate/up, where the fp8
     // form would force 64 tiles: 1.96 -> 2.24 ms); elsewhere the stage keeps the fp16 lo plane. The
-    // default takes the gate/up and down inputs only: on the 8B model their fp8 form leaves the logit
-    // error against fp32 inputs level (0.0025 against 0.0023 max-abs), while an fp8 QKV input
-    // doubles it (0.0052; the attention scores amplify it) for 0.15 ms of a 14 ms 512-token prompt.
+    // default takes the O, gate/up and down inputs: on the 8B model their fp8 form leaves the logit
+    // error against fp32 inputs about level (0.0026 against 0.0023 max-abs), while an fp8 QKV input
+    // doubles it (0.0052; the attention scores amplify it) for 0.15 ms of a 13 ms 512-token prompt.
     uint32_t prefill_lo8 = kPrefillLo8Default;
     // Block-quantized GGUF weights (Q4_0 / Q4_1 / Q8_0) are expanded at load into fp16 packs, or into
     // fp32 packs holding exactly the values the reference's dequantize_tensor returns when set.
@@ -95,8 +96,8 @@ struct EngineOptions {
     uint32_t sparse_threshold = 8192;
     bool verbose = false;
     static constexpr uint32_t kPrefillSplitAll = 0x1F;
-    static constexpr uint32_t kPrefillLo8Stages = 0x19;
-    static constexpr uint32_t kPrefillLo8Default = 0x18;
+    static constexpr uint32_t kPrefillLo8Stages = 0x1D;
+    static constexpr uint32_t kPrefillLo8Default = 0x1C;
 };
 
 // Synthetic Llama-style model: every linear weight ~ N(0, init_std) from the Philox stream keyed by
