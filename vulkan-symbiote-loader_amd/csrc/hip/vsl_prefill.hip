@@ -433,7 +433,8 @@ __global__ __launch_bounds__(256) void k_splitk_resid_rmsnorm(const float* __res
 // causal flash attention (prefill), fp16 in / fp16 out, fp32 softmax statistics
 // ---------------------------------------------------------------------------------------------
 // Causal flash attention for one chunk of S prompt rows at positions pos0.. (their K/V already in
-// the cache). Block = the G query heads of one KV head x 32 query rows, one wave per head: each
+// the cache). Block = the G query heads of one KV head x 32 query rows, one wave per head (two for
+// G <= 4, each taking one 32-key half of every tile, merged at the end): each
 // 64-position K/V tile is copied once for all G heads straight from the cache into LDS
 // (global_load_lds, three tile buffers, each tile requested two tiles ahead), both row-major with the
 // chunk swizzle of ksw. Per tile each wave computes S^T = K Q^T (two 32-position fragments), the
@@ -449,14 +450,17 @@ __device__ __forceinline__ int ksw(int r, int c) {
     else return r * HD + ((c ^ ((r >> 1) & 7)) * 8);                      // 128-byte rows: row pairs
 }
 
-template <int HD, int G, bool QX2, int OM, bool WIN>
-__global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restrict__ q, const vsl_half* __restrict__ kc,
+// KSPLIT = 2: two waves per query head, each taking one 32-key half of every tile (its own online
+// softmax state), the halves merged through LDS at the end.
+template <int HD, int G, bool QX2, int OM, bool WIN, int KSPLIT>
+__global__ __launch_bounds__(64 * G * KSPLIT) void k_attn_prefill(const vsl_half* __restrict__ q, const vsl_half* __restrict__ kc,
                                                          const vsl_half* __restrict__ vc, uint32_t S, uint32_t pos0,
                                                          uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
                                                          vsl_half* __restrict__ out, uint32_t win, uint32_t n_glob,
                                                          uint32_t thr) {
     constexpr int TK = kAttnTile;
-    constexpr int NT = 64 * G;
+    constexpr int NT = 64 * G * KSPLIT;
+    constexpr int NKB = 2 / KSPLIT;             // 32-key halves of a tile per wave
     constexpr int CPR = HD / 8;                 // 16-byte chunks per K/V row
     constexpr int NCH = TK * CPR / NT;          // chunks per thread per tile (K and V each)
     constexpr int QP = QX2 ? 2 : 1;             // q planes; with split q the probabilities are split too
@@ -467,7 +471,8 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     const uint32_t n_qb = gridDim.x;
     const uint32_t qb = n_qb - 1 - blockIdx.x;  // the longest (latest) query blocks start first
     const uint32_t kvh = blockIdx.y;
-    const uint32_t h = kvh * G + wave;          // kv_head = head * n_kv / n_q
+    const int kbase = KSPLIT == 2 ? wave / G : 0;  // this wave's first 32-key half of each tile
+    const uint32_t h = kvh * G + wave % G;      // kv_head = head * n_kv / n_q
     const uint32_t s_base = qb * 32;
     const uint32_t my_s = s_base + (lane & 31);  // query row owned by this lane (stats, O^T column)
     const uint32_t qw = n_q * HD;
@@ -542,15 +547,16 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     // 2^kLazy and most tiles skip the rescale. The quotient O / l does not depend on m.
     constexpr float kLazy = 8.f;
     // S^T[kv][q] = sum_d K[kv][d] Q[q][d] for the two 32-position halves of the tile in `buf`
-    auto qk = [&](int buf, float16v (&st)[2]) {
+    auto qk = [&](int buf, float16v (&st)[NKB]) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) st[kb][v] = 0.f;
             half8 kf[HD / 16];
 #pragma unroll
             for (int c = 0; c < HD / 16; ++c)
-                kf[c] = *reinterpret_cast<const half8*>(&Ks[buf][ksw<HD>(kb * 32 + (lane & 31), 2 * c + (lane >> 5))]);
+                kf[c] = *reinterpret_cast<const half8*>(
+                    &Ks[buf][ksw<HD>((kbase + kb) * 32 + (lane & 31), 2 * c + (lane >> 5))]);
 #pragma unroll
             for (int c = 0; c < HD / 16; ++c)
 #pragma unroll
@@ -559,13 +565,13 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     };
     // scaled scores of tile t with the causal (and window) mask, applied only on tiles that reach past
     // the block's first row; returns the tile maximum of this lane's row
-    auto mask_max = [&](float16v (&st)[2], uint32_t t) {
+    auto mask_max = [&](float16v (&st)[NKB], uint32_t t) {
         float bm = -INFINITY;
         // wave-uniform: every key of the tile is visible to every row of the block (at or below the
         // first row, and inside every row's window or among the global keys)
         if (t * TK + TK - 1 <= p_first && (!WIN || t * TK >= lo_max || t * TK + TK - 1 < n_glob)) {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     st[kb][v] *= sl2;
@@ -573,10 +579,10 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
                 }
         } else {
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const uint32_t kvp = t * TK + kb * 32 + d_row(v, lane);
+                    const uint32_t kvp = t * TK + (kbase + kb) * 32 + d_row(v, lane);
                     const bool seen = WIN ? kvp <= my_pos && (kvp >= my_lo || kvp < n_glob) : kvp <= my_pos;
                     st[kb][v] = seen ? st[kb][v] * sl2 : -INFINITY;
                     bm = fmaxf(bm, st[kb][v]);
@@ -601,10 +607,10 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     };
     // probabilities 2^(score - m) as the P^T operand (split into hi / lo planes with a split q);
     // returns their sum over the tile for this lane's row
-    auto probs = [&](const float16v (&st)[2], half8 (&pf)[QP][2][2]) {
+    auto probs = [&](const float16v (&st)[NKB], half8 (&pf)[QP][NKB][2]) {
         float ps = 0.f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const float pv = (st[kb][v] == -INFINITY) ? 0.f : fast_exp2(st[kb][v] - m);
@@ -628,17 +634,17 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     // + 4 (l/32). ds_read_b64_tr_b16 gives lane i of a 16-lane group element i%4 of the 8-byte
     // row addressed by lane 4j + i/4 of the group as its value j, so lane i addresses
     // V[r0 + i/4][d0 + 4 (i%4) .. +3] with d0 the group's first dim: value j is V[r0 + j][d0 + i].
-    auto pv = [&](int buf, const half8 (&pf)[QP][2][2]) {
+    auto pv = [&](int buf, const half8 (&pf)[QP][NKB][2]) {
         const vsl_half* Vt = Vs[buf];
         const int gi = lane & 15, gdim = ((lane >> 4) & 1) * 16 + 4 * (gi & 3);
 #pragma unroll
         for (int tt = 0; tt < HD / 32; ++tt) {
             const int d = tt * 32 + gdim;
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
                 for (int hi = 0; hi < 2; ++hi) {
-                    const int r = kb * 32 + hi * 16 + (lane >> 5) * 4 + (gi >> 2);
+                    const int r = (kbase + kb) * 32 + hi * 16 + (lane >> 5) * 4 + (gi >> 2);
                     const half4 x0 = lds_read_tr16(Vt + ksw<HD>(r, d >> 3) + (d & 7));
                     const half4 x1 = lds_read_tr16(Vt + ksw<HD>(r + 8, d >> 3) + (d & 7));
                     const half8 af = half8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
@@ -662,20 +668,49 @@ __global__ __launch_bounds__(64 * G) void k_attn_prefill(const vsl_half* __restr
     issue(1, phys(n_vt > 1 ? 1 : 0));
     VSL_VMCNT_WAIT(0);
     __syncthreads();
-    float16v st[2];
+    float16v st[NKB];
     qk(0, st);
     for (uint32_t t = 0; t < n_vt; ++t) {
         issue(buf_of(t + 2), phys(t + 2 < n_vt ? t + 2 : n_vt - 1));
         rescale(mask_max(st, phys(t)));
-        float16v sn[2];
+        float16v sn[NKB];
         qk(buf_of(t + 1), sn);
-        half8 pf[QP][2][2];
+        half8 pf[QP][NKB][2];
         l += probs(st, pf);
         pv(buf_of(t), pf);
-        st[0] = sn[0];
-        st[1] = sn[1];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) st[kb] = sn[kb];
         VSL_VMCNT_WAIT(0);
         __syncthreads();
+    }
+
+    if constexpr (KSPLIT == 2) {
+        // merge the two key halves of each head: the second wave leaves its accumulators and row
+        // statistics in the (now unused) tile buffers, the first rescales both to the larger maximum
+        // (every buffer read and every copy landed at the loop's last barrier)
+        constexpr int OSZ = HD / 32 * 16 * 64;  // accumulator floats per wave
+        const int hw = wave % G;
+        float* xo = reinterpret_cast<float*>(hw < 2 ? &Ks[0][0] : &Vs[0][0]) + (hw & 1) * (OSZ + 128);
+        static_assert(2 * (OSZ + 128) * 4 <= 3 * TK * HD * 2, "merge area exceeds a tile buffer set");
+        if (kbase == 1) {
+#pragma unroll
+            for (int tt = 0; tt < HD / 32; ++tt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) xo[(tt * 16 + v) * 64 + lane] = o[tt][v];
+            xo[OSZ + lane] = m;
+            xo[OSZ + 64 + lane] = l;
+        }
+        __syncthreads();
+        if (kbase == 1) return;
+        const float m1 = xo[OSZ + lane], l1 = xo[OSZ + 64 + lane];
+        const float mm = fmaxf(m, m1);
+        const float c0 = m == -INFINITY ? 0.f : fast_exp2(m - mm);
+        const float c1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - mm);
+        l = l * c0 + l1 * c1;
+#pragma unroll
+        for (int tt = 0; tt < HD / 32; ++tt)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[tt][v] = o[tt][v] * c0 + xo[(tt * 16 + v) * 64 + lane] * c1;
     }
 
     if (my_s >= S) return;
@@ -1019,9 +1054,13 @@ template <int HD, int G, bool WIN>
 static void launch_attn_prefill_w(dim3 grid, hipStream_t s, const vsl_half* q, const vsl_half* k, const vsl_half* v,
                                   uint32_t S, uint32_t pos0, uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
                                   vsl_half* o, bool qx2, int om, const PrefillWindow& w) {
-    constexpr int NT = 64 * G;
+    // two waves per query head (each half of every key tile) where the merge area -- the tile buffers
+    // -- holds the heads' accumulators: 8B shapes, S = 512 / 2048 rows at 0 / 2048 at 6144: 25.9 /
+    // 150 / 543 -> 25.1 / 142 / 511 us
+    constexpr int KS = G <= 4 ? 2 : 1;
+    constexpr int NT = 64 * G * KS;
     auto go = [&](auto qc, auto oc) {
-        k_attn_prefill<HD, G, decltype(qc)::value, decltype(oc)::value, WIN><<<grid, NT, 0, s>>>(
+        k_attn_prefill<HD, G, decltype(qc)::value, decltype(oc)::value, WIN, KS><<<grid, NT, 0, s>>>(
             q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
     };
     using T = std::true_type;
