@@ -451,15 +451,17 @@ __device__ __forceinline__ int ksw(int r, int c) {
 }
 
 // KSPLIT = 2: two waves per query head, each taking one 32-key half of every tile (its own online
-// softmax state), the halves merged through LDS at the end.
-template <int HD, int G, bool QX2, int OM, bool WIN, int KSPLIT>
-__global__ __launch_bounds__(64 * G * KSPLIT) void k_attn_prefill(const vsl_half* __restrict__ q, const vsl_half* __restrict__ kc,
+// softmax state), the halves merged through LDS at the end. GB: query heads per block (a divisor
+// of G); blockIdx.y = KV head * (G / GB) + the block's group of GB heads.
+template <int HD, int G, int GB, bool QX2, int OM, bool WIN, int KSPLIT>
+__global__ __launch_bounds__(64 * GB * KSPLIT) void k_attn_prefill(const vsl_half* __restrict__ q, const vsl_half* __restrict__ kc,
                                                          const vsl_half* __restrict__ vc, uint32_t S, uint32_t pos0,
                                                          uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
                                                          vsl_half* __restrict__ out, uint32_t win, uint32_t n_glob,
                                                          uint32_t thr) {
     constexpr int TK = kAttnTile;
-    constexpr int NT = 64 * G * KSPLIT;
+    constexpr int NT = 64 * GB * KSPLIT;
+    static_assert(G % GB == 0, "heads per block divide the group");
     constexpr int NKB = 2 / KSPLIT;             // 32-key halves of a tile per wave
     constexpr int CPR = HD / 8;                 // 16-byte chunks per K/V row
     constexpr int NCH = TK * CPR / NT;          // chunks per thread per tile (K and V each)
@@ -470,9 +472,9 @@ __global__ __launch_bounds__(64 * G * KSPLIT) void k_attn_prefill(const vsl_half
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n_qb = gridDim.x;
     const uint32_t qb = n_qb - 1 - blockIdx.x;  // the longest (latest) query blocks start first
-    const uint32_t kvh = blockIdx.y;
-    const int kbase = KSPLIT == 2 ? wave / G : 0;  // this wave's first 32-key half of each tile
-    const uint32_t h = kvh * G + wave % G;      // kv_head = head * n_kv / n_q
+    const uint32_t kvh = blockIdx.y / (G / GB);
+    const int kbase = KSPLIT == 2 ? wave / GB : 0;  // this wave's first 32-key half of each tile
+    const uint32_t h = kvh * G + (blockIdx.y % (G / GB)) * GB + wave % GB;  // kv_head = head * n_kv / n_q
     const uint32_t s_base = qb * 32;
     const uint32_t my_s = s_base + (lane & 31);  // query row owned by this lane (stats, O^T column)
     const uint32_t qw = n_q * HD;
@@ -689,7 +691,7 @@ __global__ __launch_bounds__(64 * G * KSPLIT) void k_attn_prefill(const vsl_half
         // statistics in the (now unused) tile buffers, the first rescales both to the larger maximum
         // (every buffer read and every copy landed at the loop's last barrier)
         constexpr int OSZ = HD / 32 * 16 * 64;  // accumulator floats per wave
-        const int hw = wave % G;
+        const int hw = wave % GB;
         float* xo = reinterpret_cast<float*>(hw < 2 ? &Ks[0][0] : &Vs[0][0]) + (hw & 1) * (OSZ + 128);
         static_assert(2 * (OSZ + 128) * 4 <= 3 * TK * HD * 2, "merge area exceeds a tile buffer set");
         if (kbase == 1) {
@@ -1056,12 +1058,21 @@ static void launch_attn_prefill_w(dim3 grid, hipStream_t s, const vsl_half* q, c
                                   vsl_half* o, bool qx2, int om, const PrefillWindow& w) {
     // two waves per query head (each half of every key tile) where the merge area -- the tile buffers
     // -- holds the heads' accumulators: 8B shapes, S = 512 / 2048 rows at 0 / 2048 at 6144: 25.9 /
-    // 150 / 543 -> 25.1 / 142 / 511 us
-    constexpr int KS = G <= 4 ? 2 : 1;
-    constexpr int NT = 64 * G * KS;
+    // 150 / 543 -> 25.1 / 142 / 511 us. Groups of 4 heads are split over two blocks when a block per
+    // (32 rows, KV head) would leave CUs idle.
+    constexpr int GB2 = G == 4 ? 2 : G;
+    const bool half = GB2 < G && (uint64_t)grid.x * grid.y < 256;
     auto go = [&](auto qc, auto oc) {
-        k_attn_prefill<HD, G, decltype(qc)::value, decltype(oc)::value, WIN, KS><<<grid, NT, 0, s>>>(
-            q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+        if (half) {
+            constexpr int KS = GB2 <= 4 ? 2 : 1;
+            const dim3 g2(grid.x, grid.y * (G / GB2));
+            k_attn_prefill<HD, G, GB2, decltype(qc)::value, decltype(oc)::value, WIN, KS><<<g2, 64 * GB2 * KS, 0, s>>>(
+                q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+        } else {
+            constexpr int KS = G <= 4 ? 2 : 1;
+            k_attn_prefill<HD, G, G, decltype(qc)::value, decltype(oc)::value, WIN, KS><<<grid, 64 * G * KS, 0, s>>>(
+                q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+        }
     };
     using T = std::true_type;
     using F = std::false_type;
