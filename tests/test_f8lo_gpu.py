@@ -228,7 +228,8 @@ def test_resid_rmsnorm_f8lo(vsl, orc, dev, H, M, N, K):
         assert_f8_encodes(hn[rows], vn[rows], nref)
 
 
-@pytest.mark.parametrize("hd,nq,nkv,S,pos0", [(128, 8, 2, 300, 0), (64, 4, 4, 97, 37), (128, 32, 8, 512, 0)])
+@pytest.mark.parametrize("hd,nq,nkv,S,pos0", [(128, 8, 2, 300, 0), (64, 4, 4, 97, 37), (128, 32, 8, 512, 0),
+                                              (128, 32, 8, 1024, 0)])
 def test_attn_prefill_f16f8_output(vsl, dev, H, hd, nq, nkv, S, pos0):
     """The prefill attention writing its output as F16F8: the same hi plane as the hi/lo fp16 output of
     the same call, bit for bit, and hi + lo8 2^-12 within e4m3 precision of hi + lo (so every byte sits

@@ -871,10 +871,13 @@ def test_gemm_swiglu_split_in_out(vsl, orc, dev, H):
     assert rel_err(c[0] + c[1], ref) < 2e-6
 
 
-@pytest.mark.parametrize("hd,nq,nkv,S,pos0", [(128, 32, 8, 77, 0), (64, 32, 8, 64, 100)])
+@pytest.mark.parametrize("hd,nq,nkv,S,pos0", [(128, 32, 8, 77, 0), (64, 32, 8, 64, 100), (128, 32, 8, 1056, 0)])
 def test_attn_prefill_split(vsl, orc, dev, H, hd, nq, nkv, S, pos0):
+    """Split q / split output prefill attention against the oracle. Fewer than 256 blocks of (32 rows,
+    KV head) split each group of four query heads over two blocks; 1056 rows on 8 KV heads (264 blocks)
+    keep one block per group."""
     rng = np.random.default_rng(hd + S + pos0 + 1)
-    cap, theta = 512, 10000.0
+    cap, theta = max(512, pos0 + S), 10000.0
     W = (nq + 2 * nkv) * hd
     qkv = rng.normal(0, 1, (S, W)).astype(np.float32)
     cs, sn = rope_tables(cap, hd, theta)
