@@ -1061,7 +1061,8 @@ static void launch_attn_prefill_w(dim3 grid, hipStream_t s, const vsl_half* q, c
     // 150 / 543 -> 25.1 / 142 / 511 us. Groups of 4 heads are split over two blocks when a block per
     // (32 rows, KV head) would leave CUs idle.
     constexpr int GB2 = G == 4 ? 2 : G;
-    const bool half = GB2 < G && (uint64_t)grid.x * grid.y < 256;
+    constexpr uint64_t kCUs = 256;  // MI355X compute units
+    const bool half = GB2 < G && (uint64_t)grid.x * grid.y < kCUs;
     auto go = [&](auto qc, auto oc) {
         if (half) {
             constexpr int KS = GB2 <= 4 ? 2 : 1;
