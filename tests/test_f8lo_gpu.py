@@ -146,13 +146,13 @@ def test_gemm_f8lo_tiles(vsl, dev, H, M, N, K, epi, cmode):
 
 @pytest.mark.parametrize("M,N,K,epi", [
     (512, 4096, 14336, 2),   # 8B down projection of a 512-row chunk
-    (512, 6144, 4096, 0),    # 8B QKV
+    (512, 6144, 4096, 0),    # 8B QKV (128 x 192 tiles)
     (128, 2048, 8192, 2),    # 1B down projection of a 128-row prompt: 32 chunks
     (300, 4096, 2048, 1),    # ragged M, fp16 store
 ])
 def test_gemm_f8lo_splitk(vsl, dev, H, M, N, K, epi):
     """Narrow shapes split over K with an F16F8 A: the partials come from the fp8 lo path of the
-    128 x 256 tiles; without the workspace the forced direct-to-LDS tiles give the same result (to
+    128 x 256 tiles (128 x 192 for the QKV width); without the workspace the forced direct-to-LDS tiles give the same result (to
     fp32 rounding of the accumulation order)."""
     rng = np.random.default_rng(3 * M + N + K + epi)
     A = rng.normal(0, 1, (M, K)).astype(np.float32)

@@ -625,7 +625,9 @@ def test_gemm_dma(vsl, orc, dev, H, M, N, K, epi, ax2, cx2):
 
 @pytest.mark.parametrize("M,N,K,epi,ax2", [
     (512, 4096, 14336, 2, True),   # down projection of a 512-row chunk: residual add, split A
-    (512, 6144, 4096, 0, True),    # QKV: fp32 store
+    (512, 6144, 4096, 0, True),    # QKV: fp32 store, 128 x 192 tiles (128 tiles x 2 chunks)
+    (512, 1536, 4096, 0, False),   # one-plane A on 128 x 192 tiles (32 tiles x 8 chunks)
+    (300, 6144, 4096, 2, True),    # ragged M on 128 x 192 tiles, residual add
     (512, 4096, 4096, 1, False),   # fp16 store
     (300, 4096, 2048, 2, False),   # ragged M
     (128, 2048, 8192, 2, True),    # 1B down projection of a 128-row prompt: 32 chunks of 256
@@ -633,8 +635,9 @@ def test_gemm_dma(vsl, orc, dev, H, M, N, K, epi, ax2, cx2):
     (128, 2048, 2048, 2, False),   # 1B O projection: the widest split (16) short of 192 items
 ])
 def test_gemm_splitk(vsl, dev, H, M, N, K, epi, ax2):
-    """Narrow shapes through vsl_gemm_f16_ws: split over K into a workspace, reduced in order with the
-    epilogue; a too-small workspace runs unsplit with the same result (to rounding)."""
+    """Narrow shapes through vsl_gemm_f16_ws: split over K into a workspace (128 x 256 tiles, or 128 x 192
+    where whole rounds of those cost less), reduced in order with the epilogue; a too-small workspace
+    runs unsplit with the same result (to rounding)."""
     rng = np.random.default_rng(M + N + K + epi)
     Af = rng.normal(0, 1, (M, K)).astype(np.float32)
     B = rng.normal(0, 0.02, (N, K)).astype(np.float16)

@@ -434,6 +434,10 @@ struct DmaPair {  // the one-plane, the split-A and the fp8-lo configuration of 
 // 106-113 for 4 x 2, 2 x 2 and 1 x 4 waves.
 using DmaBig = DmaPair<256, 256, 4, 2, 32, 2, 2, 0, 64>;
 using DmaMid = DmaPair<128, 256, 2, 4, 64>;
+// K-split partials of widths that are a multiple of 192 but whose 128 x 256 tiles leave CUs idle (the
+// QKV projection of a 512-row chunk: 6144 = 32 x 192, so 128 tiles x 2 chunks fill the 256 CUs
+// where 128 x 256 gives 192 work items): 2 x 2 waves of 64 x 96, one per SIMD.
+using DmaQ = DmaPair<128, 192, 2, 2, 64, 2, 2, 0, 64>;
 
 template <class G, int EPI>
 uint32_t dma_tiles(uint32_t M, uint32_t N) {
@@ -536,11 +540,28 @@ uint32_t vsl_gemm_splitk_plan(uint32_t M, uint32_t N, uint32_t K, int epi, uint3
     return widest && tiles * widest >= 64 ? take(widest) : 0;
 }
 
+// Which tile takes the K-split partials: the 128 x 192 tile when its whole rounds of 256 work items
+// cost less than the 128 x 256 tile's (tile area x rounds), else 128 x 256.
+static bool splitk_narrow(uint32_t M, uint32_t N, uint32_t ksplit) {
+    const uint64_t tq = dma_tiles<DmaQ::One, VSL_EPI_STORE_F32>(M, N);
+    const uint64_t tm = dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
+    if (!tq || !tm) return false;
+    const uint64_t rq = (tq * ksplit + 255) / 256, rm = (tm * ksplit + 255) / 256;
+    return rq * 192 < rm * 256;
+}
+
 void vsl_gemm_splitk_partials(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
                               uint32_t K, int am, float* ws) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const vsl_half* a = static_cast<const vsl_half*>(A);
+    const vsl_half* b = static_cast<const vsl_half*>(B);
+    if (splitk_narrow(M, N, ksplit)) {
+        const uint32_t tiles = dma_tiles<DmaQ::One, VSL_EPI_STORE_F32>(M, N);
+        launch_splitk<DmaQ>(tiles * ksplit, s, a, b, M, N, K, ws, ksplit, am);
+        return;
+    }
     const uint32_t tiles = dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
-    launch_splitk<DmaMid>(tiles * ksplit, static_cast<hipStream_t>(stream), static_cast<const vsl_half*>(A),
-                          static_cast<const vsl_half*>(B), M, N, K, ws, ksplit, am);
+    launch_splitk<DmaMid>(tiles * ksplit, s, a, b, M, N, K, ws, ksplit, am);
 }
 
 int vsl_gemm_splitk_launch(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
