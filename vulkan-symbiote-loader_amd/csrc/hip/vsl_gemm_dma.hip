@@ -304,12 +304,15 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
                 fload(nxt, Ln, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
+            // two waves per SIMD: the wave issuing matrix instructions goes first
+            if constexpr (NT > 256) __builtin_amdgcn_s_setprio(1);
             mfmas(cur);
             if constexpr (L8) {
                 const int t = BK == 64 ? ks : PAR * 2 + ks;  // k-step within the 64-column block
                 wconv(cur, t);
                 if (t == 3) mfmas8();
             }
+            if constexpr (NT > 256) __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
