@@ -42,10 +42,14 @@ constexpr int kC1 = kGemmC1, kCX2 = kGemmCX2, kCF8 = kGemmCF8;
 // Block tile BM x BN, BK halfs of K per stage, AP fp16 planes of A per stage (2: the hi and lo planes
 // of a split A share the stage's B tile), L8: an fp8 lo plane of A after the B tile, NBUF stage
 // buffers (together at most 128 KB of LDS), WGM x WGN waves of (BM / WGM) x (BN / WGN).
-template <int BM_, int BN_, int BK_, int AP_, int WGM_ = 2, int WGN_ = 2, bool L8_ = false, int NBUF_ = 0>
+template <int BM_, int BN_, int BK_, int AP_, int WGM_ = 2, int WGN_ = 2, bool L8_ = false, int NBUF_ = 0,
+          bool SF_ = false>
 struct DmaCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, AP = AP_, WGM = WGM_, WGN = WGN_;
     static constexpr bool L8 = L8_;
+    // SF: one fragment register set per wave (each k-step reads its own fragments and waits for them;
+    // the other wave of the SIMD covers the wait), for two-wave-per-SIMD tiles short of registers
+    static constexpr bool SF = SF_;
     static constexpr int NT = 64 * WGM * WGN;
     static constexpr int WM = BM / WGM, WN = BN / WGN, FM = WM / 32, FN = WN / 32;
     static constexpr int CPR = BK / 8;            // 16-byte chunks per tile row
@@ -316,6 +320,33 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
             __builtin_amdgcn_sched_barrier(0);
         }
     };
+    auto step_sf = [&](vsl_half* Lc, uint32_t s, auto par) {
+        constexpr int PAR = decltype(par)::value;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            fload(f0, Lc, ks);
+            if (ks == KS - 1) {
+                if constexpr (L8) {
+#pragma unroll
+                    for (int q = 0; q < BK / 32; ++q) lload(Lc, q, BK == 64 ? q : PAR);
+                }
+                VSL_LGKM_WAIT0();
+                VSL_VMCNT_WAIT((NBUF - 2) * kPerStage);
+                __builtin_amdgcn_s_barrier();
+                issue(Lc, s + NBUF);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (NT > 256) __builtin_amdgcn_s_setprio(1);
+            mfmas(f0);
+            if constexpr (L8) {
+                const int t = BK == 64 ? ks : PAR * 2 + ks;
+                wconv(f0, t);
+                if (t == 3) mfmas8();
+            }
+            if constexpr (NT > 256) __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
     issue(L0, 0);
@@ -326,18 +357,26 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
     }
     VSL_VMCNT_WAIT((NBUF - 1) * kPerStage);
     __builtin_amdgcn_s_barrier();
-    fload(f0, L0, 0);
-    if constexpr (NBUF == 4) {
-        for (uint32_t s = 0; s < nst; s += 4) {
-            step(L0, L1, s, P0{});
-            step(L1, L2, s + 1, P1{});
-            step(L2, L3, s + 2, P0{});
-            step(L3, L0, s + 3, P1{});
+    if constexpr (G::SF) {
+        static_assert(NBUF == 2, "the single-fragment step runs two stage buffers");
+        for (uint32_t s = 0; s < nst; s += 2) {
+            step_sf(L0, s, P0{});
+            step_sf(L1, s + 1, P1{});
         }
     } else {
-        for (uint32_t s = 0; s < nst; s += 2) {
-            step(L0, L1, s, P0{});
-            step(L1, L0, s + 1, P1{});
+        fload(f0, L0, 0);
+        if constexpr (NBUF == 4) {
+            for (uint32_t s = 0; s < nst; s += 4) {
+                step(L0, L1, s, P0{});
+                step(L1, L2, s + 1, P1{});
+                step(L2, L3, s + 2, P0{});
+                step(L3, L0, s + 3, P1{});
+            }
+        } else {
+            for (uint32_t s = 0; s < nst; s += 2) {
+                step(L0, L1, s, P0{});
+                step(L1, L0, s + 1, P1{});
+            }
         }
     }
     VSL_VMCNT_WAIT(0);  // the trailing loads land before the block's LDS is released
@@ -419,23 +458,24 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
 }
 
 template <int BM, int BN, int TWGM = 2, int TWGN = 2, int TBK = 32, int FWGM = TWGM, int FWGN = TWGN, int FNB = 0,
-          int FBK = TBK>
+          int FBK = TBK, bool FSF = false>
 struct DmaPair {  // the one-plane, the split-A and the fp8-lo configuration of a block tile
     using One = DmaCfg<BM, BN, 32, 1>;
     using Two = DmaCfg<BM, BN, TBK, 2, TWGM, TWGN>;
-    using F8 = DmaCfg<BM, BN, FBK, 1, FWGM, FWGN, true, FNB>;
+    using F8 = DmaCfg<BM, BN, FBK, 1, FWGM, FWGN, true, FNB, FSF>;
 };
 // The split-A tiles run eight waves (two per SIMD, 128 accumulators each): 4 x 2 waves of 64 x 128 for
 // 256 x 256, 2 x 4 waves of 64 x 64 for 128 x 256 (the one-plane tiles keep 2 x 2 waves of 128 x 128).
 // The split 128 x 256 tile takes BK = 64 (two 64 KB stages, half the barriers): the K-split partials
 // of a 512-row chunk, O 37.8 -> 36.6 us, down 109.9 -> 104.5 us, QKV level.
-// fp8-lo tiles: 256 x 256 as 2 x 2 waves of 128 x 128 with BK = 64 (two 80 KB stages, all of the
-// LDS; each row's 128-byte line of a stage comes in one load instruction instead of two 64-byte
-// halves): gate/up 2048 rows 754 -> 690 us, 512 rows 195 -> 185 us against 4 x 2 waves at BK = 32
-// (BK = 32 with 2 x 2 waves, or with four stage buffers: level; 4 x 2 waves at BK = 64 spill). The
-// 128 x 256 fp8-lo tile keeps 2 x 4 waves at BK = 64 (56 KB stages): down 512 rows 102 us against
-// 106-113 for 4 x 2, 2 x 2 and 1 x 4 waves.
-using DmaBig = DmaPair<256, 256, 4, 2, 32, 2, 2, 0, 64>;
+// fp8-lo tiles: 256 x 256 with BK = 64 (two 80 KB stages, all of the LDS; each row's 128-byte line
+// of a stage comes in one load instruction instead of two 64-byte halves): gate/up 2048 rows 754 ->
+// 690 us, 512 rows 195 -> 185 us for 2 x 2 waves of 128 x 128 against 4 x 2 waves at BK = 32. Since
+// then 4 x 2 waves of 64 x 128 (two per SIMD, each raising its priority for its MFMAs) with one
+// fragment register set per wave (SF; with two sets they spill): 2048 rows 688 -> 673 us, 512 rows
+// level. The 128 x 256 fp8-lo tile keeps 2 x 4 waves at BK = 64 (56 KB stages): down 512 rows 102 us
+// against 106-113 for 4 x 2, 2 x 2 and 1 x 4 waves.
+using DmaBig = DmaPair<256, 256, 4, 2, 32, 4, 2, 0, 64, true>;
 using DmaMid = DmaPair<128, 256, 2, 4, 64>;
 // K-split partials of widths that are a multiple of 192 but whose 128 x 256 tiles leave CUs idle (the
 // QKV projection of a 512-row chunk: 6144 = 32 x 192, so 128 tiles x 2 chunks fill the 256 CUs
