@@ -90,6 +90,7 @@ def test_rmsnorm_f16f8_needs_whole_blocks(vsl, dev, H):
 @pytest.mark.parametrize("M,N,K,epi,cmode", [
     (512, 14336, 2048, 3, "f8"),    # SwiGLU, 256 x 256 tiles, F16F8 output
     (512, 14336, 2048, 3, "x2"),    # F16F8 in, hi/lo fp16 out
+    (700, 14336, 1024, 3, "f8"),    # ragged M on the 256 x 256 tiles (rows 512..699 in the last tile)
     (777, 4096, 2048, 3, "f16"),    # ragged M on 128 x 256 tiles, fp16 out
     (777, 4096, 2048, 3, "f8"),
     (2048, 6144, 4096, 0, None),    # fp32 store, 256 x 256
