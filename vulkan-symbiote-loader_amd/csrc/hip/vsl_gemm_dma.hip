@@ -479,8 +479,9 @@ using DmaBig = DmaPair<256, 256, 4, 2, 32, 4, 2, 0, 64, true>;
 using DmaMid = DmaPair<128, 256, 2, 4, 64>;
 // K-split partials of widths that are a multiple of 192 but whose 128 x 256 tiles leave CUs idle (the
 // QKV projection of a 512-row chunk: 6144 = 32 x 192, so 128 tiles x 2 chunks fill the 256 CUs
-// where 128 x 256 gives 192 work items): 2 x 2 waves of 64 x 96, one per SIMD.
-using DmaQ = DmaPair<128, 192, 2, 2, 64, 2, 2, 0, 64>;
+// where 128 x 256 gives 192 work items): 4 x 2 waves of 32 x 96, two per SIMD (against 2 x 2 waves
+// of 64 x 96: hi/lo QKV with its reduce 62.9 -> 60.8 us at 512 rows, 61.3 -> 57.8 at 300).
+using DmaQ = DmaPair<128, 192, 4, 2, 64, 4, 2, 0, 64>;
 
 template <class G, int EPI>
 uint32_t dma_tiles(uint32_t M, uint32_t N) {
