@@ -679,6 +679,38 @@ def test_gemm_f16_swiglu(vsl, orc, dev, H):
     assert rel_err(dev.get(C).astype(np.float32), ref) < 2.0 ** -9
 
 
+@pytest.mark.parametrize("M,N,K,epi,ax2", [
+    (128, 8192, 2048, 3, True),     # 1B gate/up of a 128-row prompt: 2 x 128 tiles of 64 x (64 + 64)
+    (100, 8192, 2048, 3, False),    # ragged M, one-plane A
+    (128, 16384, 2048, 0, True),    # fp32 store without a workspace: 2 x 128 tiles of 64 x 128
+])
+def test_gemm_small_rows(vsl, orc, dev, H, M, N, K, epi, ax2):
+    """Few-row shapes that reach neither 192 tiles of 128 x 256 nor a K split (no workspace) run the
+    64 x 128 direct-to-LDS tiles: against the fp64 product (SwiGLU applied in fp64)."""
+    rng = np.random.default_rng(M + N + K)
+    Af = rng.normal(0, 1, (M, K)).astype(np.float32)
+    nb = 2 * N if epi == 3 else N
+    B = rng.normal(0, 0.02, (nb, K)).astype(np.float16)
+    if ax2:
+        hi = Af.astype(np.float16)
+        lo = (Af - hi.astype(np.float32)).astype(np.float16)
+        Ad, Aref = np.concatenate([hi, lo]), hi.astype(np.float64) + lo.astype(np.float64)
+    else:
+        Ad = Af.astype(np.float16)
+        Aref = Ad.astype(np.float64)
+    flags = epi | (vsl.GEMM_A_X2 if ax2 else 0)
+    C = dev.empty((M, N), np.float16 if epi == 3 else np.float32)
+    ok(vsl, H.vsl_gemm_f16(dev.p(dev.put(Ad)), dev.p(dev.put(B)), M, N, K, dev.p(C), flags, None))
+    rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, 24)]))
+    prod = Aref[rows] @ B.astype(np.float64).T
+    out = dev.get(C).astype(np.float64)[rows]
+    if epi == 3:
+        ref = prod[:, :N] / (1.0 + np.exp(-prod[:, :N])) * prod[:, N:]
+        assert rel_err(out, ref) < 2.0 ** -10
+    else:
+        assert rel_err(out, prod) < 1e-5
+
+
 @pytest.mark.parametrize("hd,nq,nkv,S,pos0", [(128, 32, 8, 77, 0), (128, 32, 8, 64, 100), (64, 32, 8, 200, 0),
                                               (64, 8, 8, 33, 5)])
 def test_rope_split_and_attn_prefill(vsl, orc, dev, H, hd, nq, nkv, S, pos0):

@@ -477,6 +477,9 @@ struct DmaPair {  // the one-plane, the split-A and the fp8-lo configuration of 
 // against 106-113 for 4 x 2, 2 x 2 and 1 x 4 waves.
 using DmaBig = DmaPair<256, 256, 4, 2, 32, 4, 2, 0, 64, true>;
 using DmaMid = DmaPair<128, 256, 2, 4, 64>;
+// Few-row shapes without a K split (a 128-row prompt's SwiGLU: 2 x 128 tiles of 64 rows x 64 outputs):
+// 2 x 2 waves of 32 x 64 (one gate and one up fragment per wave for SwiGLU).
+using DmaSmall = DmaPair<64, 128, 2, 2, 64>;
 // K-split partials of widths that are a multiple of 192 but whose 128 x 256 tiles leave CUs idle (the
 // QKV projection of a 512-row chunk: 6144 = 32 x 192, so 128 tiles x 2 chunks fill the 256 CUs
 // where 128 x 256 gives 192 work items): 4 x 2 waves of 32 x 96, two per SIMD (against 2 x 2 waves
@@ -537,18 +540,23 @@ int launch_epi(int cfg, hipStream_t s, const vsl_half* a, const vsl_half* b, uin
         const uint32_t t = dma_tiles<DmaBig::One, EPI>(M, N);
         if (!t) return -1;
         launch_cfg<DmaBig, EPI>(t, s, a, b, M, N, K, C, am, cm);
-    } else {
+    } else if (cfg == 1) {
         const uint32_t t = dma_tiles<DmaMid::One, EPI>(M, N);
         if (!t) return -1;
         launch_cfg<DmaMid, EPI>(t, s, a, b, M, N, K, C, am, cm);
+    } else {
+        const uint32_t t = dma_tiles<DmaSmall::One, EPI>(M, N);
+        if (!t) return -1;
+        launch_cfg<DmaSmall, EPI>(t, s, a, b, M, N, K, C, am, cm);
     }
     return 0;
 }
 
 }  // namespace
 
-// Tiles of the direct-to-LDS GEMM for a shape: config 0 is 256 x 256, config 1 is 128 x 256; 0 when
-// the shape does not fit the configuration (N not a multiple of the tile width, K not of 128).
+// Tiles of the direct-to-LDS GEMM for a shape: config 0 is 256 x 256, config 1 is 128 x 256, config 2
+// is 64 x 128; 0 when the shape does not fit the configuration (N not a multiple of the tile width, K
+// not of 128).
 uint32_t vsl_gemm_dma_tiles(int cfg, uint32_t M, uint32_t N, uint32_t K, int epi) {
     if (K % kKAlign || K == 0) return 0;
     const uint64_t brows = epi == VSL_EPI_SWIGLU ? 2ull * N : N;
@@ -556,7 +564,9 @@ uint32_t vsl_gemm_dma_tiles(int cfg, uint32_t M, uint32_t N, uint32_t K, int epi
     const bool sw = epi == VSL_EPI_SWIGLU;
     if (cfg == 0)
         return sw ? dma_tiles<DmaBig::One, VSL_EPI_SWIGLU>(M, N) : dma_tiles<DmaBig::One, VSL_EPI_STORE_F32>(M, N);
-    return sw ? dma_tiles<DmaMid::One, VSL_EPI_SWIGLU>(M, N) : dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
+    if (cfg == 1)
+        return sw ? dma_tiles<DmaMid::One, VSL_EPI_SWIGLU>(M, N) : dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
+    return sw ? dma_tiles<DmaSmall::One, VSL_EPI_SWIGLU>(M, N) : dma_tiles<DmaSmall::One, VSL_EPI_STORE_F32>(M, N);
 }
 
 // Split-K plan for shapes whose tiles leave CUs idle: the 128 x 256 tiling with the smallest split

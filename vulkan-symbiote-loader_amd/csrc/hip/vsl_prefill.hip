@@ -815,6 +815,9 @@ static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint
         return vsl_unsupported("vsl_gemm_f16: F16F8 operands need N %% 256 == 0 (128 for SwiGLU) and K %% 128 == 0 "
                                "(shape %ux%ux%u)", M, N, K);
     }
+    // few rows without a K split (e.g. a 128-row prompt's SwiGLU): the 64 x 128 direct-to-LDS tiles
+    if (vsl_gemm_dma_tiles(2, M, N, K, EPI) >= kDmaMinTiles && vsl_gemm_dma_launch(2, s, a, b, M, N, K, C, EPI, am, cm) == 0)
+        return VSL_OK;
     const bool ax2 = am == kGemmAX2, cx2 = cm == kGemmCX2;
     const uint32_t tb = gemm_tiles<GemmBig, EPI>(M, N), tm = gemm_tiles<GemmMid, EPI>(M, N);
     const uint32_t ts = gemm_tiles<GemmSmall, EPI>(M, N);
