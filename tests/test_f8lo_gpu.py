@@ -153,7 +153,8 @@ def test_gemm_f8lo_tiles(vsl, dev, H, M, N, K, epi, cmode):
 ])
 def test_gemm_f8lo_splitk(vsl, dev, H, M, N, K, epi):
     """Narrow shapes split over K with an F16F8 A: the partials come from the fp8 lo path of the
-    128 x 256 tiles (128 x 192 for the QKV width); without the workspace the forced direct-to-LDS tiles give the same result (to
+    128 x 256 tiles (128 x 192 for the QKV width); without the workspace the direct-to-LDS tiles (64 x
+    128 where they give 192 tiles, else the larger ones at lower occupancy) give the same result (to
     fp32 rounding of the accumulation order)."""
     rng = np.random.default_rng(3 * M + N + K + epi)
     A = rng.normal(0, 1, (M, K)).astype(np.float32)

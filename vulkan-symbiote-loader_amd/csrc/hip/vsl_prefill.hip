@@ -806,9 +806,13 @@ static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint
             return vsl_invalid("vsl_gemm_f16: split-K epilogue %d", EPI);
         return VSL_OK;
     }
-    // the fp8 lo forms exist in the direct-to-LDS kernel only: take its tiles even when they leave
-    // CUs idle
+    // the fp8 lo forms exist in the direct-to-LDS kernel only: on shapes its 128 x 256 tiles take, its
+    // 64 x 128 tiles where those cover the CUs (no workspace: O of a 512-row chunk 94 -> 56 us with its
+    // RMSNorm), else its larger tiles even when they leave CUs idle
     if (am == kGemmAF8 || cm == kGemmCF8) {
+        if (vsl_gemm_dma_tiles(1, M, N, K, EPI) && vsl_gemm_dma_tiles(2, M, N, K, EPI) >= kDmaMinTiles &&
+            vsl_gemm_dma_launch(2, s, a, b, M, N, K, C, EPI, am, cm) == 0)
+            return VSL_OK;
         for (int cfg = 1; cfg >= 0; --cfg)
             if (vsl_gemm_dma_tiles(cfg, M, N, K, EPI) && vsl_gemm_dma_launch(cfg, s, a, b, M, N, K, C, EPI, am, cm) == 0)
                 return VSL_OK;
