@@ -79,13 +79,15 @@ def test_gemv_sweep(vsl, orc, dev, H, N, K, B):
 
 
 @pytest.mark.parametrize("N,K,B", [(9000, 1536, 12), (8200, 512, 16), (16, 512, 1), (8193, 2560, 8), (8191, 1024, 9),
-                                   (9000, 2048, 12), (8191, 4096, 9), (17, 6144, 16), (1, 3072, 13)])
+                                   (9000, 2048, 12), (8191, 4096, 9), (17, 6144, 16), (1, 3072, 13),
+                                   (13000, 2048, 16), (26003, 1024, 11)])
 def test_gemv_batched_ragged(vsl, orc, dev, H, N, K, B):
     """The sweep kernel on shapes outside the sweep: N not a multiple of the 16- or 32-row tiles (the
     two-tile blocks from N >= 8192 and B >= 8), K a multiple of 512 only, B neither 1, 4 nor 16;
     X [B][K] and X [K][B] layouts. With K % 1024 == 0 and B > 8 the [B][K] product stages both
     operands through LDS (a single row, 17 rows, vectors past B masked; 1536 and 2560 keep the
-    register-fragment kernel)."""
+    register-fragment kernel), with two (N >= 12800) or four (N >= 25600) 16-row groups per block
+    sharing each staged X chunk (13000 and 26003 rows: the last block partly past N)."""
     rng = np.random.default_rng(N + K + B)
     W = rng.normal(0, 0.02, (N, K)).astype(np.float16)
     X = rng.normal(0, 1, (K, B)).astype(np.float16)

@@ -1840,6 +1840,8 @@ struct SlCfg {
 };
 using SlDefault = SlCfg<128, 2>;
 constexpr uint32_t kSlKAlign = SlDefault::KALIGN;  // K multiple: whole buffer rounds per wave
+static_assert(SlDefault::KALIGN % SlCfg<64, 2>::KALIGN == 0, "the row-group variants take the same K");
+constexpr uint32_t kSlRowsFor4 = 25600, kSlRowsFor2 = 12800;  // N from which 4 / 2 row groups per block
 
 template <class C, typename YT>
 __global__ __launch_bounds__(kSlWaves * 64) void k_skinny_lds(const vsl_half* __restrict__ W, uint32_t N, uint32_t K,
@@ -1908,6 +1910,96 @@ __global__ __launch_bounds__(kSlWaves * 64) void k_skinny_lds(const vsl_half* __
         float v = 0.f;
 #pragma unroll
         for (int w = 0; w < kSlWaves; ++w) v += part[w][m][n];
+        const uint32_t row = row0 + m;
+        if (row < N && n < B) store_elem(Y + (size_t)n * N + row, v);
+    }
+}
+
+// The same with RB 16-row groups of W per block sharing every staged X chunk (X crosses L2 -> LDS once
+// per RB x 16 rows instead of once per 16); each wave's partial tile goes through its own buffers.
+template <class C, int RB, typename YT>
+__global__ __launch_bounds__(kSlWaves * 64) void k_skinny_lds_rg(const vsl_half* __restrict__ W, uint32_t N, uint32_t K,
+                                                             const vsl_half* __restrict__ X, uint32_t B,
+                                                             YT* __restrict__ Y) {
+    constexpr uint32_t CH = C::CH, REGX = 16 * CH, REGW = RB * REGX;  // halfs per operand region
+    constexpr int NB = C::NB;
+    constexpr uint32_t NLDW = RB * C::NLD;  // W load instructions per chunk
+    constexpr uint32_t PSTRIDE = 17;        // floats per row of a wave's partial tile (padded)
+    static_assert((REGW + REGX) * 2 * NB >= 16 * RB * PSTRIDE * 4, "partials fit in a wave's buffers");
+    __shared__ __attribute__((aligned(16))) vsl_half buf[kSlWaves][NB][REGW + REGX];  // [wave][buffer][W | X]
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t row0 = blockIdx.x * 16 * RB;
+    const uint32_t kw = K / kSlWaves, k_begin = wave * kw, nch = kw / CH;
+    // load instruction j covers rows / vectors RPI j .. RPI j + RPI - 1 (LPR lanes each); lane position
+    // p of its row holds logical chunk pos(p, row) (the swizzle is its own inverse)
+    const uint32_t p = lane % C::LPR, rsub = lane / C::LPR;
+    uint32_t woff[NLDW], xoff[C::NLD];
+#pragma unroll
+    for (int j = 0; j < (int)NLDW; ++j) {
+        const uint32_t rr = C::RPI * j + rsub;
+        const uint32_t wrow = row0 + rr < N ? row0 + rr : N - 1;  // rows past N: never stored
+        woff[j] = (wrow * K + k_begin + C::pos(p, rr) * 8) * 2;
+    }
+#pragma unroll
+    for (int j = 0; j < (int)C::NLD; ++j) {
+        const uint32_t rr = C::RPI * j + rsub;
+        const uint32_t xcol = rr < B ? rr : B - 1;  // vectors past B: masked
+        xoff[j] = (xcol * K + k_begin + C::pos(p, rr) * 8) * 2;
+    }
+    auto issue = [&](uint32_t c, int bsel) {
+        const uint32_t cc = c < nch ? c : nch - 1;  // past the end: re-load the last chunk (never read)
+        vsl_half* L = buf[wave][bsel];
+#pragma unroll
+        for (int j = 0; j < (int)NLDW; ++j) lds_load16(W + cc * CH, woff[j], L + j * 512);
+#pragma unroll
+        for (int j = 0; j < (int)C::NLD; ++j) lds_load16(X + cc * CH, xoff[j], L + REGW + j * 512);
+    };
+    const uint32_t r = lane & 15, g = lane >> 4;
+    const uint32_t bmask = r < B ? 0xFFFFFFFFu : 0u;  // this lane's X fragment is vector r
+    float4v acc[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = float4v{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](int bsel) {
+        const vsl_half* L = buf[wave][bsel];
+#pragma unroll
+        for (int u = 0; u < (int)(CH / 32); ++u) {
+            const uint32_t pos = C::pos(4 * u + g, r) * 8;  // rows 16 rb + r share the swizzle of row r
+            uint4 xv = __builtin_bit_cast(uint4, *reinterpret_cast<const half8*>(L + REGW + r * CH + pos));
+            xv = make_uint4(xv.x & bmask, xv.y & bmask, xv.z & bmask, xv.w & bmask);
+            const half8 xf = __builtin_bit_cast(half8, xv);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                const half8 a = *reinterpret_cast<const half8*>(L + (rb * 16 + r) * CH + pos);
+                acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xf, acc[rb], 0, 0, 0);
+            }
+        }
+    };
+    // chunk c in buffer c % NB; chunks c + 1 .. c + NB - 1 in flight while c is consumed; nch % NB == 0
+    constexpr int kPer = NLDW + C::NLD;  // loads per chunk
+#pragma unroll
+    for (int b = 0; b < NB - 1; ++b) issue(b, b);
+    for (uint32_t c = 0; c < nch; c += NB) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            issue(c + b + NB - 1, (b + NB - 1) % NB);
+            VSL_VMCNT_WAIT((NB - 1) * kPer);
+            consume(b);
+            VSL_LGKM_WAIT0();  // buffer b fully read before it is refilled
+        }
+    }
+    VSL_VMCNT_WAIT(0);  // the trailing re-loads land before the buffers take the partials
+    // each wave's partial tile goes into its own (now idle) buffers; summed over the waves in order
+    float* part = reinterpret_cast<float*>(&buf[wave][0][0]);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[(rb * 16 + (lane >> 4) * 4 + i) * PSTRIDE + r] = acc[rb][i];
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < 16 * 16 * RB; e += kSlWaves * 64) {
+        const uint32_t m = e >> 4, n = e & 15;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kSlWaves; ++w) v += reinterpret_cast<const float*>(&buf[w][0][0])[m * PSTRIDE + n];
         const uint32_t row = row0 + m;
         if (row < N && n < B) store_elem(Y + (size_t)n * N + row, v);
     }
@@ -2173,12 +2265,25 @@ extern "C" int vsl_gemv_batched(const void* W, uint32_t N, uint32_t K, const voi
         return ydtype == VSL_DT_F16 ? launch_rows<vsl_half>(W, N, K, X, B, Y, s) : launch_rows<float>(W, N, K, X, B, Y, s);
     if (K % kSlKAlign == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ((uint64_t)N * K * 2) >> 32 == 0 &&
         ((uint64_t)B * K * 2) >> 32 == 0) {
-        if (ydtype == VSL_DT_F16)
-            k_skinny_lds<SlDefault, vsl_half><<<(N + 15) / 16, kSlWaves * 64, 0, s>>>(
-                static_cast<const vsl_half*>(W), N, K, static_cast<const vsl_half*>(X), B, static_cast<vsl_half*>(Y));
+        const vsl_half* w = static_cast<const vsl_half*>(W);
+        const vsl_half* x = static_cast<const vsl_half*>(X);
+        auto go = [&](auto rbc) {
+            using C = SlCfg<64, 2>;
+            constexpr int RB = decltype(rbc)::value;
+            const uint32_t grid = (N + 16 * RB - 1) / (16 * RB);
+            if (ydtype == VSL_DT_F16)
+                k_skinny_lds_rg<C, RB, vsl_half><<<grid, kSlWaves * 64, 0, s>>>(w, N, K, x, B, static_cast<vsl_half*>(Y));
+            else
+                k_skinny_lds_rg<C, RB, float><<<grid, kSlWaves * 64, 0, s>>>(w, N, K, x, B, static_cast<float*>(Y));
+        };
+        // tall W: several 16-row groups per block share each staged X chunk, as long as the grid keeps
+        // about two blocks per CU
+        if (N >= kSlRowsFor4) go(std::integral_constant<int, 4>{});
+        else if (N >= kSlRowsFor2) go(std::integral_constant<int, 2>{});
+        else if (ydtype == VSL_DT_F16)
+            k_skinny_lds<SlDefault, vsl_half><<<(N + 15) / 16, kSlWaves * 64, 0, s>>>(w, N, K, x, B, static_cast<vsl_half*>(Y));
         else
-            k_skinny_lds<SlDefault, float><<<(N + 15) / 16, kSlWaves * 64, 0, s>>>(
-                static_cast<const vsl_half*>(W), N, K, static_cast<const vsl_half*>(X), B, static_cast<float*>(Y));
+            k_skinny_lds<SlDefault, float><<<(N + 15) / 16, kSlWaves * 64, 0, s>>>(w, N, K, x, B, static_cast<float*>(Y));
         HIP_TRY(hipGetLastError());
         return VSL_OK;
     }
