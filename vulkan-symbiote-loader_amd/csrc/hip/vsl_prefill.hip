@@ -450,30 +450,34 @@ __device__ __forceinline__ int ksw(int r, int c) {
     else return r * HD + ((c ^ ((r >> 1) & 7)) * 8);                      // 128-byte rows: row pairs
 }
 
-// KSPLIT = 2: two waves per query head, each taking one 32-key half of every tile (its own online
-// softmax state), the halves merged through LDS at the end. GB: query heads per block (a divisor
-// of G); blockIdx.y = KV head * (G / GB) + the block's group of GB heads.
-template <int HD, int G, int GB, bool QX2, int OM, bool WIN, int KSPLIT>
+// KSPLIT = 2 / 4: two / four waves per query head, each taking one 32-key block of every tile (its
+// own online softmax state), merged through LDS at the end. GB: query heads per block (a divisor of
+// G); blockIdx.y = KV head * (G / GB) + the block's group of GB heads. TK keys per tile, NBUF tile
+// buffers (3: the next tile's scores are issued while the current tile's probabilities are formed;
+// 2: one tile copied ahead, each tile's scores after its copy landed).
+template <int HD, int G, int GB, bool QX2, int OM, bool WIN, int KSPLIT, int TK = kAttnTile, int NBUF = 3>
 __global__ __launch_bounds__(64 * GB * KSPLIT) void k_attn_prefill(const vsl_half* __restrict__ q, const vsl_half* __restrict__ kc,
                                                          const vsl_half* __restrict__ vc, uint32_t S, uint32_t pos0,
                                                          uint32_t n_q, uint32_t n_kv, uint32_t cap, float scale,
                                                          vsl_half* __restrict__ out, uint32_t win, uint32_t n_glob,
                                                          uint32_t thr) {
-    constexpr int TK = kAttnTile;
     constexpr int NT = 64 * GB * KSPLIT;
     static_assert(G % GB == 0, "heads per block divide the group");
-    constexpr int NKB = 2 / KSPLIT;             // 32-key halves of a tile per wave
+    static_assert(NBUF == 2 || NBUF == 3, "two or three tile buffers");
+    constexpr int NKB = TK / 32 / KSPLIT;       // 32-key blocks of a tile per wave
+    static_assert(NKB >= 1 && NKB * KSPLIT * 32 == TK, "a tile's key blocks divide over the waves of a head");
     constexpr int CPR = HD / 8;                 // 16-byte chunks per K/V row
     constexpr int NCH = TK * CPR / NT;          // chunks per thread per tile (K and V each)
     constexpr int QP = QX2 ? 2 : 1;             // q planes; with split q the probabilities are split too
     static_assert(NCH >= 1 && TK * CPR % NT == 0, "tile does not divide over the block");
-    __shared__ __attribute__((aligned(16))) vsl_half Ks[3][TK * HD];
-    __shared__ __attribute__((aligned(16))) vsl_half Vs[3][TK * HD];
+    __shared__ __attribute__((aligned(16))) vsl_half Ks[NBUF][TK * HD];
+    __shared__ __attribute__((aligned(16))) vsl_half Vs[NBUF][TK * HD];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n_qb = gridDim.x;
     const uint32_t qb = n_qb - 1 - blockIdx.x;  // the longest (latest) query blocks start first
     const uint32_t kvh = blockIdx.y / (G / GB);
-    const int kbase = KSPLIT == 2 ? wave / GB : 0;  // this wave's first 32-key half of each tile
+    const int ksp = wave / GB;                  // this wave's share of every tile (0 .. KSPLIT-1)
+    const int kbase = ksp * NKB;                // its first 32-key block
     const uint32_t h = kvh * G + (blockIdx.y % (G / GB)) * GB + wave % GB;  // kv_head = head * n_kv / n_q
     const uint32_t s_base = qb * 32;
     const uint32_t my_s = s_base + (lane & 31);  // query row owned by this lane (stats, O^T column)
@@ -665,36 +669,65 @@ __global__ __launch_bounds__(64 * GB * KSPLIT) void k_attn_prefill(const vsl_hal
     // products; each wave waits for its own copies and the block meets at a barrier (every copy of
     // t+2 is in LDS, every wave has finished reading buffer t, which iteration t+1 overwrites).
     // Requests past the last tile re-copy it (finite values; scores computed from them are unused).
-    auto buf_of = [](uint32_t t) { return (int)(t % 3); };
-    issue(0, phys(0));
-    issue(1, phys(n_vt > 1 ? 1 : 0));
-    VSL_VMCNT_WAIT(0);
-    __syncthreads();
-    float16v st[NKB];
-    qk(0, st);
-    for (uint32_t t = 0; t < n_vt; ++t) {
-        issue(buf_of(t + 2), phys(t + 2 < n_vt ? t + 2 : n_vt - 1));
-        rescale(mask_max(st, phys(t)));
-        float16v sn[NKB];
-        qk(buf_of(t + 1), sn);
-        half8 pf[QP][NKB][2];
-        l += probs(st, pf);
-        pv(buf_of(t), pf);
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) st[kb] = sn[kb];
+    if constexpr (NBUF == 3) {
+        auto buf_of = [](uint32_t t) { return (int)(t % 3); };
+        issue(0, phys(0));
+        issue(1, phys(n_vt > 1 ? 1 : 0));
         VSL_VMCNT_WAIT(0);
         __syncthreads();
+        float16v st[NKB];
+        qk(0, st);
+        for (uint32_t t = 0; t < n_vt; ++t) {
+            issue(buf_of(t + 2), phys(t + 2 < n_vt ? t + 2 : n_vt - 1));
+            rescale(mask_max(st, phys(t)));
+            float16v sn[NKB];
+            qk(buf_of(t + 1), sn);
+            half8 pf[QP][NKB][2];
+            l += probs(st, pf);
+            pv(buf_of(t), pf);
+#pragma unroll
+            for (int kb = 0; kb < NKB; ++kb) st[kb] = sn[kb];
+            VSL_VMCNT_WAIT(0);
+            __syncthreads();
+        }
+    } else {
+        // two buffers: tile t+1 is copied into the buffer tile t-1 used (free since the barrier that
+        // ended iteration t-1) while tile t is computed; each wave waits for its own copies and the
+        // block meets at a barrier before tile t+1 is read
+        issue(0, phys(0));
+        VSL_VMCNT_WAIT(0);
+        __syncthreads();
+        for (uint32_t t = 0; t < n_vt; ++t) {
+            issue((int)((t + 1) & 1), phys(t + 1 < n_vt ? t + 1 : n_vt - 1));
+            float16v st[NKB];
+            qk((int)(t & 1), st);
+            rescale(mask_max(st, phys(t)));
+            half8 pf[QP][NKB][2];
+            l += probs(st, pf);
+            pv((int)(t & 1), pf);
+            VSL_VMCNT_WAIT(0);
+            __syncthreads();
+        }
     }
 
-    if constexpr (KSPLIT == 2) {
-        // merge the two key halves of each head: the second wave leaves its accumulators and row
-        // statistics in the (now unused) tile buffers, the first rescales both to the larger maximum
-        // (every buffer read and every copy landed at the loop's last barrier)
+    if constexpr (KSPLIT > 1) {
+        // merge the key shares of each head: waves with ksp > 0 leave their accumulators and row
+        // statistics in the (now unused) tile buffers, the ksp = 0 wave rescales all to the largest
+        // maximum (every buffer read and every copy landed at the loop's last barrier)
         constexpr int OSZ = HD / 32 * 16 * 64;  // accumulator floats per wave
+        constexpr int SLOT = OSZ + 128;
         const int hw = wave % GB;
-        float* xo = reinterpret_cast<float*>(hw < 2 ? &Ks[0][0] : &Vs[0][0]) + (hw & 1) * (OSZ + 128);
-        static_assert(2 * (OSZ + 128) * 4 <= 3 * TK * HD * 2, "merge area exceeds a tile buffer set");
-        if (kbase == 1) {
+        static_assert(KSPLIT == 2 ? 2 * SLOT * 4 <= NBUF * TK * HD * 2 : (KSPLIT - 1) * SLOT * 4 <= NBUF * TK * HD * 2,
+                      "merge area exceeds a tile buffer set");
+        static_assert(KSPLIT == 2 || GB <= 2, "four shares per head: at most two heads per block");
+        // slot of (head hw, share j >= 1): KSPLIT = 2 packs two heads per buffer set, KSPLIT = 4 gives
+        // each head its own set (K buffers for head 0, V buffers for head 1)
+        auto slot = [&](int j) {
+            if constexpr (KSPLIT == 2) return reinterpret_cast<float*>(hw < 2 ? &Ks[0][0] : &Vs[0][0]) + (hw & 1) * SLOT;
+            else return reinterpret_cast<float*>(hw == 0 ? &Ks[0][0] : &Vs[0][0]) + (j - 1) * SLOT;
+        };
+        if (ksp > 0) {
+            float* xo = slot(ksp);
 #pragma unroll
             for (int tt = 0; tt < HD / 32; ++tt)
 #pragma unroll
@@ -703,16 +736,27 @@ __global__ __launch_bounds__(64 * GB * KSPLIT) void k_attn_prefill(const vsl_hal
             xo[OSZ + 64 + lane] = l;
         }
         __syncthreads();
-        if (kbase == 1) return;
-        const float m1 = xo[OSZ + lane], l1 = xo[OSZ + 64 + lane];
-        const float mm = fmaxf(m, m1);
+        if (ksp > 0) return;
+        float mm = m;
+#pragma unroll
+        for (int j = 1; j < KSPLIT; ++j) mm = fmaxf(mm, slot(j)[OSZ + lane]);
         const float c0 = m == -INFINITY ? 0.f : fast_exp2(m - mm);
-        const float c1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - mm);
-        l = l * c0 + l1 * c1;
+        l *= c0;
 #pragma unroll
         for (int tt = 0; tt < HD / 32; ++tt)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) o[tt][v] = o[tt][v] * c0 + xo[(tt * 16 + v) * 64 + lane] * c1;
+            for (int v = 0; v < 16; ++v) o[tt][v] *= c0;
+#pragma unroll
+        for (int j = 1; j < KSPLIT; ++j) {
+            const float* xo = slot(j);
+            const float mj = xo[OSZ + lane];
+            const float cj = mj == -INFINITY ? 0.f : fast_exp2(mj - mm);
+            l += xo[OSZ + 64 + lane] * cj;
+#pragma unroll
+            for (int tt = 0; tt < HD / 32; ++tt)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[tt][v] += xo[(tt * 16 + v) * 64 + lane] * cj;
+        }
     }
 
     if (my_s >= S) return;
@@ -1071,16 +1115,20 @@ static void launch_attn_prefill_w(dim3 grid, hipStream_t s, const vsl_half* q, c
     constexpr uint64_t kCUs = 256;  // MI355X compute units
     const bool half = GB2 < G && (uint64_t)grid.x * grid.y < kCUs;
     auto go = [&](auto qc, auto oc) {
-        if (half) {
-            constexpr int KS = GB2 <= 4 ? 2 : 1;
-            const dim3 g2(grid.x, grid.y * (G / GB2));
-            k_attn_prefill<HD, G, GB2, decltype(qc)::value, decltype(oc)::value, WIN, KS><<<g2, 64 * GB2 * KS, 0, s>>>(
-                q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
-        } else {
-            constexpr int KS = G <= 4 ? 2 : 1;
-            k_attn_prefill<HD, G, G, decltype(qc)::value, decltype(oc)::value, WIN, KS><<<grid, 64 * G * KS, 0, s>>>(
-                q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+        if constexpr (GB2 < G) {
+            if (half) {
+                // two heads per block, four waves per head over 128-key tiles (two buffers of 64 KB):
+                // eight waves, two per SIMD, and half the tiles in the longest query block's chain
+                constexpr int KS = 4;
+                const dim3 g2(grid.x, grid.y * (G / GB2));
+                k_attn_prefill<HD, G, GB2, decltype(qc)::value, decltype(oc)::value, WIN, KS, 128, 2>
+                    <<<g2, 64 * GB2 * KS, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+                return;
+            }
         }
+        constexpr int KS = G <= 4 ? 2 : 1;
+        k_attn_prefill<HD, G, G, decltype(qc)::value, decltype(oc)::value, WIN, KS><<<grid, 64 * G * KS, 0, s>>>(
+            q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
     };
     using T = std::true_type;
     using F = std::false_type;
