@@ -473,8 +473,9 @@ struct DmaPair {  // the one-plane, the split-A and the fp8-lo configuration of 
 // 690 us, 512 rows 195 -> 185 us for 2 x 2 waves of 128 x 128 against 4 x 2 waves at BK = 32. Since
 // then 4 x 2 waves of 64 x 128 (two per SIMD, each raising its priority for its MFMAs) with one
 // fragment register set per wave (SF; with two sets they spill): 2048 rows 688 -> 673 us, 512 rows
-// level. The 128 x 256 fp8-lo tile keeps 2 x 4 waves at BK = 64 (56 KB stages): down 512 rows 102 us
-// against 106-113 for 4 x 2, 2 x 2 and 1 x 4 waves.
+// level. The 128 x 256 fp8-lo tile keeps 2 x 4 waves at BK = 64 (56 KB stages) with two fragment
+// sets: down 512 rows 100-102 us against 106-113 for 4 x 2, 2 x 2 and 1 x 4 waves, 102-104 for 2 x 4
+// and 109-113 for 4 x 2 waves with one fragment set.
 using DmaBig = DmaPair<256, 256, 4, 2, 32, 4, 2, 0, 64, true>;
 using DmaMid = DmaPair<128, 256, 2, 4, 64>;
 // Few-row shapes without a K split (a 128-row prompt's SwiGLU: 2 x 128 tiles of 64 rows x 64 outputs):
