@@ -383,6 +383,8 @@ __global__ __launch_bounds__(256) void k_splitk_resid_rmsnorm(const float* __res
 #pragma unroll
             for (int j = 0; j < NV; ++j) v[j] += *reinterpret_cast<const float4v*>(ws + k * MN + base + (j * 256 + t) * 4);
     } else {
+        // unrolled so that eight chunks' loads are in flight at once (the sums stay in chunk order)
+#pragma unroll 8
         for (uint32_t k = 1; k < ks_rt; ++k)
 #pragma unroll
             for (int j = 0; j < NV; ++j) v[j] += *reinterpret_cast<const float4v*>(ws + k * MN + base + (j * 256 + t) * 4);
