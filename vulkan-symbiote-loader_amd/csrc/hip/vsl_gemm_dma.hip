@@ -445,6 +445,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
     const uint64_t e = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (e >= MN) return;
     float4v sum = *reinterpret_cast<const float4v*>(ws + e);
+#pragma unroll 8  // eight chunks' loads in flight, summed in order
     for (uint32_t k = 1; k < ksplit; ++k) sum += *reinterpret_cast<const float4v*>(ws + k * MN + e);
     if constexpr (EPI == VSL_EPI_STORE_F32) {
         *reinterpret_cast<float4v*>(static_cast<float*>(C) + e) = sum;

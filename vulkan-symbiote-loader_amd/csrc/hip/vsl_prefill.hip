@@ -324,6 +324,7 @@ __global__ __launch_bounds__(256) void k_rope_split4(const float* __restrict__ w
 #pragma unroll
         for (int k = 1; k < KS; ++k) v += *reinterpret_cast<const float4v*>(ws + k * MN + off);
     } else {
+#pragma unroll 8  // eight chunks' loads in flight, summed in order
         for (uint32_t k = 1; k < ks_rt; ++k) v += *reinterpret_cast<const float4v*>(ws + k * MN + off);
     }
     const uint32_t pos = pos0 + s, qw = n_q * hd, kw = n_kv * hd;
