@@ -280,11 +280,25 @@ int vsl_ctrl_reset(vsl_ctrl* ctrl, uint32_t pos, uint32_t max_steps, uint32_t st
  *   VSL_EPI_SWIGLU (B = [Wgate; Wup], N = F: C f16 = silu(A Wg^T) * (A Wu^T)).
  * Flags or'ed into `epilogue`: VSL_GEMM_A_X2 (A is VSL_DT_F16X2: two MFMAs per tile, hi and lo),
  * VSL_GEMM_C_X2 (SwiGLU output written as VSL_DT_F16X2), VSL_GEMM_A_F8 (A is VSL_DT_F16F8: the hi
- * plane on fp16 MFMA, the lo plane on fp8 MFMA against B rounded to e4m3 as B * 2^6, into the same
+ * plane on fp16 MFMA, the lo plane on fp8 MFMA against B rounded to e4m3 as B * 2^s, into the same
  * fp32 accumulators), VSL_GEMM_C_F8 (SwiGLU output written as VSL_DT_F16F8).  The F8 forms need
- * N % 256 == 0 (N % 128 == 0 for SwiGLU) and K % 128 == 0, else VSL_E_UNSUPPORTED. */
+ * N % 256 == 0 (N % 128 == 0 for SwiGLU) and K % 128 == 0, else VSL_E_UNSUPPORTED.
+ * The weight shift s of the fp8 lo product is or'ed in as VSL_GEMM_B8_SHIFT(s), -16 <= s <= 30
+ * (without it s = 6).  e4m3 holds magnitudes up to 448 and the conversion does not saturate, so
+ * every |B| * 2^s must be <= 448: vsl_gemm_b8_shift gives the largest such s for a matrix's
+ * largest magnitude (vsl_absmax_f16), which also keeps the small weights out of e4m3's subnormal
+ * range as far as the large ones allow. */
 enum { VSL_EPI_STORE_F32 = 0, VSL_EPI_STORE_F16 = 1, VSL_EPI_RESID = 2, VSL_EPI_SWIGLU = 3 };
 enum { VSL_GEMM_A_X2 = 0x100, VSL_GEMM_C_X2 = 0x200, VSL_GEMM_A_F8 = 0x400, VSL_GEMM_C_F8 = 0x800 };
+#define VSL_GEMM_B8_SHIFT(s) ((int)((((s) + 128) & 0xFF) << 16))
+enum { VSL_GEMM_B8_SHIFT_MIN = -16, VSL_GEMM_B8_SHIFT_MAX = 30, VSL_GEMM_B8_SHIFT_DEFAULT = 6 };
+/* The largest s in [VSL_GEMM_B8_SHIFT_MIN, VSL_GEMM_B8_SHIFT_MAX] with max_abs * 2^s <= 448 (e4m3's
+ * largest finite value); VSL_GEMM_B8_SHIFT_DEFAULT for max_abs 0 or not finite. */
+int vsl_gemm_b8_shift(float max_abs);
+/* The largest finite |x| over n fp16 values (NaN and infinities skipped) folded into *max_abs (a
+ * device float, which the caller sets to 0 first or which holds a previous maximum to extend) by
+ * device-scope atomic maxima. */
+int vsl_absmax_f16(const void* x, uint64_t n, float* max_abs, void* stream);
 int vsl_gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K, void* C, int epilogue,
                  void* stream);
 /* The same with an fp32 workspace (16-byte aligned): shapes whose output tiles would leave CUs idle
@@ -311,7 +325,7 @@ int vsl_rope_split_append(const float* qkv, uint32_t S, uint32_t n_q, uint32_t n
 /* The attention stage's entry for S prompt rows (forward_layer_with_weights,
  * VulkanSymbioteEngine.cpp:777-806, normed -> attention_with_weights): the QKV projection of A
  * [S][K] against Wqkv [(n_q+2 n_kv) hd][K] followed by vsl_rope_split_append.  `a_flags` is 0,
- * VSL_GEMM_A_X2 or VSL_GEMM_A_F8.  When the shape splits over K (workspace as for vsl_gemm_f16_ws), the partials are
+ * VSL_GEMM_A_X2 or VSL_GEMM_A_F8 (with an optional VSL_GEMM_B8_SHIFT).  When the shape splits over K (workspace as for vsl_gemm_f16_ws), the partials are
  * summed, rotated and stored by one launch and qkv is not touched; otherwise qkv (f32 [S][(n_q+2 n_kv)
  * hd]) receives the projection first.  Checks (capacity, dtypes) happen before anything is launched. */
 int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uint32_t S, uint32_t K, int a_flags,

@@ -299,6 +299,56 @@ def test_long_context_oracle_small_model(vsl, orc):
     m.close()
 
 
+def _plant_outliers(vsl, path, names, values, per_tensor, seed):
+    """Overwrite `per_tensor` random fp16 weights of each named tensor of a GGUF file in place with
+    `values` (cycled); the file's other bytes are unchanged."""
+    import ctypes
+    L = vsl.engine_lib()
+    h = ctypes.c_void_p()
+    vsl.check(L.vsl_gguf_open(str(path).encode(), ctypes.byref(h)), L)
+    rng = np.random.default_rng(seed)
+    try:
+        mm = np.memmap(path, dtype=np.uint8, mode="r+")
+        for n in names:
+            off, size, rt, nd = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint32(), ctypes.c_uint32()
+            dims = (ctypes.c_uint64 * 4)()
+            vsl.check(L.vsl_gguf_tensor(h, n.encode(), ctypes.byref(off), ctypes.byref(size), ctypes.byref(rt),
+                                        ctypes.byref(nd), dims), L)
+            w = mm[off.value:off.value + size.value].view(np.float16)
+            idx = rng.choice(w.size, per_tensor, replace=False)
+            w[idx] = np.resize(np.asarray(values, np.float16), per_tensor)
+        mm.flush()
+        del mm
+    finally:
+        L.vsl_gguf_close(h)
+
+
+@pytest.mark.slow
+@pytest.mark.timeout(900)
+def test_fp8_prefill_with_outlier_weights(vsl, orc, tmp_path):
+    """The prompt pass's fp8 lo products on a model file whose gate/up, down and O weights hold outliers
+    (+-7.5 and +-40 among N(0, 0.02): past e4m3's 448 at the fixed 2^6 weight scale). d 1024 and FFN 2816
+    with a 2048-row chunk put the O, gate/up and down GEMMs on the F16F8 path; each layer's weight shift
+    comes from its own largest weight. 16 teacher-forced greedy steps against the oracle reading the same
+    file: every logit finite and within max-abs 2e-2, picks identical."""
+    cfg = dict(LONG_SMALL, max_position_embeddings=4096)
+    p = tmp_path / "outliers.gguf"
+    vsl.write_synthetic_gguf(p, cfg, seed=0)
+    names = [f"blk.{l}.{t}.weight" for l in range(cfg["num_layers"])
+             for t in ("ffn_gate", "ffn_up", "ffn_down", "attn_o")]
+    _plant_outliers(vsl, p, names, [7.5, -7.5, 40.0, -40.0], 48, 3)
+    prompt = np.random.default_rng(12).integers(0, cfg["vocab_size"], 2048).astype(np.uint32)
+    m = orc.Model(p)
+    with vsl.Engine(p, kv_capacity=2048 + 32, batched_prefill=True, prefill_chunk=2048) as e:
+        w = e.read_tensor("blk.1.ffn_down.weight", 2 * cfg["hidden_size"] * cfg["intermediate_size"])
+        assert w.dtype == np.float16 and np.max(np.abs(w.astype(np.float32))) == 40.0
+        rep = _forced_parity(e, m, prompt, 16, 2e-2)
+        toks, lg = e.generate_ids(prompt, 4, return_logits=True)
+        assert np.all(np.isfinite(lg))
+    m.close()
+    assert rep and np.all(np.isfinite(rep[0][1]))
+
+
 def test_engine_stats_and_packs(vsl):
     with vsl.Engine(spec=vsl.LLAMA_1B, kv_capacity=512) as e:
         cfg = e.config

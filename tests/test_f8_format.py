@@ -78,3 +78,42 @@ def test_f8lo_product_model():
     hi, plane, val = T.f16f8_split(a)
     got = T.f8lo_product(hi, val - hi.astype(np.float64), B)
     assert np.allclose(got, val @ B.astype(np.float64).T, rtol=0, atol=1e-12)
+
+
+def test_b8_shift_closed_form(vsl):
+    """vsl_gemm_b8_shift (host arithmetic): the largest shift that keeps max_abs * 2^s within e4m3's 448,
+    against a search over every shift and against values worked out by hand: 7 * 2^6 = 448 exactly,
+    7.5 and 40 need 5 and 3, fp16's largest 65504 needs -8, N(0, 0.02) weights (max ~0.1) get 11."""
+    H = vsl.hip()
+    hand = {7.0: 6, 7.5: 5, 40.0: 3, 448.0: 0, 448.5: -1, 65504.0: -8, 0.1: 12, 0.109: 12, 0.11: 11,
+            1.0: 8, 1e-30: 30, 0.0: 6, float("inf"): 6, float("nan"): 6, -3.0: 6}
+    for m, s in hand.items():
+        assert H.vsl_gemm_b8_shift(m) == s, m
+        assert T.b8_shift_model(m) == s, m
+    rng = np.random.default_rng(5)
+    vals = np.concatenate([np.exp(rng.uniform(-20, 12, 2000)), T.e4m3_table()[1:127] / 64.0,
+                           np.ldexp(448.0, -np.arange(0, 30))]).astype(np.float32)
+    for m in vals:
+        s = H.vsl_gemm_b8_shift(float(m))
+        assert s == T.b8_shift_model(m), m
+        assert np.ldexp(np.float64(m), s) <= 448.0 and (s == 30 or np.ldexp(np.float64(m), s + 1) > 448.0)
+
+
+def test_f8lo_product_shift_is_exact_scaling():
+    """With every |B| 2^s <= 448 the model's e4m3 rounding of B never saturates, and a different shift
+    changes B8 only by the subnormal floor: two shifts 4 apart agree wherever |B| 2^s stays normal."""
+    rng = np.random.default_rng(2)
+    B = rng.normal(0, 0.5, (8, 64)).astype(np.float16)
+    B[0, :4] = [40.0, -7.5, 100.0, -300.0]
+    a = rng.normal(0, 1, (4, 64)).astype(np.float32)
+    hi, plane, val = T.f16f8_split(a)
+    s = T.b8_shift_model(np.max(np.abs(B.astype(np.float32))))
+    assert s == 0
+    lo = val - hi.astype(np.float64)
+    p0 = T.f8lo_product(hi, lo, B, s)
+    assert np.all(np.isfinite(p0))
+    B8 = np.ldexp(T.e4m3_table()[T.e4m3_encode(np.ldexp(B.astype(np.float64), s))], -s)
+    assert np.all(np.abs(B8 - B) <= 2.0 ** -4 * np.abs(B) + np.ldexp(2.0 ** -10, -s))
+    normal = np.abs(np.ldexp(B.astype(np.float64), s - 4)) >= 2.0 ** -6
+    B8b = np.ldexp(T.e4m3_table()[T.e4m3_encode(np.ldexp(B.astype(np.float64), s - 4))], 4 - s)
+    assert np.array_equal(B8[normal], B8b[normal])

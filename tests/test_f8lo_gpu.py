@@ -180,6 +180,136 @@ def test_gemm_f8lo_splitk(vsl, dev, H, M, N, K, epi):
             assert rel_err(out - (C0[rows] if epi == 2 else 0.0), ref) < 5e-6
 
 
+@pytest.mark.parametrize("n,off", [(1, 0), (7, 0), (8, 0), (1000, 1), (4097, 3), (1 << 20, 0), ((1 << 20) + 5, 8)])
+def test_absmax_f16(vsl, dev, H, n, off):
+    """vsl_absmax_f16: the largest finite |x| (infinities and NaN skipped) over any length and start
+    (16-byte aligned or not), folded into the value already there."""
+    rng = np.random.default_rng(n + off)
+    x = rng.normal(0, 1, n + off).astype(np.float16)
+    if n > 16:
+        x[off + rng.integers(0, n, 3)] = [np.inf, -np.inf, np.nan]
+        x[off + rng.integers(0, n)] = np.float16(-3000.0)
+    body = x[off:].astype(np.float32)
+    want = float(np.max(np.abs(body[np.isfinite(body)]))) if np.any(np.isfinite(body)) else 0.0
+    buf = dev.put(x)
+    base = dev.p(buf) + 2 * off
+    out = dev.put(np.zeros(1, np.float32))
+    ok(vsl, H.vsl_absmax_f16(base, n, dev.p(out), None))
+    assert float(dev.get(out)[0]) == want
+    out2 = dev.put(np.array([want * 2 + 1], np.float32))
+    ok(vsl, H.vsl_absmax_f16(base, n, dev.p(out2), None))
+    assert float(dev.get(out2)[0]) == want * 2 + 1
+
+
+def _weights(kind, rows, K, rng):
+    """fp16 weights of a range scenario: N(0, 0.002), N(0, 0.2), or N(0, 0.02) with planted outliers."""
+    if kind == "std0.002":
+        return rng.normal(0, 0.002, (rows, K)).astype(np.float16)
+    if kind == "std0.2":
+        return rng.normal(0, 0.2, (rows, K)).astype(np.float16)
+    B = rng.normal(0, 0.02, (rows, K)).astype(np.float16)
+    big = {"out40": [7.5, -7.5, 40.0, -40.0], "out1000": [7.5, -40.0, 100.0, -1000.0]}[kind]
+    idx = rng.choice(rows * K, 64, replace=False)
+    B.reshape(-1)[idx] = np.resize(np.array(big, np.float16), 64)
+    return B
+
+
+@pytest.mark.parametrize("kind", ["std0.002", "std0.2", "out40", "out1000"])
+@pytest.mark.parametrize("M,N,K,epi,ks", [
+    (1536, 8192, 1024, 3, False),   # SwiGLU on 256 x 256 tiles
+    (512, 4096, 1024, 3, False),    # SwiGLU on 64 x 128 tiles
+    (2048, 4096, 1024, 2, False),   # residual on 128 x 256 tiles
+    (512, 4096, 4096, 2, True),     # K split on 128 x 256 tiles
+    (512, 6144, 4096, 0, True),     # K split on 128 x 192 tiles
+])
+def test_gemm_f8lo_weight_ranges(vsl, dev, H, kind, M, N, K, epi, ks):
+    """The fp8 lo product over weight ranges other than N(0, 0.02): small (std 0.002), wide (std 0.2) and
+    planted outliers up to 40 or 1000. The shift from vsl_absmax_f16 + vsl_gemm_b8_shift keeps every
+    weight within e4m3's range: the result is finite, equals the model of hi B^T + lo e4m3(B 2^s) 2^-s,
+    and stays within one fp16 rounding of the fp32-input product (much closer without outliers)."""
+    rng = np.random.default_rng(M + N + K + epi + len(kind))
+    nb = 2 * N if epi == 3 else N
+    A = rng.normal(0, 1, (M, K)).astype(np.float32)
+    B = _weights(kind, nb, K, rng)
+    dB = dev.put(B)
+    mx = dev.put(np.zeros(1, np.float32))
+    ok(vsl, H.vsl_absmax_f16(dev.p(dB), nb * K, dev.p(mx), None))
+    amax = float(dev.get(mx)[0])
+    assert amax == float(np.max(np.abs(B.astype(np.float32))))
+    s = H.vsl_gemm_b8_shift(amax)
+    assert s == T.b8_shift_model(amax)
+    dA, hi, val = f8_buffer(dev, A)
+    lo = val - hi.astype(np.float64)
+    # SwiGLU writes hi/lo fp16 planes (~22 bits, no clamped remainder however large the outputs grow)
+    flags = epi | vsl.GEMM_A_F8 | vsl.GEMM_B8_SHIFT(s) | (vsl.GEMM_C_X2 if epi == 3 else 0)
+    if epi == 3:
+        C = dev.empty((4 * M * N,), np.uint8)
+    else:
+        C0 = rng.normal(0, 1, (M, N)).astype(np.float32) if epi == 2 else np.zeros((M, N), np.float32)
+        C = dev.put(C0)
+    if ks:
+        need = H.vsl_gemm_f16_ws_bytes(M, N, K, flags)
+        assert need > 0
+        ws = dev.empty((need // 4 + 4,), np.float32)
+        ok(vsl, H.vsl_gemm_f16_ws(dev.p(dA), dev.p(dB), M, N, K, dev.p(C), flags, dev.p(ws), need, None))
+    else:
+        ok(vsl, H.vsl_gemm_f16(dev.p(dA), dev.p(dB), M, N, K, dev.p(C), flags, None))
+    rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, 40)]))
+    prod = T.f8lo_product(hi[rows], lo[rows], B, s)
+    exact = A[rows].astype(np.float64) @ B.astype(np.float64).T
+    bound = 2.0 ** -11 if kind == "out1000" else 2.0 ** -13
+    if epi == 3:
+        o = dev.get(C).reshape(-1).view(np.uint8)[:4 * M * N].view(np.float16).reshape(2, M, N).astype(np.float64)
+        got = o[0, rows] + o[1, rows]
+        assert np.all(np.isfinite(got))
+        g, u = prod[:, :N], prod[:, N:]
+        assert rel_err(got, g / (1.0 + np.exp(-g)) * u) < 5e-6
+        ge, ue = exact[:, :N], exact[:, N:]
+        assert rel_err(got, ge / (1.0 + np.exp(-ge)) * ue) < bound
+    else:
+        out = dev.get(C).astype(np.float64)[rows] - (C0[rows] if epi == 2 else 0.0)
+        assert np.all(np.isfinite(out))
+        assert rel_err(out, prod) < 5e-6
+        assert rel_err(out, exact) < bound
+
+
+def test_gemm_f8lo_default_shift_is_not_saturating(vsl, dev, H):
+    """Why the shift exists: at the default 2^6 a weight of 40 becomes 2560, past e4m3's 448, and the
+    conversion does not saturate -- the output columns of that weight's row are not finite, every other
+    column is the model's. With the measured shift all columns are."""
+    rng = np.random.default_rng(9)
+    M, N, K = 2048, 4096, 1024
+    A = rng.normal(0, 1, (M, K)).astype(np.float32)
+    B = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    B[[5, 300], [17, 900]] = [40.0, -40.0]
+    dA, hi, val = f8_buffer(dev, A)
+    lo = val - hi.astype(np.float64)
+    dB = dev.put(B)
+    rows = np.arange(0, M, 97)
+    for shift in (None, 3):
+        C = dev.put(np.zeros((M, N), np.float32))
+        flags = 2 | vsl.GEMM_A_F8 | (vsl.GEMM_B8_SHIFT(shift) if shift is not None else 0)
+        ok(vsl, H.vsl_gemm_f16(dev.p(dA), dev.p(dB), M, N, K, dev.p(C), flags, None))
+        out = dev.get(C).astype(np.float64)[rows]
+        cols = np.setdiff1d(np.arange(N), [5, 300])
+        ref = T.f8lo_product(hi[rows], lo[rows], B, 6 if shift is None else shift)
+        assert rel_err(out[:, cols], ref[:, cols]) < 5e-6
+        if shift is None:
+            assert not np.any(np.isfinite(out[:, [5, 300]]))
+        else:
+            assert np.all(np.isfinite(out)) and rel_err(out, ref) < 5e-6
+
+
+def test_gemm_b8_shift_flags_refused(vsl, dev, H):
+    A = dev.put(np.zeros((3 * 64 * 4096,), np.uint8))
+    B = dev.put(np.zeros((4096, 4096), np.float16))
+    C = dev.put(np.zeros((64, 4096), np.float32))
+    for s in (vsl.GEMM_B8_SHIFT(-17), vsl.GEMM_B8_SHIFT(31)):
+        assert H.vsl_gemm_f16(dev.p(A), dev.p(B), 64, 4096, 4096, dev.p(C), vsl.GEMM_A_F8 | s, None) == vsl.VSL_E_INVALID
+    ok(vsl, H.vsl_gemm_f16(dev.p(A), dev.p(B), 64, 4096, 4096, dev.p(C), vsl.GEMM_A_F8 | vsl.GEMM_B8_SHIFT(-16), None))
+    ok(vsl, H.vsl_gemm_f16(dev.p(A), dev.p(B), 64, 4096, 4096, dev.p(C), vsl.GEMM_A_F8 | vsl.GEMM_B8_SHIFT(30), None))
+
+
 def test_gemm_f8lo_forms_refused(vsl, dev, H):
     A = dev.put(np.zeros((3 * 64 * 4096,), np.uint8))
     B = dev.put(np.zeros((4096, 4096), np.float16))

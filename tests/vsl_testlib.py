@@ -85,7 +85,7 @@ class Dev:
 
 # ------------------------------------------------------------------------------------------
 # fp8 e4m3 (OCP) and the VSL_DT_F16F8 activation form, in numpy: the values the GEMM's fp8 lo path is
-# defined to multiply (the lo plane, and B rounded to e4m3 as B * 2^6)
+# defined to multiply (the lo plane, and B rounded to e4m3 as B * 2^s)
 # ------------------------------------------------------------------------------------------
 def e4m3_table():
     """Value of every byte code (NaN for 0x7f / 0xff)."""
@@ -134,7 +134,18 @@ def f16f8_value(hi, plane):
     return hi.astype(np.float64) + e4m3_table()[codes] / 4096.0
 
 
-def f8lo_product(hi, lo_val, B):
-    """What a GEMM with an F16F8 A computes: hi B^T + lo B8^T, B8 = e4m3(B * 2^6) / 2^6 (float64)."""
-    B8 = e4m3_table()[e4m3_encode(B.astype(np.float64) * 64.0)] / 64.0
-    return hi.astype(np.float64) @ B.astype(np.float64).T + lo_val @ B8.T
+def f8lo_product(hi, lo_val, B, shift=6):
+    """What a GEMM with an F16F8 A computes: hi B^T + lo B8^T, B8 = e4m3(B * 2^s) / 2^s (float64), s the
+    weight shift (VSL_GEMM_B8_SHIFT; 6 without one)."""
+    B8 = e4m3_table()[e4m3_encode(np.ldexp(B.astype(np.float64), shift))]
+    return hi.astype(np.float64) @ B.astype(np.float64).T + lo_val @ np.ldexp(B8, -shift).T
+
+
+def b8_shift_model(max_abs):
+    """The weight shift for a matrix whose largest finite magnitude is max_abs, by search: the largest s
+    in [-16, 30] with max_abs * 2^s <= 448 (6 for 0 or a non-finite value)."""
+    m = float(max_abs)
+    if not (m > 0) or not np.isfinite(m):
+        return 6
+    ok = [s for s in range(-16, 31) if np.ldexp(np.float32(m), s) <= 448.0]
+    return max(ok) if ok else -16

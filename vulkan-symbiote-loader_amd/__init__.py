@@ -25,6 +25,11 @@ VSL_DT_F32, VSL_DT_F16, VSL_DT_F16X2, VSL_DT_F16F8 = 0, 1, 2, 3
 VSL_WF_F32, VSL_WF_F16, VSL_WF_Q4_0, VSL_WF_Q4_1, VSL_WF_Q8_0 = 0, 1, 2, 3, 4
 VSL_QL_REFERENCE, VSL_QL_GGML = 0, 1
 GEMM_A_X2, GEMM_C_X2, GEMM_A_F8, GEMM_C_F8 = 0x100, 0x200, 0x400, 0x800
+
+
+def GEMM_B8_SHIFT(s):
+    """VSL_GEMM_B8_SHIFT(s): the weight shift of the fp8 lo product (B rounded to e4m3 as B * 2^s)."""
+    return ((s + 128) & 0xFF) << 16
 SAMPLE_GREEDY, SAMPLE_REFERENCE, SAMPLE_TOPK_SEEDED = 0, 1, 2
 EPI_STORE_F32, EPI_STORE_F16, EPI_RESID, EPI_SWIGLU = 0, 1, 2, 3
 _MODES = {"greedy": SAMPLE_GREEDY, "reference": SAMPLE_REFERENCE, "topk": SAMPLE_TOPK_SEEDED}
@@ -108,6 +113,8 @@ _HIP_SIGS = {
     "vsl_gemm_f16_ws": (_I32, [_P, _P, _U32, _U32, _U32, _P, _I32, _P, _U64, _P]),
     "vsl_gemm_f16_ws_bytes": (_U64, [_U32, _U32, _U32, _I32]),
     "vsl_gemm_f16_direct": (_I32, [_U32, _U32, _U32, _I32]),
+    "vsl_gemm_b8_shift": (_I32, [_F32]),
+    "vsl_absmax_f16": (_I32, [_P, _U64, _P, _P]),
     "vsl_convert_weights": (_I32, [_P, _I32, _I32, _U64, _P, _I32, _P]),
     "vsl_attn_decode_window": (_I32, [_P, _P, _P, _I32, _U32, _U32, _U32, _U32, _F32, _U32, _P, _P, _P, _P,
                                       _U32, _U32, _U32, _P]),

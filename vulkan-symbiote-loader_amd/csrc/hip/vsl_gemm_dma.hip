@@ -27,6 +27,8 @@
 // one-byte-per-element lo tile; the lo plane is multiplied on the fp8 matrix cores (see k_gemm_dma).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "vsl_device.h"
@@ -84,17 +86,26 @@ __device__ __forceinline__ int chunk_pos(int r, int c) {
 typedef int int8v __attribute__((ext_vector_type(8)));
 typedef int int4v __attribute__((ext_vector_type(4)));
 
-// Two fp16 values to two fp8 e4m3 bytes of v * 2^6 (round to nearest even), into the low or high
-// half of a dword. The weights (about N(0, 0.02)) then sit in e4m3's normal range.
+// Two fp16 values to two fp8 e4m3 bytes of v * 2^s (round to nearest even; `div` = 2^-s), into the
+// low or high half of a dword. The conversion does not saturate (a magnitude past 448 becomes NaN),
+// so the launcher's s keeps every |v| * 2^s of the matrix within 448.
 template <bool HI_WORD>
-__device__ __forceinline__ int w8_pack(int old, vsl_half a, vsl_half b) {
+__device__ __forceinline__ int w8_pack(int old, vsl_half a, vsl_half b, float div) {
     typedef short s2 __attribute__((ext_vector_type(2)));
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const h2 v = {a, b};
     s2 o = __builtin_bit_cast(s2, old);
-    o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, v, 0.015625f, HI_WORD);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, v, div, HI_WORD);
     return __builtin_bit_cast(int, o);
 }
+
+// The weight shift s of the fp8 lo product as the kernels take it: the conversion divisor 2^-s and
+// the E8M0 code 127 - s of the MFMA's B scale.
+struct B8Shift {
+    float div;
+    int e8m0;
+};
+inline B8Shift b8_shift(int s) { return {std::ldexp(1.0f, -s), 127 - s}; }
 
 // SK (split K): the block's work item is (k chunk, tile); it multiplies K / ksplit of K and stores
 // the fp32 partial tile to ws[chunk][M][N]; k_splitk_reduce sums the chunks in order and applies the
@@ -102,14 +113,14 @@ __device__ __forceinline__ int w8_pack(int old, vsl_half a, vsl_half b) {
 //
 // AM == kAF8: each k-step multiplies the hi plane on v_mfma_f32_32x32x16_f16; every 64 columns of K
 // the lo plane is multiplied on v_mfma_scale_f32_32x32x64_f8f6f4 against the same B fragments
-// converted to e4m3 (B * 2^6) in registers, with E8M0 scales 2^-12 and 2^-6, into the same
-// accumulators. Operand slot j of lane group g in that MFMA is column 16 (j / 8) + 8 g + j % 8 of
+// converted to e4m3 (B * 2^s, s = the launch's weight shift) in registers, with E8M0 scales 2^-12
+// and 2^-s, into the same accumulators. Operand slot j of lane group g in that MFMA is column 16 (j / 8) + 8 g + j % 8 of
 // the 64: the B fragment of k-step t supplies slots 8t..8t+7, and the lo plane's byte order
 // (lo8_pos) puts the A slots of a 32-column block in one 16-byte chunk per lane group.
 template <class G, int EPI, int AM, int CM, bool SK>
 __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__ A, const vsl_half* __restrict__ B,
                                                        uint32_t M, uint32_t N, uint32_t K, void* __restrict__ C,
-                                                       float* __restrict__ ws, uint32_t ksplit) {
+                                                       float* __restrict__ ws, uint32_t ksplit, B8Shift b8) {
     constexpr int BM = G::BM, BN = G::BN, BK = G::BK, WM = G::WM, WN = G::WN, FM = G::FM, FN = G::FN;
     constexpr int ACH = G::ACH, BCH = G::BCH, LCH = G::LCH, STAGE = G::STAGE, CPR = G::CPR, CPR8 = G::CPR8;
     constexpr int NBUF = G::NBUF, KS = G::KS;
@@ -257,10 +268,10 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             int d0 = w8[j][2 * t], d1 = w8[j][2 * t + 1];
-            d0 = w8_pack<false>(d0, f.b[j][0], f.b[j][1]);
-            d0 = w8_pack<true>(d0, f.b[j][2], f.b[j][3]);
-            d1 = w8_pack<false>(d1, f.b[j][4], f.b[j][5]);
-            d1 = w8_pack<true>(d1, f.b[j][6], f.b[j][7]);
+            d0 = w8_pack<false>(d0, f.b[j][0], f.b[j][1], b8.div);
+            d0 = w8_pack<true>(d0, f.b[j][2], f.b[j][3], b8.div);
+            d1 = w8_pack<false>(d1, f.b[j][4], f.b[j][5], b8.div);
+            d1 = w8_pack<true>(d1, f.b[j][6], f.b[j][7], b8.div);
             w8[j][2 * t] = d0;
             w8[j][2 * t + 1] = d1;
         }
@@ -273,7 +284,7 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
 #pragma unroll
             for (int j = 0; j < FN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, w8[j], acc[i][j], 0, 0, 0, 127 - 12, 0,
-                                                                            127 - 6);
+                                                                            b8.e8m0);
         }
     };
     constexpr int kPerStage = AP * ACH + BCH + LCH;  // loads per thread per stage
@@ -496,60 +507,60 @@ uint32_t dma_tiles(uint32_t M, uint32_t N) {
 
 template <class G, int EPI, int AM>
 void launch_cm(uint32_t blocks, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N,
-               uint32_t K, void* C, int cm) {
+               uint32_t K, void* C, int cm, B8Shift b8) {
     if constexpr (EPI == VSL_EPI_SWIGLU) {
         if (cm == kCX2) {
-            k_gemm_dma<G, EPI, AM, kCX2, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+            k_gemm_dma<G, EPI, AM, kCX2, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1, b8);
             return;
         }
         if (cm == kCF8) {
-            k_gemm_dma<G, EPI, AM, kCF8, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+            k_gemm_dma<G, EPI, AM, kCF8, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1, b8);
             return;
         }
     }
-    k_gemm_dma<G, EPI, AM, kC1, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1);
+    k_gemm_dma<G, EPI, AM, kC1, false><<<blocks, G::NT, 0, s>>>(a, b, M, N, K, C, nullptr, 1, b8);
 }
 
 template <class P, int EPI>
 void launch_cfg(uint32_t tiles, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N,
-                uint32_t K, void* C, int am, int cm) {
+                uint32_t K, void* C, int am, int cm, B8Shift b8) {
     const uint32_t blocks = ((tiles + 7) / 8) * 8;  // whole XCD ranges
-    if (am == kAX2) launch_cm<typename P::Two, EPI, kAX2>(blocks, s, a, b, M, N, K, C, cm);
-    else if (am == kAF8) launch_cm<typename P::F8, EPI, kAF8>(blocks, s, a, b, M, N, K, C, cm);
-    else launch_cm<typename P::One, EPI, kA1>(blocks, s, a, b, M, N, K, C, cm);
+    if (am == kAX2) launch_cm<typename P::Two, EPI, kAX2>(blocks, s, a, b, M, N, K, C, cm, b8);
+    else if (am == kAF8) launch_cm<typename P::F8, EPI, kAF8>(blocks, s, a, b, M, N, K, C, cm, b8);
+    else launch_cm<typename P::One, EPI, kA1>(blocks, s, a, b, M, N, K, C, cm, b8);
 }
 
 // split-K GEMM (partials, the epilogue's type only selects the reduce kernel)
 template <class P>
 void launch_splitk(uint32_t items, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N,
-                   uint32_t K, float* ws, uint32_t ksplit, int am) {
+                   uint32_t K, float* ws, uint32_t ksplit, int am, B8Shift b8) {
     const uint32_t blocks = ((items + 7) / 8) * 8;
     if (am == kAX2)
         k_gemm_dma<typename P::Two, VSL_EPI_STORE_F32, kAX2, kC1, true><<<blocks, P::Two::NT, 0, s>>>(
-            a, b, M, N, K, nullptr, ws, ksplit);
+            a, b, M, N, K, nullptr, ws, ksplit, b8);
     else if (am == kAF8)
         k_gemm_dma<typename P::F8, VSL_EPI_STORE_F32, kAF8, kC1, true><<<blocks, P::F8::NT, 0, s>>>(
-            a, b, M, N, K, nullptr, ws, ksplit);
+            a, b, M, N, K, nullptr, ws, ksplit, b8);
     else
         k_gemm_dma<typename P::One, VSL_EPI_STORE_F32, kA1, kC1, true><<<blocks, P::One::NT, 0, s>>>(
-            a, b, M, N, K, nullptr, ws, ksplit);
+            a, b, M, N, K, nullptr, ws, ksplit, b8);
 }
 
 template <int EPI>
 int launch_epi(int cfg, hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N, uint32_t K,
-               void* C, int am, int cm) {
+               void* C, int am, int cm, B8Shift b8) {
     if (cfg == 0) {
         const uint32_t t = dma_tiles<DmaBig::One, EPI>(M, N);
         if (!t) return -1;
-        launch_cfg<DmaBig, EPI>(t, s, a, b, M, N, K, C, am, cm);
+        launch_cfg<DmaBig, EPI>(t, s, a, b, M, N, K, C, am, cm, b8);
     } else if (cfg == 1) {
         const uint32_t t = dma_tiles<DmaMid::One, EPI>(M, N);
         if (!t) return -1;
-        launch_cfg<DmaMid, EPI>(t, s, a, b, M, N, K, C, am, cm);
+        launch_cfg<DmaMid, EPI>(t, s, a, b, M, N, K, C, am, cm, b8);
     } else {
         const uint32_t t = dma_tiles<DmaSmall::One, EPI>(M, N);
         if (!t) return -1;
-        launch_cfg<DmaSmall, EPI>(t, s, a, b, M, N, K, C, am, cm);
+        launch_cfg<DmaSmall, EPI>(t, s, a, b, M, N, K, C, am, cm, b8);
     }
     return 0;
 }
@@ -607,23 +618,24 @@ static bool splitk_narrow(uint32_t M, uint32_t N, uint32_t ksplit) {
 }
 
 void vsl_gemm_splitk_partials(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
-                              uint32_t K, int am, float* ws) {
+                              uint32_t K, int am, float* ws, int b8s) {
+    const B8Shift b8 = b8_shift(b8s);
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const vsl_half* a = static_cast<const vsl_half*>(A);
     const vsl_half* b = static_cast<const vsl_half*>(B);
     if (splitk_narrow(M, N, ksplit)) {
         const uint32_t tiles = dma_tiles<DmaQ::One, VSL_EPI_STORE_F32>(M, N);
-        launch_splitk<DmaQ>(tiles * ksplit, s, a, b, M, N, K, ws, ksplit, am);
+        launch_splitk<DmaQ>(tiles * ksplit, s, a, b, M, N, K, ws, ksplit, am, b8);
         return;
     }
     const uint32_t tiles = dma_tiles<DmaMid::One, VSL_EPI_STORE_F32>(M, N);
-    launch_splitk<DmaMid>(tiles * ksplit, s, a, b, M, N, K, ws, ksplit, am);
+    launch_splitk<DmaMid>(tiles * ksplit, s, a, b, M, N, K, ws, ksplit, am, b8);
 }
 
 int vsl_gemm_splitk_launch(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
-                           uint32_t K, void* C, int epi, int am, float* ws) {
+                           uint32_t K, void* C, int epi, int am, float* ws, int b8s) {
     hipStream_t s = static_cast<hipStream_t>(stream);
-    vsl_gemm_splitk_partials(ksplit, stream, A, B, M, N, K, am, ws);
+    vsl_gemm_splitk_partials(ksplit, stream, A, B, M, N, K, am, ws, b8s);
     const uint64_t MN = (uint64_t)M * N;
     const uint32_t rblocks = (uint32_t)((MN / 4 + 255) / 256);
     switch (epi) {
@@ -637,18 +649,80 @@ int vsl_gemm_splitk_launch(uint32_t ksplit, void* stream, const void* A, const v
 
 // Launches the direct-to-LDS GEMM; returns 0, or -1 when the shape does not fit `cfg`.
 int vsl_gemm_dma_launch(int cfg, void* stream, const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K,
-                        void* C, int epi, int am, int cm) {
+                        void* C, int epi, int am, int cm, int b8s) {
     if (K % kKAlign || K == 0) return -1;
     const uint64_t brows = epi == VSL_EPI_SWIGLU ? 2ull * N : N;
     if (((uint64_t)M * K * 2) >> 32 || (brows * K * 2) >> 32) return -1;  // 32-bit byte offsets
     hipStream_t s = static_cast<hipStream_t>(stream);
     const vsl_half* a = static_cast<const vsl_half*>(A);
     const vsl_half* b = static_cast<const vsl_half*>(B);
+    const B8Shift b8 = b8_shift(b8s);
     switch (epi) {
-        case VSL_EPI_STORE_F32: return launch_epi<VSL_EPI_STORE_F32>(cfg, s, a, b, M, N, K, C, am, kC1);
-        case VSL_EPI_STORE_F16: return launch_epi<VSL_EPI_STORE_F16>(cfg, s, a, b, M, N, K, C, am, kC1);
-        case VSL_EPI_RESID: return launch_epi<VSL_EPI_RESID>(cfg, s, a, b, M, N, K, C, am, kC1);
-        case VSL_EPI_SWIGLU: return launch_epi<VSL_EPI_SWIGLU>(cfg, s, a, b, M, N, K, C, am, cm);
+        case VSL_EPI_STORE_F32: return launch_epi<VSL_EPI_STORE_F32>(cfg, s, a, b, M, N, K, C, am, kC1, b8);
+        case VSL_EPI_STORE_F16: return launch_epi<VSL_EPI_STORE_F16>(cfg, s, a, b, M, N, K, C, am, kC1, b8);
+        case VSL_EPI_RESID: return launch_epi<VSL_EPI_RESID>(cfg, s, a, b, M, N, K, C, am, kC1, b8);
+        case VSL_EPI_SWIGLU: return launch_epi<VSL_EPI_SWIGLU>(cfg, s, a, b, M, N, K, C, am, cm, b8);
         default: return -1;
     }
+}
+
+// ------------------------------------------------------------------------------------------
+// Weight range of the fp8 lo product: the largest finite |w| of a matrix, and the shift s that keeps
+// every |w| * 2^s within e4m3's 448.
+// ------------------------------------------------------------------------------------------
+
+// Each thread folds eight fp16 values per 16-byte load (one value per load when x is not 16-byte
+// aligned) as integers: a finite binary16's magnitude bits order like its value, and an exponent field
+// of all ones (infinity, NaN) is skipped. One device-scope atomic maximum per wave on the float bits
+// of the result (non-negative floats order like their bits).
+__global__ __launch_bounds__(256) void k_absmax_f16(const uint16_t* __restrict__ x, uint64_t n, bool vec,
+                                                     uint32_t* __restrict__ out) {
+    uint32_t m = 0;
+    auto fold = [&](uint32_t h) {
+        h &= 0x7FFFu;
+        if ((h & 0x7C00u) != 0x7C00u) m = h > m ? h : m;
+    };
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    const uint64_t tid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t nv = vec ? n / 8 : 0;
+    for (uint64_t i = tid; i < nv; i += stride) {
+        const uint4 v = reinterpret_cast<const uint4*>(x)[i];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            fold(w[e] & 0xFFFFu);
+            fold(w[e] >> 16);
+        }
+    }
+    for (uint64_t i = nv * 8 + tid; i < n; i += stride) fold(x[i]);
+#pragma unroll
+    for (int off = 32; off; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)m, off);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) {
+        const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)m);
+        atomicMax(out, __float_as_uint(f));
+    }
+}
+
+extern "C" int vsl_absmax_f16(const void* x, uint64_t n, float* max_abs, void* stream) {
+    if (!x || !max_abs) return vsl_invalid("vsl_absmax_f16: null argument");
+    if (reinterpret_cast<uintptr_t>(x) & 1) return vsl_invalid("vsl_absmax_f16: x must be 2-byte aligned");
+    if (n == 0) return VSL_OK;
+    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    const uint64_t items = vec ? n / 8 + 1 : n;
+    const uint32_t grid = (uint32_t)std::min<uint64_t>((items + 255) / 256, 2048);
+    k_absmax_f16<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(static_cast<const uint16_t*>(x), n, vec,
+                                                                      reinterpret_cast<uint32_t*>(max_abs));
+    HIP_TRY(hipGetLastError());
+    return VSL_OK;
+}
+
+extern "C" int vsl_gemm_b8_shift(float max_abs) {
+    if (!(max_abs > 0.0f) || !std::isfinite(max_abs)) return VSL_GEMM_B8_SHIFT_DEFAULT;
+    int s = VSL_GEMM_B8_SHIFT_MAX;
+    // exact in float: max_abs * 2^s is a power-of-two scaling of a finite value
+    while (s > VSL_GEMM_B8_SHIFT_MIN && std::ldexp(max_abs, s) > 448.0f) --s;
+    return s;
 }

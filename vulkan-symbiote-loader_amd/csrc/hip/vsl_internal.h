@@ -40,13 +40,14 @@ static inline int vsl_capacity(const char* fmt, A... a) {
 enum { kGemmA1 = 0, kGemmAX2 = 1, kGemmAF8 = 2 };
 enum { kGemmC1 = 0, kGemmCX2 = 1, kGemmCF8 = 2 };
 uint32_t vsl_gemm_dma_tiles(int cfg, uint32_t M, uint32_t N, uint32_t K, int epi);
+// b8s: the weight shift of the fp8 lo product (VSL_GEMM_B8_SHIFT), used by the kGemmAF8 form only.
 int vsl_gemm_dma_launch(int cfg, void* stream, const void* A, const void* B, uint32_t M, uint32_t N, uint32_t K,
-                        void* C, int epi, int am, int cm);
+                        void* C, int epi, int am, int cm, int b8s);
 // Split-K plan of the direct-to-LDS GEMM (k chunks of the 128 x 256 tiling, fp32 partials in a
 // workspace, an ordered reduction applying the epilogue): returns the split (0: none).
 uint32_t vsl_gemm_splitk_plan(uint32_t M, uint32_t N, uint32_t K, int epi, uint32_t min_items, uint64_t* ws_bytes);
 // The k-chunk partials alone, ws[chunk][M][N] fp32, for a caller that sums them itself.
 void vsl_gemm_splitk_partials(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
-                              uint32_t K, int am, float* ws);
+                              uint32_t K, int am, float* ws, int b8s);
 int vsl_gemm_splitk_launch(uint32_t ksplit, void* stream, const void* A, const void* B, uint32_t M, uint32_t N,
-                           uint32_t K, void* C, int epi, int am, float* ws);
+                           uint32_t K, void* C, int epi, int am, float* ws, int b8s);

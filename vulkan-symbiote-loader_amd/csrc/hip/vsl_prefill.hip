@@ -823,6 +823,23 @@ static int gemm_a_mode(int flags) {
     return (flags & VSL_GEMM_A_X2) ? kGemmAX2 : (flags & VSL_GEMM_A_F8) ? kGemmAF8 : kGemmA1;
 }
 
+constexpr int kB8Field = 0xFF << 16;  // the VSL_GEMM_B8_SHIFT field of the flags
+
+// The weight shift of a GEMM's flags (VSL_GEMM_B8_SHIFT_DEFAULT without the field); false when the
+// field is outside [VSL_GEMM_B8_SHIFT_MIN, VSL_GEMM_B8_SHIFT_MAX].
+static bool gemm_b8_shift(int flags, int* shift) {
+    const int f = (flags & kB8Field) >> 16;
+    *shift = f ? f - 128 : VSL_GEMM_B8_SHIFT_DEFAULT;
+    return *shift >= VSL_GEMM_B8_SHIFT_MIN && *shift <= VSL_GEMM_B8_SHIFT_MAX;
+}
+
+// The A-operand flags of the stage entries: A_X2 or A_F8 (not both), a weight shift in range.
+static bool a_flags_valid(int a_flags, int* shift) {
+    const int form = a_flags & (VSL_GEMM_A_X2 | VSL_GEMM_A_F8);
+    return !(a_flags & ~(VSL_GEMM_A_X2 | VSL_GEMM_A_F8 | kB8Field)) && form != (VSL_GEMM_A_X2 | VSL_GEMM_A_F8) &&
+           gemm_b8_shift(a_flags, shift);
+}
+
 // The K split launch_gemm takes for a shape and workspace (0: unsplit kernels).
 static uint32_t splitk_choice(uint32_t M, uint32_t N, uint32_t K, int epi, const float* ws, uint64_t ws_bytes) {
     for (int cfg = 0; cfg < 2; ++cfg)
@@ -838,18 +855,18 @@ static bool aligned_to(const void* p, uintptr_t a) { return (reinterpret_cast<ui
 // Tile configuration by occupancy: the largest tiles that still give every CU a tile.
 template <int EPI>
 static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint32_t M, uint32_t N, uint32_t K,
-                       void* C, int am, int cm, float* ws, uint64_t ws_bytes) {
+                       void* C, int am, int cm, float* ws, uint64_t ws_bytes, int b8s) {
     auto blocks = [](uint32_t tiles) { return ((tiles + 7) / 8) * 8; };  // whole XCD ranges (tile_of)
     // shapes whose 256 x 256 (else 128 x 256) tiles cover at least three quarters of the CUs take
     // the direct-to-LDS kernel
     for (int cfg = 0; cfg < 2; ++cfg)
         if (vsl_gemm_dma_tiles(cfg, M, N, K, EPI) >= kDmaMinTiles)
-            return vsl_gemm_dma_launch(cfg, s, a, b, M, N, K, C, EPI, am, cm) == 0
+            return vsl_gemm_dma_launch(cfg, s, a, b, M, N, K, C, EPI, am, cm, b8s) == 0
                        ? VSL_OK
                        : vsl_invalid("vsl_gemm_f16: shape %ux%ux%u does not fit the direct-to-LDS tiles", M, N, K);
     // otherwise, with a workspace, split K over enough blocks
     if (const uint32_t ks = splitk_choice(M, N, K, EPI, ws, ws_bytes)) {
-        if (vsl_gemm_splitk_launch(ks, s, a, b, M, N, K, C, EPI, am, ws))
+        if (vsl_gemm_splitk_launch(ks, s, a, b, M, N, K, C, EPI, am, ws, b8s))
             return vsl_invalid("vsl_gemm_f16: split-K epilogue %d", EPI);
         return VSL_OK;
     }
@@ -858,16 +875,18 @@ static int launch_gemm(hipStream_t s, const vsl_half* a, const vsl_half* b, uint
     // RMSNorm), else its larger tiles even when they leave CUs idle
     if (am == kGemmAF8 || cm == kGemmCF8) {
         if (vsl_gemm_dma_tiles(1, M, N, K, EPI) && vsl_gemm_dma_tiles(2, M, N, K, EPI) >= kDmaMinTiles &&
-            vsl_gemm_dma_launch(2, s, a, b, M, N, K, C, EPI, am, cm) == 0)
+            vsl_gemm_dma_launch(2, s, a, b, M, N, K, C, EPI, am, cm, b8s) == 0)
             return VSL_OK;
         for (int cfg = 1; cfg >= 0; --cfg)
-            if (vsl_gemm_dma_tiles(cfg, M, N, K, EPI) && vsl_gemm_dma_launch(cfg, s, a, b, M, N, K, C, EPI, am, cm) == 0)
+            if (vsl_gemm_dma_tiles(cfg, M, N, K, EPI) &&
+                vsl_gemm_dma_launch(cfg, s, a, b, M, N, K, C, EPI, am, cm, b8s) == 0)
                 return VSL_OK;
         return vsl_unsupported("vsl_gemm_f16: F16F8 operands need N %% 256 == 0 (128 for SwiGLU) and K %% 128 == 0 "
                                "(shape %ux%ux%u)", M, N, K);
     }
     // few rows without a K split (e.g. a 128-row prompt's SwiGLU): the 64 x 128 direct-to-LDS tiles
-    if (vsl_gemm_dma_tiles(2, M, N, K, EPI) >= kDmaMinTiles && vsl_gemm_dma_launch(2, s, a, b, M, N, K, C, EPI, am, cm) == 0)
+    if (vsl_gemm_dma_tiles(2, M, N, K, EPI) >= kDmaMinTiles &&
+        vsl_gemm_dma_launch(2, s, a, b, M, N, K, C, EPI, am, cm, b8s) == 0)
         return VSL_OK;
     const bool ax2 = am == kGemmAX2, cx2 = cm == kGemmCX2;
     const uint32_t tb = gemm_tiles<GemmBig, EPI>(M, N), tm = gemm_tiles<GemmMid, EPI>(M, N);
@@ -884,9 +903,10 @@ static int gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32
     if (!A || !B || !C) return vsl_invalid("vsl_gemm_f16: null pointer");
     if (M == 0) return VSL_OK;
     const int epi = epilogue & 0xFF;
-    if ((epilogue & ~(0xFF | VSL_GEMM_A_X2 | VSL_GEMM_C_X2 | VSL_GEMM_A_F8 | VSL_GEMM_C_F8)) ||
+    int b8s = 0;
+    if ((epilogue & ~(0xFF | VSL_GEMM_A_X2 | VSL_GEMM_C_X2 | VSL_GEMM_A_F8 | VSL_GEMM_C_F8 | kB8Field)) ||
         (epilogue & (VSL_GEMM_A_X2 | VSL_GEMM_A_F8)) == (VSL_GEMM_A_X2 | VSL_GEMM_A_F8) ||
-        (epilogue & (VSL_GEMM_C_X2 | VSL_GEMM_C_F8)) == (VSL_GEMM_C_X2 | VSL_GEMM_C_F8))
+        (epilogue & (VSL_GEMM_C_X2 | VSL_GEMM_C_F8)) == (VSL_GEMM_C_X2 | VSL_GEMM_C_F8) || !gemm_b8_shift(epilogue, &b8s))
         return vsl_invalid("vsl_gemm_f16: flags 0x%x", epilogue);
     const int am = gemm_a_mode(epilogue);
     const int cm = (epilogue & VSL_GEMM_C_X2) ? kGemmCX2 : (epilogue & VSL_GEMM_C_F8) ? kGemmCF8 : kGemmC1;
@@ -899,10 +919,10 @@ static int gemm_f16(const void* A, const void* B, uint32_t M, uint32_t N, uint32
     const vsl_half* b = static_cast<const vsl_half*>(B);
     int rc;
     switch (epi) {
-        case VSL_EPI_STORE_F32: rc = launch_gemm<VSL_EPI_STORE_F32>(s, a, b, M, N, K, C, am, kGemmC1, ws, ws_bytes); break;
-        case VSL_EPI_STORE_F16: rc = launch_gemm<VSL_EPI_STORE_F16>(s, a, b, M, N, K, C, am, kGemmC1, ws, ws_bytes); break;
-        case VSL_EPI_RESID: rc = launch_gemm<VSL_EPI_RESID>(s, a, b, M, N, K, C, am, kGemmC1, ws, ws_bytes); break;
-        case VSL_EPI_SWIGLU: rc = launch_gemm<VSL_EPI_SWIGLU>(s, a, b, M, N, K, C, am, cm, ws, ws_bytes); break;
+        case VSL_EPI_STORE_F32: rc = launch_gemm<VSL_EPI_STORE_F32>(s, a, b, M, N, K, C, am, kGemmC1, ws, ws_bytes, b8s); break;
+        case VSL_EPI_STORE_F16: rc = launch_gemm<VSL_EPI_STORE_F16>(s, a, b, M, N, K, C, am, kGemmC1, ws, ws_bytes, b8s); break;
+        case VSL_EPI_RESID: rc = launch_gemm<VSL_EPI_RESID>(s, a, b, M, N, K, C, am, kGemmC1, ws, ws_bytes, b8s); break;
+        case VSL_EPI_SWIGLU: rc = launch_gemm<VSL_EPI_SWIGLU>(s, a, b, M, N, K, C, am, cm, ws, ws_bytes, b8s); break;
         default: return vsl_invalid("vsl_gemm_f16: epilogue %d", epi);
     }
     if (rc) return rc;
@@ -1012,8 +1032,8 @@ extern "C" int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uin
                                             void* workspace, uint64_t ws_bytes, void* stream) {
     const char* fn = "vsl_gemm_f16_qkv_rope_append";
     if (!A || !Wqkv) return vsl_invalid("%s: null pointer", fn);
-    if ((a_flags & ~(VSL_GEMM_A_X2 | VSL_GEMM_A_F8)) || a_flags == (VSL_GEMM_A_X2 | VSL_GEMM_A_F8))
-        return vsl_invalid("%s: flags 0x%x", fn, a_flags);
+    int b8s = 0;
+    if (!a_flags_valid(a_flags, &b8s)) return vsl_invalid("%s: flags 0x%x", fn, a_flags);
     if (const int rc = check_rope_split(fn, qkv, S, hd, pos0, rope_cos, rope_sin, q_out, q_dtype, kcache, vcache,
                                         kv_dtype, cap))
         return rc;
@@ -1026,7 +1046,7 @@ extern "C" int vsl_gemm_f16_qkv_rope_append(const void* A, const void* Wqkv, uin
     if (ks && rope_split4_fits(ws, hd, rope_cos, rope_sin, q_out, kcache, vcache, kv32)) {
         hipStream_t s = static_cast<hipStream_t>(stream);
         vsl_half* qo = static_cast<vsl_half*>(q_out);
-        vsl_gemm_splitk_partials(ks, stream, A, Wqkv, S, N, K, gemm_a_mode(a_flags), ws);
+        vsl_gemm_splitk_partials(ks, stream, A, Wqkv, S, N, K, gemm_a_mode(a_flags), ws, b8s);
         switch (ks) {
             case 2: launch_rope_split4<2>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
             case 4: launch_rope_split4<4>(s, ws, S, n_q, n_kv, hd, pos0, rope_cos, rope_sin, qo, x2, kcache, vcache, kv32, cap); break;
@@ -1069,8 +1089,8 @@ extern "C" int vsl_gemm_f16_resid_rmsnorm(const void* A, const void* B, uint32_t
                                           int xn_dtype, void* workspace, uint64_t ws_bytes, void* stream) {
     const char* fn = "vsl_gemm_f16_resid_rmsnorm";
     if (!A || !B || !x || !xn || N == 0) return vsl_invalid("%s: bad arguments", fn);
-    if ((a_flags & ~(VSL_GEMM_A_X2 | VSL_GEMM_A_F8)) || a_flags == (VSL_GEMM_A_X2 | VSL_GEMM_A_F8))
-        return vsl_invalid("%s: flags 0x%x", fn, a_flags);
+    int b8s = 0;
+    if (!a_flags_valid(a_flags, &b8s)) return vsl_invalid("%s: flags 0x%x", fn, a_flags);
     if (xn_dtype != VSL_DT_F16 && xn_dtype != VSL_DT_F16X2 && xn_dtype != VSL_DT_F16F8 && xn_dtype != VSL_DT_F32)
         return vsl_unsupported("%s: dtype %d", fn, xn_dtype);
     if (xn_dtype == VSL_DT_F16F8 && N % 32) return vsl_invalid("%s: F16F8 needs N %% 32 == 0 (N = %u)", fn, N);
@@ -1088,7 +1108,7 @@ extern "C" int vsl_gemm_f16_resid_rmsnorm(const void* A, const void* B, uint32_t
         return vsl_rmsnorm(x, gamma, M, N, eps, xn, xn_dtype, stream);
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
-    vsl_gemm_splitk_partials(ks, stream, A, B, M, N, K, gemm_a_mode(a_flags), ws);
+    vsl_gemm_splitk_partials(ks, stream, A, B, M, N, K, gemm_a_mode(a_flags), ws, b8s);
     if (xn_dtype == VSL_DT_F16)
         launch_resid_rmsnorm<vsl_half, 0>(s, ks, ws, M, N, x, gamma, eps, static_cast<vsl_half*>(xn));
     else if (xn_dtype == VSL_DT_F16X2)

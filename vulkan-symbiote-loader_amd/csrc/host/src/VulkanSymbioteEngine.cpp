@@ -206,6 +206,7 @@ VulkanSymbioteEngine::VulkanSymbioteEngine(const Path& model_path, const EngineO
     try {
         init_device(cfg, pack_dtype(qf) == VSL_DT_F16, pack_dtype(ef));
         load_weights_from_gguf();
+        measure_weight_ranges();
     } catch (...) {
         release();
         throw;
@@ -217,6 +218,7 @@ VulkanSymbioteEngine::VulkanSymbioteEngine(const SyntheticSpec& spec, const Engi
     try {
         init_device(spec.config, spec.fp16, spec.fp16 ? VSL_DT_F16 : VSL_DT_F32);
         init_synthetic_weights(spec);
+        measure_weight_ranges();
     } catch (...) {
         release();
         throw;
@@ -336,6 +338,7 @@ void VulkanSymbioteEngine::plan_and_allocate() {
     add(nq * hd * 4, reinterpret_cast<void**>(&attn_));
     add(F * 4, reinterpret_cast<void**>(&h_));
     add(V * 4, reinterpret_cast<void**>(&logits_));
+    add(4 * L * 4, reinterpret_cast<void**>(&wrange_));
     add(nq * nsplit_ * hd * 4, reinterpret_cast<void**>(&part_o_));
     add(nq * nsplit_ * 2 * 4, reinterpret_cast<void**>(&part_ml_));
     add(vsl_lm_head_ws_blocks() * 4, reinterpret_cast<void**>(&lm_val_));
@@ -633,6 +636,32 @@ void VulkanSymbioteEngine::prefill_tokenwise(uint32_t n_prompt, const SamplingPa
           "vsl_lm_head_sample");
 }
 
+void VulkanSymbioteEngine::measure_weight_ranges() {
+    // Only fp16 packs reach the fp8 lo products (the prompt pass runs on fp16 models).
+    if (wdt_ != VSL_DT_F16) return;
+    const ModelConfig& c = config_;
+    const uint64_t d = c.hidden_size, hd = c.head_dim, nq = c.num_attention_heads, nkv = c.num_key_value_heads,
+                   F = c.intermediate_size, L = c.num_layers;
+    check(vsl_memset_d(wrange_, 0, 4 * L * 4, stream_), "memset");
+    for (uint64_t l = 0; l < L; ++l) {
+        const Layer& y = layers_[l];
+        check(vsl_absmax_f16(y.wqkv, (nq + 2 * nkv) * hd * d, wrange_ + 4 * l + 0, stream_), "vsl_absmax_f16");
+        check(vsl_absmax_f16(y.wo, d * nq * hd, wrange_ + 4 * l + 1, stream_), "vsl_absmax_f16");
+        check(vsl_absmax_f16(y.wgu, 2 * F * d, wrange_ + 4 * l + 2, stream_), "vsl_absmax_f16");
+        check(vsl_absmax_f16(y.wdown, d * F, wrange_ + 4 * l + 3, stream_), "vsl_absmax_f16");
+    }
+    std::vector<float> mx(4 * L);
+    check(vsl_copy_d2h(mx.data(), wrange_, mx.size() * 4, stream_), "copy");
+    check(vsl_stream_sync(stream_), "sync");
+    for (uint64_t l = 0; l < L; ++l) {
+        Layer& y = layers_[l];
+        y.b8_qkv = VSL_GEMM_B8_SHIFT(vsl_gemm_b8_shift(mx[4 * l + 0]));
+        y.b8_o = VSL_GEMM_B8_SHIFT(vsl_gemm_b8_shift(mx[4 * l + 1]));
+        y.b8_gu = VSL_GEMM_B8_SHIFT(vsl_gemm_b8_shift(mx[4 * l + 2]));
+        y.b8_down = VSL_GEMM_B8_SHIFT(vsl_gemm_b8_shift(mx[4 * l + 3]));
+    }
+}
+
 uint32_t VulkanSymbioteEngine::prefill_lo8_stages() const {
     // VSL_GEMM_A_F8 / VSL_GEMM_C_F8 need N % 256 == 0 (128 for SwiGLU) and K % 128 == 0
     const ModelConfig& c = config_;
@@ -679,7 +708,12 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
         check(vsl_rmsnorm(px_, layers_[0].attn_norm, S, d, eps, pxn_, n1, stream_), "vsl_rmsnorm");
         for (uint32_t l = 0; l < c.num_layers; ++l) {
             const Layer& y = layers_[l];
-            check(vsl_gemm_f16_qkv_rope_append(pxn_, y.wqkv, S, d, a_qkv, nq, nkv, hd, c0, rope_cos_, rope_sin_, pq_,
+            // the fp8 lo products take this layer's weight shifts
+            const int a_qkv_l = a_qkv | (a_qkv == VSL_GEMM_A_F8 ? y.b8_qkv : 0);
+            const int a_o_l = a_o | (a_o == VSL_GEMM_A_F8 ? y.b8_o : 0);
+            const int g_gu_l = g_gu | ((g_gu & VSL_GEMM_A_F8) ? y.b8_gu : 0);
+            const int a_dn_l = a_dn | (a_dn == VSL_GEMM_A_F8 ? y.b8_down : 0);
+            check(vsl_gemm_f16_qkv_rope_append(pxn_, y.wqkv, S, d, a_qkv_l, nq, nkv, hd, c0, rope_cos_, rope_sin_, pq_,
                                                qdt, y.kc, y.vc, kvdt_, cap_, pqkv_, gws_, gws_bytes_, stream_),
                   "qkv + rope");
             if (config_.use_sparse_attention)
@@ -690,16 +724,16 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
             else
                 check(vsl_attn_prefill(pq_, qdt, y.kc, y.vc, S, c0, nq, nkv, hd, cap_, scale, pattn_, odt, stream_),
                       "vsl_attn_prefill");
-            check(vsl_gemm_f16_resid_rmsnorm(pattn_, y.wo, S, d, nq * hd, a_o, px_, y.ffn_norm, eps, pxn_, n2, gws_,
+            check(vsl_gemm_f16_resid_rmsnorm(pattn_, y.wo, S, d, nq * hd, a_o_l, px_, y.ffn_norm, eps, pxn_, n2, gws_,
                                              gws_bytes_, stream_),
                   "o + ffn norm");
-            check(vsl_gemm_f16(pxn_, y.wgu, S, F, d, ph_, g_gu, stream_), "gemm gate/up");
+            check(vsl_gemm_f16(pxn_, y.wgu, S, F, d, ph_, g_gu_l, stream_), "gemm gate/up");
             if (l + 1 < c.num_layers)
-                check(vsl_gemm_f16_resid_rmsnorm(ph_, y.wdown, S, d, F, a_dn, px_, layers_[l + 1].attn_norm, eps, pxn_,
-                                                 n1, gws_, gws_bytes_, stream_),
+                check(vsl_gemm_f16_resid_rmsnorm(ph_, y.wdown, S, d, F, a_dn_l, px_, layers_[l + 1].attn_norm, eps,
+                                                 pxn_, n1, gws_, gws_bytes_, stream_),
                       "down + attention norm");
             else
-                check(vsl_gemm_f16_ws(ph_, y.wdown, S, d, F, px_, VSL_EPI_RESID | a_dn, gws_, gws_bytes_, stream_),
+                check(vsl_gemm_f16_ws(ph_, y.wdown, S, d, F, px_, VSL_EPI_RESID | a_dn_l, gws_, gws_bytes_, stream_),
                       "gemm down");
         }
     }

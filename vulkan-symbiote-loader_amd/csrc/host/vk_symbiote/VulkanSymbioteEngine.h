@@ -202,6 +202,9 @@ class VulkanSymbioteEngine {
         void* wdown = nullptr;
         void* kc = nullptr;
         void* vc = nullptr;
+        // VSL_GEMM_B8_SHIFT flags of the fp8 lo products against [Wq; Wk; Wv], Wo, [Wgate; Wup], Wdown:
+        // each matrix's own shift, from its largest weight (measure_weight_ranges)
+        int b8_qkv = 0, b8_o = 0, b8_gu = 0, b8_down = 0;
     };
 
     ModelConfig config_;
@@ -230,6 +233,7 @@ class VulkanSymbioteEngine {
     float* rope_cos_ = nullptr;
     float* rope_sin_ = nullptr;
     float *x_ = nullptr, *q_ = nullptr, *attn_ = nullptr, *h_ = nullptr, *logits_ = nullptr;
+    float* wrange_ = nullptr;  // [L][4] largest weight magnitudes (measure_weight_ranges)
     float *part_o_ = nullptr, *part_ml_ = nullptr;
     float* lm_val_ = nullptr;
     uint32_t* lm_idx_ = nullptr;
@@ -263,6 +267,9 @@ class VulkanSymbioteEngine {
     void prefill_batched(uint32_t n_prompt, const SamplingParams& p);
     // the stages of options_.prefill_lo8 whose GEMM shapes have the fp8 lo form
     uint32_t prefill_lo8_stages() const;
+    // the fp8 lo products' weight shifts of every layer (Layer::b8_*), from each fp16 matrix's largest
+    // finite magnitude, so that no weight leaves e4m3's range
+    void measure_weight_ranges();
     vsl_graph* step_graph(const SamplingParams& p);
     void release();
     void check(int rc, const char* what) const;
