@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <string>
 #include <vector>
 
@@ -75,6 +76,33 @@ int main(int argc, char** argv) {
     CHECK(tc.model_type == "llama" && tc.bos_token_id == 1 && tc.eos_token_id == 2);
     CHECK(tc.add_bos_token && !tc.add_eos_token && tc.chat_template == "{{x}}");
     std::printf("vocabulary ok\n");
+
+    // metadata arrays (GGUFMetadataKV, GGUFLoader.h:95-104): the element type, and the element bytes
+    // without the u32 type + u64 count header
+    const GGUFMetadataKV* sc = g.get_metadata("tokenizer.ggml.scores");
+    CHECK(sc != nullptr && sc->value_type == GGUFValueType::ARRAY);
+    CHECK(sc->get_array_element_type() == GGUFValueType::FLOAT32);
+    const std::vector<uint8_t> sb = sc->get_array_data();
+    const float want_scores[4] = {0.0f, -1.5f, -2.5f, 3.25f};
+    CHECK(sb.size() == sizeof(want_scores) && std::memcmp(sb.data(), want_scores, sizeof(want_scores)) == 0);
+    const GGUFMetadataKV* ty = g.get_metadata("tokenizer.ggml.token_type");
+    CHECK(ty != nullptr && ty->get_array_element_type() == GGUFValueType::INT32);
+    const std::vector<uint8_t> tb = ty->get_array_data();
+    int32_t t3 = 0;
+    CHECK(tb.size() == 16);
+    std::memcpy(&t3, tb.data() + 12, 4);
+    CHECK(t3 == 1);
+    const GGUFMetadataKV* tk = g.get_metadata("tokenizer.ggml.tokens");
+    CHECK(tk != nullptr && tk->get_array_element_type() == GGUFValueType::STRING);
+    CHECK(tk->get_array_data().size() == 4 * 8 + 5 + 3 + 4 + 3);  // (u64 length, bytes) per string
+    const GGUFMetadataKV* bos = g.get_metadata("tokenizer.ggml.bos_token_id");
+    CHECK(bos != nullptr && bos->get_array_element_type() == GGUFValueType::UINT8 && bos->get_array_data().empty());
+    // every tensor-type id of the reference's enum is declared
+    static_assert(static_cast<uint32>(GGUFValueType::Q8_1) == 18 && static_cast<uint32>(GGUFValueType::Q6_K) == 23 &&
+                      static_cast<uint32>(GGUFValueType::IQ4_NL) == 31 && static_cast<uint32>(GGUFValueType::IQ4_XS_2) == 46 &&
+                      static_cast<uint32>(GGUFValueType::IQ2_M) == 49 && static_cast<uint32>(GGUFValueType::IQ4_XS_3) == 53,
+                  "GGUFValueType ids");
+    std::printf("metadata arrays ok\n");
 
     // shards
     CHECK(!g.is_sharded());

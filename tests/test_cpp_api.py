@@ -32,7 +32,7 @@ def test_gguf_loader_cpp_api(vsl, tmp_path):
     exe = compile_cpp(vsl, "gguf_api_check.cpp", tmp_path / "gguf_api_check")
     r = subprocess.run([exe, str(tmp_path)], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
-    for part in ("vocabulary ok", "shards ok", "stream ok", "cache ok", "expected ok"):
+    for part in ("vocabulary ok", "metadata arrays ok", "shards ok", "stream ok", "cache ok", "expected ok"):
         assert part in r.stdout
     assert "checks passed" in r.stdout
 

@@ -52,9 +52,16 @@ bool GGUFMetadataKV::get_bool() const {
     if (value_type != GGUFValueType::BOOL || raw_value.empty()) return false;
     return raw_value[0] != 0;
 }
+// arrays are stored as (u32 element type, u64 count, elements); the accessors split that header off
 std::vector<uint8_t> GGUFMetadataKV::get_array_data() const {
     if (value_type != GGUFValueType::ARRAY || raw_value.size() < 12) return {};
-    return raw_value;
+    return std::vector<uint8_t>(raw_value.begin() + 12, raw_value.end());
+}
+GGUFValueType GGUFMetadataKV::get_array_element_type() const {
+    if (value_type != GGUFValueType::ARRAY || raw_value.size() < 4) return GGUFValueType::UINT8;
+    uint32_t t;
+    std::memcpy(&t, raw_value.data(), 4);
+    return static_cast<GGUFValueType>(t);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -412,10 +419,10 @@ ModelConfig GGUFLoader::get_model_config() const {  // GGUFLoader.cpp:673-728
     if (auto* kv = get_metadata("llama.vocab_size")) {
         c.vocab_size = kv->get_uint32();
     } else if (auto* kv2 = get_metadata("tokenizer.ggml.tokens")) {
-        auto arr = kv2->get_array_data();
-        if (arr.size() >= 12) {
+        // the array's element count (the u64 after its element type)
+        if (kv2->value_type == GGUFValueType::ARRAY && kv2->raw_value.size() >= 12) {
             uint64_t cnt;
-            std::memcpy(&cnt, arr.data() + 4, 8);
+            std::memcpy(&cnt, kv2->raw_value.data() + 4, 8);
             c.vocab_size = static_cast<uint32_t>(cnt);
         }
     }

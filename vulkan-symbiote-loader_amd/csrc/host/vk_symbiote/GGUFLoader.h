@@ -31,11 +31,20 @@
 
 namespace vk_symbiote {
 
+// Every id of the reference's enum (GGUFLoader.h:18-73), so that caller code naming any of them
+// compiles. Metadata value types use 0-12; as tensor types the loader reads F32 (6 in the reference's
+// convention), FLOAT16 (48), Q4_0, Q4_1 and Q8_0; the other block types are recognised by id and
+// rejected when read (-20), as the reference's read_tensor_data does.
 enum class GGUFValueType : uint32 {
     UINT8 = 0, INT8 = 1, UINT16 = 2, INT16 = 3, UINT32 = 4, INT32 = 5, FLOAT32 = 6, BOOL = 7,
     STRING = 8, ARRAY = 9, UINT64 = 10, INT64 = 11, FLOAT64 = 12,
-    Q4_0 = 13, Q4_1 = 14, Q5_0 = 15, Q5_1 = 16, Q8_0 = 17,
-    BFLOAT16 = 47, FLOAT16 = 48
+    Q4_0 = 13, Q4_1 = 14, Q5_0 = 15, Q5_1 = 16, Q8_0 = 17, Q8_1 = 18,
+    Q2_K = 19, Q3_K = 20, Q4_K = 21, Q5_K = 22, Q6_K = 23, Q8_K = 24,
+    IQ1_S = 25, IQ1_M = 26, IQ2_XXS = 27, IQ2_XS = 28, IQ3_XXS = 29, IQ4_XS = 30, IQ4_NL = 31,
+    IQ5_S = 32, IQ5_M = 33, IQ6_N = 34, IQ6_1 = 35, IQ2_S = 36, IQ3_S = 37, IQ4_1 = 38, IQ3_1 = 39,
+    IQ2_1 = 40, IQ1_1 = 41, IQ4_NL_2 = 42, IQ3_L = 43, IQ3_XS = 44, IQ3_M = 45, IQ4_XS_2 = 46,
+    BFLOAT16 = 47, FLOAT16 = 48,
+    IQ2_M = 49, IQ3_XS_2 = 50, IQ3_L_2 = 51, IQ3_M_2 = 52, IQ4_XS_3 = 53
 };
 
 enum class GGUFConvention : int { REFERENCE = 0, GGML = 1 };
@@ -69,7 +78,10 @@ struct GGUFMetadataKV {
     int32_t get_int32() const;
     float get_float32() const;
     bool get_bool() const;
+    // an array's element bytes (without the u32 element type and u64 count that precede them)
     std::vector<uint8_t> get_array_data() const;
+    // an array's element type (UINT8 for a value that is not an array)
+    GGUFValueType get_array_element_type() const;
 };
 
 // A vocabulary entry of the model file (GGUFLoader.h:110-116): token text and bytes from
