@@ -323,7 +323,31 @@ def run_long(a):
     print(json.dumps(out), flush=True)
 
 
-def llama_1b_leg(vsl, eager, prefill_runs=5):
+def decode_ops_table(eng, cfg, p_att, iterations=3):
+    """Each decode op's average device time per launch (HIP events on the engine's stream, every layer
+    visited per round, so no weight is served from the MALL) with its algorithmic bytes and rate."""
+    d, F, V = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"]
+    nq, nkv = cfg["num_heads"], cfg["num_kv_heads"]
+    hd = d // nq
+    names = ["qkv_rope_append", "attn_decode", "o_proj_resid", "norm_gateup_swiglu", "down_proj_resid",
+             "lm_head_argmax"]
+    bytes_per_launch = [
+        2 * (nq + 2 * nkv) * hd * d + 8 * d + 4 * nq * hd + 2 * 2 * nkv * hd,
+        2 * 2 * nkv * hd * p_att + 8 * nq * hd,
+        2 * d * nq * hd + 4 * nq * hd + 8 * d,
+        2 * 2 * F * d + 8 * d + 4 * F,
+        2 * d * F + 4 * F + 8 * d,
+        2 * V * d + 8 * d + 4 * V,
+    ]
+    ops = {}
+    for op, nm in enumerate(names):
+        ms = eng.time_op(op, iterations)
+        ops[nm] = {"avg_us": round(ms * 1e3, 2), "bytes": bytes_per_launch[op],
+                   "gbps": round(bytes_per_launch[op] / (ms * 1e-3) / 1e9, 1)}
+    return ops
+
+
+def llama_1b_leg(vsl, eager, prefill_runs=5, kernel_timing=True):
     """1B-class fp16 (16 layers, d 2048, 32/8 heads, FFN 8192, V 32000): prompt 128, greedy decode 256."""
     n_prompt, steps = 128, 256
     prompt = np.random.default_rng(2).integers(0, LLAMA_1B["vocab_size"], n_prompt).astype(np.uint32)
@@ -338,16 +362,38 @@ def llama_1b_leg(vsl, eager, prefill_runs=5):
             eng.begin(prompt, 1)
             eng.finish()
             pre.append(eng.last_stats()["prefill_ms"])
+        # per-op times at the decode's last position (the KV length of the final step)
+        ops = decode_ops_table(eng, LLAMA_1B, n_prompt + steps) if kernel_timing else None
     finally:
         eng.close()
     pre_ms = float(np.median(pre))
     pre_flops = prefill_flops(LLAMA_1B, n_prompt)
-    return {"workload": f"1B-class Llama decoder fp16 bs=1 (16L, d2048, 32/8 heads, FFN 8192, V32000): prompt "
-                        f"{n_prompt}, greedy decode {steps}",
-            "decode": decode_rates(LLAMA_1B, n_prompt, steps, dec_s),
-            "prefill_ms": round(pre_ms, 3), "prefill_tok_s": round(n_prompt / (pre_ms / 1e3), 1),
-            "prefill_tflops": round(pre_flops / (pre_ms / 1e3) / 1e12, 1),
-            "prefill_mfma_frac": round(pre_flops / (pre_ms / 1e3) / PEAK_F16, 4)}
+    out = {"workload": f"1B-class Llama decoder fp16 bs=1 (16L, d2048, 32/8 heads, FFN 8192, V32000): prompt "
+                       f"{n_prompt}, greedy decode {steps}",
+           "decode": decode_rates(LLAMA_1B, n_prompt, steps, dec_s),
+           "prefill_ms": round(pre_ms, 3), "prefill_tok_s": round(n_prompt / (pre_ms / 1e3), 1),
+           "prefill_tflops": round(pre_flops / (pre_ms / 1e3) / 1e12, 1),
+           "prefill_mfma_frac": round(pre_flops / (pre_ms / 1e3) / PEAK_F16, 4)}
+    if ops is not None:
+        out["decode_ops"] = ops
+    return out
+
+
+def copy_calibration(vsl, mb):
+    """One device-to-device copy of `mb` MiB: a kernel of known traffic for scaling rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters. Returns the bytes copied."""
+    import ctypes
+    H = vsl.hip()
+    nbytes = mb << 20
+    arena = ctypes.c_void_p()
+    vsl.check(H.vsl_arena_create(0, 2 * nbytes + (1 << 20), ctypes.byref(arena)))
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    vsl.check(H.vsl_arena_alloc(arena, nbytes, 256, ctypes.byref(src)))
+    vsl.check(H.vsl_arena_alloc(arena, nbytes, 256, ctypes.byref(dst)))
+    vsl.check(H.vsl_copy_d2d(dst, src, nbytes, None))
+    vsl.check(H.vsl_device_sync())
+    vsl.check(H.vsl_arena_destroy(arena))
+    return nbytes
 
 
 def main():
@@ -390,12 +436,15 @@ def main():
         return
     if a.llama_1b:
         gpus_or_exit(a)
-        lg = llama_1b_leg(load_package(), a.eager)
+        vsl = load_package()
+        lg = llama_1b_leg(vsl, a.eager, kernel_timing=not a.no_kernel_timing)
         out = {"metric": "decode tok/s + HBM GB/s (% peak), 1B fp16 bs=1; prefill tok/s",
                "value": lg["decode"]["tok_s"], "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
                "dtype": "f16", "data": "synthetic: random-init N(0,0.02) fp16 weights, uniform-random prompt ids",
                "config": {"workload": lg["workload"]}}
         out.update(lg)
+        if a.copy_calibration_mb:
+            out["copy_calibration_bytes"] = copy_calibration(vsl, a.copy_calibration_mb)
         print(json.dumps(out), flush=True)
         return
     gpus_or_exit(a)
@@ -469,25 +518,7 @@ def main():
     }
 
     if not a.no_kernel_timing:
-        d, F, V = CFG["hidden_size"], CFG["intermediate_size"], CFG["vocab_size"]
-        nq, nkv = CFG["num_heads"], CFG["num_kv_heads"]
-        hd = d // nq
-        names = ["qkv_rope_append", "attn_decode", "o_proj_resid", "norm_gateup_swiglu", "down_proj_resid",
-                 "lm_head_argmax"]
-        p_att = a.prompt + a.steps
-        bytes_per_launch = [
-            2 * (nq + 2 * nkv) * hd * d + 8 * d + 4 * nq * hd + 2 * 2 * nkv * hd,
-            2 * 2 * nkv * hd * p_att + 8 * nq * hd,
-            2 * d * nq * hd + 4 * nq * hd + 8 * d,
-            2 * 2 * F * d + 8 * d + 4 * F,
-            2 * d * F + 4 * F + 8 * d,
-            2 * V * d + 8 * d + 4 * V,
-        ]
-        ops = {}
-        for op, nm in enumerate(names):
-            ms = eng.time_op(op, 3)
-            ops[nm] = {"avg_us": round(ms * 1e3, 2), "bytes": bytes_per_launch[op],
-                       "gbps": round(bytes_per_launch[op] / (ms * 1e-3) / 1e9, 1)}
+        ops = decode_ops_table(eng, CFG, a.prompt + a.steps)
         dom = ops["norm_gateup_swiglu"]
         achieved = dom["bytes"] / (dom["avg_us"] * 1e-6)
         out["roofline"] = {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
@@ -514,7 +545,7 @@ def main():
     eng.close()
     if not a.quick:
         # the other configurations, each in its own engine after the 8B one is released
-        for key, leg in (("llama_1b", lambda: llama_1b_leg(vsl, a.eager)),
+        for key, leg in (("llama_1b", lambda: llama_1b_leg(vsl, a.eager, kernel_timing=not a.no_kernel_timing)),
                          ("gemv_sweep", lambda: sweep_leg(vsl, graph=not a.eager)),
                          ("long_context", lambda: long_leg(vsl, 128, a.eager))):
             try:
@@ -522,18 +553,7 @@ def main():
             except Exception as ex:  # reported, never fatal to the headline measurement
                 out[key] = {"failed": str(ex)}
     if a.copy_calibration_mb:
-        import ctypes
-        H = vsl.hip()
-        nbytes = a.copy_calibration_mb << 20
-        arena = ctypes.c_void_p()
-        vsl.check(H.vsl_arena_create(0, 2 * nbytes + (1 << 20), ctypes.byref(arena)))
-        src, dst = ctypes.c_void_p(), ctypes.c_void_p()
-        vsl.check(H.vsl_arena_alloc(arena, nbytes, 256, ctypes.byref(src)))
-        vsl.check(H.vsl_arena_alloc(arena, nbytes, 256, ctypes.byref(dst)))
-        vsl.check(H.vsl_copy_d2d(dst, src, nbytes, None))
-        vsl.check(H.vsl_device_sync())
-        vsl.check(H.vsl_arena_destroy(arena))
-        out["copy_calibration_bytes"] = nbytes
+        out["copy_calibration_bytes"] = copy_calibration(vsl, a.copy_calibration_mb)
     print(json.dumps(out), flush=True)
 
 

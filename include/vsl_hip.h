@@ -189,7 +189,8 @@ int vsl_gemv(const void* W, int wdtype, uint32_t N, uint32_t K, const void* X, i
              void* Y, int ydtype, void* stream);
 
 /* The same product for a batch of B activation vectors, each contiguous: X fp16 [B][K], Y [B][N]
- * (f16 or f32), W fp16 [N][K]; 1 <= B <= 16, K % 512 == 0.  One pass over W: whole rows streamed
+ * (f16 or f32), W fp16 [N][K]; 1 <= B <= 16, K % 512 == 0.  One pass over W: B = 1 runs the decode
+ * GEMV when X is 8-byte aligned and K <= 16384; whole rows streamed
  * with fp16 dot products into fp32 for 2 <= B <= 8 when X (B * K * 2 bytes) is at most 128 KB, K %
  * 1024 == 0 and X is 16-byte aligned; MFMA otherwise (W and X staged through LDS in whole-line runs
  * when K % 1024 == 0 and X is 16-byte aligned, register fragments else).  No reference
@@ -310,9 +311,12 @@ int vsl_gemm_f16_ws(const void* A, const void* B, uint32_t M, uint32_t N, uint32
                     void* workspace, uint64_t ws_bytes, void* stream);
 uint64_t vsl_gemm_f16_ws_bytes(uint32_t M, uint32_t N, uint32_t K, int epilogue);
 /* 1 when vsl_gemm_f16_ws (with vsl_gemm_f16_ws_bytes of workspace) runs this shape on the
- * direct-to-LDS kernel -- the one with the F8 forms -- with enough tiles or K-split items to cover
- * three quarters of the CUs; 0 when it would take the register-staged kernel instead (an F8 form
- * then forces the direct-to-LDS tiles at lower occupancy, e.g. a 128-row SwiGLU on 64 tiles). */
+ * direct-to-LDS kernel -- the one with the F8 forms -- through whole tiles that cover three quarters
+ * of the CUs (192 tiles of 256 x 256 or 128 x 256), or through a K split: the smallest split giving
+ * 192 work items where K allows one, else the widest split K allows when that gives at least 64
+ * items (few-row shapes such as a 128-row prompt against N = 2048); 0 when it would take the
+ * register-staged kernel instead (an F8 form then forces the direct-to-LDS tiles at lower occupancy,
+ * e.g. a 128-row SwiGLU on 64 tiles). */
 int vsl_gemm_f16_direct(uint32_t M, uint32_t N, uint32_t K, int epilogue);
 
 /* Q/K/V split of a prefill QKV GEMM output (f32 [S][(n_q+2 n_kv) hd]) with RoPE at positions

@@ -125,6 +125,21 @@ def test_gemv_batched_rows(vsl, orc, dev, H, N, K, B, ydt):
         assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -11 + 1e-4 * np.max(np.abs(ref)))
 
 
+@pytest.mark.parametrize("B,off", [(1, 1), (1, 4), (4, 1), (12, 3)])
+def test_gemv_batched_x_offset(vsl, orc, dev, H, B, off):
+    """X starting `off` halfs past an aligned address: B = 1 takes the decode GEMV (8-byte X loads) only
+    when X is 8-byte aligned, the other routes take X at any 2-byte alignment; the same result."""
+    N, K = 2048, 4096
+    rng = np.random.default_rng(B * 10 + off)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    X = rng.normal(0, 1, (B, K)).astype(np.float16)
+    ref = orc.gemm_nt(W, np.ascontiguousarray(X.T).astype(np.float32))
+    buf = dev.put(np.concatenate([np.zeros(off, np.float16), X.reshape(-1), np.zeros(8, np.float16)]))
+    dY = dev.empty((B, N), np.float32)
+    ok(vsl, H.vsl_gemv_batched(dev.p(dev.put(W)), N, K, dev.p(buf) + 2 * off, B, dev.p(dY), vsl.VSL_DT_F32, None))
+    assert rel_err(dev.get(dY).T, ref) < 1e-5
+
+
 def test_gemv_rejects_bad_shapes(vsl, dev, H):
     d = dev.empty((16,), np.float32)
     assert H.vsl_gemv_batched(dev.p(d), 4, 1000, dev.p(d), 1, dev.p(d), 0, None) == -100  # K % 512

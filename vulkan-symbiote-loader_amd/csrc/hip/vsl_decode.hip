@@ -2264,7 +2264,8 @@ extern "C" int vsl_gemv_batched(const void* W, uint32_t N, uint32_t K, const voi
     if (K % kSkKAlign) return vsl_invalid("vsl_gemv_batched: K=%u must be a multiple of %u", K, kSkKAlign);
     if (ydtype != VSL_DT_F16 && ydtype != VSL_DT_F32) return vsl_unsupported("vsl_gemv_batched: Y dtype %d", ydtype);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (B == 1 && K <= kMaxK) return gemv_one_f16x(W, N, K, X, Y, ydtype, s);
+    // the decode GEMV stages X with 8-byte loads; an X that is only 2-byte aligned takes the MFMA kernel
+    if (B == 1 && K <= kMaxK && (reinterpret_cast<uintptr_t>(X) & 7) == 0) return gemv_one_f16x(W, N, K, X, Y, ydtype, s);
     if (rows_fits(B, K, X))
         return ydtype == VSL_DT_F16 ? launch_rows<vsl_half>(W, N, K, X, B, Y, s) : launch_rows<float>(W, N, K, X, B, Y, s);
     if (K % kSlKAlign == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 && ((uint64_t)N * K * 2) >> 32 == 0 &&

@@ -673,8 +673,9 @@ int vsl_gemm_dma_launch(int cfg, void* stream, const void* A, const void* B, uin
 
 // Each thread folds eight fp16 values per 16-byte load (one value per load when x is not 16-byte
 // aligned) as integers: a finite binary16's magnitude bits order like its value, and an exponent field
-// of all ones (infinity, NaN) is skipped. One device-scope atomic maximum per wave on the float bits
-// of the result (non-negative floats order like their bits).
+// of all ones (infinity, NaN) is skipped. One device-scope atomic maximum per block on the float bits
+// of the result (non-negative floats order like their bits; same-address atomics serialise at about
+// 10 ns each, so the grid is kept to a few hundred blocks).
 __global__ __launch_bounds__(256) void k_absmax_f16(const uint16_t* __restrict__ x, uint64_t n, bool vec,
                                                      uint32_t* __restrict__ out) {
     uint32_t m = 0;
@@ -700,7 +701,11 @@ __global__ __launch_bounds__(256) void k_absmax_f16(const uint16_t* __restrict__
         const uint32_t o = (uint32_t)__shfl_xor((int)m, off);
         m = o > m ? o : m;
     }
-    if ((threadIdx.x & 63) == 0) {
+    __shared__ uint32_t wmax[4];
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) m = wmax[w] > m ? wmax[w] : m;
         const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)m);
         atomicMax(out, __float_as_uint(f));
     }
@@ -712,7 +717,7 @@ extern "C" int vsl_absmax_f16(const void* x, uint64_t n, float* max_abs, void* s
     if (n == 0) return VSL_OK;
     const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
     const uint64_t items = vec ? n / 8 + 1 : n;
-    const uint32_t grid = (uint32_t)std::min<uint64_t>((items + 255) / 256, 2048);
+    const uint32_t grid = (uint32_t)std::min<uint64_t>((items + 255) / 256, 512);
     k_absmax_f16<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(static_cast<const uint16_t*>(x), n, vec,
                                                                       reinterpret_cast<uint32_t*>(max_abs));
     HIP_TRY(hipGetLastError());
