@@ -347,9 +347,10 @@ def decode_ops_table(eng, cfg, p_att, iterations=3):
     return ops
 
 
-def llama_1b_leg(vsl, eager, prefill_runs=5, kernel_timing=True):
-    """1B-class fp16 (16 layers, d 2048, 32/8 heads, FFN 8192, V 32000): prompt 128, greedy decode 256."""
-    n_prompt, steps = 128, 256
+def llama_1b_leg(vsl, eager, prefill_runs=5, kernel_timing=True, steps=256):
+    """1B-class fp16 (16 layers, d 2048, 32/8 heads, FFN 8192, V 32000): prompt 128, greedy decode 256
+    (`steps` shortens the decode for profiling runs)."""
+    n_prompt = 128
     prompt = np.random.default_rng(2).integers(0, LLAMA_1B["vocab_size"], n_prompt).astype(np.uint32)
     eng = vsl.Engine(spec=LLAMA_1B, seed=0, kv_capacity=1024, use_graph=not eager)
     try:
@@ -407,6 +408,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--llama-1b", action="store_true",
                     help="the 1B-class workload alone (prompt 128, greedy decode 256): one JSON line")
+    ap.add_argument("--steps-1b", type=int, default=256,
+                    help="decode steps of the 1B-class workload (256 as configured; fewer for profiling runs)")
     ap.add_argument("--attn-splits", type=int, default=0,
                     help="decode attention split count of the 8B engine (0: the engine's choice)")
     ap.add_argument("--quick", action="store_true",
@@ -437,7 +440,7 @@ def main():
     if a.llama_1b:
         gpus_or_exit(a)
         vsl = load_package()
-        lg = llama_1b_leg(vsl, a.eager, kernel_timing=not a.no_kernel_timing)
+        lg = llama_1b_leg(vsl, a.eager, kernel_timing=not a.no_kernel_timing, steps=a.steps_1b)
         out = {"metric": "decode tok/s + HBM GB/s (% peak), 1B fp16 bs=1; prefill tok/s",
                "value": lg["decode"]["tok_s"], "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
                "dtype": "f16", "data": "synthetic: random-init N(0,0.02) fp16 weights, uniform-random prompt ids",
