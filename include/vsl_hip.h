@@ -60,8 +60,9 @@ enum {
     VSL_SAMPLE_TOPK_SEEDED = 2 /* Utils.cpp:140-172 top-k with a Philox4x32-10 uniform             */
 };
 /* Limit of the seeded top-k sampler (TOPK_SEEDED with T > 0): 1 <= top_k <= VSL_MAX_TOP_K (top_k > V
- * means all of V); other k return VSL_E_UNSUPPORTED.  No sampler limits V. */
-enum { VSL_MAX_TOP_K = 64 };
+ * means all of V); other k return VSL_E_UNSUPPORTED (the reference's Utils.cpp top_k_sampling takes
+ * any k <= V).  No sampler limits V. */
+enum { VSL_MAX_TOP_K = 1024 };
 
 const char* vsl_last_error(void);
 int vsl_device_count(int* n);

@@ -108,10 +108,14 @@ def test_tiny_seeded_topk(vsl, orc, tiny_path):
         t = e.generate_ids(g["prompt"], 32, mode="reference", temperature=0.7)
         r = m.generate(g["prompt"], 32, sampler=orc.SAMPLE_REFERENCE, temperature=0.7)
         assert np.array_equal(t, r) and np.array_equal(t, g["tokens"])
-        for k in (0, 65):  # outside the seeded sampler's 1..64
+        for k in (0, 1025):  # outside the seeded sampler's 1..1024
             with pytest.raises(vsl.VslError):
                 e.generate_ids(g["prompt"], 4, mode="topk", temperature=0.7, top_k=k, seed=1)
         assert len(e.generate_ids(g["prompt"], 4, mode="topk", temperature=0.7, top_k=64, seed=1)) == 4
+        # k past the one-wave path (the radix select), against the oracle
+        t = e.generate_ids(g["prompt"], 16, mode="topk", temperature=0.9, top_k=300, seed=3)
+        r = m.generate(g["prompt"], 16, sampler=orc.SAMPLE_TOPK_SEEDED, temperature=0.9, top_k=300, seed=3)
+        assert np.array_equal(t, r)
 
 
 def _oracle_from_engine(orc, e, cfg):

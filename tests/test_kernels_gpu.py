@@ -423,17 +423,19 @@ def test_sample_logits_greedy_ties_and_topk(vsl, orc, dev, H):
 
 
 def test_sample_logits_topk_limits(vsl, orc, dev, H):
-    """Seeded top-k at the largest supported k (64) against the oracle; k = 65 and k = 0 (which the
-    oracle would read as all of V) are refused with VSL_E_UNSUPPORTED by vsl_sample_logits and by
+    """Seeded top-k at the largest k of the one-wave path (64), the first k of the radix-select path
+    (65) and the largest supported k (1024) against the oracle; k = 1025 and k = 0 (which the oracle
+    would read as all of V) are refused with VSL_E_UNSUPPORTED by vsl_sample_logits and by
     vsl_lm_head_sample before anything is launched; top_k above a small V means all of V; every mode
     serves a 128256-entry vocabulary."""
     out = dev.empty((1,), np.int32)
     l = np.random.default_rng(21).normal(0, 1.0, 32000).astype(np.float32)
     dl = dev.put(l)
-    for step in range(16):
-        ok(vsl, H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 1.5, 64, 0, 5), step, dev.p(out), None))
-        assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_TOPK_SEEDED, 1.5, 64, 5, step)
-    for k in (65, 0):
+    for k in (64, 65, 1024):
+        for step in range(16):
+            ok(vsl, H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 1.5, k, 0, 5), step, dev.p(out), None))
+            assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_TOPK_SEEDED, 1.5, k, 5, step), (k, step)
+    for k in (1025, 0):
         assert H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 0.7, k, 0, 5), 0, dev.p(out), None) == -103
     big = np.random.default_rng(23).normal(0, 2.0, 128256).astype(np.float32)
     dbig = dev.put(big)
@@ -453,7 +455,7 @@ def test_sample_logits_topk_limits(vsl, orc, dev, H):
     x = dev.empty((d,), np.float32)
     c = ctrl_buf(vsl, dev, H, 3, max_steps=4, cap=64)
     before = dev.get(c).copy()
-    for k in (0, 65):
+    for k in (0, 1025):
         rc = H.vsl_lm_head_sample(None, 1e-5, dev.p(W), 1, V, d, dev.p(x), dev.p(W), 1, dev.p(logits),
                                   vsl.Sampler(2, 0.7, k, 0, 1), dev.p(ws_v), dev.p(ws_i), dev.p(toks), dev.p(c), None)
         assert rc == -103
@@ -483,11 +485,12 @@ def _topk_cases():
 
 @pytest.mark.parametrize("name", list(_topk_cases()))
 def test_sample_topk_selection_routes(vsl, orc, dev, H, name):
-    """Seeded top-k against the oracle on every selection route, k in {1, 40, 64}."""
+    """Seeded top-k against the oracle on every selection route: k in {1, 40, 64} (the threshold from
+    per-thread maxima) and {65, 300, 1024} (the radix select, whose index passes the tied cases need)."""
     l = _topk_cases()[name]
     out = dev.empty((1,), np.int32)
     dl = dev.put(l)
-    for k in (1, 40, 64):
+    for k in (1, 40, 64, 65, 300, 1024):
         for step in range(6):
             ok(vsl, H.vsl_sample_logits(dev.p(dl), l.size, vsl.Sampler(2, 0.8, k, 0, 3), step, dev.p(out), None))
             assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_TOPK_SEEDED, 0.8, k, 3, step), (name, k, step)
@@ -502,14 +505,17 @@ def test_sample_topk_nan_logits(vsl, orc, dev, H):
     l = np.random.default_rng(51).normal(0, 1.0, 32000).astype(np.float32)
     l[::2] = np.nan
     masked = np.where(np.isnan(l), -np.inf, l).astype(np.float32)
-    for step in range(8):
-        ok(vsl, H.vsl_sample_logits(dev.p(dev.put(l)), l.size, vsl.Sampler(2, 0.7, 40, 0, 8), step, dev.p(out), None))
-        assert dev.get(out)[0] == orc.sample(masked, orc.SAMPLE_TOPK_SEEDED, 0.7, 40, 8, step)
+    for k in (40, 500):
+        for step in range(8):
+            ok(vsl, H.vsl_sample_logits(dev.p(dev.put(l)), l.size, vsl.Sampler(2, 0.7, k, 0, 8), step, dev.p(out), None))
+            assert dev.get(out)[0] == orc.sample(masked, orc.SAMPLE_TOPK_SEEDED, 0.7, k, 8, step)
     few = np.full(5000, np.nan, np.float32)
     few[[9, 3]] = [1.0, 1.0]
-    for step in range(4):
-        ok(vsl, H.vsl_sample_logits(dev.p(dev.put(few)), few.size, vsl.Sampler(2, 0.7, 40, 0, 8), step, dev.p(out), None))
-        assert dev.get(out)[0] == 3
+    for k in (40, 500):
+        for step in range(4):
+            ok(vsl, H.vsl_sample_logits(dev.p(dev.put(few)), few.size, vsl.Sampler(2, 0.7, k, 0, 8), step, dev.p(out),
+                                        None))
+            assert dev.get(out)[0] == 3
 
 
 def test_sample_greedy_any_vocabulary(vsl, orc, dev, H):

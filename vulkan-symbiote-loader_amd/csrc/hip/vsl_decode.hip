@@ -1223,9 +1223,11 @@ int launch_attn_g(uint32_t G, dim3 grid, hipStream_t s, const float* q, const vo
 // samplers on logits in memory (top-k seeded, greedy) -- one block
 // ---------------------------------------------------------------------------------------------
 constexpr int kSampBlock = 1024;
-constexpr int kMaxTopK = VSL_MAX_TOP_K;
+constexpr int kMaxTopK = VSL_MAX_TOP_K;  // larger k: VSL_E_UNSUPPORTED
+constexpr int kWaveTopK = 64;            // k up to this: the threshold from per-thread maxima, weights one per lane
 constexpr int kTauPerWave = 8;  // per-wave maxima entering the threshold: 16 waves x 8 = 128 keys
-static_assert(kSampBlock / 64 * kTauPerWave == 2 * VSL_WAVE && kMaxTopK <= VSL_WAVE, "threshold sort holds two keys per lane");
+static_assert(kSampBlock / 64 * kTauPerWave == 2 * VSL_WAVE && kWaveTopK <= VSL_WAVE, "threshold sort holds two keys per lane");
+static_assert(kMaxTopK <= kSampBlock, "the selected keys are sorted one per thread");
 
 __device__ __forceinline__ float sample_uniform(uint32_t k0, uint32_t k1, uint64_t step) {
     uint32_t c[4] = {(uint32_t)step, (uint32_t)(step >> 32), 0u, 0u};
@@ -1341,6 +1343,83 @@ __device__ __forceinline__ void for_each_logit(const float* __restrict__ logits,
     });
 }
 
+// Seeded top-k for kWaveTopK < k <= kMaxTopK (Utils.cpp:151-171). The k-th largest rank key tau
+// comes from a most-significant-digit radix select over the 64-bit rank keys -- 8 bits per pass, each
+// pass streaming the logits and counting, in a 256-bin LDS histogram, the keys that share the digits
+// chosen so far; the index half of the key is needed only when several logits share the k-th value
+// and not all of them are taken. Rank keys are unique, so exactly k logits have a key >= tau; they
+// are gathered, sorted by the block, and weighted and walked by one thread in rank order, with the
+// arithmetic of the one-wave path (so both paths draw the same token from the same candidates).
+// cand and sorted hold kSampBlock keys of the caller's LDS.
+__device__ uint32_t topk_sample_large(const float* __restrict__ logits, uint32_t V, uint32_t k, float temperature,
+                                      uint32_t k0, uint32_t k1, uint64_t step, uint64_t* cand, uint64_t* sorted) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint64_t s_pref;
+    __shared__ uint32_t s_rem, s_full, s_n, s_pick;
+    const uint32_t tid = threadIdx.x;
+    uint64_t prefix = 0, mask = 0;
+    uint32_t remaining = k;  // how many of the keys matching `prefix` are still to be taken
+    for (int pass = 0; pass < 8; ++pass) {
+        const int shift = 56 - 8 * pass;
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        for_each_logit(logits, V, tid, [&](float l, uint32_t i) {
+            const uint64_t e = rank_key(value_key(l), i);
+            if ((e & mask) == prefix) atomicAdd(&hist[(uint32_t)(e >> shift) & 255u], 1u);
+        });
+        __syncthreads();
+        if (tid == 0) {
+            // the digit holding the remaining-th largest key: the bins above it hold fewer keys
+            uint32_t above = 0;
+            int d = 255;
+            for (; d > 0 && above + hist[d] < remaining; --d) above += hist[d];
+            s_pref = prefix | ((uint64_t)d << shift);
+            s_rem = remaining - above;
+            s_full = hist[d] == remaining - above ? 1u : 0u;  // every key with these digits is taken
+        }
+        __syncthreads();
+        prefix = s_pref;
+        remaining = s_rem;
+        mask |= (uint64_t)255u << shift;
+        if (s_full) break;  // tau: the chosen digits with zeros below (the least key with them)
+        __syncthreads();
+    }
+    const uint64_t tau = prefix;
+    if (tid == 0) s_n = 0;
+    __syncthreads();
+    for_each_logit(logits, V, tid, [&](float l, uint32_t i) {
+        const uint64_t e = rank_key(value_key(l), i);
+        if (e >= tau) {
+            const uint32_t slot = atomicAdd(&s_n, 1u);
+            if (slot < (uint32_t)kSampBlock) cand[slot] = e;
+        }
+    });
+    __syncthreads();
+    uint64_t x = tid < k ? cand[tid] : 0ull;
+    x = bitonic_desc<kSampBlock>(x, tid, sorted);
+    if (tid < k) cand[tid] = x;  // rank r in cand[r]
+    __syncthreads();
+    if (tid == 0) {
+        // exp((l_i - max) / T), summed and then walked in rank order, as Utils.cpp:153-170
+        const float mx = key_value((uint32_t)(cand[0] >> 32));
+        float sum = 0.f;
+        for (uint32_t i = 0; i < k; ++i) sum += expf((key_value((uint32_t)(cand[i] >> 32)) - mx) / temperature);
+        const float r = sample_uniform(k0, k1, step);
+        float cum = 0.f;
+        uint32_t pick = 0;
+        for (uint32_t i = 0; i < k; ++i) {
+            cum += expf((key_value((uint32_t)(cand[i] >> 32)) - mx) / temperature) / sum;
+            if (r < cum) {
+                pick = i;
+                break;
+            }
+        }
+        s_pick = ~(uint32_t)cand[pick];
+    }
+    __syncthreads();
+    return s_pick;
+}
+
 // Returns the sampled token (valid in every thread through LDS).  Every mode streams the logits
 // from memory once per pass (the first pass brings them into the cache); nothing is held per
 // element in registers.
@@ -1350,7 +1429,7 @@ __device__ __forceinline__ uint32_t block_sample(const float* __restrict__ logit
     __shared__ uint32_t wi[kSampBlock / 64];
     __shared__ uint64_t s_sort[kSampBlock];
     __shared__ uint64_t s_cand[kSampBlock];
-    __shared__ uint64_t s_top[kMaxTopK];
+    __shared__ uint64_t s_top[kWaveTopK];
     __shared__ uint64_t s_best[kSampBlock / 64];
     __shared__ uint64_t s_tau;
     __shared__ uint32_t s_count;
@@ -1413,6 +1492,7 @@ __device__ __forceinline__ uint32_t block_sample(const float* __restrict__ logit
     // elements (many equal logits) take k rounds of "largest key below the last" instead.
     uint32_t k = top_k > V ? V : top_k;
     if (k > (uint32_t)kMaxTopK) k = kMaxTopK;
+    if (k > (uint32_t)kWaveTopK) return topk_sample_large(logits, V, k, temperature, k0, k1, step, s_cand, s_sort);
     float bf = -INFINITY;  // per-thread maximum, first index among equals; NaNs skipped
     uint32_t bi = 0xFFFFFFFFu;
     for_each_logit(logits, V, tid, [&](float l, uint32_t i) {
@@ -1487,7 +1567,7 @@ __device__ __forceinline__ uint32_t block_sample(const float* __restrict__ logit
         const float e = lane < k ? expf((key_value((uint32_t)(t >> 32)) - mx) / temperature) : 0.f;
         float sum = 0.f;
 #pragma unroll
-        for (int i = 0; i < kMaxTopK; ++i)
+        for (int i = 0; i < kWaveTopK; ++i)
             if ((uint32_t)i < k) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), i));
         const int wi_bits = __float_as_int(e / sum);
         const float r = sample_uniform(k0, k1, step);
@@ -1495,7 +1575,7 @@ __device__ __forceinline__ uint32_t block_sample(const float* __restrict__ logit
         int pick = 0;
         bool found = false;
 #pragma unroll
-        for (int i = 0; i < kMaxTopK; ++i) {
+        for (int i = 0; i < kWaveTopK; ++i) {
             if ((uint32_t)i < k && !found) {
                 cum += __int_as_float(__builtin_amdgcn_readlane(wi_bits, i));
                 if (r < cum) { pick = i; found = true; }
