@@ -280,6 +280,23 @@ def test_llama_8b_fp16_parity(vsl, orc):
     m.close()
 
 
+@pytest.mark.slow
+@pytest.mark.timeout(900)
+def test_llama_8b_long_path_oracle(vsl, orc):
+    """The full 32-layer 8B model on the long-context path against the oracle: a KV capacity of 16384
+    (above 8192, so decode attention runs on the matrix-core kernel), a 768-token prompt in three
+    256-row MFMA chunks (each chunk attending to the cache the previous ones filled), then 16 teacher-
+    forced greedy steps and 16 teacher-forced T = 0.7 top-k 40 seeded steps on another prompt than
+    the 512-token test: logits within max-abs 2e-2 at every step, picks identical."""
+    cfg = vsl.LLAMA_8B
+    prompt = orc.random_ids(768, cfg["vocab_size"], 7)
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=16384, batched_prefill=True, prefill_chunk=256) as e:
+        m = _oracle_from_engine(orc, e, cfg)
+        _forced_parity(e, m, prompt, 16, 2e-2,
+                       runs=[dict(n=16), dict(n=16, sampler=orc.SAMPLE_TOPK_SEEDED, temperature=0.7, top_k=40, seed=5)])
+    m.close()
+
+
 # A small model with the 8B attention geometry (head_dim 128, GQA 4, theta 500000) so that the oracle can
 # follow an 8192-token prompt: the chunked MFMA prompt pass (four 2048-row chunks), RoPE at positions
 # past 8K, and the matrix-core decode attention that caches above 8192 positions select.
