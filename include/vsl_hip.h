@@ -59,10 +59,11 @@ enum {
                                   probabilities next to the maximum)                              */
     VSL_SAMPLE_TOPK_SEEDED = 2 /* Utils.cpp:140-172 top-k with a Philox4x32-10 uniform             */
 };
-/* Limit of the seeded top-k sampler (TOPK_SEEDED with T > 0): 1 <= top_k <= VSL_MAX_TOP_K (top_k > V
- * means all of V); other k return VSL_E_UNSUPPORTED (the reference's Utils.cpp top_k_sampling takes
- * any k <= V).  No sampler limits V. */
-enum { VSL_MAX_TOP_K = 1024 };
+/* Limit of the seeded top-k sampler (TOPK_SEEDED with T > 0): top_k >= 1 and min(top_k, V) <=
+ * VSL_MAX_TOP_K (top_k > V means all of V, so every k <= V is served for V up to 262144, as the
+ * reference's Utils.cpp top_k_sampling takes any k <= V); top_k = 0 and larger k return
+ * VSL_E_UNSUPPORTED.  No sampler limits V. */
+enum { VSL_MAX_TOP_K = 262144 };
 
 const char* vsl_last_error(void);
 int vsl_device_count(int* n);
@@ -256,7 +257,7 @@ int vsl_norm_swiglu(const float* x, const float* gamma, float eps, const void* W
  *   f = RMSNorm(x, gamma) (gamma may be NULL: no final norm); logits = W f (fp32 [V]);
  *   greedy: per-block argmax fused into the GEMV, reduced by a second launch;
  *   reference and top-k modes (T > 0): the GEMV writes logits and a sampling launch follows
- *   (top-k limit VSL_MAX_TOP_K; otherwise VSL_E_UNSUPPORTED before any launch).
+ *   (top-k limit: min(top_k, V) <= VSL_MAX_TOP_K; otherwise VSL_E_UNSUPPORTED before any launch).
  *   The sampled token is written to tokens[ctrl->step]; then x <- embed[token] (the next step's
  *   embedding_lookup), ctrl->pos += 1, ctrl->step += 1, and done is set on max_steps / EOS.
  *   Workspace: ws_val/ws_idx >= vsl_lm_head_ws_blocks() entries. */

@@ -108,10 +108,13 @@ def test_tiny_seeded_topk(vsl, orc, tiny_path):
         t = e.generate_ids(g["prompt"], 32, mode="reference", temperature=0.7)
         r = m.generate(g["prompt"], 32, sampler=orc.SAMPLE_REFERENCE, temperature=0.7)
         assert np.array_equal(t, r) and np.array_equal(t, g["tokens"])
-        for k in (0, 1025):  # outside the seeded sampler's 1..1024
-            with pytest.raises(vsl.VslError):
-                e.generate_ids(g["prompt"], 4, mode="topk", temperature=0.7, top_k=k, seed=1)
+        with pytest.raises(vsl.VslError):  # k = 0 is refused
+            e.generate_ids(g["prompt"], 4, mode="topk", temperature=0.7, top_k=0, seed=1)
         assert len(e.generate_ids(g["prompt"], 4, mode="topk", temperature=0.7, top_k=64, seed=1)) == 4
+        # top_k above V (4096) means all of V: four chunks of 1024 candidates
+        t = e.generate_ids(g["prompt"], 8, mode="topk", temperature=1.0, top_k=5000, seed=4)
+        r = m.generate(g["prompt"], 8, sampler=orc.SAMPLE_TOPK_SEEDED, temperature=1.0, top_k=5000, seed=4)
+        assert np.array_equal(t, r)
         # k past the one-wave path (the radix select), against the oracle
         t = e.generate_ids(g["prompt"], 16, mode="topk", temperature=0.9, top_k=300, seed=3)
         r = m.generate(g["prompt"], 16, sampler=orc.SAMPLE_TOPK_SEEDED, temperature=0.9, top_k=300, seed=3)

@@ -40,6 +40,18 @@ def test_c_abi_exports_every_declared_symbol(vsl):
     assert set(decl_hip) <= set(vsl._HIP_SIGS) and set(decl_eng) <= set(vsl._ENGINE_SIGS)
 
 
+def test_header_constants_match_the_binding(vsl):
+    """The Python binding's copies of the header's enum values (status codes, sampler modes, the
+    seeded top-k limit) equal the header's."""
+    src = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "vsl_hip.h")).read(), flags=re.S)
+    val = {n: int(v) for n, v in re.findall(r"\b(VSL_[A-Z0-9_]+)\s*=\s*(-?\d+)", src)}
+    assert val["VSL_MAX_TOP_K"] == vsl.MAX_TOP_K
+    assert (val["VSL_E_INVALID"], val["VSL_E_UNSUPPORTED"], val["VSL_E_CAPACITY"]) == (
+        vsl.VSL_E_INVALID, vsl.VSL_E_UNSUPPORTED, vsl.VSL_E_CAPACITY)
+    assert (val["VSL_SAMPLE_GREEDY"], val["VSL_SAMPLE_REFERENCE"], val["VSL_SAMPLE_TOPK_SEEDED"]) == (
+        vsl.SAMPLE_GREEDY, vsl.SAMPLE_REFERENCE, vsl.SAMPLE_TOPK_SEEDED)
+
+
 def test_gemm_direct_query(vsl):
     """vsl_gemm_f16_direct (host arithmetic only): whole 256 x 256 or 128 x 256 tiles covering >= 192
     CUs, or a K split reaching 192 items, count as direct-to-LDS; a 128-row SwiGLU (64 tiles, no K split

@@ -424,19 +424,28 @@ def test_sample_logits_greedy_ties_and_topk(vsl, orc, dev, H):
 
 def test_sample_logits_topk_limits(vsl, orc, dev, H):
     """Seeded top-k at the largest k of the one-wave path (64), the first k of the radix-select path
-    (65) and the largest supported k (1024) against the oracle; k = 1025 and k = 0 (which the oracle
-    would read as all of V) are refused with VSL_E_UNSUPPORTED by vsl_sample_logits and by
-    vsl_lm_head_sample before anything is launched; top_k above a small V means all of V; every mode
-    serves a 128256-entry vocabulary."""
+    (65), the largest single chunk (1024), the first two-chunk k (1025), k = V and top_k above V (all
+    of V: 32 chunks, the walk gathering each again) against the oracle; k = 0 (which the oracle would
+    read as all of V) and min(top_k, V) above VSL_MAX_TOP_K are refused with VSL_E_UNSUPPORTED by
+    vsl_sample_logits and by vsl_lm_head_sample before anything is launched, and k = VSL_MAX_TOP_K
+    (256 chunks) is served; top_k above a small V means all of V; every mode serves a 128256-entry
+    vocabulary."""
     out = dev.empty((1,), np.int32)
     l = np.random.default_rng(21).normal(0, 1.0, 32000).astype(np.float32)
     dl = dev.put(l)
-    for k in (64, 65, 1024):
-        for step in range(16):
+    for k in (64, 65, 1024, 1025, 32000, 0xFFFFFFFF):
+        for step in range(16 if k <= 1025 else 6):
             ok(vsl, H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 1.5, k, 0, 5), step, dev.p(out), None))
             assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_TOPK_SEEDED, 1.5, k, 5, step), (k, step)
-    for k in (1025, 0):
-        assert H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 0.7, k, 0, 5), 0, dev.p(out), None) == -103
+    assert H.vsl_sample_logits(dev.p(dl), 32000, vsl.Sampler(2, 0.7, 0, 0, 5), 0, dev.p(out), None) == -103
+    kmax = vsl.MAX_TOP_K
+    huge = np.random.default_rng(24).normal(0, 1.0, kmax + 4000).astype(np.float32)
+    dh = dev.put(huge)
+    for k in (kmax + 1, 0xFFFFFFFF):
+        assert H.vsl_sample_logits(dev.p(dh), huge.size, vsl.Sampler(2, 0.7, k, 0, 5), 0, dev.p(out), None) == -103
+    for step in range(2):
+        ok(vsl, H.vsl_sample_logits(dev.p(dh), huge.size, vsl.Sampler(2, 4.0, kmax, 0, 5), step, dev.p(out), None))
+        assert dev.get(out)[0] == orc.sample(huge, orc.SAMPLE_TOPK_SEEDED, 4.0, kmax, 5, step), step
     big = np.random.default_rng(23).normal(0, 2.0, 128256).astype(np.float32)
     dbig = dev.put(big)
     for mode, T in ((0, 0.0), (1, 0.7), (2, 0.7)):
@@ -455,10 +464,9 @@ def test_sample_logits_topk_limits(vsl, orc, dev, H):
     x = dev.empty((d,), np.float32)
     c = ctrl_buf(vsl, dev, H, 3, max_steps=4, cap=64)
     before = dev.get(c).copy()
-    for k in (0, 1025):
-        rc = H.vsl_lm_head_sample(None, 1e-5, dev.p(W), 1, V, d, dev.p(x), dev.p(W), 1, dev.p(logits),
-                                  vsl.Sampler(2, 0.7, k, 0, 1), dev.p(ws_v), dev.p(ws_i), dev.p(toks), dev.p(c), None)
-        assert rc == -103
+    rc = H.vsl_lm_head_sample(None, 1e-5, dev.p(W), 1, V, d, dev.p(x), dev.p(W), 1, dev.p(logits),
+                              vsl.Sampler(2, 0.7, 0, 0, 1), dev.p(ws_v), dev.p(ws_i), dev.p(toks), dev.p(c), None)
+    assert rc == -103
     assert np.array_equal(dev.get(c), before)  # nothing ran
 
 
@@ -486,11 +494,12 @@ def _topk_cases():
 @pytest.mark.parametrize("name", list(_topk_cases()))
 def test_sample_topk_selection_routes(vsl, orc, dev, H, name):
     """Seeded top-k against the oracle on every selection route: k in {1, 40, 64} (the threshold from
-    per-thread maxima) and {65, 300, 1024} (the radix select, whose index passes the tied cases need)."""
+    per-thread maxima), {65, 300, 1024} (the radix select, whose index passes the tied cases need) and
+    {1025, 3000} (chunks of 1024 below each other's boundary key, the walk gathering them again)."""
     l = _topk_cases()[name]
     out = dev.empty((1,), np.int32)
     dl = dev.put(l)
-    for k in (1, 40, 64, 65, 300, 1024):
+    for k in (1, 40, 64, 65, 300, 1024, 1025, 3000):
         for step in range(6):
             ok(vsl, H.vsl_sample_logits(dev.p(dl), l.size, vsl.Sampler(2, 0.8, k, 0, 3), step, dev.p(out), None))
             assert dev.get(out)[0] == orc.sample(l, orc.SAMPLE_TOPK_SEEDED, 0.8, k, 3, step), (name, k, step)

@@ -31,6 +31,7 @@ def GEMM_B8_SHIFT(s):
     """VSL_GEMM_B8_SHIFT(s): the weight shift of the fp8 lo product (B rounded to e4m3 as B * 2^s)."""
     return ((s + 128) & 0xFF) << 16
 SAMPLE_GREEDY, SAMPLE_REFERENCE, SAMPLE_TOPK_SEEDED = 0, 1, 2
+MAX_TOP_K = 262144  # VSL_MAX_TOP_K: the seeded top-k serves 1 <= min(top_k, V) <= MAX_TOP_K
 EPI_STORE_F32, EPI_STORE_F16, EPI_RESID, EPI_SWIGLU = 0, 1, 2, 3
 _MODES = {"greedy": SAMPLE_GREEDY, "reference": SAMPLE_REFERENCE, "topk": SAMPLE_TOPK_SEEDED}
 

@@ -1223,11 +1223,12 @@ int launch_attn_g(uint32_t G, dim3 grid, hipStream_t s, const float* q, const vo
 // samplers on logits in memory (top-k seeded, greedy) -- one block
 // ---------------------------------------------------------------------------------------------
 constexpr int kSampBlock = 1024;
-constexpr int kMaxTopK = VSL_MAX_TOP_K;  // larger k: VSL_E_UNSUPPORTED
+constexpr int kMaxTopK = VSL_MAX_TOP_K;  // larger k (k = min(top_k, V)): VSL_E_UNSUPPORTED
 constexpr int kWaveTopK = 64;            // k up to this: the threshold from per-thread maxima, weights one per lane
 constexpr int kTauPerWave = 8;  // per-wave maxima entering the threshold: 16 waves x 8 = 128 keys
+constexpr int kTopKChunks = kMaxTopK / kSampBlock;  // larger k: chunks of kSampBlock keys, one boundary each
 static_assert(kSampBlock / 64 * kTauPerWave == 2 * VSL_WAVE && kWaveTopK <= VSL_WAVE, "threshold sort holds two keys per lane");
-static_assert(kMaxTopK <= kSampBlock, "the selected keys are sorted one per thread");
+static_assert(kMaxTopK % kSampBlock == 0, "the selected keys are sorted one per thread, kSampBlock at a time");
 
 __device__ __forceinline__ float sample_uniform(uint32_t k0, uint32_t k1, uint64_t step) {
     uint32_t c[4] = {(uint32_t)step, (uint32_t)(step >> 32), 0u, 0u};
@@ -1343,29 +1344,25 @@ __device__ __forceinline__ void for_each_logit(const float* __restrict__ logits,
     });
 }
 
-// Seeded top-k for kWaveTopK < k <= kMaxTopK (Utils.cpp:151-171). The k-th largest rank key tau
-// comes from a most-significant-digit radix select over the 64-bit rank keys -- 8 bits per pass, each
-// pass streaming the logits and counting, in a 256-bin LDS histogram, the keys that share the digits
-// chosen so far; the index half of the key is needed only when several logits share the k-th value
-// and not all of them are taken. Rank keys are unique, so exactly k logits have a key >= tau; they
-// are gathered, sorted by the block, and weighted and walked by one thread in rank order, with the
-// arithmetic of the one-wave path (so both paths draw the same token from the same candidates).
-// cand and sorted hold kSampBlock keys of the caller's LDS.
-__device__ uint32_t topk_sample_large(const float* __restrict__ logits, uint32_t V, uint32_t k, float temperature,
-                                      uint32_t k0, uint32_t k1, uint64_t step, uint64_t* cand, uint64_t* sorted) {
-    __shared__ uint32_t hist[256];
+// The m-th largest rank key below ub (1 <= m <= the number of keys below ub): a most-significant-digit
+// radix select over the 64-bit rank keys, 8 bits per pass, each pass streaming the logits and counting,
+// in a 256-bin LDS histogram, the keys below ub that share the digits chosen so far.  The index half of
+// the key is reached only when several logits share the boundary value and not all of them are taken;
+// a pass whose chosen digit bin is taken whole ends the select (the boundary is then those digits with
+// zeros below: the least key carrying them).
+__device__ uint64_t select_below(const float* __restrict__ logits, uint32_t V, uint64_t ub, uint32_t m, uint32_t* hist) {
     __shared__ uint64_t s_pref;
-    __shared__ uint32_t s_rem, s_full, s_n, s_pick;
+    __shared__ uint32_t s_rem, s_full;
     const uint32_t tid = threadIdx.x;
     uint64_t prefix = 0, mask = 0;
-    uint32_t remaining = k;  // how many of the keys matching `prefix` are still to be taken
+    uint32_t remaining = m;  // how many of the keys matching `prefix` are still to be taken
     for (int pass = 0; pass < 8; ++pass) {
         const int shift = 56 - 8 * pass;
         if (tid < 256) hist[tid] = 0;
         __syncthreads();
         for_each_logit(logits, V, tid, [&](float l, uint32_t i) {
             const uint64_t e = rank_key(value_key(l), i);
-            if ((e & mask) == prefix) atomicAdd(&hist[(uint32_t)(e >> shift) & 255u], 1u);
+            if (e < ub && (e & mask) == prefix) atomicAdd(&hist[(uint32_t)(e >> shift) & 255u], 1u);
         });
         __syncthreads();
         if (tid == 0) {
@@ -1381,43 +1378,102 @@ __device__ uint32_t topk_sample_large(const float* __restrict__ logits, uint32_t
         prefix = s_pref;
         remaining = s_rem;
         mask |= (uint64_t)255u << shift;
-        if (s_full) break;  // tau: the chosen digits with zeros below (the least key with them)
+        const bool full = s_full != 0u;
         __syncthreads();
+        if (full) break;
     }
-    const uint64_t tau = prefix;
+    return prefix;
+}
+
+// Gathers the m keys in [lo, ub) into cand and sorts them: rank r of the range in cand[r] (sorted:
+// kSampBlock keys of LDS for the exchange).
+__device__ void gather_sorted(const float* __restrict__ logits, uint32_t V, uint64_t lo, uint64_t ub, uint32_t m,
+                              uint64_t* cand, uint64_t* sorted) {
+    __shared__ uint32_t s_n;
+    const uint32_t tid = threadIdx.x;
     if (tid == 0) s_n = 0;
     __syncthreads();
     for_each_logit(logits, V, tid, [&](float l, uint32_t i) {
         const uint64_t e = rank_key(value_key(l), i);
-        if (e >= tau) {
+        if (e >= lo && e < ub) {
             const uint32_t slot = atomicAdd(&s_n, 1u);
             if (slot < (uint32_t)kSampBlock) cand[slot] = e;
         }
     });
     __syncthreads();
-    uint64_t x = tid < k ? cand[tid] : 0ull;
+    uint64_t x = tid < m ? cand[tid] : 0ull;  // key 0 (a NaN at index 2^32 - 1) ranks below every key
     x = bitonic_desc<kSampBlock>(x, tid, sorted);
-    if (tid < k) cand[tid] = x;  // rank r in cand[r]
+    if (tid < m) cand[tid] = x;
     __syncthreads();
-    if (tid == 0) {
-        // exp((l_i - max) / T), summed and then walked in rank order, as Utils.cpp:153-170
-        const float mx = key_value((uint32_t)(cand[0] >> 32));
-        float sum = 0.f;
-        for (uint32_t i = 0; i < k; ++i) sum += expf((key_value((uint32_t)(cand[i] >> 32)) - mx) / temperature);
-        const float r = sample_uniform(k0, k1, step);
-        float cum = 0.f;
-        uint32_t pick = 0;
-        for (uint32_t i = 0; i < k; ++i) {
-            cum += expf((key_value((uint32_t)(cand[i] >> 32)) - mx) / temperature) / sum;
-            if (r < cum) {
-                pick = i;
-                break;
+}
+
+// Seeded top-k for kWaveTopK < k <= kMaxTopK (Utils.cpp:151-171).  The k largest rank keys are taken in
+// chunks of up to kSampBlock from the largest down: the chunk below ub (the previous chunk's last key;
+// above every key at first) ends at the m-th largest key below ub (select_below), and its m keys are
+// gathered and sorted by the block.  Rank keys are unique, so the chunks partition the top k exactly.
+// The weights exp((l - max) / T) of a chunk are computed one per thread and added by one thread in rank
+// order across the chunks (Utils.cpp:153-157); the walk then adds the weights w / sum in rank order
+// chunk by chunk (:158-168), the chunks gathered again from their stored boundaries when there are
+// several.  The arithmetic is that of the one-wave path, so both paths draw the same token from the
+// same candidates.  cand and sorted hold kSampBlock keys of the caller's LDS.
+__device__ uint32_t topk_sample_large(const float* __restrict__ logits, uint32_t V, uint32_t k, float temperature,
+                                      uint32_t k0, uint32_t k1, uint64_t step, uint64_t* cand, uint64_t* sorted) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint64_t s_lo[kTopKChunks];
+    __shared__ float s_w[kSampBlock];
+    __shared__ float s_sum;
+    __shared__ uint32_t s_pick, s_found;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t nch = (k + kSampBlock - 1) / kSampBlock;
+    auto chunk_len = [&](uint32_t c) { return k - c * kSampBlock < (uint32_t)kSampBlock ? k - c * kSampBlock : (uint32_t)kSampBlock; };
+    float mx = 0.f, sum = 0.f;  // sum: thread 0's running total
+    uint64_t top = 0, ub = ~0ull;
+    for (uint32_t c = 0; c < nch; ++c) {
+        const uint32_t m = chunk_len(c);
+        const uint64_t lo = select_below(logits, V, ub, m, hist);
+        if (tid == 0) s_lo[c] = lo;
+        gather_sorted(logits, V, lo, ub, m, cand, sorted);
+        if (c == 0) {
+            top = cand[0];
+            mx = key_value((uint32_t)(top >> 32));
+        }
+        if (tid < m) s_w[tid] = expf((key_value((uint32_t)(cand[tid] >> 32)) - mx) / temperature);
+        __syncthreads();
+        if (tid == 0)
+            for (uint32_t i = 0; i < m; ++i) sum += s_w[i];
+        __syncthreads();
+        ub = lo;
+    }
+    if (tid == 0) s_sum = sum;
+    __syncthreads();
+    sum = s_sum;
+    const float r = sample_uniform(k0, k1, step);
+    float cum = 0.f;  // thread 0's cumulative weight
+    ub = ~0ull;
+    for (uint32_t c = 0; c < nch; ++c) {
+        const uint32_t m = chunk_len(c);
+        if (nch > 1) gather_sorted(logits, V, s_lo[c], ub, m, cand, sorted);  // one chunk: still in cand
+        if (tid < m) s_w[tid] = expf((key_value((uint32_t)(cand[tid] >> 32)) - mx) / temperature) / sum;
+        __syncthreads();
+        if (tid == 0) {
+            s_found = 0u;
+            for (uint32_t i = 0; i < m; ++i) {
+                cum += s_w[i];
+                if (r < cum) {
+                    s_pick = ~(uint32_t)cand[i];
+                    s_found = 1u;
+                    break;
+                }
             }
         }
-        s_pick = ~(uint32_t)cand[pick];
+        __syncthreads();
+        const bool found = s_found != 0u;
+        const uint32_t pick = s_pick;
+        __syncthreads();
+        if (found) return pick;
+        ub = s_lo[c];
     }
-    __syncthreads();
-    return s_pick;
+    return ~(uint32_t)top;  // no cumulative weight passed r: the first element (Utils.cpp:169-170)
 }
 
 // Returns the sampled token (valid in every thread through LDS).  Every mode streams the logits
@@ -1491,7 +1547,7 @@ __device__ __forceinline__ uint32_t block_sample(const float* __restrict__ logit
     // k of them for ordinary logits -- hold the k and are sorted.  More than kSampBlock such
     // elements (many equal logits) take k rounds of "largest key below the last" instead.
     uint32_t k = top_k > V ? V : top_k;
-    if (k > (uint32_t)kMaxTopK) k = kMaxTopK;
+    if (k > (uint32_t)kMaxTopK) k = kMaxTopK;  // refused by the launchers
     if (k > (uint32_t)kWaveTopK) return topk_sample_large(logits, V, k, temperature, k0, k1, step, s_cand, s_sort);
     float bf = -INFINITY;  // per-thread maximum, first index among equals; NaNs skipped
     uint32_t bi = 0xFFFFFFFFu;
@@ -2514,13 +2570,15 @@ extern "C" int vsl_norm_swiglu(const float* x, const float* gamma, float eps, co
 
 extern "C" uint32_t vsl_lm_head_ws_blocks(void) { return kMaxLmBlocks; }
 
-// Sampler arguments the kernels serve: a known mode, and for seeded top-k 1 <= top_k <= 64 (top_k > V
-// means all of V).
+// Sampler arguments the kernels serve: a known mode, and for seeded top-k 1 <= min(top_k, V) <=
+// kMaxTopK (top_k > V means all of V).
 static int check_sampler(const vsl_sampler& sp, uint32_t V, const char* who) {
     if (sp.mode < VSL_SAMPLE_GREEDY || sp.mode > VSL_SAMPLE_TOPK_SEEDED) return vsl_invalid("%s: sampler mode %d", who, sp.mode);
     if (sp.temperature <= 0.f || sp.mode == VSL_SAMPLE_GREEDY) return VSL_OK;  // greedy: no limits
-    if (sp.mode == VSL_SAMPLE_TOPK_SEEDED && (sp.top_k == 0 || sp.top_k > (uint32_t)kMaxTopK))
-        return vsl_unsupported("%s: seeded top-k supports 1 <= top_k <= %d (got %u)", who, kMaxTopK, sp.top_k);
+    const uint32_t k = sp.top_k < V ? sp.top_k : V;
+    if (sp.mode == VSL_SAMPLE_TOPK_SEEDED && (sp.top_k == 0 || k > (uint32_t)kMaxTopK))
+        return vsl_unsupported("%s: seeded top-k supports 1 <= min(top_k, V) <= %d (got top_k %u, V %u)", who,
+                               kMaxTopK, sp.top_k, V);
     return VSL_OK;
 }
 

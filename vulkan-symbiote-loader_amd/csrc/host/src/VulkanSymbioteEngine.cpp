@@ -11,6 +11,7 @@
 // sequence every token, :710,718-726), and each decode step replayed from a captured hipGraph.
 #include "VulkanSymbioteEngine.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -757,7 +758,7 @@ int VulkanSymbioteEngine::begin_generation(const std::vector<uint32_t>& prompt, 
     // the samplers' limits are checked before anything is enqueued (vsl_lm_head_sample would refuse
     // the same request inside the prompt pass)
     if (params.temperature > 0.0f && params.mode == VSL_SAMPLE_TOPK_SEEDED &&
-        (params.top_k == 0 || params.top_k > VSL_MAX_TOP_K))
+        (params.top_k == 0 || std::min<uint32_t>(params.top_k, config_.vocab_size) > VSL_MAX_TOP_K))
         return VSL_E_UNSUPPORTED;
     std::memcpy(host_tokens_, prompt.data(), (size_t)n * 4);
     check(vsl_copy_h2d(prompt_dev_, host_tokens_, (size_t)n * 4, stream_), "prompt upload");

@@ -129,7 +129,7 @@ extern "C" int vsl_engine_generate_ids(vsl_engine* e, const uint32_t* prompt, ui
         if (rc < 0) {
             const char* why = rc == kErrCapacity ? "prompt + max_new exceeds the KV capacity"
                               : rc == kErrInvalid ? "empty prompt or bad sampling mode"
-                              : rc == VSL_E_UNSUPPORTED ? "seeded top-k needs 1 <= top_k <= 64"
+                              : rc == VSL_E_UNSUPPORTED ? "seeded top-k needs 1 <= min(top_k, vocab) <= VSL_MAX_TOP_K"
                                                         : "generation failed";
             return fail(rc, std::string("vsl_engine_generate_ids: ") + why);
         }
