@@ -87,6 +87,48 @@ def test_rmsnorm_f16f8_needs_whole_blocks(vsl, dev, H):
     assert H.vsl_rmsnorm(dev.p(x), None, 2, 1000, 1e-5, dev.p(out), vsl.VSL_DT_F16F8, None) == vsl.VSL_E_INVALID
 
 
+@pytest.mark.parametrize("M,N,K,epi,amode", [
+    (128, 8192, 640, 3, "x2"),      # SwiGLU, hi/lo fp16 A: 2 x 128 tiles of 64 x (64 + 64), 10 stages of 64
+    (128, 16384, 896, 0, "x2"),     # fp32 store, hi/lo fp16 A, 14 stages
+    (128, 16384, 384, 0, "f8"),     # fp32 store, F16F8 A, 6 stages
+    (128, 8192, 640, 3, "f8"),      # SwiGLU, F16F8 A
+    (100, 8192, 1152, 3, "one"),    # one fp16 plane (32-column stages), ragged M
+])
+def test_gemm_small_tiles_odd_k_stages(vsl, dev, H, M, N, K, epi, amode):
+    """The 64 x 128 direct-to-LDS tiles run the split-A and fp8-lo forms with four 64-column stage
+    buffers; K an odd multiple of 128 leaves a last pair of stages after the four-stage rounds, which
+    must be multiplied once each (rows 0, M-1 and a sample against the fp64 product of what the form
+    carries)."""
+    rng = np.random.default_rng(M + N + K + epi)
+    nb = 2 * N if epi == 3 else N
+    A = rng.normal(0, 1, (M, K)).astype(np.float32)
+    B = rng.normal(0, 0.02, (nb, K)).astype(np.float16)
+    rows = np.unique(np.concatenate([[0, M - 1, M // 2], rng.integers(0, M, 24)]))
+    if amode == "f8":
+        dA, hi, val = f8_buffer(dev, A)
+        prod = T.f8lo_product(hi[rows], val[rows] - hi[rows].astype(np.float64), B)
+        flags = vsl.GEMM_A_F8
+    elif amode == "x2":
+        hi = A.astype(np.float16)
+        lo = (A - hi.astype(np.float32)).astype(np.float16)
+        dA = dev.put(np.concatenate([hi, lo]))
+        prod = (hi[rows].astype(np.float64) + lo[rows].astype(np.float64)) @ B.astype(np.float64).T
+        flags = vsl.GEMM_A_X2
+    else:
+        a16 = A.astype(np.float16)
+        dA = dev.put(a16)
+        prod = a16[rows].astype(np.float64) @ B.astype(np.float64).T
+        flags = 0
+    C = dev.empty((M, N), np.float16 if epi == 3 else np.float32)
+    ok(vsl, H.vsl_gemm_f16(dev.p(dA), dev.p(dev.put(B)), M, N, K, dev.p(C), epi | flags, None))
+    out = dev.get(C).astype(np.float64)[rows]
+    if epi == 3:
+        ref = prod[:, :N] / (1.0 + np.exp(-prod[:, :N])) * prod[:, N:]
+        assert rel_err(out, ref) < 2.0 ** -10
+    else:
+        assert rel_err(out, prod) < 1e-5
+
+
 @pytest.mark.parametrize("M,N,K,epi,cmode", [
     (512, 14336, 2048, 3, "f8"),    # SwiGLU, 256 x 256 tiles, F16F8 output
     (512, 14336, 2048, 3, "x2"),    # F16F8 in, hi/lo fp16 out

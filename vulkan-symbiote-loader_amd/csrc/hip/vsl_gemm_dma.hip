@@ -36,7 +36,7 @@
 
 namespace {
 
-constexpr uint32_t kKAlign = 128;  // K granularity: NBUF * BK for every configuration
+constexpr uint32_t kKAlign = 128;  // K granularity: whole pairs of stages for every configuration
 
 constexpr int kA1 = kGemmA1, kAX2 = kGemmAX2, kAF8 = kGemmAF8;
 constexpr int kC1 = kGemmC1, kCX2 = kGemmCX2, kCF8 = kGemmCF8;
@@ -293,9 +293,10 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
     // then issues its MFMAs (the reads land meanwhile). Before the last k-step's MFMAs: wait for this
     // wave's reads (Lc is fully read) and for its loads of stage s+1, meet at the barrier (every
     // wave has read Lc, every load of stage s+1 is in LDS), request stage s+NBUF into Lc, and
-    // request stage s+1's first k-step from Ln. The stage count is a multiple of NBUF
-    // (K % (NBUF * BK) == 0), so no step is ever skipped. PAR is the stage's parity: with BK = 32 an
-    // fp8 lo block spans an even stage and the odd stage after it.
+    // request stage s+1's first k-step from Ln. The stage count is even (K % 128 == 0 and BK <= 64)
+    // and a multiple of NBUF except with four 64-column buffers, whose last round may be a pair of
+    // stages; no stage is skipped or repeated. PAR is the stage's parity: with BK = 32 an fp8 lo block
+    // spans an even stage and the odd stage after it.
     Frags f0, f1;
     auto step = [&](vsl_half* Lc, const vsl_half* Ln, uint32_t s, auto par) {
         constexpr int PAR = decltype(par)::value;
@@ -377,11 +378,19 @@ __global__ __launch_bounds__(G::NT) void k_gemm_dma(const vsl_half* __restrict__
     } else {
         fload(f0, L0, 0);
         if constexpr (NBUF == 4) {
-            for (uint32_t s = 0; s < nst; s += 4) {
+            uint32_t s = 0;
+            for (; s + 4 <= nst; s += 4) {
                 step(L0, L1, s, P0{});
                 step(L1, L2, s + 1, P1{});
                 step(L2, L3, s + 2, P0{});
                 step(L3, L0, s + 3, P1{});
+            }
+            // 64-column stages in four buffers take K in multiples of 128, so a round may end with
+            // one pair of stages (the requests past the last stage re-load it into buffers that are
+            // not multiplied again)
+            if (s < nst) {
+                step(L0, L1, s, P0{});
+                step(L1, L2, s + 1, P1{});
             }
         } else {
             for (uint32_t s = 0; s < nst; s += 2) {
