@@ -323,6 +323,26 @@ def test_long_context_oracle_small_model(vsl, orc):
     m.close()
 
 
+# Model dimensions that are odd multiples of 128 (d 640, [Wq; Wk; Wv] 1920 rows), with an FFN wide enough
+# that a prompt chunk of 128 rows or more takes the 64 x 128 direct-to-LDS tiles for gate/up at K = 640
+# (ten 64-column stages: four-stage rounds and a closing pair); the narrow projections run on the
+# register-staged tiles.
+ODD128 = dict(hidden_size=640, num_layers=2, num_heads=5, num_kv_heads=5, intermediate_size=6144,
+              vocab_size=32000, max_position_embeddings=4096, rope_theta=10000.0, rms_eps=1e-5, dtype=1)
+
+
+@pytest.mark.parametrize("chunk", [128, 0])
+def test_odd_multiple_of_128_dimensions(vsl, orc, chunk):
+    """d = 640 (head_dim 128, five heads, no GQA) against the oracle: a 300-token prompt through the
+    MFMA prompt pass in 128-row chunks (128, 128, 44 rows) or one 300-row chunk, then 24 teacher-forced
+    greedy steps: logits within max-abs 2e-2 at every step, picks identical."""
+    cfg = ODD128
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=512, batched_prefill=True, prefill_chunk=chunk) as e:
+        m = _oracle_from_engine(orc, e, cfg)
+        _forced_parity(e, m, orc.random_ids(300, cfg["vocab_size"], 3), 24, 2e-2)
+    m.close()
+
+
 def _plant_outliers(vsl, path, names, values, per_tensor, seed):
     """Overwrite `per_tensor` random fp16 weights of each named tensor of a GGUF file in place with
     `values` (cycled); the file's other bytes are unchanged."""
