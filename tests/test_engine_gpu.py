@@ -331,11 +331,12 @@ ODD128 = dict(hidden_size=640, num_layers=2, num_heads=5, num_kv_heads=5, interm
               vocab_size=32000, max_position_embeddings=4096, rope_theta=10000.0, rms_eps=1e-5, dtype=1)
 
 
-@pytest.mark.parametrize("chunk", [128, 0])
+@pytest.mark.parametrize("chunk", [128, 299, 0])
 def test_odd_multiple_of_128_dimensions(vsl, orc, chunk):
     """d = 640 (head_dim 128, five heads, no GQA) against the oracle: a 300-token prompt through the
-    MFMA prompt pass in 128-row chunks (128, 128, 44 rows) or one 300-row chunk, then 24 teacher-forced
-    greedy steps: logits within max-abs 2e-2 at every step, picks identical."""
+    MFMA prompt pass in 128-row chunks (128, 128, 44 rows), in chunks of 299 and 1 rows, or in one
+    300-row chunk, then 24 teacher-forced greedy steps: logits within max-abs 2e-2 at every step, picks
+    identical."""
     cfg = ODD128
     with vsl.Engine(spec=cfg, seed=0, kv_capacity=512, batched_prefill=True, prefill_chunk=chunk) as e:
         m = _oracle_from_engine(orc, e, cfg)

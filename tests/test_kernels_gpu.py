@@ -744,7 +744,8 @@ def test_gemm_small_rows(vsl, orc, dev, H, M, N, K, epi, ax2):
 
 
 @pytest.mark.parametrize("hd,nq,nkv,S,pos0", [(128, 32, 8, 77, 0), (128, 32, 8, 64, 100), (64, 32, 8, 200, 0),
-                                              (64, 8, 8, 33, 5)])
+                                              (64, 8, 8, 33, 5), (128, 32, 8, 1, 0), (128, 16, 8, 1, 300),
+                                              (64, 16, 2, 5, 40)])
 def test_rope_split_and_attn_prefill(vsl, orc, dev, H, hd, nq, nkv, S, pos0):
     rng = np.random.default_rng(hd + S + pos0)
     cap, theta = 512, 10000.0
