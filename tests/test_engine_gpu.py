@@ -344,6 +344,24 @@ def test_odd_multiple_of_128_dimensions(vsl, orc, chunk):
     m.close()
 
 
+# Three query heads per KV head (the Llama-3.2-3B grouping, 24 / 8 heads), at head_dim 128.
+GQA3 = dict(hidden_size=768, num_layers=2, num_heads=6, num_kv_heads=2, intermediate_size=2048,
+            vocab_size=32000, max_position_embeddings=4096, rope_theta=500000.0, rms_eps=1e-5, dtype=1)
+
+
+@pytest.mark.parametrize("batched,cap", [(True, 1024), (False, 1024), (True, 9216)])
+def test_gqa_group_of_three(vsl, orc, batched, cap):
+    """GQA with three query heads per KV head against the oracle: a 200-token prompt through the MFMA
+    prompt pass (one head per attention block) or the per-token pass, then 24 teacher-forced greedy
+    steps on the vector decode attention (capacity 1024) or the matrix-core one (capacity 9216):
+    logits within max-abs 2e-2 at every step, picks identical."""
+    cfg = GQA3
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=cap, batched_prefill=batched) as e:
+        m = _oracle_from_engine(orc, e, cfg)
+        _forced_parity(e, m, orc.random_ids(200, cfg["vocab_size"], 5), 24, 2e-2)
+    m.close()
+
+
 def _plant_outliers(vsl, path, names, values, per_tensor, seed):
     """Overwrite `per_tensor` random fp16 weights of each named tensor of a GGUF file in place with
     `values` (cycled); the file's other bytes are unchanged."""

@@ -216,10 +216,13 @@ def test_qkv_capacity_guard(vsl, dev, H):
 
 
 _LAYOUTS = [(1, 128, 32, 8), (1, 64, 32, 8), (0, 64, 4, 4), (1, 128, 8, 8)]
+# GQA groups that are not powers of two: 3 (24/8 heads, the Llama-3.2-3B layout), 5, 6 and 7
+_ODD_GQA = [(1, 128, 24, 8), (0, 64, 15, 3), (1, 64, 12, 2), (1, 128, 14, 2)]
 _LENGTHS = [1, 5, 300, 1025]
 # every head layout at the engine's 32 splits; the split sweep on two layouts
-_ATTN_CASES = ([(lay, n, 32) for lay in _LAYOUTS for n in _LENGTHS] +
-               [(lay, n, s) for lay in ((1, 128, 32, 8), (0, 64, 4, 4)) for n in _LENGTHS for s in (1, 7, 48, 100)])
+_ATTN_CASES = ([(lay, n, 32) for lay in _LAYOUTS + _ODD_GQA for n in _LENGTHS] +
+               [(lay, n, s) for lay in ((1, 128, 32, 8), (0, 64, 4, 4)) for n in _LENGTHS for s in (1, 7, 48, 100)] +
+               [(lay, n, 7) for lay in _ODD_GQA for n in (5, 1025)])
 
 
 def _nan_past(cache, length):
@@ -258,14 +261,15 @@ _LONG_LENGTHS = [1, 5, 17, 300, 1025, 9000, 16384]
 # GQA groups of 4, 1, 2 and 8 heads at 32 splits; the split sweep on the 8B layout (one block over
 # the whole 16384-position cache is left to the 9000-position case)
 _LONG_CASES = ([(nq, n, 32) for nq in (32, 8, 16, 64) for n in _LONG_LENGTHS] +
-               [(32, n, s) for s in (1, 7, 100) for n in _LONG_LENGTHS if not (n == 16384 and s == 1)])
+               [(32, n, s) for s in (1, 7, 100) for n in _LONG_LENGTHS if not (n == 16384 and s == 1)] +
+               [(nq, n, 32) for nq in (24, 40, 48, 56) for n in (5, 9000, 16384)])
 
 
 @pytest.mark.parametrize("nq,length,nsplit", _LONG_CASES)
 def test_attn_decode_long_cache(vsl, orc, dev, H, nq, length, nsplit):
     """fp16 caches of head_dim 128 above 8192 positions of capacity run the matrix-core kernel (scores
     from hi + lo fp16 planes of q on MFMA, 16-position tiles per wave): against the oracle for GQA
-    groups of 4, 1, 2 and 8 heads, lengths from one position to the full cache, the split counts of
+    groups of 4, 1, 2, 8, 3, 5, 6 and 7 heads, lengths from one position to the full cache, the split counts of
     the short-cache test; cache rows past the length are NaN (the kernel requests its first two tiles
     before it knows the length)."""
     nkv, hd, cap = 8, 128, 16384
@@ -286,7 +290,7 @@ def test_attn_decode_long_cache(vsl, orc, dev, H, nq, length, nsplit):
     assert rel_err(got, ref) < 2e-5
 
 
-@pytest.mark.parametrize("kvdt,hd,nq,nkv", [(1, 128, 32, 8), (0, 64, 4, 4)])
+@pytest.mark.parametrize("kvdt,hd,nq,nkv", [(1, 128, 32, 8), (0, 64, 4, 4), (1, 128, 24, 8)])
 @pytest.mark.parametrize("length,window,n_glob,thr", [
     (300, 64, 4, 100),    # windowed: globals 0..3 and keys 235..299
     (300, 64, 4, 300),    # threshold not passed: dense
@@ -331,6 +335,8 @@ def test_attn_decode_window(vsl, orc, dev, H, kvdt, hd, nq, nkv, length, window,
     (64, 8, 8, 96, 0, 512, 16, 8192, False),      # threshold not reached: dense
     (128, 32, 8, 192, 1000, 512, 16, 900, True),  # every row windowed, tiles wholly inside every window
     (64, 8, 8, 160, 700, 256, 128, 600, False),   # two whole global tiles, then the windows
+    (128, 24, 8, 200, 0, 100, 70, 60, True),      # GQA 3 (one head per block), split q / out
+    (64, 12, 2, 160, 300, 32, 0, 0, False),       # GQA 6 (two heads per block), every row windowed
 ])
 def test_attn_prefill_window(vsl, orc, dev, H, hd, nq, nkv, S, pos0, window, n_glob, thr, x2):
     rng = np.random.default_rng(hd + S + pos0 + window)
@@ -745,7 +751,8 @@ def test_gemm_small_rows(vsl, orc, dev, H, M, N, K, epi, ax2):
 
 @pytest.mark.parametrize("hd,nq,nkv,S,pos0", [(128, 32, 8, 77, 0), (128, 32, 8, 64, 100), (64, 32, 8, 200, 0),
                                               (64, 8, 8, 33, 5), (128, 32, 8, 1, 0), (128, 16, 8, 1, 300),
-                                              (64, 16, 2, 5, 40)])
+                                              (64, 16, 2, 5, 40), (128, 24, 8, 77, 3), (64, 15, 3, 40, 0),
+                                              (128, 12, 2, 100, 9), (64, 14, 2, 33, 0)])
 def test_rope_split_and_attn_prefill(vsl, orc, dev, H, hd, nq, nkv, S, pos0):
     rng = np.random.default_rng(hd + S + pos0)
     cap, theta = 512, 10000.0

@@ -1205,8 +1205,12 @@ int launch_attn_g(uint32_t G, dim3 grid, hipStream_t s, const float* q, const vo
         case 1: launch_attn_w<KT, HD, 1>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
         case 2: launch_attn_w<KT, HD, 2>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
         case 4: launch_attn_w<KT, HD, 4>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+        case 3: launch_attn_w<KT, HD, 3>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+        case 5: launch_attn_w<KT, HD, 5>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+        case 6: launch_attn_w<KT, HD, 6>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
+        case 7: launch_attn_w<KT, HD, 7>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
         case 8: launch_attn_w<KT, HD, 8>(grid, s, q, kc, vc, n_q, n_kv, cap, scale, nsplit, po, pml, ctrl, w); break;
-        default: return vsl_unsupported("vsl_attn_decode: GQA ratio %u (supported 1,2,4,8)", G);
+        default: return vsl_unsupported("vsl_attn_decode: GQA ratio %u (supported 1..8)", G);
     }
     HIP_TRY(hipGetLastError());
     if (nsplit <= 32)

@@ -1138,20 +1138,29 @@ static void launch_attn_prefill_w(dim3 grid, hipStream_t s, const vsl_half* q, c
     constexpr uint64_t kCUs = 256;  // MI355X compute units
     const bool half = GB2 < G && (uint64_t)grid.x * grid.y < kCUs;
     auto go = [&](auto qc, auto oc) {
-        if constexpr (GB2 < G) {
-            if (half) {
-                // two heads per block, four waves per head over 128-key tiles (two buffers of 64 KB):
-                // eight waves, two per SIMD, and half the tiles in the longest query block's chain
-                constexpr int KS = 4;
-                const dim3 g2(grid.x, grid.y * (G / GB2));
-                k_attn_prefill<HD, G, GB2, decltype(qc)::value, decltype(oc)::value, WIN, KS, 128, 2>
-                    <<<g2, 64 * GB2 * KS, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
-                return;
+        if constexpr ((G & (G - 1)) != 0) {
+            // groups of 3, 5, 6 or 7 heads: blocks of one head (two for 6), two waves per head, each
+            // block copying its KV head's tiles (the thread count of a block must divide a tile's copy)
+            constexpr int GBO = G % 2 == 0 ? 2 : 1;
+            const dim3 g2(grid.x, grid.y * (G / GBO));
+            k_attn_prefill<HD, G, GBO, decltype(qc)::value, decltype(oc)::value, WIN, 2><<<g2, 64 * GBO * 2, 0, s>>>(
+                q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+        } else {
+            if constexpr (GB2 < G) {
+                if (half) {
+                    // two heads per block, four waves per head over 128-key tiles (two buffers of 64
+                    // KB): eight waves, two per SIMD, and half the tiles in the longest query block's chain
+                    constexpr int KS = 4;
+                    const dim3 g2(grid.x, grid.y * (G / GB2));
+                    k_attn_prefill<HD, G, GB2, decltype(qc)::value, decltype(oc)::value, WIN, KS, 128, 2>
+                        <<<g2, 64 * GB2 * KS, 0, s>>>(q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
+                    return;
+                }
             }
+            constexpr int KS = G <= 4 ? 2 : 1;
+            k_attn_prefill<HD, G, G, decltype(qc)::value, decltype(oc)::value, WIN, KS><<<grid, 64 * G * KS, 0, s>>>(
+                q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
         }
-        constexpr int KS = G <= 4 ? 2 : 1;
-        k_attn_prefill<HD, G, G, decltype(qc)::value, decltype(oc)::value, WIN, KS><<<grid, 64 * G * KS, 0, s>>>(
-            q, k, v, S, pos0, n_q, n_kv, cap, scale, o, w.win, w.n_glob, w.thr);
     };
     using T = std::true_type;
     using F = std::false_type;
@@ -1185,8 +1194,12 @@ static int launch_attn_prefill(dim3 grid, hipStream_t s, const vsl_half* q, cons
         case 1: launch_attn_prefill_g<HD, 1>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
         case 2: launch_attn_prefill_g<HD, 2>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
         case 4: launch_attn_prefill_g<HD, 4>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
+        case 3: launch_attn_prefill_g<HD, 3>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
+        case 5: launch_attn_prefill_g<HD, 5>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
+        case 6: launch_attn_prefill_g<HD, 6>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
+        case 7: launch_attn_prefill_g<HD, 7>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
         case 8: launch_attn_prefill_g<HD, 8>(grid, s, q, k, v, S, pos0, n_q, n_kv, cap, scale, o, qx2, om, w); break;
-        default: return vsl_unsupported("vsl_attn_prefill: GQA ratio %u (supported 1, 2, 4, 8)", n_q / n_kv);
+        default: return vsl_unsupported("vsl_attn_prefill: GQA ratio %u (supported 1..8)", n_q / n_kv);
     }
     return VSL_OK;
 }

@@ -275,7 +275,7 @@ void VulkanSymbioteEngine::init_device(const ModelConfig& cfg, bool fp16_weights
     const uint32_t hd = config_.head_dim;
     if (hd != 64 && hd != 128) throw std::runtime_error("head_dim must be 64 or 128");
     const uint32_t G = cfg.num_attention_heads / cfg.num_key_value_heads;
-    if (G != 1 && G != 2 && G != 4 && G != 8) throw std::runtime_error("GQA ratio must be 1, 2, 4 or 8");
+    if (G < 1 || G > 8) throw std::runtime_error("GQA ratio must be 1..8");
     if (cfg.hidden_size % 8 || cfg.intermediate_size % 8) throw std::runtime_error("hidden/ffn sizes must be multiples of 8");
     cap_ = options_.kv_capacity ? options_.kv_capacity : std::min<uint32_t>(cfg.max_position_embeddings ? cfg.max_position_embeddings : 4096, 4096);
     if (cap_ == 0) throw std::runtime_error("KV capacity must be positive");
