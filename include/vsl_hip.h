@@ -185,14 +185,15 @@ int vsl_rmsnorm(const float* x, const float* gamma, uint32_t rows, uint32_t d, f
                 int out_dtype, void* stream);
 
 /* GEMV / skinny GEMM (the GEMV sweep): Y[N][B] = W[N][K] * X[K][B] (X, Y row-major), fp32
- * accumulation.  W f16/f32; X, Y f16 or f32; 1 <= B <= 16; K % 8 == 0.  f16 W with f16 X and
+ * accumulation.  W f16/f32; X, Y f16 or f32; 1 <= B <= 16; K % 8 == 0 and K <= 32768 (the limit of
+ * every decode GEMV: the activation vector is staged in LDS as fp32).  f16 W with f16 X and
  * K % 512 == 0 runs on MFMA (any B, including 1); B = 1 otherwise needs fp32 X. */
 int vsl_gemv(const void* W, int wdtype, uint32_t N, uint32_t K, const void* X, int xdtype, uint32_t B,
              void* Y, int ydtype, void* stream);
 
 /* The same product for a batch of B activation vectors, each contiguous: X fp16 [B][K], Y [B][N]
  * (f16 or f32), W fp16 [N][K]; 1 <= B <= 16, K % 512 == 0.  One pass over W: B = 1 runs the decode
- * GEMV when X is 8-byte aligned and K <= 16384; whole rows streamed
+ * GEMV when X is 8-byte aligned and K <= 32768; whole rows streamed
  * with fp16 dot products into fp32 for 2 <= B <= 8 when X (B * K * 2 bytes) is at most 128 KB, K %
  * 1024 == 0 and X is 16-byte aligned; MFMA otherwise (W and X staged through LDS in whole-line runs
  * when K % 1024 == 0 and X is 16-byte aligned, register fragments else).  No reference
@@ -243,7 +244,8 @@ int vsl_attn_decode_window(const float* q, const void* kcache, const void* vcach
                            float* part_ml, float* out, vsl_ctrl* ctrl, uint32_t window, uint32_t n_global,
                            uint32_t threshold, void* stream);
 
-/* y[N] += W[N][K] x[K]  (O projection / FFN down projection with the residual add fused) */
+/* y[N] += W[N][K] x[K]  (O projection / FFN down projection with the residual add fused);
+ * K % 8 == 0, K <= 32768 */
 int vsl_gemv_residual(const void* W, int wdtype, uint32_t N, uint32_t K, const float* x, float* resid,
                       vsl_ctrl* ctrl, void* stream);
 

@@ -362,6 +362,22 @@ def test_gqa_group_of_three(vsl, orc, batched, cap):
     m.close()
 
 
+# An FFN wider than 16384 (the 70B-class 28672 needs the same path): the decode down projection stages
+# its 20480-wide input with one 16-wave block per CU.
+WIDE_FFN = dict(hidden_size=512, num_layers=2, num_heads=4, num_kv_heads=1, intermediate_size=20480,
+                vocab_size=4096, max_position_embeddings=4096, rope_theta=10000.0, rms_eps=1e-5, dtype=1)
+
+
+def test_ffn_wider_than_16384(vsl, orc):
+    """FFN 20480 against the oracle: a 256-token prompt through the MFMA prompt pass, then 24 teacher-
+    forced greedy steps: logits within max-abs 2e-2 at every step, picks identical."""
+    cfg = WIDE_FFN
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=512, batched_prefill=True) as e:
+        m = _oracle_from_engine(orc, e, cfg)
+        _forced_parity(e, m, orc.random_ids(256, cfg["vocab_size"], 9), 24, 2e-2)
+    m.close()
+
+
 def _plant_outliers(vsl, path, names, values, per_tensor, seed):
     """Overwrite `per_tensor` random fp16 weights of each named tensor of a GGUF file in place with
     `values` (cycled); the file's other bytes are unchanged."""

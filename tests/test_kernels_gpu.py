@@ -385,6 +385,45 @@ def test_gemv_residual_and_swiglu(vsl, orc, dev, H):
     assert rel_err(dev.get(dh), orc.swiglu(gu[:F], gu[F:])) < 1e-4
 
 
+@pytest.mark.parametrize("N,K", [(4100, 28672), (1000, 20480), (333, 32768)])
+def test_gemv_wide_k(vsl, orc, dev, H, N, K):
+    """Decode GEMVs wider than 16384 columns (70B-class down projections: K = 28672) stage the fp32
+    activation in up to 128 KB of LDS with one 16-wave block per CU: the residual GEMV, the fp32-X and
+    the fp16-X GEMV against the oracle, and K past 32768 refused."""
+    rng = np.random.default_rng(N + K)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    h = rng.normal(0, 1, K).astype(np.float32)
+    r = rng.normal(0, 1, N).astype(np.float32)
+    dW, dr = dev.put(W), dev.put(r)
+    ref = orc.gemm_nt(W, h)[:, 0]
+    ok(vsl, H.vsl_gemv_residual(dev.p(dW), 1, N, K, dev.p(dev.put(h)), dev.p(dr), None, None))
+    assert rel_err(dev.get(dr), r + ref) < 1e-5
+    dy = dev.empty((N,), np.float32)
+    ok(vsl, H.vsl_gemv(dev.p(dW), vsl.VSL_DT_F16, N, K, dev.p(dev.put(h)), vsl.VSL_DT_F32, 1, dev.p(dy),
+                       vsl.VSL_DT_F32, None))
+    assert rel_err(dev.get(dy), ref) < 1e-5
+    h16 = h.astype(np.float16)
+    ok(vsl, H.vsl_gemv(dev.p(dW), vsl.VSL_DT_F16, N, K, dev.p(dev.put(h16)), vsl.VSL_DT_F16, 1, dev.p(dy),
+                       vsl.VSL_DT_F32, None))
+    assert rel_err(dev.get(dy), orc.gemm_nt(W, h16.astype(np.float32))[:, 0]) < 1e-5
+    assert H.vsl_gemv_residual(dev.p(dW), 1, 8, 32776, dev.p(dW), dev.p(dr), None, None) == vsl.VSL_E_INVALID
+
+
+def test_norm_swiglu_wide_k(vsl, orc, dev, H):
+    """The RMSNorm + [Wgate; Wup] + SwiGLU GEMV past 16384 input columns (16-wave blocks, the norm
+    over the staged vector) against the oracle."""
+    rng = np.random.default_rng(77)
+    d, F = 18432, 600
+    Wgu = rng.normal(0, 0.02, (2 * F, d)).astype(np.float16)
+    x = rng.normal(0, 1, d).astype(np.float32)
+    gm = rng.normal(1, 0.1, d).astype(np.float32)
+    dh = dev.empty((F,), np.float32)
+    ok(vsl, H.vsl_norm_swiglu(dev.p(dev.put(x)), dev.p(dev.put(gm)), 1e-5, dev.p(dev.put(Wgu)), 1, d, F, dev.p(dh),
+                              None, None))
+    gu = orc.gemm_nt(Wgu, orc.rmsnorm(x, gm, 1e-5))[:, 0]
+    assert rel_err(dev.get(dh), orc.swiglu(gu[:F], gu[F:])) < 1e-4
+
+
 def test_lm_head_greedy_and_bookkeeping(vsl, orc, dev, H):
     rng = np.random.default_rng(12)
     V, d = 32000, 4096

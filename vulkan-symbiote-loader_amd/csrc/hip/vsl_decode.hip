@@ -526,7 +526,7 @@ uint32_t gemv_blocks(uint32_t N, uint32_t max_blocks) {
     return blocks == 0 ? 1 : blocks;
 }
 
-constexpr uint32_t kMaxK = 16384;  // activation vector held in LDS as fp32 (64 KB)
+constexpr uint32_t kMaxK = 32768;  // activation vector held in LDS as fp32 (up to 128 KB)
 
 // XPT: float4 of the activation vector staged per thread, the smallest power of two covering K
 template <class WT, int R, int U, int EPI, int WAVES, class ET = WF32>
@@ -549,8 +549,9 @@ int launch_gemv(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
 }
 
 // Block size by K: the fp32 activation vector takes K*4 bytes of LDS per block; past 8192
-// columns, 8-wave blocks keep 16 waves resident per CU within the 160 KB of LDS.
-constexpr uint32_t kWideK = 8192;
+// columns, 8-wave blocks keep 16 waves resident per CU within the 160 KB of LDS; past 16384 (the
+// down projection of 70B-class FFNs, 28672), one 16-wave block per CU holds up to 128 KB.
+constexpr uint32_t kWideK = 8192, kXWideK = 16384;
 
 int gemv_waves_env() {
     static int w = -1;
@@ -566,10 +567,11 @@ template <class WT, int R, int U, int EPI, class ET = WF32>
 int launch_gemv_k(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
     switch (gemv_waves_env()) {
         case 16: return launch_gemv<WT, R, U, EPI, 16, ET>(a, max_blocks, s);
-        case 8: return launch_gemv<WT, R, U, EPI, 8, ET>(a, max_blocks, s);
+        case 8: if (a.K <= kXWideK) return launch_gemv<WT, R, U, EPI, 8, ET>(a, max_blocks, s); break;
         case 4: if (a.K <= kWideK) return launch_gemv<WT, R, U, EPI, 4, ET>(a, max_blocks, s); break;
         default: break;
     }
+    if (a.K > kXWideK) return launch_gemv<WT, R, U, EPI, 16, ET>(a, max_blocks, s);
     return a.K > kWideK ? launch_gemv<WT, R, U, EPI, 8, ET>(a, max_blocks, s)
                         : launch_gemv<WT, R, U, EPI, 4, ET>(a, max_blocks, s);
 }
@@ -579,10 +581,11 @@ uint32_t gemv_blocks_k(uint32_t N, uint32_t K, uint32_t max_blocks) {
     // the grid launch_gemv_k chooses
     switch (gemv_waves_env()) {
         case 16: return gemv_blocks<R, EPI, 16>(N, max_blocks);
-        case 8: return gemv_blocks<R, EPI, 8>(N, max_blocks);
+        case 8: if (K <= kXWideK) return gemv_blocks<R, EPI, 8>(N, max_blocks); break;
         case 4: if (K <= kWideK) return gemv_blocks<R, EPI, 4>(N, max_blocks); break;
         default: break;
     }
+    if (K > kXWideK) return gemv_blocks<R, EPI, 16>(N, max_blocks);
     return K > kWideK ? gemv_blocks<R, EPI, 8>(N, max_blocks) : gemv_blocks<R, EPI, 4>(N, max_blocks);
 }
 

@@ -277,6 +277,10 @@ void VulkanSymbioteEngine::init_device(const ModelConfig& cfg, bool fp16_weights
     const uint32_t G = cfg.num_attention_heads / cfg.num_key_value_heads;
     if (G < 1 || G > 8) throw std::runtime_error("GQA ratio must be 1..8");
     if (cfg.hidden_size % 8 || cfg.intermediate_size % 8) throw std::runtime_error("hidden/ffn sizes must be multiples of 8");
+    // every decode GEMV stages its input vector in LDS as fp32 (vsl_hip.h: K <= 32768)
+    if (cfg.hidden_size > 32768 || cfg.intermediate_size > 32768 ||
+        (uint64_t)cfg.num_attention_heads * config_.head_dim > 32768)
+        throw std::runtime_error("hidden / ffn / attention widths above 32768 are not supported");
     cap_ = options_.kv_capacity ? options_.kv_capacity : std::min<uint32_t>(cfg.max_position_embeddings ? cfg.max_position_embeddings : 4096, 4096);
     if (cap_ == 0) throw std::runtime_error("KV capacity must be positive");
     nsplit_ = options_.attn_splits ? options_.attn_splits : 32u;
