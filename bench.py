@@ -8,8 +8,9 @@ cache fp16 with capacity 4096; prompt of 512 uniform-random token ids (prefill t
 then greedy decode.  A step is one decode token; K steps are timed between two synchronisations.
 
 The same run also measures, as extra keys of the one JSON line: the configured 512-step decode
-(positions 513..1024), the 1B-class model (prompt 128, greedy decode 256), the fp16 GEMV sweep and the
-long-context workload (8192-token prompt in 2048-token chunks, KV capacity 32768); --quick skips them.
+(positions 513..1024), the 1B-class model (prompt 128, greedy decode 256), the fp16 GEMV sweep, the
+long-context workload (8192-token prompt in 2048-token chunks, KV capacity 32768) and a 70B-class model
+(137.5 GB of fp16 weights in one GPU's HBM; prompt 128, greedy decode 64); --quick skips them.
 
 Prints one JSON line.  --gpus N with N > 1 exits: this build targets one GPU.
 """
@@ -380,6 +381,39 @@ def llama_1b_leg(vsl, eager, prefill_runs=5, kernel_timing=True, steps=256):
     return out
 
 
+# A 70B-class decoder (Llama-2/3-70B geometry: 80 layers, d 8192, 64/8 heads, FFN 28672), fp16: 137.5 GB
+# of weights, which one MI355X holds in its 288 GB of HBM.
+LLAMA_70B = dict(hidden_size=8192, num_layers=80, num_heads=64, num_kv_heads=8, intermediate_size=28672,
+                 vocab_size=32000, max_position_embeddings=4096, rope_theta=500000.0, rms_eps=1e-5, dtype=1)
+
+
+def llama_70b_leg(vsl, eager, steps=64, prefill_runs=3):
+    """70B-class fp16 on one GPU: prompt 128, greedy decode `steps`."""
+    n_prompt = 128
+    prompt = np.random.default_rng(3).integers(0, LLAMA_70B["vocab_size"], n_prompt).astype(np.uint32)
+    eng = vsl.Engine(spec=LLAMA_70B, seed=0, kv_capacity=1024, use_graph=not eager)
+    try:
+        eng.begin(prompt, 5)
+        eng.decode(4)
+        eng.finish()
+        dec_s, st = timed_decode(eng, prompt, steps)
+        pre = [st["prefill_ms"]]
+        for _ in range(prefill_runs - 1):
+            eng.begin(prompt, 1)
+            eng.finish()
+            pre.append(eng.last_stats()["prefill_ms"])
+    finally:
+        eng.close()
+    pre_ms = float(np.median(pre))
+    pre_flops = prefill_flops(LLAMA_70B, n_prompt)
+    return {"workload": f"70B-class Llama decoder fp16 bs=1 (80L, d8192, 64/8 heads, FFN 28672, V32000; "
+                        f"137.5 GB of weights on one GPU): prompt {n_prompt}, greedy decode {steps}",
+            "decode": decode_rates(LLAMA_70B, n_prompt, steps, dec_s),
+            "prefill_ms": round(pre_ms, 3), "prefill_tok_s": round(n_prompt / (pre_ms / 1e3), 1),
+            "prefill_tflops": round(pre_flops / (pre_ms / 1e3) / 1e12, 1),
+            "prefill_mfma_frac": round(pre_flops / (pre_ms / 1e3) / PEAK_F16, 4)}
+
+
 def copy_calibration(vsl, mb):
     """One device-to-device copy of `mb` MiB: a kernel of known traffic for scaling rocprofv3's
     FETCH_SIZE / WRITE_SIZE counters. Returns the bytes copied."""
@@ -413,7 +447,8 @@ def main():
     ap.add_argument("--attn-splits", type=int, default=0,
                     help="decode attention split count of the 8B engine (0: the engine's choice)")
     ap.add_argument("--quick", action="store_true",
-                    help="the headline decode / prefill only (no 512-step decode, 1B, sweep or long-context legs)")
+                    help="the headline decode / prefill only (no 512-step decode, 1B, sweep, long-context or 70B "
+                         "legs)")
     ap.add_argument("--no-kernel-timing", action="store_true")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="after the run, copy this many MB device-to-device once (a kernel of known traffic "
@@ -550,7 +585,8 @@ def main():
         # the other configurations, each in its own engine after the 8B one is released
         for key, leg in (("llama_1b", lambda: llama_1b_leg(vsl, a.eager, kernel_timing=not a.no_kernel_timing)),
                          ("gemv_sweep", lambda: sweep_leg(vsl, graph=not a.eager)),
-                         ("long_context", lambda: long_leg(vsl, 128, a.eager))):
+                         ("long_context", lambda: long_leg(vsl, 128, a.eager)),
+                         ("llama_70b", lambda: llama_70b_leg(vsl, a.eager))):
             try:
                 out[key] = leg()
             except Exception as ex:  # reported, never fatal to the headline measurement
