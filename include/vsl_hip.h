@@ -147,6 +147,34 @@ uint64_t vsl_weight_bytes(int fmt, uint64_t n);
 int vsl_convert_weights(const void* src, int src_fmt, int layout, uint64_t n, void* dst, int dst_dtype,
                         void* stream);
 
+/* Resident block-quantized weight packs, multiplied block by block inside the decode GEMVs (no
+ * reference counterpart: the reference expands every block to fp32 at load, GGUFLoader.cpp:1121-1223,
+ * and reads 32 bits per weight per token; a pack reads 8.5 / 4.5 / 5 bits).  A pack holds a matrix
+ * of `rows` x K values (K % 32 == 0) in 32-value blocks, row-major block order, as planes that each
+ * start at a multiple of 256 bytes from the pack's 256-byte aligned base:
+ *   VSL_DT_Q8_0  int8 values [rows][K], then fp32 scales d [rows][K/32]             w = q d
+ *   VSL_DT_Q4_0  [rows][K/2] bytes (value 2j of a block in the low nibble of byte j, 2j + 1 in the
+ *                high nibble), then fp32 scales d [rows][K/32]                      w = (q - 8) d
+ *   VSL_DT_Q4_1  as Q4_0, then fp32 offsets m [rows][K/32]                          w = q d + m
+ * The decode entry points (vsl_qkv_rope_append, vsl_gemv_residual, vsl_norm_swiglu,
+ * vsl_lm_head_sample, and vsl_gemv at B = 1 with fp32 X) take these as `wdtype`; matrices stacked
+ * into one operand ([Wq; Wk; Wv], [Wgate; Wup]) are consecutive rows of one pack.  Each GEMV forms
+ * d * sum(q x) (+ m * sum(x)) per block in fp32. */
+enum { VSL_DT_Q8_0 = 4, VSL_DT_Q4_0 = 5, VSL_DT_Q4_1 = 6 };
+/* bytes of a pack of rows x K (0 for K % 32 != 0 or another dtype) */
+uint64_t vsl_quant_pack_bytes(int dtype, uint32_t rows, uint32_t K);
+/* n_blocks GGUF blocks (fmt VSL_WF_Q8_0 / VSL_WF_Q4_0 / VSL_WF_Q4_1 in `layout`, device memory, as
+ * vsl_convert_weights reads them, same scale semantics) into blocks block0 .. block0 + n_blocks - 1
+ * of the pack of the matching dtype (block b: row b / (K/32), values 32 (b % (K/32)) ..). */
+int vsl_quant_pack(const void* src, int fmt, int layout, uint64_t n_blocks, void* pack, uint32_t rows, uint32_t K,
+                   uint64_t block0, void* stream);
+/* fp16 / fp32 weights [rows][K] into a pack, round to nearest per block: Q8_0 d = max|w| / 127;
+ * Q4_0 d = -w_max / 8 (w_max the value of largest magnitude), q = clamp(round(w / d) + 8, 0, 15);
+ * Q4_1 d = (max - min) / 15, m = min. */
+int vsl_quantize_pack(const void* w, int wdtype, uint32_t rows, uint32_t K, int dtype, void* pack, void* stream);
+/* a pack back into fp16 / fp32 weights [rows][K] (w as above, in fp32, then rounded for fp16) */
+int vsl_dequant_pack(const void* pack, int dtype, uint32_t rows, uint32_t K, void* w, int wdtype, void* stream);
+
 /* ------------------------------------------------------------------------------------------
  * Decode control block (device memory).  One per engine; read by every decode kernel.
  * ------------------------------------------------------------------------------------------ */

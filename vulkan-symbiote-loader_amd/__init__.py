@@ -22,6 +22,7 @@ ENGINE_LIB = os.path.join(LIB_DIR, "libvsl_engine.so")
 
 VSL_OK, VSL_E_INVALID, VSL_E_HIP, VSL_E_OOM, VSL_E_UNSUPPORTED, VSL_E_CAPACITY = 0, -100, -101, -102, -103, -104
 VSL_DT_F32, VSL_DT_F16, VSL_DT_F16X2, VSL_DT_F16F8 = 0, 1, 2, 3
+VSL_DT_Q8_0, VSL_DT_Q4_0, VSL_DT_Q4_1 = 4, 5, 6  # resident block-quantized weight packs
 VSL_WF_F32, VSL_WF_F16, VSL_WF_Q4_0, VSL_WF_Q4_1, VSL_WF_Q8_0 = 0, 1, 2, 3, 4
 VSL_QL_REFERENCE, VSL_QL_GGML = 0, 1
 GEMM_A_X2, GEMM_C_X2, GEMM_A_F8, GEMM_C_F8 = 0x100, 0x200, 0x400, 0x800
@@ -154,6 +155,10 @@ _HIP_SIGS = {
     "vsl_attn_decode": (_I32, [_P, _P, _P, _I32, _U32, _U32, _U32, _U32, _F32, _U32, _P, _P, _P, _P, _P]),
     "vsl_attn_decode_noalloc": (_I32, [_P, _P, _P, _I32, _U32, _U32, _U32, _U32, _F32, _U32, _P, _P, _P]),
     "vsl_gemv_residual": (_I32, [_P, _I32, _U32, _U32, _P, _P, _P, _P]),
+    "vsl_quant_pack_bytes": (ctypes.c_uint64, [_I32, _U32, _U32]),
+    "vsl_quant_pack": (_I32, [_P, _I32, _I32, ctypes.c_uint64, _P, _U32, _U32, ctypes.c_uint64, _P]),
+    "vsl_quantize_pack": (_I32, [_P, _I32, _U32, _U32, _I32, _P, _P]),
+    "vsl_dequant_pack": (_I32, [_P, _I32, _U32, _U32, _P, _I32, _P]),
     "vsl_norm_swiglu": (_I32, [_P, _P, _F32, _P, _I32, _U32, _U32, _P, _P, _P]),
     "vsl_lm_head_sample": (_I32, [_P, _F32, _P, _I32, _U32, _U32, _P, _P, _I32, _P, Sampler, _P, _P, _P, _P, _P]),
     "vsl_lm_head_ws_blocks": (_U32, []),

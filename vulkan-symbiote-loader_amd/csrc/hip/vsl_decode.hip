@@ -165,9 +165,15 @@ __device__ __forceinline__ void load_x(const float* xs, uint32_t kk, float* xv) 
         float4 b = *reinterpret_cast<const float4*>(xs + kk + 4);
         xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
         xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
-    } else {
+    } else if constexpr (WT::kVec == 4) {
         float4 a = *reinterpret_cast<const float4*>(xs + kk);
         xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < WT::kVec; j += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(xs + kk + j);
+            xv[j] = a.x; xv[j + 1] = a.y; xv[j + 2] = a.z; xv[j + 3] = a.w;
+        }
     }
 }
 
@@ -212,14 +218,19 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
     __shared__ uint32_t bidx[WAVES];
     extern __shared__ float xs[];
 
-    typedef typename WT::T T;
     constexpr int VEC = WT::kVec;
+    constexpr bool QW = WT::kQuant;  // block-quantized pack: values, then scales (and offsets)
     constexpr uint32_t SPAN = 64 * VEC;
     constexpr uint32_t CHUNK = SPAN * U;
     constexpr int RG = (EPI == EPI_SWIGLU) ? R / 2 : R;  // logical rows per group
     static_assert(EPI != EPI_SWIGLU || R % 2 == 0, "SwiGLU groups pair gate and up rows");
     static_assert(EPI != EPI_QKV || R % 2 == 0, "QKV groups hold whole RoPE pairs");
-    const T* __restrict__ W = static_cast<const T*>(a.W);
+    static_assert(!QW || VEC <= 32, "a lane's quantized values lie in one 32-value block");
+    const char* __restrict__ W = static_cast<const char*>(a.W);
+    // quantized packs: the scale (and offset) of the 32-value block of element e is plane[e / 32]
+    const uint64_t w_rows = EPI == EPI_SWIGLU ? 2ull * a.N : a.N;
+    const float* __restrict__ Qs = QW ? reinterpret_cast<const float*>(W + qpack_scales_off(WT::kBits, w_rows, a.K)) : nullptr;
+    const float* __restrict__ Qm = WT::kMin ? reinterpret_cast<const float*>(W + qpack_mins_off(WT::kBits, w_rows, a.K)) : nullptr;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const uint32_t n_groups = (a.N + RG - 1) / RG;
@@ -243,8 +254,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
             }
         }
     };
-    // weights of tile t
-    auto issue_w = [&](uint4 (&w)[R][U], uint32_t t) {
+    // weights of tile t (with the block scales and offsets of a quantized pack)
+    auto issue_w = [&](uint4 (&w)[R][U], float (&qs)[R][U], float (&qm)[R][U], uint32_t t) {
         const uint32_t gi = t / cpg, c = t - gi * cpg;
         const uint32_t k0 = c * CHUNK;
         uint32_t rows[R];
@@ -259,7 +270,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
                 // or select touches a tile between its loads and its use (columns past K are
                 // skipped in consume, rows past N never reach an output).
                 const bool in = ok[r] && kk < a.K;
-                w[r][u] = load16<true>(W + (in ? (size_t)rows[r] * a.K + kk : 0));
+                const uint64_t e = in ? (uint64_t)rows[r] * a.K + kk : 0;
+                w[r][u] = load16<true>(W + wt_bytes<WT>(e));
+                if constexpr (QW) qs[r][u] = Qs[e / 32];
+                if constexpr (WT::kMin) qm[r][u] = Qm[e / 32];
             }
         }
     };
@@ -284,8 +298,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
             }
         }
     };
-    auto issue = [&](uint4 (&w)[R][U], float (&pf)[R], uint32_t t) {
-        issue_w(w, t);
+    auto issue = [&](uint4 (&w)[R][U], float (&qs)[R][U], float (&qm)[R][U], float (&pf)[R], uint32_t t) {
+        issue_w(w, qs, qm, t);
         issue_pf(pf, t);
     };
 
@@ -366,7 +380,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
     };
     // Every register of a tile is read on every path (columns past K are zeroed by selects, not
     // skipped by branches), so no path leaves a load pending into the next issue of its buffer.
-    auto consume = [&](const uint4 (&w)[R][U], const float (&pf)[R], uint32_t t) {
+    auto consume = [&](const uint4 (&w)[R][U], const float (&qs)[R][U], const float (&qm)[R][U], const float (&pf)[R],
+                       uint32_t t) {
         const uint32_t gi = t / cpg, c = t - gi * cpg;
         const uint32_t k0 = c * CHUNK;
 #pragma unroll
@@ -375,6 +390,33 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
             const bool in = kk < a.K;
             float xv[VEC];
             load_x<WT>(xs, in ? kk : 0, xv);
+            if constexpr (QW) {
+                // the lane's values share one block: acc += d * sum(q x) (Q8), d * (sum(q x) - 8 sum(x))
+                // (Q4_0) or d * sum(q x) + m * sum(x) (Q4_1), with d = m = 0 past K
+                float xsum = 0.f;
+                if constexpr (WT::kBits == 4) {
+#pragma unroll
+                    for (int i = 0; i < VEC; ++i) xsum += xv[i];
+                }
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float wf[VEC];
+                    unpack(w[r][u], WT(), wf);
+                    float b = 0.f;
+#pragma unroll
+                    for (int i = 0; i < VEC; ++i) b = fmaf(wf[i], xv[i], b);
+                    const float d = in ? qs[r][u] : 0.f;
+                    if constexpr (WT::kMin) {
+                        acc[r] = fmaf(d, b, acc[r]);
+                        acc[r] = fmaf(in ? qm[r][u] : 0.f, xsum, acc[r]);
+                    } else if constexpr (WT::kBits == 4) {
+                        acc[r] = fmaf(d, fmaf(-8.f, xsum, b), acc[r]);
+                    } else {
+                        acc[r] = fmaf(d, b, acc[r]);
+                    }
+                }
+                continue;
+            }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const uint4 wr = in ? w[r][u] : make_uint4(0u, 0u, 0u, 0u);
@@ -396,9 +438,10 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
     XStage<WAVES, XPT> st;
     st.load(a.x, a.xh, a.gamma, a.K);
     uint4 wa[R][U], wb[R][U];
+    float sa[R][U], sb[R][U], ma[R][U], mb[R][U];  // block scales / offsets of a quantized pack
     float pa[R], pb[R];
-    issue_w(wa, 0);
-    issue_w(wb, 1);
+    issue_w(wa, sa, ma, 0);
+    issue_w(wb, sb, mb, 1);
     __builtin_amdgcn_sched_barrier(0);
     if (a.ctrl) {
         if (a.ctrl->done) return;
@@ -428,15 +471,15 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
     const uint32_t n_pairs = n_tiles ? (n_tiles + 1) / 2 : 1;
     // (sched_barrier: keep each issue ahead of the next tile's arithmetic in the schedule)
     for (uint32_t p = 0; p + 1 < n_pairs; ++p) {
-        consume(wa, pa, 2 * p);
-        issue(wa, pa, 2 * p + 2);
+        consume(wa, sa, ma, pa, 2 * p);
+        issue(wa, sa, ma, pa, 2 * p + 2);
         __builtin_amdgcn_sched_barrier(0);
-        consume(wb, pb, 2 * p + 1);
-        issue(wb, pb, 2 * p + 3);
+        consume(wb, sb, mb, pb, 2 * p + 1);
+        issue(wb, sb, mb, pb, 2 * p + 3);
         __builtin_amdgcn_sched_barrier(0);
     }
-    consume(wa, pa, 2 * n_pairs - 2);
-    consume(wb, pb, 2 * n_pairs - 1);
+    consume(wa, sa, ma, pa, 2 * n_pairs - 2);
+    consume(wb, sb, mb, pb, 2 * n_pairs - 1);
 
     if constexpr (EPI == EPI_ARGMAX) {
         // per-block partial argmax; k_argmax_finish reduces the partials in the next launch (a
@@ -595,6 +638,27 @@ int check_gemv_shape(uint32_t N, uint32_t K, const char* who) {
     if (K % 8) return vsl_invalid("%s: K=%u must be a multiple of 8", who, K);
     if (K > kMaxK) return vsl_invalid("%s: K=%u exceeds %u", who, K, kMaxK);
     return VSL_OK;
+}
+
+bool quant_dtype(int wdtype) { return wdtype == VSL_DT_Q8_0 || wdtype == VSL_DT_Q4_0 || wdtype == VSL_DT_Q4_1; }
+
+// The decode GEMV over the weight dtype: fp16 / fp32 matrices with four 16-byte loads per lane and row
+// per tile; block-quantized packs with the same 2048 columns per tile (Q8: two loads of 16 values,
+// Q4: one of 32).
+template <int R, int EPI, class ET = WF32>
+int launch_gemv_w(int wdtype, const GemvArgs& a, uint32_t max_blocks, hipStream_t s, const char* who) {
+    if (quant_dtype(wdtype)) {
+        if (a.K % 32) return vsl_invalid("%s: a block-quantized pack needs K %% 32 == 0 (K=%u)", who, a.K);
+        if (reinterpret_cast<uintptr_t>(a.W) & 255) return vsl_invalid("%s: a block-quantized pack must be 256-byte aligned", who);
+    }
+    switch (wdtype) {
+        case VSL_DT_F16: return launch_gemv_k<WF16, R, 4, EPI, ET>(a, max_blocks, s);
+        case VSL_DT_F32: return launch_gemv_k<WF32, R, 4, EPI, ET>(a, max_blocks, s);
+        case VSL_DT_Q8_0: return launch_gemv_k<WQ8, R, 2, EPI, ET>(a, max_blocks, s);
+        case VSL_DT_Q4_0: return launch_gemv_k<WQ4, R, 1, EPI, ET>(a, max_blocks, s);
+        case VSL_DT_Q4_1: return launch_gemv_k<WQ41, R, 1, EPI, ET>(a, max_blocks, s);
+        default: return vsl_unsupported("%s: weight dtype %d", who, wdtype);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -2362,10 +2426,21 @@ extern "C" int vsl_gemv(const void* W, int wdtype, uint32_t N, uint32_t K, const
     if (!W || !X || !Y) return vsl_invalid("vsl_gemv: null pointer");
     if (int rc = check_gemv_shape(N, K, "vsl_gemv")) return rc;
     if (B < 1 || B > 16) return vsl_invalid("vsl_gemv: B=%u must be in [1,16]", B);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (quant_dtype(wdtype) && B == 1 && xdtype == VSL_DT_F32 && (ydtype == VSL_DT_F16 || ydtype == VSL_DT_F32)) {
+        // a block-quantized pack: the decode GEMV (B = 1, fp32 X)
+        GemvArgs a{};
+        a.W = W;
+        a.N = N;
+        a.K = K;
+        a.x = static_cast<const float*>(X);
+        a.y = static_cast<float*>(Y);
+        return ydtype == VSL_DT_F16 ? launch_gemv_w<2, EPI_STORE_F16>(wdtype, a, 1u << 20, s, "vsl_gemv")
+                                    : launch_gemv_w<2, EPI_STORE>(wdtype, a, 1u << 20, s, "vsl_gemv");
+    }
     if ((wdtype != VSL_DT_F16 && wdtype != VSL_DT_F32) || (xdtype != VSL_DT_F16 && xdtype != VSL_DT_F32) ||
         (ydtype != VSL_DT_F16 && ydtype != VSL_DT_F32))
         return vsl_unsupported("vsl_gemv: dtype combination %d/%d/%d", wdtype, xdtype, ydtype);
-    hipStream_t s = static_cast<hipStream_t>(stream);
     if (wdtype == VSL_DT_F16 && xdtype == VSL_DT_F16 && B == 1 && K % 8 == 0 && K <= kMaxK &&
         (reinterpret_cast<uintptr_t>(X) & 7) == 0)
         return gemv_one_f16x(W, N, K, X, Y, ydtype, s);
@@ -2453,15 +2528,8 @@ extern "C" int vsl_qkv_rope_append(const float* x, const float* gamma, float eps
     a.n_q = n_q; a.n_kv = n_kv; a.hd = hd; a.cap = cap; a.rope_cos = rope_cos; a.rope_sin = rope_sin;
     a.kc = kcache; a.vc = vcache; a.q_out = q_out; a.ctrl = ctrl;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (wdtype == VSL_DT_F16) {
-        if (kv_dtype == VSL_DT_F16) return launch_gemv_k<WF16, 2, 4, EPI_QKV, WF16>(a, 1u << 20, s);
-        return launch_gemv_k<WF16, 2, 4, EPI_QKV, WF32>(a, 1u << 20, s);
-    }
-    if (wdtype == VSL_DT_F32) {
-        if (kv_dtype == VSL_DT_F16) return launch_gemv_k<WF32, 2, 4, EPI_QKV, WF16>(a, 1u << 20, s);
-        return launch_gemv_k<WF32, 2, 4, EPI_QKV, WF32>(a, 1u << 20, s);
-    }
-    return vsl_unsupported("vsl_qkv_rope_append: dtype %d", wdtype);
+    if (kv_dtype == VSL_DT_F16) return launch_gemv_w<2, EPI_QKV, WF16>(wdtype, a, 1u << 20, s, "vsl_qkv_rope_append");
+    return launch_gemv_w<2, EPI_QKV, WF32>(wdtype, a, 1u << 20, s, "vsl_qkv_rope_append");
 }
 
 static int attn_decode(const float* q, const void* kcache, const void* vcache, int kv_dtype, uint32_t n_q,
@@ -2558,9 +2626,7 @@ extern "C" int vsl_gemv_residual(const void* W, int wdtype, uint32_t N, uint32_t
     GemvArgs a{};
     a.W = W; a.N = N; a.K = K; a.x = x; a.y = resid; a.ctrl = ctrl;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (wdtype == VSL_DT_F16) return launch_gemv_k<WF16, 1, 4, EPI_RESID>(a, 1u << 20, s);
-    if (wdtype == VSL_DT_F32) return launch_gemv_k<WF32, 1, 4, EPI_RESID>(a, 1u << 20, s);
-    return vsl_unsupported("vsl_gemv_residual: dtype %d", wdtype);
+    return launch_gemv_w<1, EPI_RESID>(wdtype, a, 1u << 20, s, "vsl_gemv_residual");
 }
 
 extern "C" int vsl_norm_swiglu(const float* x, const float* gamma, float eps, const void* Wgu, int wdtype, uint32_t d,
@@ -2570,9 +2636,7 @@ extern "C" int vsl_norm_swiglu(const float* x, const float* gamma, float eps, co
     GemvArgs a{};
     a.W = Wgu; a.N = F; a.K = d; a.x = x; a.gamma = gamma; a.eps = eps; a.y = h_out; a.ctrl = ctrl;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (wdtype == VSL_DT_F16) return launch_gemv_k<WF16, 2, 4, EPI_SWIGLU>(a, 1u << 20, s);
-    if (wdtype == VSL_DT_F32) return launch_gemv_k<WF32, 2, 4, EPI_SWIGLU>(a, 1u << 20, s);
-    return vsl_unsupported("vsl_norm_swiglu: dtype %d", wdtype);
+    return launch_gemv_w<2, EPI_SWIGLU>(wdtype, a, 1u << 20, s, "vsl_norm_swiglu");
 }
 
 extern "C" uint32_t vsl_lm_head_ws_blocks(void) { return kMaxLmBlocks; }
@@ -2596,7 +2660,9 @@ extern "C" int vsl_lm_head_sample(const float* gamma, float eps, const void* W, 
         return vsl_invalid("vsl_lm_head_sample: null pointer");
     if (int rc = check_gemv_shape(V, d, "vsl_lm_head_sample")) return rc;
     if (embed_dtype != VSL_DT_F16 && embed_dtype != VSL_DT_F32) return vsl_unsupported("embed dtype %d", embed_dtype);
-    if (wdtype != VSL_DT_F16 && wdtype != VSL_DT_F32) return vsl_unsupported("vsl_lm_head_sample: dtype %d", wdtype);
+    if (wdtype != VSL_DT_F16 && wdtype != VSL_DT_F32 && !quant_dtype(wdtype))
+        return vsl_unsupported("vsl_lm_head_sample: dtype %d", wdtype);
+    if (quant_dtype(wdtype) && d % 32) return vsl_invalid("vsl_lm_head_sample: a block-quantized pack needs d %% 32 == 0");
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (int rc = check_sampler(sampler, V, "vsl_lm_head_sample")) return rc;
     const bool fused = sampler.mode == VSL_SAMPLE_GREEDY || sampler.temperature <= 0.f;
@@ -2605,8 +2671,7 @@ extern "C" int vsl_lm_head_sample(const float* gamma, float eps, const void* W, 
     a.ws_val = ws_val; a.ws_idx = ws_idx; a.tokens = tokens; a.embed = embed; a.x_next = x;
     a.ctrl = ctrl;
     if (fused) {
-        int rc = wdtype == VSL_DT_F16 ? launch_gemv_k<WF16, 2, 4, EPI_ARGMAX>(a, kMaxLmBlocks, s)
-                                      : launch_gemv_k<WF32, 2, 4, EPI_ARGMAX>(a, kMaxLmBlocks, s);
+        int rc = launch_gemv_w<2, EPI_ARGMAX>(wdtype, a, kMaxLmBlocks, s, "vsl_lm_head_sample");
         if (rc) return rc;
         const uint32_t nb = gemv_blocks_k<2, EPI_ARGMAX>(V, d, kMaxLmBlocks);
         if (embed_dtype == VSL_DT_F16)
@@ -2617,8 +2682,7 @@ extern "C" int vsl_lm_head_sample(const float* gamma, float eps, const void* W, 
         return VSL_OK;
     }
     // logits only (EPI_STORE with the norm prologue), then the sampling kernel
-    int rc = wdtype == VSL_DT_F16 ? launch_gemv_k<WF16, 2, 4, EPI_STORE>(a, 1u << 20, s)
-                                  : launch_gemv_k<WF32, 2, 4, EPI_STORE>(a, 1u << 20, s);
+    int rc = launch_gemv_w<2, EPI_STORE>(wdtype, a, 1u << 20, s, "vsl_lm_head_sample");
     if (rc) return rc;
     const uint64_t key = vsl_derive_key(sampler.seed, "sampler");
     if (embed_dtype == VSL_DT_F16)

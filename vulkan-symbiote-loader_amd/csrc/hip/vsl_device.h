@@ -12,9 +12,31 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
-// Weight / cache element types used as template parameters.
-struct WF16 { typedef vsl_half T; static constexpr int kVec = 8; };   // 16-byte vector = 8 halfs
-struct WF32 { typedef float T; static constexpr int kVec = 4; };      // 16-byte vector = 4 floats
+// Weight / cache element types used as template parameters. kBits: bits per stored weight value;
+// kQuant: a resident block-quantized pack (values plane, then one fp32 scale per 32 values, for WQ41
+// also one fp32 offset per 32 values; see vsl_hip.h, VSL_DT_Q8_0 .. VSL_DT_Q4_1).
+struct WF16 { typedef vsl_half T; static constexpr int kVec = 8, kBits = 16; static constexpr bool kQuant = false, kMin = false; };
+struct WF32 { typedef float T; static constexpr int kVec = 4, kBits = 32; static constexpr bool kQuant = false, kMin = false; };
+struct WQ8 { typedef int8_t T; static constexpr int kVec = 16, kBits = 8; static constexpr bool kQuant = true, kMin = false; };
+struct WQ4 { typedef uint8_t T; static constexpr int kVec = 32, kBits = 4; static constexpr bool kQuant = true, kMin = false; };
+struct WQ41 { typedef uint8_t T; static constexpr int kVec = 32, kBits = 4; static constexpr bool kQuant = true, kMin = true; };
+
+// Byte offset of element e of a row-major weight matrix.
+template <class WT>
+__device__ __host__ __forceinline__ constexpr uint64_t wt_bytes(uint64_t e) {
+    return WT::kBits >= 8 ? e * (WT::kBits / 8) : e / (8 / WT::kBits);
+}
+
+// Planes of a block-quantized pack of `rows` x K values (K % 32 == 0): the values, then the fp32
+// scales (one per 32 values, row-major block order), then for Q4_1 the fp32 offsets; each plane
+// starts at a multiple of 256 bytes.
+__device__ __host__ __forceinline__ constexpr uint64_t qpack_align(uint64_t b) { return (b + 255) & ~(uint64_t)255; }
+__device__ __host__ __forceinline__ constexpr uint64_t qpack_scales_off(int bits, uint64_t rows, uint64_t K) {
+    return qpack_align(rows * K * (uint64_t)bits / 8);
+}
+__device__ __host__ __forceinline__ constexpr uint64_t qpack_mins_off(int bits, uint64_t rows, uint64_t K) {
+    return qpack_scales_off(bits, rows, K) + qpack_align(rows * (K / 32) * 4);
+}
 
 __device__ __forceinline__ float to_f32(vsl_half h) { return (float)h; }
 __device__ __forceinline__ float to_f32(float f) { return f; }
@@ -122,6 +144,30 @@ __device__ __forceinline__ void unpack(const uint4& v, WF32, float* out) {
     out[2] = __builtin_bit_cast(float, v.z);
     out[3] = __builtin_bit_cast(float, v.w);
 }
+// Block-quantized values as stored: Q8 the signed bytes, Q4 the unsigned nibbles (element 2j of a
+// byte in the low nibble, 2j + 1 in the high one); the scale / offset are applied by the caller.
+__device__ __forceinline__ void unpack(const uint4& v, WQ8, float* out) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) out[4 * i + k] = (float)(int8_t)(w[i] >> (8 * k));
+}
+template <class W4>
+__device__ __forceinline__ void unpack_q4(const uint4& v, float* out) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            out[8 * i + 2 * k] = (float)((lo >> (8 * k)) & 0xFFu);
+            out[8 * i + 2 * k + 1] = (float)((hi >> (8 * k)) & 0xFFu);
+        }
+    }
+}
+__device__ __forceinline__ void unpack(const uint4& v, WQ4, float* out) { unpack_q4<WQ4>(v, out); }
+__device__ __forceinline__ void unpack(const uint4& v, WQ41, float* out) { unpack_q4<WQ41>(v, out); }
 
 // Butterfly sum across the full wave (every lane ends with the total).
 __device__ __forceinline__ float wave_sum(float v) {
