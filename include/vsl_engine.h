@@ -32,8 +32,11 @@ typedef struct vsl_model_spec {
     float rope_theta, rms_eps;
     float init_std;    /* synthetic weights only: N(0, init_std) */
     uint32_t dtype;    /* storage of the linear weights: VSL_WF_F32 (== VSL_DT_F32) or VSL_WF_F16
-                          (== VSL_DT_F16); vsl_write_synthetic_gguf also takes VSL_WF_Q4_0 / Q4_1 /
-                          Q8_0 (every 2-D weight block-quantized from the fp32 draws) */
+                          (== VSL_DT_F16); VSL_WF_Q4_0 / Q4_1 / Q8_0: vsl_write_synthetic_gguf stores
+                          every 2-D weight block-quantized from the fp32 draws, and
+                          vsl_engine_open_synthetic quantizes fp16 draws of every linear weight on the
+                          device into resident packs (vsl_quantize_pack; needs quant_decode), whose
+                          values the expanded packs hold in fp16 (fp32 with dequant_f32) */
     uint32_t head_dim; /* filled by vsl_engine_get_config; ignored on input */
 } vsl_model_spec;
 
@@ -60,6 +63,9 @@ typedef struct vsl_engine_options {
                                    bit 4 down input;
                                    taken where the shapes allow it (d, F and the QKV width multiples of
                                    256), else the fp16 lo plane; vsl_engine_default_options sets 0x1C */
+    uint32_t quant_decode;      /* 1 (default): block-quantized weights also stay resident as blocks
+                                   (vsl_quant_pack) and the decode GEMVs read those; the prompt pass
+                                   uses the expanded packs */
 } vsl_engine_options;
 
 typedef struct vsl_gen_params {

@@ -126,16 +126,16 @@ def test_quantized_model_fp32_packs(vsl, orc, qfiles, fmt, conv):
 
 @pytest.mark.parametrize("fmt,conv", [("q4_0", "reference"), ("q8_0", "ggml"), ("q4_1", "reference")])
 def test_quantized_model_fp16_packs(vsl, orc, qfiles, fmt, conv):
-    """Default fp16 packs: each pack is the binary16 rounding of the dequantized values; the forward
-    pass over those packs (MFMA prefill, fp16 KV cache) matches the oracle over the same resident
-    weights: greedy tokens identical, logits within max-abs 2e-2."""
+    """Default fp16 packs (the decode on them too, quant_decode off): each pack is the binary16 rounding
+    of the dequantized values; the forward pass over those packs (MFMA prefill, fp16 KV cache) matches
+    the oracle over the same resident weights: greedy tokens identical, logits within max-abs 2e-2."""
     from test_engine_gpu import _oracle_from_engine
     p = qfiles[fmt, conv]
     prompt = _prompt(orc)
     L = orc.lib()
     h_ = ctypes.c_void_p()
     assert L.orc_gguf_open(str(p).encode(), ctypes.byref(h_)) == 0
-    with vsl.Engine(p, kv_capacity=64) as e:
+    with vsl.Engine(p, kv_capacity=64, quant_decode=False) as e:
         assert e.config["dtype"] == 1
         for name, n in (("token_embd.weight", QTINY["vocab_size"] * 256), ("blk.0.ffn_gate.weight", 256 * 768)):
             want = np.zeros(n, np.float32)
@@ -149,3 +149,52 @@ def test_quantized_model_fp16_packs(vsl, orc, qfiles, fmt, conv):
     m.close()
     assert np.max(np.abs(lg - ref_lg)) < 2e-2, np.max(np.abs(lg - ref_lg))
     assert np.array_equal(toks, ref_toks)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_1", "q8_0"])
+@pytest.mark.parametrize("conv", ["reference", "ggml"])
+def test_quant_decode_against_the_file(vsl, orc, qfiles, fmt, conv):
+    """The default engine on a quantized file: the decode GEMVs read the resident blocks (the exact
+    dequantized values), the MFMA prompt pass the fp16 packs; against the oracle that dequantizes the
+    file (fp32 weights, fp16 KV cache): greedy tokens identical, logits within max-abs 2e-2; and the
+    same tokens as the engine with quant_decode off."""
+    p = qfiles[fmt, conv]
+    prompt = _prompt(orc)
+    m = orc.Model(p)
+    ref_toks, ref_lg = m.generate(prompt, 32, kv_f16=True, logits=True)
+    m.close()
+    with vsl.Engine(p, kv_capacity=64) as e:
+        toks, lg = e.generate_ids(prompt, 32, return_logits=True)
+    with vsl.Engine(p, kv_capacity=64, quant_decode=False) as e:
+        toks_off = e.generate_ids(prompt, 32)
+    assert np.max(np.abs(lg - ref_lg)) < 2e-2, np.max(np.abs(lg - ref_lg))
+    assert np.array_equal(toks, ref_toks)
+    assert np.array_equal(toks, toks_off)
+
+
+@pytest.mark.parametrize("fmt", ["q4_0", "q4_1", "q8_0"])
+def test_synthetic_quantized_engine(vsl, orc, fmt):
+    """A synthetic model quantized on the device (vsl_quantize_pack), expanded packs in fp32
+    (dequant_f32): those hold exactly the values the decode GEMVs read from the blocks, so the oracle
+    over the engine's resident fp32 weights is the same model: greedy 24 tokens identical, logits
+    within 1e-4 relative; and the fp16-pack variant (MFMA prompt pass on the fp16-rounded values)
+    within max-abs 2e-2 of its own oracle with identical tokens."""
+    from test_engine_gpu import _oracle_from_engine
+    cfg = dict(QTINY, dtype=FMT_CODE[fmt])
+    prompt = _prompt(orc)
+    with vsl.Engine(spec=cfg, seed=4, kv_capacity=64, dequant_f32=True) as e:
+        assert e.config["dtype"] == 0
+        toks, lg = e.generate_ids(prompt, 24, return_logits=True)
+        m = _oracle_from_engine(orc, e, dict(cfg, dtype=0))
+    ref_toks, ref_lg = m.generate(prompt, 24, logits=True)
+    m.close()
+    assert np.array_equal(toks, ref_toks)
+    assert np.max(np.abs(lg - ref_lg)) < 1e-4 * np.max(np.abs(ref_lg))
+    with vsl.Engine(spec=cfg, seed=4, kv_capacity=64) as e:
+        assert e.config["dtype"] == 1
+        toks16, lg16 = e.generate_ids(prompt, 24, return_logits=True)
+        m = _oracle_from_engine(orc, e, dict(cfg, dtype=1))
+    ref_toks16, ref_lg16 = m.generate(prompt, 24, kv_f16=True, logits=True)
+    m.close()
+    assert np.max(np.abs(lg16 - ref_lg16)) < 2e-2
+    assert np.array_equal(toks16, ref_toks16)

@@ -66,7 +66,8 @@ class EngineOptions(ctypes.Structure):
                 ("batched_prefill", ctypes.c_uint32), ("prefill_split", ctypes.c_uint32),
                 ("dequant_f32", ctypes.c_uint32), ("sparse_attention", ctypes.c_uint32),
                 ("sparse_window", ctypes.c_uint32), ("sparse_global", ctypes.c_uint32),
-                ("sparse_threshold", ctypes.c_uint32), ("prefill_lo8", ctypes.c_uint32)]
+                ("sparse_threshold", ctypes.c_uint32), ("prefill_lo8", ctypes.c_uint32),
+                ("quant_decode", ctypes.c_uint32)]
 
 
 class GenParams(ctypes.Structure):
@@ -352,7 +353,7 @@ class Engine:
 
     def __init__(self, gguf_path=None, spec=None, seed=0, device=0, kv_capacity=0, use_graph=True,
                  prefill_chunk=0, attn_splits=0, batched_prefill=True, init_std=0.02, prefill_split=None,
-                 dequant_f32=False, window=None, prefill_lo8=None):
+                 dequant_f32=False, window=None, prefill_lo8=None, quant_decode=True):
         """window: None (dense attention) or (sparse_window, sparse_global, sparse_threshold) for the
         windowed long-context mode; (512, 16, 8192) are the reference's values. prefill_split /
         prefill_lo8: None keeps vsl_engine_default_options' stage masks."""
@@ -366,6 +367,7 @@ class Engine:
         if prefill_lo8 is not None:
             opt.prefill_lo8 = prefill_lo8
         opt.dequant_f32 = int(bool(dequant_f32))
+        opt.quant_decode = int(bool(quant_decode))
         if window is not None:
             opt.sparse_attention = 1
             opt.sparse_window, opt.sparse_global, opt.sparse_threshold = window

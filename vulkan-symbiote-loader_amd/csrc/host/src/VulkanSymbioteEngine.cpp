@@ -205,6 +205,7 @@ VulkanSymbioteEngine::VulkanSymbioteEngine(const Path& model_path, const EngineO
     };
     tokenizer_ = Tokenizer::from_gguf(model_path);  // VulkanSymbioteEngine.cpp:1140
     try {
+        plan_quant_gguf(cfg);
         init_device(cfg, pack_dtype(qf) == VSL_DT_F16, pack_dtype(ef));
         load_weights_from_gguf();
         measure_weight_ranges();
@@ -217,6 +218,7 @@ VulkanSymbioteEngine::VulkanSymbioteEngine(const Path& model_path, const EngineO
 VulkanSymbioteEngine::VulkanSymbioteEngine(const SyntheticSpec& spec, const EngineOptions& options) : options_(options) {
     tokenizer_ = Tokenizer::create_simple_tokenizer();
     try {
+        plan_quant_uniform(spec.config, spec.quant_format);
         init_device(spec.config, spec.fp16, spec.fp16 ? VSL_DT_F16 : VSL_DT_F32);
         init_synthetic_weights(spec);
         measure_weight_ranges();
@@ -241,6 +243,55 @@ void VulkanSymbioteEngine::release() {
     if (stream_) { vsl_stream_destroy(stream_); stream_ = nullptr; }
     if (upload_stream_) { vsl_stream_destroy(upload_stream_); upload_stream_ = nullptr; }
     pack_manager_.clear();
+}
+
+static int quant_pack_dtype(int wf) {
+    return wf == VSL_WF_Q8_0 ? VSL_DT_Q8_0 : wf == VSL_WF_Q4_0 ? VSL_DT_Q4_0 : VSL_DT_Q4_1;
+}
+static bool quant_wf(int wf) { return wf == VSL_WF_Q4_0 || wf == VSL_WF_Q4_1 || wf == VSL_WF_Q8_0; }
+
+// Which decode operands keep a resident block-quantized pack: those whose tensors share one quantized
+// format, with an input width (the pack's K) a multiple of 32.
+void VulkanSymbioteEngine::plan_quant_gguf(const ModelConfig& cfg) {
+    qfmt_.assign(cfg.num_layers, {-1, -1, -1, -1});
+    qfmt_out_ = -1;
+    if (!options_.quant_decode) return;
+    GGUFLoader& g = *loader_;
+    auto fmt = [&](const std::string& n) {
+        const GGUFTensorInfo* t = g.get_tensor(n);
+        return t ? g.weight_format(*t) : -1;
+    };
+    auto same = [&](std::initializer_list<std::string> names, uint64_t K) {
+        int f = -2;
+        for (const auto& n : names) {
+            const int x = fmt(n);
+            if (f == -2) f = x;
+            else if (x != f) return -1;
+        }
+        return quant_wf(f) && K % 32 == 0 ? f : -1;
+    };
+    const uint64_t d = cfg.hidden_size, F = cfg.intermediate_size, hd = cfg.head_dim ? cfg.head_dim : d / cfg.num_attention_heads;
+    for (uint32_t l = 0; l < cfg.num_layers; ++l) {
+        const std::string o = g.get_tensor(layer_name(l, "attn_o.weight")) ? layer_name(l, "attn_o.weight")
+                                                                         : layer_name(l, "attn_output.weight");
+        qfmt_[l] = {same({layer_name(l, "attn_q.weight"), layer_name(l, "attn_k.weight"), layer_name(l, "attn_v.weight")}, d),
+                    same({o}, cfg.num_attention_heads * hd),
+                    same({layer_name(l, "ffn_gate.weight"), layer_name(l, "ffn_up.weight")}, d),
+                    same({layer_name(l, "ffn_down.weight")}, F)};
+    }
+    qfmt_out_ = same({"output.weight"}, d);
+}
+
+void VulkanSymbioteEngine::plan_quant_uniform(const ModelConfig& cfg, int fmt) {
+    qfmt_.assign(cfg.num_layers, {-1, -1, -1, -1});
+    qfmt_out_ = -1;
+    if (!quant_wf(fmt)) return;
+    if (!options_.quant_decode) throw std::runtime_error("a quantized synthetic model needs quant_decode");
+    const uint64_t d = cfg.hidden_size, F = cfg.intermediate_size, hd = cfg.head_dim ? cfg.head_dim : d / cfg.num_attention_heads;
+    if (d % 32 || F % 32 || (cfg.num_attention_heads * hd) % 32)
+        throw std::runtime_error("a quantized synthetic model needs d, FFN and n_q * head_dim multiples of 32");
+    for (auto& f : qfmt_) f = {fmt, fmt, fmt, fmt};
+    qfmt_out_ = fmt;
 }
 
 int VulkanSymbioteEngine::attend(const Layer& y, float scale) {
@@ -329,6 +380,23 @@ void VulkanSymbioteEngine::plan_and_allocate() {
         add(d * F * es, &y.wdown);
         wbytes += 8 * d + ((nq + 2 * nkv) * hd * d + d * nq * hd + 3 * F * d) * es;
     }
+    // resident block-quantized packs of the decode operands
+    auto qadd = [&](int wf, uint64_t rows, uint64_t K, void** p, int* dt) {
+        if (wf < 0) return;
+        *dt = quant_pack_dtype(wf);
+        const uint64_t b = vsl_quant_pack_bytes(*dt, (uint32_t)rows, (uint32_t)K);
+        if (!b) throw std::runtime_error("block-quantized pack: bad shape");
+        add(b, p);
+        wbytes += b;
+    };
+    for (uint64_t l = 0; l < L && l < qfmt_.size(); ++l) {
+        Layer& y = layers_[l];
+        qadd(qfmt_[l][0], (nq + 2 * nkv) * hd, d, &y.qqkv, &y.qdt_qkv);
+        qadd(qfmt_[l][1], d, nq * hd, &y.qo, &y.qdt_o);
+        qadd(qfmt_[l][2], 2 * F, d, &y.qgu, &y.qdt_gu);
+        qadd(qfmt_[l][3], d, F, &y.qdown, &y.qdt_down);
+    }
+    qadd(qfmt_out_, V, d, &out_q_, &out_qdt_);
     weight_bytes_ = wbytes;
     kv_bytes_ = 0;
     for (uint64_t l = 0; l < L; ++l) {
@@ -445,6 +513,21 @@ void VulkanSymbioteEngine::init_synthetic_weights(const SyntheticSpec& spec) {
     }
     ones(out_norm_, "output_norm.weight");
     fill(out_w_, wdt_, V * d, "output.weight", d, V);
+    // a quantized synthetic model: each operand quantized into its pack, and its expanded pack
+    // replaced by the quantized values, so that the prompt pass and the decode use the same weights
+    auto quantize = [&](void* w, uint64_t rows, uint64_t K, void* pack, int dt) {
+        if (!pack) return;
+        check(vsl_quantize_pack(w, wdt_, (uint32_t)rows, (uint32_t)K, dt, pack, stream_), "vsl_quantize_pack");
+        check(vsl_dequant_pack(pack, dt, (uint32_t)rows, (uint32_t)K, w, wdt_, stream_), "vsl_dequant_pack");
+    };
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        Layer& y = layers_[l];
+        quantize(y.wqkv, (nq + 2 * nkv) * hd, d, y.qqkv, y.qdt_qkv);
+        quantize(y.wo, d, nq * hd, y.qo, y.qdt_o);
+        quantize(y.wgu, 2 * F, d, y.qgu, y.qdt_gu);
+        quantize(y.wdown, d, F, y.qdown, y.qdt_down);
+    }
+    quantize(out_w_, V, d, out_q_, out_qdt_);
     check(vsl_stream_sync(stream_), "sync");
 }
 
@@ -479,7 +562,13 @@ void VulkanSymbioteEngine::load_weights_from_gguf() {
     // form into a device staging slot and are expanded there by vsl_convert_weights.
     std::unique_ptr<vsl_arena, int (*)(vsl_arena*)> conv_arena(nullptr, vsl_arena_destroy);
     void* dstage[2] = {nullptr, nullptr};
-    auto upload_convert = [&](void* dst, const uint8_t* src, int fmt, int layout, uint64_t n, int dst_dt) {
+    // A resident block-quantized pack the staged blocks also go to: `rows` x K, this tensor's rows from row0.
+    struct QTarget {
+        void* pack = nullptr;
+        uint32_t rows = 0, K = 0, row0 = 0;
+    };
+    auto upload_convert = [&](void* dst, const uint8_t* src, int fmt, int layout, uint64_t n, int dst_dt,
+                              const QTarget& qt) {
         if (!conv_arena) {
             vsl_arena* a = nullptr;
             check(vsl_arena_create(options_.device, 2 * kStageBytes + (1u << 20), &a), "staging arena");
@@ -499,6 +588,10 @@ void VulkanSymbioteEngine::load_weights_from_gguf() {
             check(vsl_convert_weights(dstage[slot], fmt, layout, cnt, static_cast<char*>(dst) + e0 * es,
                                       dst_dt, upload_stream_),
                   "vsl_convert_weights");
+            if (qt.pack)  // whole blocks: the tensor holds whole rows of K % 32 == 0 values
+                check(vsl_quant_pack(dstage[slot], fmt, layout, cnt / 32, qt.pack, qt.rows, qt.K,
+                                     (uint64_t)qt.row0 * (qt.K / 32) + e0 / 32, upload_stream_),
+                      "vsl_quant_pack");
             check(vsl_event_record(ev_[2 + slot], upload_stream_), "staging event");
             pending[slot] = true;
             slot ^= 1;
@@ -515,17 +608,20 @@ void VulkanSymbioteEngine::load_weights_from_gguf() {
             throw std::runtime_error("tensor " + name + " data out of range");
         return *t;
     };
-    // a weight tensor into a pack of dtype `dt`: raw bytes when stored in that dtype, else expanded
-    auto load_weight = [&](void* dst, const std::string& name, uint64_t elems, int dt) {
+    // a weight tensor into a pack of dtype `dt`: raw bytes when stored in that dtype, else expanded (and,
+    // with a QTarget, also kept as blocks)
+    auto load_weight = [&](void* dst, const std::string& name, uint64_t elems, int dt, const QTarget& qt) {
         const GGUFTensorInfo& t = need(name, elems);
         const int fmt = g.weight_format(t);
         if (fmt == (dt == VSL_DT_F16 ? VSL_WF_F16 : VSL_WF_F32))
             upload(dst, g.tensor_bytes(t), vsl_weight_bytes(fmt, elems));
         else
-            upload_convert(dst, g.tensor_bytes(t), fmt, g.block_layout(t), elems, dt);
+            upload_convert(dst, g.tensor_bytes(t), fmt, g.block_layout(t), elems, dt, qt);
         pack_manager_.register_pack(meta_of(name), dst, elems * (dt == VSL_DT_F16 ? 2 : 4), dt);
     };
-    auto load_linear = [&](void* dst, const std::string& name, uint64_t elems) { load_weight(dst, name, elems, wdt_); };
+    auto load_linear = [&](void* dst, const std::string& name, uint64_t elems, QTarget qt = QTarget{}) {
+        load_weight(dst, name, elems, wdt_, qt);
+    };
     std::vector<std::vector<float>> norm_host;
     norm_host.reserve(2 * c.num_layers + 1);
     auto load_norm = [&](float* dst, const std::string& name) {
@@ -536,22 +632,27 @@ void VulkanSymbioteEngine::load_weights_from_gguf() {
         check(vsl_copy_h2d(dst, norm_host.back().data(), d * 4, upload_stream_), "norm upload");
         pack_manager_.register_pack(meta_of(name), dst, d * 4, VSL_DT_F32);
     };
-    load_weight(embed_, "token_embd.weight", V * d, edt_);
+    load_weight(embed_, "token_embd.weight", V * d, edt_, QTarget{});
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         Layer& y = layers_[l];
         const uint64_t es = wdt_ == VSL_DT_F16 ? 2 : 4;
         char* qkv = static_cast<char*>(y.wqkv);
+        const uint32_t nr = (uint32_t)((nq + 2 * nkv) * hd);
+        auto qt = [](void* pack, uint32_t rows, uint32_t K, uint32_t row0) { return QTarget{pack, rows, K, row0}; };
         load_norm(y.attn_norm, layer_name(l, "attn_norm.weight"));
-        load_linear(qkv, layer_name(l, "attn_q.weight"), nq * hd * d);
-        load_linear(qkv + nq * hd * d * es, layer_name(l, "attn_k.weight"), nkv * hd * d);
-        load_linear(qkv + (nq + nkv) * hd * d * es, layer_name(l, "attn_v.weight"), nkv * hd * d);
+        load_linear(qkv, layer_name(l, "attn_q.weight"), nq * hd * d, qt(y.qqkv, nr, (uint32_t)d, 0));
+        load_linear(qkv + nq * hd * d * es, layer_name(l, "attn_k.weight"), nkv * hd * d,
+                    qt(y.qqkv, nr, (uint32_t)d, (uint32_t)(nq * hd)));
+        load_linear(qkv + (nq + nkv) * hd * d * es, layer_name(l, "attn_v.weight"), nkv * hd * d,
+                    qt(y.qqkv, nr, (uint32_t)d, (uint32_t)((nq + nkv) * hd)));
         const std::string oname = g.get_tensor(layer_name(l, "attn_o.weight")) ? layer_name(l, "attn_o.weight")
                                                                                : layer_name(l, "attn_output.weight");
-        load_linear(y.wo, oname, d * nq * hd);
+        load_linear(y.wo, oname, d * nq * hd, qt(y.qo, (uint32_t)d, (uint32_t)(nq * hd), 0));
         load_norm(y.ffn_norm, layer_name(l, "ffn_norm.weight"));
-        load_linear(y.wgu, layer_name(l, "ffn_gate.weight"), F * d);
-        load_linear(static_cast<char*>(y.wgu) + F * d * es, layer_name(l, "ffn_up.weight"), F * d);
-        load_linear(y.wdown, layer_name(l, "ffn_down.weight"), d * F);
+        load_linear(y.wgu, layer_name(l, "ffn_gate.weight"), F * d, qt(y.qgu, (uint32_t)(2 * F), (uint32_t)d, 0));
+        load_linear(static_cast<char*>(y.wgu) + F * d * es, layer_name(l, "ffn_up.weight"), F * d,
+                    qt(y.qgu, (uint32_t)(2 * F), (uint32_t)d, (uint32_t)F));
+        load_linear(y.wdown, layer_name(l, "ffn_down.weight"), d * F, qt(y.qdown, (uint32_t)d, (uint32_t)F, 0));
     }
     if (g.get_tensor("output_norm.weight")) {
         load_norm(out_norm_, "output_norm.weight");
@@ -559,7 +660,7 @@ void VulkanSymbioteEngine::load_weights_from_gguf() {
         out_norm_ = nullptr;  // the reference has no final norm; a file without one runs without it
     }
     if (g.get_tensor("output.weight")) {
-        load_linear(out_w_, "output.weight", V * d);
+        load_linear(out_w_, "output.weight", V * d, QTarget{out_q_, (uint32_t)V, (uint32_t)d, 0});
     } else if (edt_ == wdt_) {  // tied output projection
         check(vsl_copy_d2d(out_w_, embed_, V * d * (wdt_ == VSL_DT_F16 ? 2 : 4), upload_stream_), "tied output");
     } else {
@@ -580,12 +681,18 @@ void VulkanSymbioteEngine::enqueue_layers(uint32_t l0, uint32_t l1) {
     const float eps = c.rms_epsilon, scale = 1.0f / std::sqrt((float)hd);
     for (uint32_t l = l0; l < l1; ++l) {
         const Layer& y = layers_[l];
-        check(vsl_qkv_rope_append(x_, y.attn_norm, eps, y.wqkv, wdt_, d, nq, nkv, hd, rope_cos_, rope_sin_, y.kc, y.vc,
-                                  kvdt_, cap_, q_, ctrl_, stream_), "vsl_qkv_rope_append");
+        // each operand's resident block-quantized pack where it has one, else its expanded pack
+        check(vsl_qkv_rope_append(x_, y.attn_norm, eps, y.qqkv ? y.qqkv : y.wqkv, y.qqkv ? y.qdt_qkv : wdt_, d, nq,
+                                  nkv, hd, rope_cos_, rope_sin_, y.kc, y.vc, kvdt_, cap_, q_, ctrl_, stream_),
+              "vsl_qkv_rope_append");
         check(attend(y, scale), "vsl_attn_decode");
-        check(vsl_gemv_residual(y.wo, wdt_, d, nq * hd, attn_, x_, ctrl_, stream_), "vsl_gemv_residual(o)");
-        check(vsl_norm_swiglu(x_, y.ffn_norm, eps, y.wgu, wdt_, d, F, h_, ctrl_, stream_), "vsl_norm_swiglu");
-        check(vsl_gemv_residual(y.wdown, wdt_, d, F, h_, x_, ctrl_, stream_), "vsl_gemv_residual(down)");
+        check(vsl_gemv_residual(y.qo ? y.qo : y.wo, y.qo ? y.qdt_o : wdt_, d, nq * hd, attn_, x_, ctrl_, stream_),
+              "vsl_gemv_residual(o)");
+        check(vsl_norm_swiglu(x_, y.ffn_norm, eps, y.qgu ? y.qgu : y.wgu, y.qgu ? y.qdt_gu : wdt_, d, F, h_, ctrl_,
+                              stream_),
+              "vsl_norm_swiglu");
+        check(vsl_gemv_residual(y.qdown ? y.qdown : y.wdown, y.qdown ? y.qdt_down : wdt_, d, F, h_, x_, ctrl_, stream_),
+              "vsl_gemv_residual(down)");
     }
 }
 
@@ -600,8 +707,9 @@ static vsl_sampler to_vsl_sampler(const SamplingParams& p) {
 
 void VulkanSymbioteEngine::enqueue_step(const SamplingParams& p) {
     enqueue_layers(0, config_.num_layers);
-    check(vsl_lm_head_sample(out_norm_, config_.rms_epsilon, out_w_, wdt_, config_.vocab_size, config_.hidden_size, x_,
-                             embed_, edt_, logits_, to_vsl_sampler(p), lm_val_, lm_idx_, tokens_, ctrl_, stream_),
+    check(vsl_lm_head_sample(out_norm_, config_.rms_epsilon, lm_w(), lm_dt(), config_.vocab_size,
+                             config_.hidden_size, x_, embed_, edt_, logits_, to_vsl_sampler(p), lm_val_, lm_idx_,
+                             tokens_, ctrl_, stream_),
           "vsl_lm_head_sample");
 }
 
@@ -636,7 +744,7 @@ void VulkanSymbioteEngine::prefill_tokenwise(uint32_t n_prompt, const SamplingPa
         check(vsl_embed(embed_, edt_, c.vocab_size, c.hidden_size, prompt_dev_ + i, 1, x_, stream_), "vsl_embed");
         enqueue_layers(0, c.num_layers);
     }
-    check(vsl_lm_head_sample(out_norm_, c.rms_epsilon, out_w_, wdt_, c.vocab_size, c.hidden_size, x_, embed_, edt_,
+    check(vsl_lm_head_sample(out_norm_, c.rms_epsilon, lm_w(), lm_dt(), c.vocab_size, c.hidden_size, x_, embed_, edt_,
                              logits_, to_vsl_sampler(p), lm_val_, lm_idx_, tokens_, ctrl_, stream_),
           "vsl_lm_head_sample");
 }
@@ -745,8 +853,8 @@ void VulkanSymbioteEngine::prefill_batched(uint32_t n_prompt, const SamplingPara
     check(vsl_copy_d2d(x_, px_ + (size_t)(last_rows - 1) * d, (size_t)d * 4, stream_), "last row");
     check(vsl_ctrl_reset(ctrl_, n_prompt - 1, host_ctrl_->max_steps, host_ctrl_->stop_on_eos, cap_, stream_),
           "vsl_ctrl_reset");
-    check(vsl_lm_head_sample(out_norm_, eps, out_w_, wdt_, V, d, x_, embed_, edt_, logits_, to_vsl_sampler(p), lm_val_,
-                             lm_idx_, tokens_, ctrl_, stream_),
+    check(vsl_lm_head_sample(out_norm_, eps, lm_w(), lm_dt(), V, d, x_, embed_, edt_, logits_, to_vsl_sampler(p),
+                             lm_val_, lm_idx_, tokens_, ctrl_, stream_),
           "vsl_lm_head_sample");
 }
 
@@ -892,7 +1000,7 @@ double VulkanSymbioteEngine::time_op(int op, uint32_t iterations) {
             default: {
                 SamplingParams p;
                 check(vsl_ctrl_reset(ctrl_, pos, 0xFFFFFFFFu, 0, cap_, stream_), "vsl_ctrl_reset");
-                check(vsl_lm_head_sample(out_norm_, eps, out_w_, wdt_, c.vocab_size, d, x_, embed_, edt_, logits_,
+                check(vsl_lm_head_sample(out_norm_, eps, lm_w(), lm_dt(), c.vocab_size, d, x_, embed_, edt_, logits_,
                                          to_vsl_sampler(p), lm_val_, lm_idx_, tokens_, ctrl_, stream_), "lm_head");
             }
         }

@@ -31,6 +31,7 @@ extern "C" void vsl_engine_default_options(vsl_engine_options* o) {
     o->batched_prefill = 1;
     o->prefill_split = EngineOptions::kPrefillSplitAll;
     o->prefill_lo8 = EngineOptions::kPrefillLo8Default;
+    o->quant_decode = 1;
     const EngineOptions d;
     o->sparse_window = d.sparse_window;
     o->sparse_global = d.sparse_global;
@@ -49,6 +50,7 @@ static EngineOptions to_options(const vsl_engine_options* o) {
     e.prefill_split = o->prefill_split & EngineOptions::kPrefillSplitAll;
     e.prefill_lo8 = o->prefill_lo8 & EngineOptions::kPrefillLo8Stages;
     e.dequant_f32 = o->dequant_f32 != 0;
+    e.quant_decode = o->quant_decode != 0;
     e.sparse_attention = o->sparse_attention != 0;
     e.sparse_window = o->sparse_window;
     e.sparse_global = o->sparse_global;
@@ -90,12 +92,14 @@ extern "C" int vsl_engine_open_synthetic(const vsl_model_spec* spec, uint64_t se
     if (!spec || !out) return fail(VSL_E_INVALID, "vsl_engine_open_synthetic: null argument");
     *out = nullptr;
     try {
-        if (spec->dtype > VSL_DT_F16)
-            return fail(VSL_E_UNSUPPORTED, "vsl_engine_open_synthetic: weights are F32 or F16 (quantized "
-                                           "models are opened from a GGUF file)");
+        if (spec->dtype > VSL_WF_Q8_0)
+            return fail(VSL_E_UNSUPPORTED, "vsl_engine_open_synthetic: weights are F32, F16, Q4_0, Q4_1 or Q8_0");
         SyntheticSpec s;
         s.config = to_config(spec);
-        s.fp16 = spec->dtype == VSL_DT_F16;
+        // quantized: fp16 draws quantized on the device into the decode packs; the expanded packs hold
+        // the quantized values in fp16, or exactly in fp32 with dequant_f32
+        s.quant_format = spec->dtype >= VSL_WF_Q4_0 ? static_cast<int>(spec->dtype) : -1;
+        s.fp16 = spec->dtype == VSL_DT_F16 || (s.quant_format >= 0 && !(opt && opt->dequant_f32));
         s.init_std = spec->init_std > 0 ? spec->init_std : 0.02f;
         s.seed = seed;
         auto e = std::make_unique<vsl_engine>();

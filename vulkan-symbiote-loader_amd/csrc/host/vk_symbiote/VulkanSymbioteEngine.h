@@ -12,6 +12,7 @@
 #pragma once
 
 #include <map>
+#include <array>
 #include <memory>
 #include <string>
 #include <tuple>
@@ -86,6 +87,12 @@ struct EngineOptions {
     // Block-quantized GGUF weights (Q4_0 / Q4_1 / Q8_0) are expanded at load into fp16 packs, or into
     // fp32 packs holding exactly the values the reference's dequantize_tensor returns when set.
     bool dequant_f32 = false;
+    // Block-quantized weights also stay resident as blocks (vsl_quant_pack: 8.5 / 4.5 / 5 bits per
+    // weight) and the decode GEMVs multiply those directly, reading a quarter to a half of the fp16
+    // bytes per token; the prompt pass keeps its MFMA GEMMs on the expanded packs. Taken per
+    // operand ([Wq; Wk; Wv], Wo, [Wgate; Wup], Wdown, the output projection) when its tensors share
+    // one quantized format and its input width is a multiple of 32.
+    bool quant_decode = true;
     // Windowed long-context mode (the reference's use_sparse_attention, Common.h:70-75, taken when
     // seq_len > 8192, VulkanSymbioteEngine.cpp:788): a query at position p with p + 1 > threshold
     // attends to the first sparse_global keys and to the sparse_window keys before it (and itself)
@@ -105,8 +112,10 @@ struct EngineOptions {
 struct SyntheticSpec {
     ModelConfig config;
     bool fp16 = true;
-    // write_synthetic_gguf only: VSL_WF_Q4_0 / Q4_1 / Q8_0 stores every 2-D weight (embeddings and
-    // output included) block-quantized from the fp32 draws; -1 keeps F16 / F32 per `fp16`
+    // VSL_WF_Q4_0 / Q4_1 / Q8_0: write_synthetic_gguf stores every 2-D weight (embeddings and output
+    // included) block-quantized from the fp32 draws; a synthetic engine draws fp16 weights, quantizes
+    // every linear weight on the device (vsl_quantize_pack) into the decode packs and replaces the
+    // fp16 packs with the quantized values (the embedding stays fp16). -1 keeps F16 / F32 per `fp16`.
     int quant_format = -1;
     // write_synthetic_gguf only: a vocabulary, written as the string array "tokenizer.ggml.tokens"
     // or, with vocab_keyed, as one string key "tokenizer.ggml.tokens.<id>" per entry
@@ -205,7 +214,20 @@ class VulkanSymbioteEngine {
         // VSL_GEMM_B8_SHIFT flags of the fp8 lo products against [Wq; Wk; Wv], Wo, [Wgate; Wup], Wdown:
         // each matrix's own shift, from its largest weight (measure_weight_ranges)
         int b8_qkv = 0, b8_o = 0, b8_gu = 0, b8_down = 0;
+        // resident block-quantized packs of the same operands for the decode GEMVs (nullptr: none)
+        // and their VSL_DT_Q* dtypes
+        void* qqkv = nullptr;
+        void* qo = nullptr;
+        void* qgu = nullptr;
+        void* qdown = nullptr;
+        int qdt_qkv = 0, qdt_o = 0, qdt_gu = 0, qdt_down = 0;
     };
+    // VSL_WF_* format of each decode operand's resident pack, -1 for none: per layer [Wq; Wk; Wv],
+    // Wo, [Wgate; Wup], Wdown; and the output projection
+    std::vector<std::array<int, 4>> qfmt_;
+    int qfmt_out_ = -1;
+    void plan_quant_gguf(const ModelConfig& cfg);
+    void plan_quant_uniform(const ModelConfig& cfg, int fmt);
 
     ModelConfig config_;
     EngineOptions options_;
@@ -228,6 +250,11 @@ class VulkanSymbioteEngine {
     // device buffers
     void* embed_ = nullptr;
     void* out_w_ = nullptr;
+    void* out_q_ = nullptr;  // the output projection's block-quantized pack (nullptr: none)
+    int out_qdt_ = 0;
+    // the output projection operand of the lm_head GEMV: its pack where it has one
+    const void* lm_w() const { return out_q_ ? out_q_ : out_w_; }
+    int lm_dt() const { return out_q_ ? out_qdt_ : wdt_; }
     float* out_norm_ = nullptr;
     std::vector<Layer> layers_;
     float* rope_cos_ = nullptr;
