@@ -9,8 +9,9 @@ then greedy decode.  A step is one decode token; K steps are timed between two s
 
 The same run also measures, as extra keys of the one JSON line: the configured 512-step decode
 (positions 513..1024), the 1B-class model (prompt 128, greedy decode 256), the fp16 GEMV sweep, the
-long-context workload (8192-token prompt in 2048-token chunks, KV capacity 32768) and a 70B-class model
-(137.5 GB of fp16 weights in one GPU's HBM; prompt 128, greedy decode 64); --quick skips them.
+long-context workload (8192-token prompt in 2048-token chunks, KV capacity 32768), a 70B-class model
+(137.5 GB of fp16 weights in one GPU's HBM; prompt 128, greedy decode 64) and the 8B-class model with
+Q8_0 / Q4_0 weight blocks read by the decode (prompt 512, greedy decode 128); --quick skips them.
 
 Prints one JSON line.  --gpus N with N > 1 exits: this build targets one GPU.
 """
@@ -97,11 +98,16 @@ def model_bytes(c):
     return p_lin, p_norm, kvb
 
 
+# bytes per linear weight read by the decode, by the model's weight storage (VSL_WF_*): fp32, fp16, and
+# the resident block-quantized packs (values plus one fp32 scale per 32 weights; Q4_1 also an offset)
+WEIGHT_BYTES = {0: 4.0, 1: 2.0, 2: 0.5 + 4 / 32, 3: 0.5 + 8 / 32, 4: 1.0 + 4 / 32}
+
+
 def decode_bytes(c, attended):
     """Algorithmic HBM bytes of one decode token that attends `attended` positions: every weight
     once, the embedding row, K/V of the attended positions and the new position's K/V write."""
     p_lin, p_norm, kvb = model_bytes(c)
-    return 2 * p_lin + 2 * p_norm + 2 * c["hidden_size"] + kvb * attended + kvb
+    return WEIGHT_BYTES[c.get("dtype", 1)] * p_lin + 2 * p_norm + 2 * c["hidden_size"] + kvb * attended + kvb
 
 
 def prefill_flops(c, S):
@@ -330,20 +336,21 @@ def decode_ops_table(eng, cfg, p_att, iterations=3):
     d, F, V = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"]
     nq, nkv = cfg["num_heads"], cfg["num_kv_heads"]
     hd = d // nq
+    wb = WEIGHT_BYTES[cfg.get("dtype", 1)]  # bytes per linear weight
     names = ["qkv_rope_append", "attn_decode", "o_proj_resid", "norm_gateup_swiglu", "down_proj_resid",
              "lm_head_argmax"]
     bytes_per_launch = [
-        2 * (nq + 2 * nkv) * hd * d + 8 * d + 4 * nq * hd + 2 * 2 * nkv * hd,
+        wb * (nq + 2 * nkv) * hd * d + 8 * d + 4 * nq * hd + 2 * 2 * nkv * hd,
         2 * 2 * nkv * hd * p_att + 8 * nq * hd,
-        2 * d * nq * hd + 4 * nq * hd + 8 * d,
-        2 * 2 * F * d + 8 * d + 4 * F,
-        2 * d * F + 4 * F + 8 * d,
-        2 * V * d + 8 * d + 4 * V,
+        wb * d * nq * hd + 4 * nq * hd + 8 * d,
+        wb * 2 * F * d + 8 * d + 4 * F,
+        wb * d * F + 4 * F + 8 * d,
+        wb * V * d + 8 * d + 4 * V,
     ]
     ops = {}
     for op, nm in enumerate(names):
         ms = eng.time_op(op, iterations)
-        ops[nm] = {"avg_us": round(ms * 1e3, 2), "bytes": bytes_per_launch[op],
+        ops[nm] = {"avg_us": round(ms * 1e3, 2), "bytes": int(bytes_per_launch[op]),
                    "gbps": round(bytes_per_launch[op] / (ms * 1e-3) / 1e9, 1)}
     return ops
 
@@ -412,6 +419,32 @@ def llama_70b_leg(vsl, eager, steps=64, prefill_runs=3):
             "prefill_ms": round(pre_ms, 3), "prefill_tok_s": round(n_prompt / (pre_ms / 1e3), 1),
             "prefill_tflops": round(pre_flops / (pre_ms / 1e3) / 1e12, 1),
             "prefill_mfma_frac": round(pre_flops / (pre_ms / 1e3) / PEAK_F16, 4)}
+
+
+def llama_8b_quant_leg(vsl, fmt, eager, steps=128, prefill_runs=3):
+    """The 8B-class model with every linear weight block-quantized (VSL_WF_Q8_0 / Q4_0, quantized on the
+    device from the fp16 draws): the decode GEMVs read the resident blocks, the prompt pass runs on the
+    expanded fp16 packs. Prompt 512, greedy decode `steps`."""
+    cfg = dict(CFG, dtype=fmt)
+    prompt = np.random.default_rng(1).integers(0, cfg["vocab_size"], 512).astype(np.uint32)
+    eng = vsl.Engine(spec=cfg, seed=0, kv_capacity=KV_CAPACITY, use_graph=not eager)
+    try:
+        eng.begin(prompt, 9)
+        eng.decode(8)
+        eng.finish()
+        dec_s, st = timed_decode(eng, prompt, steps)
+        pre = [st["prefill_ms"]]
+        for _ in range(prefill_runs - 1):
+            eng.begin(prompt, 1)
+            eng.finish()
+            pre.append(eng.last_stats()["prefill_ms"])
+    finally:
+        eng.close()
+    name = {vsl.VSL_WF_Q8_0: "Q8_0", vsl.VSL_WF_Q4_0: "Q4_0", vsl.VSL_WF_Q4_1: "Q4_1"}[fmt]
+    return {"workload": f"8B-class Llama decoder, linear weights {name} resident blocks (quantized on the device "
+                        f"from N(0, 0.02) fp16 draws), bs=1: prompt 512, greedy decode {steps}, KV cap {KV_CAPACITY}",
+            "decode": decode_rates(cfg, 512, steps, dec_s),
+            "prefill_ms": round(float(np.median(pre)), 3)}
 
 
 def copy_calibration(vsl, mb):
@@ -586,7 +619,9 @@ def main():
         for key, leg in (("llama_1b", lambda: llama_1b_leg(vsl, a.eager, kernel_timing=not a.no_kernel_timing)),
                          ("gemv_sweep", lambda: sweep_leg(vsl, graph=not a.eager)),
                          ("long_context", lambda: long_leg(vsl, 128, a.eager)),
-                         ("llama_70b", lambda: llama_70b_leg(vsl, a.eager))):
+                         ("llama_70b", lambda: llama_70b_leg(vsl, a.eager)),
+                         ("llama_8b_q8_0", lambda: llama_8b_quant_leg(vsl, vsl.VSL_WF_Q8_0, a.eager)),
+                         ("llama_8b_q4_0", lambda: llama_8b_quant_leg(vsl, vsl.VSL_WF_Q4_0, a.eager))):
             try:
                 out[key] = leg()
             except Exception as ex:  # reported, never fatal to the headline measurement

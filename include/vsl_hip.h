@@ -149,7 +149,8 @@ int vsl_convert_weights(const void* src, int src_fmt, int layout, uint64_t n, vo
 
 /* Resident block-quantized weight packs, multiplied block by block inside the decode GEMVs (no
  * reference counterpart: the reference expands every block to fp32 at load, GGUFLoader.cpp:1121-1223,
- * and reads 32 bits per weight per token; a pack reads 8.5 / 4.5 / 5 bits).  A pack holds a matrix
+ * and reads 32 bits per weight per token; a pack reads 9 / 5 / 6 bits for Q8_0 / Q4_0 / Q4_1, its
+ * scales held as fp32).  A pack holds a matrix
  * of `rows` x K values (K % 32 == 0) in 32-value blocks, row-major block order, as planes that each
  * start at a multiple of 256 bytes from the pack's 256-byte aligned base:
  *   VSL_DT_Q8_0  int8 values [rows][K], then fp32 scales d [rows][K/32]             w = q d

@@ -385,6 +385,34 @@ def test_gemv_residual_and_swiglu(vsl, orc, dev, H):
     assert rel_err(dev.get(dh), orc.swiglu(gu[:F], gu[F:])) < 1e-4
 
 
+@pytest.mark.parametrize("N,K", [(77, 8), (300, 40), (1000, 1000), (4099, 4104), (129, 8200), (64, 14344),
+                                 (20, 16392)])
+def test_gemv_ragged_k(vsl, orc, dev, H, N, K):
+    """Decode GEMVs whose K is a multiple of 8 but not of 32: the staged activation vector's last
+    aligned group of eight float4 slots is partial (4-, 8- and 16-wave blocks). Residual GEMV, fp32-X
+    GEMV and RMSNorm + SwiGLU against the oracle."""
+    rng = np.random.default_rng(3 * N + K)
+    W = rng.normal(0, 0.02, (N, K)).astype(np.float16)
+    h = rng.normal(0, 1, K).astype(np.float32)
+    r = rng.normal(0, 1, N).astype(np.float32)
+    dW, dr = dev.put(W), dev.put(r)
+    ref = orc.gemm_nt(W, h)[:, 0]
+    ok(vsl, H.vsl_gemv_residual(dev.p(dW), 1, N, K, dev.p(dev.put(h)), dev.p(dr), None, None))
+    assert rel_err(dev.get(dr), r + ref) < 1e-5
+    dy = dev.empty((N,), np.float32)
+    ok(vsl, H.vsl_gemv(dev.p(dW), vsl.VSL_DT_F16, N, K, dev.p(dev.put(h)), vsl.VSL_DT_F32, 1, dev.p(dy),
+                       vsl.VSL_DT_F32, None))
+    assert rel_err(dev.get(dy), ref) < 1e-5
+    F = N // 2
+    if F:
+        gm = rng.normal(1, 0.1, K).astype(np.float32)
+        dh = dev.empty((F,), np.float32)
+        ok(vsl, H.vsl_norm_swiglu(dev.p(dev.put(h)), dev.p(dev.put(gm)), 1e-5, dev.p(dW), 1, K, F, dev.p(dh),
+                                  None, None))
+        gu = orc.gemm_nt(W[:2 * F], orc.rmsnorm(h, gm, 1e-5))[:, 0]
+        assert rel_err(dev.get(dh), orc.swiglu(gu[:F], gu[F:])) < 1e-4
+
+
 @pytest.mark.parametrize("N,K", [(4100, 28672), (1000, 20480), (333, 32768)])
 def test_gemv_wide_k(vsl, orc, dev, H, N, K):
     """Decode GEMVs wider than 16384 columns (70B-class down projections: K = 28672) stage the fp32

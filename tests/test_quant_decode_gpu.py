@@ -120,6 +120,25 @@ def test_quant_gemv(vsl, orc, dev, H, fmt, N, K):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("N,K", [(4096, 14336), (300, 28672), (1000, 4096), (33, 96), (70, 32768)])
+def test_quant_gemv_residual_shapes(vsl, orc, dev, H, fmt, N, K):
+    """The residual GEMV over a pack (the O / down projection; one row per wave on 16-wave blocks)
+    against the pack's dequantized values in float64, at the 8B down shape, past 16384 columns, a
+    short row and a row of one block."""
+    conv = 1
+    raw = _raw(fmt, conv, N, K, 3 * N + K)
+    W = _values(orc, raw, fmt, conv, N * K).reshape(N, K).astype(np.float64)
+    pack = _pack(vsl, H, dev, [(N, raw)], fmt, conv, K)
+    rng = np.random.default_rng(N + 7)
+    h = rng.normal(0, 1, K).astype(np.float32)
+    r = rng.normal(0, 1, N).astype(np.float32)
+    y = dev.put(r)
+    ok(vsl, H.vsl_gemv_residual(dev.p(pack), DT[fmt], N, K, dev.p(dev.put(h)), dev.p(y), None, None))
+    want = r.astype(np.float64) + W @ h.astype(np.float64)
+    assert rel_err(dev.get(y), want) < 1e-5
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 def test_quant_decode_ops(vsl, orc, dev, H, fmt):
     """The fused decode entry points over a pack against the same launches over the pack's fp32
     values: residual GEMV, RMSNorm + [Wgate; Wup] + SwiGLU, RMSNorm + [Wq; Wk; Wv] + RoPE + KV append

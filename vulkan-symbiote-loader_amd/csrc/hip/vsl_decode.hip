@@ -64,6 +64,19 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Float4 slot of the activation vector's float4 q in LDS for the block-quantized tiles. A lane reads
+// kVec / 4 consecutive float4s per weight load (lanes kVec floats apart), so in the plain layout the
+// lanes of one LDS pass hit the same banks 4-fold (Q8) or 8-fold (Q4). XOR-ing the slot within its
+// aligned group of eight with bits 3-5 ^ 4-6 of q spreads every such pass, and the staging stores of
+// consecutive float4s, over distinct banks for 32 or 64 banks of 4 bytes; it only permutes slots
+// within aligned groups of 8 float4s, so the vector fits in K rounded up to 32 floats. (fp16 tiles,
+// 2-fold in the plain layout, keep it: with the slot XORs the 8B decode's down and O projections took
+// 19.80 / 7.16 us against 19.64 / 7.04, kernel-trace medians.)
+__device__ __forceinline__ uint32_t xs_slot(uint32_t q) { return q ^ (((q >> 3) ^ (q >> 4)) & 7u); }
+template <class WT>
+__device__ __host__ constexpr bool xs_swizzled() { return WT::kQuant; }
+__device__ __host__ __forceinline__ constexpr uint32_t xs_floats(uint32_t K) { return (K + 31u) & ~31u; }
+
 // The block's activation slice lives in registers between its loads and the LDS store, so that
 // the loads can be issued ahead of the first weight tile (vector loads complete in issue order:
 // waiting for the activations then never waits for the weights behind them).
@@ -109,7 +122,10 @@ struct XStage {
             for (int j = 0; j < XPT; ++j) gr[j] = make_float4(1.f, 1.f, 1.f, 1.f);
         }
     }
-    // RMS-normalise (rms_norm.comp:24-34) when gamma is given, and store to LDS as fp32
+    // RMS-normalise (rms_norm.comp:24-34) when gamma is given, and store to LDS as fp32 (with SWZ,
+    // float4 q at slot xs_slot(q)); with BSUM (K % 32 == 0) also the sum of every 32-value block, at
+    // xs[K + i / 32]
+    template <bool SWZ, bool BSUM>
     __device__ __forceinline__ void store(const float* __restrict__ gamma, float eps, uint32_t K, float* __restrict__ xs,
                                           float* red) {
         const uint32_t tid = threadIdx.x;
@@ -142,7 +158,8 @@ struct XStage {
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
             const uint32_t i = (j * NT + tid) * 4;
-            if (j * NT * 4 < K && i < K) {
+            if (j * NT * 4 < K) {  // uniform: the block sums below take whole lane groups
+                const bool in = i < K;
                 float4 v = xr[j];
                 if (gamma) {
                     const float4 g = gr[j];
@@ -151,29 +168,31 @@ struct XStage {
                     v.z = v.z * inv * g.z;
                     v.w = v.w * inv * g.w;
                 }
-                *reinterpret_cast<float4*>(xs + i) = v;
+                if (in) reinterpret_cast<float4*>(xs)[SWZ ? xs_slot(i / 4) : i / 4] = v;
+                if constexpr (BSUM) {
+                    // a 32-value block is the float4s of 8 adjacent lanes
+                    float bs = in ? (v.x + v.y) + (v.z + v.w) : 0.f;
+                    bs = group_sum_dpp<8>(bs);
+                    if (in && (tid & 7) == 0) xs[K + i / 32] = bs;
+                }
             }
         }
         lds_barrier();
     }
 };
 
+// The kVec activations of columns kk .. kk + kVec - 1 (kk a multiple of kVec). Quantized tiles: the
+// float4s q0 .. q0 + F - 1 of one aligned group of eight, at slots xs_slot(q0) ^ j = (q0 ^ g) ^ j, with
+// g = xs_slot(q0) ^ q0 the lane's constant (bits 0-6 of q0 = kk / 4 come from lane * F alone, the
+// tile's column base being a multiple of 512 floats).
 template <class WT>
-__device__ __forceinline__ void load_x(const float* xs, uint32_t kk, float* xv) {
-    if constexpr (WT::kVec == 8) {
-        float4 a = *reinterpret_cast<const float4*>(xs + kk);
-        float4 b = *reinterpret_cast<const float4*>(xs + kk + 4);
-        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
-    } else if constexpr (WT::kVec == 4) {
-        float4 a = *reinterpret_cast<const float4*>(xs + kk);
-        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-    } else {
+__device__ __forceinline__ void load_x(const float* xs, uint32_t kk, float* xv, uint32_t g) {
+    const float4* x4 = reinterpret_cast<const float4*>(xs);
+    const uint32_t p0 = xs_swizzled<WT>() ? (kk >> 2) ^ g : kk >> 2;
 #pragma unroll
-        for (int j = 0; j < WT::kVec; j += 4) {
-            const float4 a = *reinterpret_cast<const float4*>(xs + kk + j);
-            xv[j] = a.x; xv[j + 1] = a.y; xv[j + 2] = a.z; xv[j + 3] = a.w;
-        }
+    for (int j = 0; j < WT::kVec / 4; ++j) {
+        const float4 a = x4[xs_swizzled<WT>() ? p0 ^ (uint32_t)j : p0 + j];
+        xv[4 * j] = a.x; xv[4 * j + 1] = a.y; xv[4 * j + 2] = a.z; xv[4 * j + 3] = a.w;
     }
 }
 
@@ -233,6 +252,8 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
     const float* __restrict__ Qm = WT::kMin ? reinterpret_cast<const float*>(W + qpack_mins_off(WT::kBits, w_rows, a.K)) : nullptr;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    static_assert(!xs_swizzled<WT>() || SPAN % 512 == 0, "the activation slot constant needs 512-float column bases");
+    const uint32_t xg = xs_slot(lane * (VEC / 4)) ^ (lane * (VEC / 4));  // load_x's slot constant
     const uint32_t n_groups = (a.N + RG - 1) / RG;
     const uint32_t stride = gridDim.x * WAVES;
     const uint32_t g0 = blockIdx.x * WAVES + wave;
@@ -389,15 +410,53 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
             const uint32_t kk = k0 + u * SPAN + lane * VEC;
             const bool in = kk < a.K;
             float xv[VEC];
-            load_x<WT>(xs, in ? kk : 0, xv);
-            if constexpr (QW) {
-                // the lane's values share one block: acc += d * sum(q x) (Q8), d * (sum(q x) - 8 sum(x))
-                // (Q4_0) or d * sum(q x) + m * sum(x) (Q4_1), with d = m = 0 past K
-                float xsum = 0.f;
-                if constexpr (WT::kBits == 4) {
+            load_x<WT>(xs, in ? kk : 0, xv, xg);
+            if constexpr (QW && WT::kBits == 4) {
+                // The lane's 32 values are one block: acc += d * (sum(q x) - 8 sum(x)) (Q4_0) or
+                // d * sum(q x) + m * sum(x) (Q4_1), with d = m = 0 past K and sum(x) the block sum
+                // staged beside the activations. Each nibble is masked in place into an fp16 lane
+                // of a pair, where it reads as the subnormal q * 2^-24 (bits 0-3) or q * 2^-20
+                // (bits 4-7), and v_fma_mix multiplies it by the fp32 activation exactly as a
+                // converted integer would be: products of the two bit positions go to separate
+                // sums, rescaled by 2^24 and 2^20 once per block.
+                const float xsum = xs[a.K + (in ? kk : 0) / 32];
 #pragma unroll
-                    for (int i = 0; i < VEC; ++i) xsum += xv[i];
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t wd[4] = {w[r][u].x, w[r][u].y, w[r][u].z, w[r][u].w};
+                    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        // dword m holds values 8m .. 8m+7: value 2b in the low, 2b+1 in the high
+                        // nibble of byte b; the pairs are (8m, 8m+4), (8m+1, 8m+5) from the
+                        // dword, (8m+2, 8m+6), (8m+3, 8m+7) from the dword shifted by one byte
+                        const uint32_t t = wd[m] >> 8;
+                        const half2v p0 = __builtin_bit_cast(half2v, wd[m] & 0x000F000Fu);
+                        const half2v p1 = __builtin_bit_cast(half2v, wd[m] & 0x00F000F0u);
+                        const half2v p2 = __builtin_bit_cast(half2v, t & 0x000F000Fu);
+                        const half2v p3 = __builtin_bit_cast(half2v, t & 0x00F000F0u);
+                        const float* xm = xv + 8 * m;
+                        s0 = fmaf((float)p0[0], xm[0], s0);
+                        s0 = fmaf((float)p0[1], xm[4], s0);
+                        s0 = fmaf((float)p2[0], xm[2], s0);
+                        s0 = fmaf((float)p2[1], xm[6], s0);
+                        s1 = fmaf((float)p1[0], xm[1], s1);
+                        s1 = fmaf((float)p1[1], xm[5], s1);
+                        s1 = fmaf((float)p3[0], xm[3], s1);
+                        s1 = fmaf((float)p3[1], xm[7], s1);
+                    }
+                    const float b = fmaf(s1, 0x1p20f, s0 * 0x1p24f);  // sum(q x)
+                    const float d = in ? qs[r][u] : 0.f;
+                    if constexpr (WT::kMin) {
+                        acc[r] = fmaf(d, b, acc[r]);
+                        acc[r] = fmaf(in ? qm[r][u] : 0.f, xsum, acc[r]);
+                    } else {
+                        acc[r] = fmaf(d, fmaf(-8.f, xsum, b), acc[r]);
+                    }
                 }
+                continue;
+            }
+            if constexpr (QW) {
+                // Q8: two lanes share a block; acc += d * sum(q x), with d = 0 past K
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     float wf[VEC];
@@ -405,15 +464,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
                     float b = 0.f;
 #pragma unroll
                     for (int i = 0; i < VEC; ++i) b = fmaf(wf[i], xv[i], b);
-                    const float d = in ? qs[r][u] : 0.f;
-                    if constexpr (WT::kMin) {
-                        acc[r] = fmaf(d, b, acc[r]);
-                        acc[r] = fmaf(in ? qm[r][u] : 0.f, xsum, acc[r]);
-                    } else if constexpr (WT::kBits == 4) {
-                        acc[r] = fmaf(d, fmaf(-8.f, xsum, b), acc[r]);
-                    } else {
-                        acc[r] = fmaf(d, b, acc[r]);
-                    }
+                    acc[r] = fmaf(in ? qs[r][u] : 0.f, b, acc[r]);
                 }
                 continue;
             }
@@ -458,7 +509,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_gemv_dec(GemvArgs a) {
     }
     issue_pf(pa, 0);  // the RoPE angles depend on pos
     issue_pf(pb, 1);
-    st.store(a.gamma, a.eps, a.K, xs, red);
+    st.template store<xs_swizzled<WT>(), QW && WT::kBits == 4>(a.gamma, a.eps, a.K, xs, red);
 
     // Straight-line pairs with a single loop exit: the compiler's memory-counter waits merge over
     // every control-flow edge, so a conditional issue, a skipped consume or a mid-loop exit would
@@ -575,7 +626,8 @@ constexpr uint32_t kMaxK = 32768;  // activation vector held in LDS as fp32 (up 
 template <class WT, int R, int U, int EPI, int WAVES, class ET = WF32>
 int launch_gemv(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
     const uint32_t blocks = gemv_blocks<R, EPI, WAVES>(a.N, max_blocks);
-    const size_t lds = (size_t)a.K * sizeof(float);
+    // the fp32 activation vector, and for 4-bit packs its 32-value block sums
+    const size_t lds = (size_t)xs_floats(a.K) * sizeof(float) + (WT::kBits == 4 ? (size_t)a.K / 32 * sizeof(float) : 0);
     const uint32_t per = WAVES * 64 * 4;
     if (a.K <= per)
         k_gemv_dec<WT, R, U, EPI, ET, WAVES, 1><<<blocks, WAVES * 64, lds, s>>>(a);
@@ -642,6 +694,26 @@ int check_gemv_shape(uint32_t N, uint32_t K, const char* who) {
 
 bool quant_dtype(int wdtype) { return wdtype == VSL_DT_Q8_0 || wdtype == VSL_DT_Q4_0 || wdtype == VSL_DT_Q4_1; }
 
+// Block-quantized packs: every block stages the whole fp32 activation vector (4K bytes) for weights of
+// 0.56 - 1.13 bytes per value, so that with the fp16 launch shapes the staging traffic approaches the
+// weight bytes where a block covers few rows. Larger blocks (fewer of them, each CU's resident waves
+// sharing one copy) measured faster for the SwiGLU GEMV (8 waves) and the wide-K residual GEMV (the
+// down projection, 16 waves); kernel-trace medians on the 8B decode, Q4_0 / Q8_0, fp16 shape -> this
+// one: gate/up 15.9 -> 14.6 / 23.0 -> 22.3 us, down 11.2 -> 10.4 / 13.5 -> 13.4 us. The QKV GEMV
+// (4 waves: 6.5 / 7.4 us against 7.1 / 8.5 at 8), the O projection (level within 0.3 us at 4, 8 or
+// 16 waves for Q4_0; 5.6 at 4 against 6.3 at 16 for Q8_0) and lm_head keep the fp16 shapes.
+template <class WT, int R, int U, int EPI, class ET>
+int launch_gemv_q(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
+    if (gemv_waves_env() == 0) {
+        if constexpr (EPI == EPI_SWIGLU) {
+            if (a.K <= kXWideK) return launch_gemv<WT, R, U, EPI, 8, ET>(a, max_blocks, s);
+        } else if constexpr (EPI == EPI_RESID) {
+            if (a.K > kWideK) return launch_gemv<WT, R, U, EPI, 16, ET>(a, max_blocks, s);
+        }
+    }
+    return launch_gemv_k<WT, R, U, EPI, ET>(a, max_blocks, s);
+}
+
 // The decode GEMV over the weight dtype: fp16 / fp32 matrices with four 16-byte loads per lane and row
 // per tile; block-quantized packs with the same 2048 columns per tile (Q8: two loads of 16 values,
 // Q4: one of 32).
@@ -654,9 +726,9 @@ int launch_gemv_w(int wdtype, const GemvArgs& a, uint32_t max_blocks, hipStream_
     switch (wdtype) {
         case VSL_DT_F16: return launch_gemv_k<WF16, R, 4, EPI, ET>(a, max_blocks, s);
         case VSL_DT_F32: return launch_gemv_k<WF32, R, 4, EPI, ET>(a, max_blocks, s);
-        case VSL_DT_Q8_0: return launch_gemv_k<WQ8, R, 2, EPI, ET>(a, max_blocks, s);
-        case VSL_DT_Q4_0: return launch_gemv_k<WQ4, R, 1, EPI, ET>(a, max_blocks, s);
-        case VSL_DT_Q4_1: return launch_gemv_k<WQ41, R, 1, EPI, ET>(a, max_blocks, s);
+        case VSL_DT_Q8_0: return launch_gemv_q<WQ8, R, 2, EPI, ET>(a, max_blocks, s);
+        case VSL_DT_Q4_0: return launch_gemv_q<WQ4, R, 1, EPI, ET>(a, max_blocks, s);
+        case VSL_DT_Q4_1: return launch_gemv_q<WQ41, R, 1, EPI, ET>(a, max_blocks, s);
         default: return vsl_unsupported("%s: weight dtype %d", who, wdtype);
     }
 }

@@ -988,15 +988,25 @@ double VulkanSymbioteEngine::time_op(int op, uint32_t iterations) {
         const Layer& y = layers_[l];
         switch (op) {
             case 0:
-                check(vsl_qkv_rope_append(x_, y.attn_norm, eps, y.wqkv, wdt_, d, nq, nkv, hd, rope_cos_, rope_sin_, y.kc,
-                                          y.vc, kvdt_, cap_, q_, ctrl_, stream_), "qkv");
+                check(vsl_qkv_rope_append(x_, y.attn_norm, eps, y.qqkv ? y.qqkv : y.wqkv, y.qqkv ? y.qdt_qkv : wdt_, d,
+                                          nq, nkv, hd, rope_cos_, rope_sin_, y.kc, y.vc, kvdt_, cap_, q_, ctrl_,
+                                          stream_), "qkv");
                 break;
             case 1:
                 check(attend(y, scale), "attn");
                 break;
-            case 2: check(vsl_gemv_residual(y.wo, wdt_, d, nq * hd, attn_, x_, ctrl_, stream_), "o"); break;
-            case 3: check(vsl_norm_swiglu(x_, y.ffn_norm, eps, y.wgu, wdt_, d, F, h_, ctrl_, stream_), "gate/up"); break;
-            case 4: check(vsl_gemv_residual(y.wdown, wdt_, d, F, h_, x_, ctrl_, stream_), "down"); break;
+            case 2:
+                check(vsl_gemv_residual(y.qo ? y.qo : y.wo, y.qo ? y.qdt_o : wdt_, d, nq * hd, attn_, x_, ctrl_,
+                                        stream_), "o");
+                break;
+            case 3:
+                check(vsl_norm_swiglu(x_, y.ffn_norm, eps, y.qgu ? y.qgu : y.wgu, y.qgu ? y.qdt_gu : wdt_, d, F, h_,
+                                      ctrl_, stream_), "gate/up");
+                break;
+            case 4:
+                check(vsl_gemv_residual(y.qdown ? y.qdown : y.wdown, y.qdown ? y.qdt_down : wdt_, d, F, h_, x_, ctrl_,
+                                        stream_), "down");
+                break;
             default: {
                 SamplingParams p;
                 check(vsl_ctrl_reset(ctrl_, pos, 0xFFFFFFFFu, 0, cap_, stream_), "vsl_ctrl_reset");

@@ -87,9 +87,9 @@ struct EngineOptions {
     // Block-quantized GGUF weights (Q4_0 / Q4_1 / Q8_0) are expanded at load into fp16 packs, or into
     // fp32 packs holding exactly the values the reference's dequantize_tensor returns when set.
     bool dequant_f32 = false;
-    // Block-quantized weights also stay resident as blocks (vsl_quant_pack: 8.5 / 4.5 / 5 bits per
-    // weight) and the decode GEMVs multiply those directly, reading a quarter to a half of the fp16
-    // bytes per token; the prompt pass keeps its MFMA GEMMs on the expanded packs. Taken per
+    // Block-quantized weights also stay resident as blocks (vsl_quant_pack: 9 / 5 / 6 bits per weight
+    // for Q8_0 / Q4_0 / Q4_1) and the decode GEMVs multiply those directly, reading 31 to 56 % of the
+    // fp16 bytes per token; the prompt pass keeps its MFMA GEMMs on the expanded packs. Taken per
     // operand ([Wq; Wk; Wv], Wo, [Wgate; Wup], Wdown, the output projection) when its tensors share
     // one quantized format and its input width is a multiple of 32.
     bool quant_decode = true;
