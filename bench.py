@@ -421,10 +421,11 @@ def llama_70b_leg(vsl, eager, steps=64, prefill_runs=3):
             "prefill_mfma_frac": round(pre_flops / (pre_ms / 1e3) / PEAK_F16, 4)}
 
 
-def llama_8b_quant_leg(vsl, fmt, eager, steps=128, prefill_runs=3):
-    """The 8B-class model with every linear weight block-quantized (VSL_WF_Q8_0 / Q4_0, quantized on the
-    device from the fp16 draws): the decode GEMVs read the resident blocks, the prompt pass runs on the
-    expanded fp16 packs. Prompt 512, greedy decode `steps`."""
+def llama_8b_quant_leg(vsl, fmt, eager, steps=128, prefill_runs=3, kernel_timing=False):
+    """The 8B-class model with every linear weight block-quantized (VSL_WF_Q8_0 / Q4_0 / Q4_1, quantized
+    on the device from the fp16 draws): the decode GEMVs read the resident blocks, the prompt pass runs
+    on the expanded fp16 packs. Prompt 512, greedy decode `steps`; with kernel_timing also the per-op
+    table at the last decode position."""
     cfg = dict(CFG, dtype=fmt)
     prompt = np.random.default_rng(1).integers(0, cfg["vocab_size"], 512).astype(np.uint32)
     eng = vsl.Engine(spec=cfg, seed=0, kv_capacity=KV_CAPACITY, use_graph=not eager)
@@ -438,13 +439,17 @@ def llama_8b_quant_leg(vsl, fmt, eager, steps=128, prefill_runs=3):
             eng.begin(prompt, 1)
             eng.finish()
             pre.append(eng.last_stats()["prefill_ms"])
+        ops = decode_ops_table(eng, cfg, 512 + steps) if kernel_timing else None
     finally:
         eng.close()
     name = {vsl.VSL_WF_Q8_0: "Q8_0", vsl.VSL_WF_Q4_0: "Q4_0", vsl.VSL_WF_Q4_1: "Q4_1"}[fmt]
-    return {"workload": f"8B-class Llama decoder, linear weights {name} resident blocks (quantized on the device "
-                        f"from N(0, 0.02) fp16 draws), bs=1: prompt 512, greedy decode {steps}, KV cap {KV_CAPACITY}",
-            "decode": decode_rates(cfg, 512, steps, dec_s),
-            "prefill_ms": round(float(np.median(pre)), 3)}
+    out = {"workload": f"8B-class Llama decoder, linear weights {name} resident blocks (quantized on the device "
+                       f"from N(0, 0.02) fp16 draws), bs=1: prompt 512, greedy decode {steps}, KV cap {KV_CAPACITY}",
+           "decode": decode_rates(cfg, 512, steps, dec_s),
+           "prefill_ms": round(float(np.median(pre)), 3)}
+    if ops is not None:
+        out["decode_ops"] = ops
+    return out
 
 
 def copy_calibration(vsl, mb):
@@ -494,6 +499,9 @@ def main():
                     help="the standalone fp16 GEMV / skinny-GEMM sweep instead: Y = W X for (N, K) in "
                          "{(4096,4096), (14336,4096), (4096,14336), (32000,4096)} and B in {1, 4, 16}, W rotated "
                          "over >= 512 MB of distinct copies so the 256 MB MALL cannot serve it")
+    ap.add_argument("--quant", choices=["q8_0", "q4_0", "q4_1"],
+                    help="the 8B-class model with block-quantized linear weights alone (resident blocks read "
+                         "by the decode; prompt 512, greedy decode 128) with its per-op table: one JSON line")
     ap.add_argument("--long", action="store_true",
                     help="the long-context workload instead: 8192-token prompt prefilled in 2048-token chunks "
                          "into a 32768-position KV cache, greedy decode (default 128 steps), then the same "
@@ -504,6 +512,18 @@ def main():
         return
     if a.sweep:
         run_sweep(a)
+        return
+    if a.quant:
+        gpus_or_exit(a)
+        vsl = load_package()
+        fmt = {"q8_0": vsl.VSL_WF_Q8_0, "q4_0": vsl.VSL_WF_Q4_0, "q4_1": vsl.VSL_WF_Q4_1}[a.quant]
+        lg = llama_8b_quant_leg(vsl, fmt, a.eager, kernel_timing=not a.no_kernel_timing)
+        out = {"metric": f"decode tok/s + HBM GB/s (% peak), 8B {a.quant.upper()} bs=1; prefill ms",
+               "value": lg["decode"]["tok_s"], "unit": "tok/s", "n_gpus": 1, "higher_is_better": True,
+               "dtype": a.quant, "data": "synthetic: N(0,0.02) fp16 draws quantized on the device, uniform-random "
+                                         "prompt ids", "config": {"workload": lg["workload"]}}
+        out.update(lg)
+        print(json.dumps(out), flush=True)
         return
     if a.llama_1b:
         gpus_or_exit(a)
