@@ -144,7 +144,7 @@ def _oracle_from_engine(orc, e, cfg):
     return m
 
 
-def _forced_parity(e, m, prompt, n_new, tol, runs=None):
+def _forced_parity(e, m, prompt, n_new, tol, runs=None, kv_f16=True):
     """The oracle generates from the prompt (greedy unless `runs` says otherwise), then the engine is
     teacher-forced with the oracle's tokens, so both compute every step on the same token history:
     every step's logits within max-abs `tol`, and the engine's own pick at every step equal to the
@@ -152,7 +152,7 @@ def _forced_parity(e, m, prompt, n_new, tol, runs=None):
     oracle's top1-top2 margin and the logit error there.  Returns the per-step oracle margins and
     logit errors of each run."""
     runs = runs or [dict(n=n_new)]
-    ref = m.continuations(prompt, runs, kv_f16=True)
+    ref = m.continuations(prompt, runs, kv_f16=kv_f16)
     report = []
     for r, (rt, rl) in zip(runs, ref):
         kw = dict(mode={0: "greedy", 1: "reference", 2: "topk"}[r.get("sampler", 0)],
@@ -280,6 +280,24 @@ def test_llama_8b_fp16_parity(vsl, orc):
     with vsl.Engine(spec=cfg, seed=0, kv_capacity=1024, batched_prefill=True) as e:
         m = _oracle_from_engine(orc, e, cfg)
         _forced_parity(e, m, orc.random_ids(512, cfg["vocab_size"], 1), 32, 2e-2)
+    m.close()
+
+
+@pytest.mark.slow
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_llama_8b_resident_blocks_parity(vsl, orc, fmt):
+    """The 8B-class model with every linear weight quantized on the device (Q4_0 / Q8_0) and decoded
+    from the resident blocks at the full shapes (the 16-wave down projection, the 8-wave SwiGLU GEMV,
+    the quantized lm_head): the expanded packs in fp32 hold exactly the blocks' values, so the oracle
+    over them is the same model. A 256-token prompt (per-token steps over the blocks: an fp32 model
+    has no MFMA prompt pass), then 32 teacher-forced greedy steps: logits within max-abs 2e-2 at every
+    step, picks identical."""
+    cfg = dict(vsl.LLAMA_8B, dtype={"q4_0": vsl.VSL_WF_Q4_0, "q8_0": vsl.VSL_WF_Q8_0}[fmt])
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=512, dequant_f32=True) as e:
+        assert e.config["dtype"] == 0
+        m = _oracle_from_engine(orc, e, dict(cfg, dtype=0))
+        _forced_parity(e, m, orc.random_ids(256, cfg["vocab_size"], 3), 32, 2e-2, kv_f16=False)
     m.close()
 
 
