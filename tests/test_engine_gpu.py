@@ -303,6 +303,27 @@ def test_llama_8b_resident_blocks_parity(vsl, orc, fmt):
 
 @pytest.mark.slow
 @pytest.mark.timeout(900)
+@pytest.mark.parametrize("fmt,conv", [("q4_0", "ggml"), ("q8_0", "reference")])
+def test_llama_1b_quantized_file_default_path(vsl, orc, tmp_path, fmt, conv):
+    """A 1B-class GGUF file with every 2-D weight block-quantized, opened with the engine's defaults:
+    the blocks expanded into fp16 packs for the MFMA prompt pass (128 rows: K-split direct-to-LDS
+    tiles) and kept resident for the decode GEMVs. Against the oracle that dequantizes the same file
+    (fp32 weights, fp16 KV cache): 32 teacher-forced greedy steps after a 128-token prompt, logits
+    within max-abs 2e-2 at every step, picks identical."""
+    cfg = dict(vsl.LLAMA_1B, dtype={"q4_0": vsl.VSL_WF_Q4_0, "q8_0": vsl.VSL_WF_Q8_0}[fmt])
+    p = tmp_path / f"llama1b_{fmt}.gguf"
+    vsl.write_synthetic_gguf(p, cfg, seed=11, convention=conv)
+    m = orc.Model(p)
+    try:
+        with vsl.Engine(p, kv_capacity=512) as e:
+            _forced_parity(e, m, orc.random_ids(128, cfg["vocab_size"], 5), 32, 2e-2)
+    finally:
+        m.close()
+        p.unlink()
+
+
+@pytest.mark.slow
+@pytest.mark.timeout(900)
 def test_llama_8b_long_path_oracle(vsl, orc):
     """The full 32-layer 8B model on the long-context path against the oracle: a KV capacity of 16384
     (above 8192, so decode attention runs on the matrix-core kernel), a 768-token prompt in three
