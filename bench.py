@@ -10,8 +10,9 @@ then greedy decode.  A step is one decode token; K steps are timed between two s
 The same run also measures, as extra keys of the one JSON line: the configured 512-step decode
 (positions 513..1024), the 1B-class model (prompt 128, greedy decode 256), the fp16 GEMV sweep, the
 long-context workload (8192-token prompt in 2048-token chunks, KV capacity 32768), a 70B-class model
-(137.5 GB of fp16 weights in one GPU's HBM; prompt 128, greedy decode 64) and the 8B-class model with
-Q8_0 / Q4_0 weight blocks read by the decode (prompt 512, greedy decode 128); --quick skips them.
+(137.5 GB of fp16 weights in one GPU's HBM; prompt 128, greedy decode 64; again with Q4_0 weight
+blocks read by the decode) and the 8B-class model with Q8_0 / Q4_0 weight blocks read by the decode
+(prompt 512, greedy decode 128); --quick skips them.
 
 Prints one JSON line.  --gpus N with N > 1 exits: this build targets one GPU.
 """
@@ -394,11 +395,14 @@ LLAMA_70B = dict(hidden_size=8192, num_layers=80, num_heads=64, num_kv_heads=8, 
                  vocab_size=32000, max_position_embeddings=4096, rope_theta=500000.0, rms_eps=1e-5, dtype=1)
 
 
-def llama_70b_leg(vsl, eager, steps=64, prefill_runs=3):
-    """70B-class fp16 on one GPU: prompt 128, greedy decode `steps`."""
+def llama_70b_leg(vsl, eager, steps=64, prefill_runs=3, fmt=1):
+    """70B-class on one GPU: prompt 128, greedy decode `steps`; fmt 1 fp16 weights, or VSL_WF_Q4_0 /
+    Q4_1 / Q8_0: every linear weight quantized on the device into resident blocks for the decode (the
+    prompt pass on the expanded fp16 packs)."""
     n_prompt = 128
+    cfg = dict(LLAMA_70B, dtype=fmt)
     prompt = np.random.default_rng(3).integers(0, LLAMA_70B["vocab_size"], n_prompt).astype(np.uint32)
-    eng = vsl.Engine(spec=LLAMA_70B, seed=0, kv_capacity=1024, use_graph=not eager)
+    eng = vsl.Engine(spec=cfg, seed=0, kv_capacity=1024, use_graph=not eager)
     try:
         eng.begin(prompt, 5)
         eng.decode(4)
@@ -413,9 +417,12 @@ def llama_70b_leg(vsl, eager, steps=64, prefill_runs=3):
         eng.close()
     pre_ms = float(np.median(pre))
     pre_flops = prefill_flops(LLAMA_70B, n_prompt)
-    return {"workload": f"70B-class Llama decoder fp16 bs=1 (80L, d8192, 64/8 heads, FFN 28672, V32000; "
-                        f"137.5 GB of weights on one GPU): prompt {n_prompt}, greedy decode {steps}",
-            "decode": decode_rates(LLAMA_70B, n_prompt, steps, dec_s),
+    name = {1: "fp16", vsl.VSL_WF_Q8_0: "Q8_0 resident blocks", vsl.VSL_WF_Q4_0: "Q4_0 resident blocks",
+            vsl.VSL_WF_Q4_1: "Q4_1 resident blocks"}[fmt]
+    wgb = decode_bytes(cfg, 0) / 1e9
+    return {"workload": f"70B-class Llama decoder {name} bs=1 (80L, d8192, 64/8 heads, FFN 28672, V32000; "
+                        f"{wgb:.1f} GB read per token on one GPU): prompt {n_prompt}, greedy decode {steps}",
+            "decode": decode_rates(cfg, n_prompt, steps, dec_s),
             "prefill_ms": round(pre_ms, 3), "prefill_tok_s": round(n_prompt / (pre_ms / 1e3), 1),
             "prefill_tflops": round(pre_flops / (pre_ms / 1e3) / 1e12, 1),
             "prefill_mfma_frac": round(pre_flops / (pre_ms / 1e3) / PEAK_F16, 4)}
@@ -485,8 +492,8 @@ def main():
     ap.add_argument("--attn-splits", type=int, default=0,
                     help="decode attention split count of the 8B engine (0: the engine's choice)")
     ap.add_argument("--quick", action="store_true",
-                    help="the headline decode / prefill only (no 512-step decode, 1B, sweep, long-context or 70B "
-                         "legs)")
+                    help="the headline decode / prefill only (no 512-step decode, 1B, sweep, long-context, 70B "
+                         "or quantized legs)")
     ap.add_argument("--no-kernel-timing", action="store_true")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="after the run, copy this many MB device-to-device once (a kernel of known traffic "
@@ -640,6 +647,7 @@ def main():
                          ("gemv_sweep", lambda: sweep_leg(vsl, graph=not a.eager)),
                          ("long_context", lambda: long_leg(vsl, 128, a.eager)),
                          ("llama_70b", lambda: llama_70b_leg(vsl, a.eager)),
+                         ("llama_70b_q4_0", lambda: llama_70b_leg(vsl, a.eager, fmt=vsl.VSL_WF_Q4_0)),
                          ("llama_8b_q8_0", lambda: llama_8b_quant_leg(vsl, vsl.VSL_WF_Q8_0, a.eager)),
                          ("llama_8b_q4_0", lambda: llama_8b_quant_leg(vsl, vsl.VSL_WF_Q4_0, a.eager))):
             try:
