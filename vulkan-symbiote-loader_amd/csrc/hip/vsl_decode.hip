@@ -697,18 +697,19 @@ bool quant_dtype(int wdtype) { return wdtype == VSL_DT_Q8_0 || wdtype == VSL_DT_
 // Block-quantized packs: every block stages the whole fp32 activation vector (4K bytes) for weights of
 // 0.56 - 1.13 bytes per value, so that with the fp16 launch shapes the staging traffic approaches the
 // weight bytes where a block covers few rows. Larger blocks (fewer of them, each CU's resident waves
-// sharing one copy) measured faster for the SwiGLU GEMV (8 waves) and the wide-K residual GEMV (the
-// down projection, 16 waves); kernel-trace medians on the 8B decode, Q4_0 / Q8_0, fp16 shape -> this
-// one: gate/up 15.9 -> 14.6 / 23.0 -> 22.3 us, down 11.2 -> 10.4 / 13.5 -> 13.4 us. The QKV GEMV
-// (4 waves: 6.5 / 7.4 us against 7.1 / 8.5 at 8), the O projection (level within 0.3 us at 4, 8 or
-// 16 waves for Q4_0; 5.6 at 4 against 6.3 at 16 for Q8_0) and lm_head keep the fp16 shapes.
+// sharing one copy) measured faster for the SwiGLU GEMV (8 waves) and the residual GEMV from 8192
+// input columns (16 waves); kernel-trace medians, Q4_0 / Q8_0, fp16 shape -> this one: 8B gate/up
+// 15.9 -> 14.6 / 23.0 -> 22.3 us, 8B down 11.2 -> 10.4 / 13.5 -> 13.4 us, 70B-class O projection
+// (8192 x 8192) 13.1 -> 11.6 us for Q4_0. The QKV GEMV (4 waves: 6.5 / 7.4 us against 7.1 / 8.5 at
+// 8), the 8B O projection (K 4096: level within 0.3 us at 4, 8 or 16 waves for Q4_0; 5.6 at 4 against
+// 6.3 at 16 for Q8_0) and lm_head keep the fp16 shapes.
 template <class WT, int R, int U, int EPI, class ET>
 int launch_gemv_q(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
     if (gemv_waves_env() == 0) {
         if constexpr (EPI == EPI_SWIGLU) {
             if (a.K <= kXWideK) return launch_gemv<WT, R, U, EPI, 8, ET>(a, max_blocks, s);
         } else if constexpr (EPI == EPI_RESID) {
-            if (a.K > kWideK) return launch_gemv<WT, R, U, EPI, 16, ET>(a, max_blocks, s);
+            if (a.K >= kWideK) return launch_gemv<WT, R, U, EPI, 16, ET>(a, max_blocks, s);
         }
     }
     return launch_gemv_k<WT, R, U, EPI, ET>(a, max_blocks, s);
