@@ -120,11 +120,11 @@ def test_quant_gemv(vsl, orc, dev, H, fmt, N, K):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("N,K", [(4096, 14336), (300, 28672), (1000, 4096), (33, 96), (70, 32768)])
+@pytest.mark.parametrize("N,K", [(4096, 14336), (300, 28672), (1000, 4096), (33, 96), (70, 32768), (8193, 8192)])
 def test_quant_gemv_residual_shapes(vsl, orc, dev, H, fmt, N, K):
-    """The residual GEMV over a pack (the O / down projection; one row per wave on 16-wave blocks)
-    against the pack's dequantized values in float64, at the 8B down shape, past 16384 columns, a
-    short row and a row of one block."""
+    """The residual GEMV over a pack (the O / down projection; from 8192 columns on 16-wave blocks, two
+    rows per wave from 8192 rows) against the pack's dequantized values in float64, at the 8B down
+    shape, past 16384 columns, a short row, a row of one block and an odd row count past 8192."""
     conv = 1
     raw = _raw(fmt, conv, N, K, 3 * N + K)
     W = _values(orc, raw, fmt, conv, N * K).reshape(N, K).astype(np.float64)

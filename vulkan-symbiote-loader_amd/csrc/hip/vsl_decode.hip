@@ -702,14 +702,24 @@ bool quant_dtype(int wdtype) { return wdtype == VSL_DT_Q8_0 || wdtype == VSL_DT_
 // 15.9 -> 14.6 / 23.0 -> 22.3 us, 8B down 11.2 -> 10.4 / 13.5 -> 13.4 us, 70B-class O projection
 // (8192 x 8192) 13.1 -> 11.6 us for Q4_0. The QKV GEMV (4 waves: 6.5 / 7.4 us against 7.1 / 8.5 at
 // 8), the 8B O projection (K 4096: level within 0.3 us at 4, 8 or 16 waves for Q4_0; 5.6 at 4 against
-// 6.3 at 16 for Q8_0) and lm_head keep the fp16 shapes.
+// 6.3 at 16 for Q8_0) and lm_head keep the fp16 shapes. Two rows per wave in those residual GEMVs:
+// 70B-class down projection (8192 rows) 30.5 -> 28.0 us, O 11.3 -> 11.1 us; with 4096 rows (8B: half
+// the waves idle) 10.4 -> 13.4 / 13.6 -> 17.4 us, so only from 8192 rows.
 template <class WT, int R, int U, int EPI, class ET>
 int launch_gemv_q(const GemvArgs& a, uint32_t max_blocks, hipStream_t s) {
     if (gemv_waves_env() == 0) {
         if constexpr (EPI == EPI_SWIGLU) {
             if (a.K <= kXWideK) return launch_gemv<WT, R, U, EPI, 8, ET>(a, max_blocks, s);
         } else if constexpr (EPI == EPI_RESID) {
-            if (a.K >= kWideK) return launch_gemv<WT, R, U, EPI, 16, ET>(a, max_blocks, s);
+            if (a.K >= kWideK) {
+                // two rows per wave once the rows fill every resident wave twice over (each staged
+                // activation read then serves two rows)
+                if constexpr (R == 1) {
+                    if ((uint64_t)a.N >= 2ull * 16ull * gemv_grid_cap(16, EPI_RESID))
+                        return launch_gemv<WT, 2, U, EPI, 16, ET>(a, max_blocks, s);
+                }
+                return launch_gemv<WT, R, U, EPI, 16, ET>(a, max_blocks, s);
+            }
         }
     }
     return launch_gemv_k<WT, R, U, EPI, ET>(a, max_blocks, s);
