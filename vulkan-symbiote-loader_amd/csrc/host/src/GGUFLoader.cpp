@@ -244,49 +244,58 @@ std::vector<uint8_t> quantize_blocks(const float* x, uint64 n, int fmt, int layo
     std::vector<uint8_t> out(nb * bb, 0);
     if (!bb) return {};
     const bool ref = layout == VSL_QL_REFERENCE;
-    for (uint64_t b = 0; b < nb; ++b) {
-        float v[kBlock] = {0};
-        const uint64_t cnt = std::min<uint64_t>(kBlock, n - b * kBlock);
-        std::memcpy(v, x + b * kBlock, cnt * sizeof(float));
-        uint8_t* blk = out.data() + b * bb;
-        auto put_half = [](uint8_t* p, float f) {
-            const uint16_t h = float_to_half(f);
-            std::memcpy(p, &h, 2);
-            return half_to_float(h);  // the scale the reader will see
-        };
-        if (fmt == VSL_WF_Q8_0) {
-            float amax = 0.0f;
-            for (float f : v) amax = std::max(amax, std::fabs(f));
-            const float d = put_half(blk, amax / 127.0f);
-            const float inv = d != 0.0f ? 1.0f / d : 0.0f;
-            for (uint32_t j = 0; j < kBlock; ++j) {
-                const float q = std::nearbyint(v[j] * inv);
-                blk[2 + j] = static_cast<uint8_t>(static_cast<int8_t>(std::min(127.0f, std::max(-128.0f, q))));
+    // blocks are independent: contiguous ranges of them on up to 32 threads
+    auto quantize_range = [&](uint64_t b0, uint64_t b1) {
+        for (uint64_t b = b0; b < b1; ++b) {
+            float v[kBlock] = {0};
+            const uint64_t cnt = std::min<uint64_t>(kBlock, n - b * kBlock);
+            std::memcpy(v, x + b * kBlock, cnt * sizeof(float));
+            uint8_t* blk = out.data() + b * bb;
+            auto put_half = [](uint8_t* p, float f) {
+                const uint16_t h = float_to_half(f);
+                std::memcpy(p, &h, 2);
+                return half_to_float(h);  // the scale the reader will see
+            };
+            if (fmt == VSL_WF_Q8_0) {
+                float amax = 0.0f;
+                for (float f : v) amax = std::max(amax, std::fabs(f));
+                const float d = put_half(blk, amax / 127.0f);
+                const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+                for (uint32_t j = 0; j < kBlock; ++j) {
+                    const float q = std::nearbyint(v[j] * inv);
+                    blk[2 + j] = static_cast<uint8_t>(static_cast<int8_t>(std::min(127.0f, std::max(-128.0f, q))));
+                }
+                continue;
             }
-            continue;
+            uint8_t nib[kBlock];
+            if (fmt == VSL_WF_Q4_0) {
+                float ext = 0.0f;
+                for (float f : v)
+                    if (std::fabs(f) > std::fabs(ext)) ext = f;
+                const float d = put_half(blk, ext / -8.0f);
+                const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+                for (uint32_t j = 0; j < kBlock; ++j)
+                    nib[j] = static_cast<uint8_t>(std::min(15.0f, std::max(0.0f, std::floor(v[j] * inv + 8.5f))));
+            } else {
+                float lo = v[0], hi = v[0];
+                for (float f : v) { lo = std::min(lo, f); hi = std::max(hi, f); }
+                const float d = put_half(blk, (hi - lo) / 15.0f);
+                const float m = put_half(blk + 2, lo);
+                const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+                for (uint32_t j = 0; j < kBlock; ++j)
+                    nib[j] = static_cast<uint8_t>(std::min(15.0f, std::max(0.0f, std::floor((v[j] - m) * inv + 0.5f))));
+            }
+            uint8_t* qs = blk + (fmt == VSL_WF_Q4_1 ? 4 : 2);
+            for (uint32_t i = 0; i < 16; ++i)
+                qs[i] = static_cast<uint8_t>(nib[nibble_element(i, 0, ref)] | (nib[nibble_element(i, 1, ref)] << 4));
         }
-        uint8_t nib[kBlock];
-        if (fmt == VSL_WF_Q4_0) {
-            float ext = 0.0f;
-            for (float f : v)
-                if (std::fabs(f) > std::fabs(ext)) ext = f;
-            const float d = put_half(blk, ext / -8.0f);
-            const float inv = d != 0.0f ? 1.0f / d : 0.0f;
-            for (uint32_t j = 0; j < kBlock; ++j)
-                nib[j] = static_cast<uint8_t>(std::min(15.0f, std::max(0.0f, std::floor(v[j] * inv + 8.5f))));
-        } else {
-            float lo = v[0], hi = v[0];
-            for (float f : v) { lo = std::min(lo, f); hi = std::max(hi, f); }
-            const float d = put_half(blk, (hi - lo) / 15.0f);
-            const float m = put_half(blk + 2, lo);
-            const float inv = d != 0.0f ? 1.0f / d : 0.0f;
-            for (uint32_t j = 0; j < kBlock; ++j)
-                nib[j] = static_cast<uint8_t>(std::min(15.0f, std::max(0.0f, std::floor((v[j] - m) * inv + 0.5f))));
-        }
-        uint8_t* qs = blk + (fmt == VSL_WF_Q4_1 ? 4 : 2);
-        for (uint32_t i = 0; i < 16; ++i)
-            qs[i] = static_cast<uint8_t>(nib[nibble_element(i, 0, ref)] | (nib[nibble_element(i, 1, ref)] << 4));
-    }
+    };
+    unsigned nt = std::max(1u, std::min(32u, std::thread::hardware_concurrency()));
+    if (nb < 16384) nt = 1;
+    std::vector<std::thread> th;
+    for (unsigned t = 1; t < nt; ++t) th.emplace_back(quantize_range, nb * t / nt, nb * (t + 1) / nt);
+    quantize_range(0, nb / nt);
+    for (auto& t : th) t.join();
     return out;
 }
 
