@@ -172,6 +172,40 @@ def test_quant_decode_against_the_file(vsl, orc, qfiles, fmt, conv):
     assert np.array_equal(toks, toks_off)
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q8_0"])
+def test_quant_decode_mixed_operands(vsl, orc, tmp_path, fmt):
+    """A reference-layout file whose FFN width (712) is a multiple of 8 but not of 32: blocks straddle
+    the rows of ffn_down, so the down projection decodes from its expanded pack while the QKV, O and
+    gate/up GEMVs read resident blocks (and the prompt runs token by token: FFN is not a multiple of
+    64). Against the oracle that dequantizes the file: greedy tokens identical, logits within max-abs
+    2e-2, and the same tokens as with quant_decode off."""
+    cfg = dict(QTINY, intermediate_size=712, dtype=FMT_CODE[fmt])
+    p = tmp_path / f"mixed_{fmt}.gguf"
+    vsl.write_synthetic_gguf(p, cfg, seed=9, convention="reference")
+    prompt = _prompt(orc)
+    m = orc.Model(p)
+    ref_toks, ref_lg = m.generate(prompt, 24, kv_f16=True, logits=True)
+    m.close()
+    with vsl.Engine(p, kv_capacity=64) as e:
+        toks, lg = e.generate_ids(prompt, 24, return_logits=True)
+        wb_on = e.weight_bytes()
+    with vsl.Engine(p, kv_capacity=64, quant_decode=False) as e:
+        toks_off = e.generate_ids(prompt, 24)
+        wb_off = e.weight_bytes()
+    # the block packs held: [Wq;Wk;Wv], Wo and [Wgate;Wup] of every layer and W_out, not Wdown
+    H = vsl.hip()
+    d, F, V, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_layers"]
+    hd = d // cfg["num_heads"]
+    dt = {"q4_0": vsl.VSL_DT_Q4_0, "q8_0": vsl.VSL_DT_Q8_0}[fmt]
+    per_layer = (H.vsl_quant_pack_bytes(dt, (cfg["num_heads"] + 2 * cfg["num_kv_heads"]) * hd, d)
+                 + H.vsl_quant_pack_bytes(dt, d, cfg["num_heads"] * hd) + H.vsl_quant_pack_bytes(dt, 2 * F, d))
+    assert H.vsl_quant_pack_bytes(dt, d, F) == 0  # K % 32 != 0: no pack for the down projection
+    assert wb_on - wb_off == L * per_layer + H.vsl_quant_pack_bytes(dt, V, d)
+    assert np.max(np.abs(lg - ref_lg)) < 2e-2, np.max(np.abs(lg - ref_lg))
+    assert np.array_equal(toks, ref_toks)
+    assert np.array_equal(toks, toks_off)
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "q4_1", "q8_0"])
 def test_synthetic_quantized_engine(vsl, orc, fmt):
     """A synthetic model quantized on the device (vsl_quantize_pack), expanded packs in fp32
