@@ -694,7 +694,7 @@ int check_gemv_shape(uint32_t N, uint32_t K, const char* who) {
 
 bool quant_dtype(int wdtype) { return wdtype == VSL_DT_Q8_0 || wdtype == VSL_DT_Q4_0 || wdtype == VSL_DT_Q4_1; }
 
-// Block-quantized packs: every block stages the whole fp32 activation vector (4K bytes) for weights of
+// Block-quantized packs: every block stages the whole fp32 activation vector (4 bytes per column) for weights of
 // 0.56 - 1.13 bytes per value, so that with the fp16 launch shapes the staging traffic approaches the
 // weight bytes where a block covers few rows. Larger blocks (fewer of them, each CU's resident waves
 // sharing one copy) measured faster for the SwiGLU GEMV (8 waves) and the residual GEMV from 8192
