@@ -401,6 +401,27 @@ def test_gqa_group_of_three(vsl, orc, batched, cap):
     m.close()
 
 
+# Eight query heads per KV head (the 70B-class grouping, 64 / 8 heads) at head_dim 128 and 64.
+GQA8 = {128: dict(hidden_size=2048, num_layers=2, num_heads=16, num_kv_heads=2, intermediate_size=4096,
+                  vocab_size=32000, max_position_embeddings=4096, rope_theta=500000.0, rms_eps=1e-5, dtype=1),
+        64: dict(hidden_size=1024, num_layers=2, num_heads=16, num_kv_heads=2, intermediate_size=2816,
+                 vocab_size=32000, max_position_embeddings=4096, rope_theta=10000.0, rms_eps=1e-5, dtype=1)}
+
+
+@pytest.mark.parametrize("hd,batched,cap", [(128, True, 1024), (128, False, 1024), (128, True, 9216),
+                                            (64, True, 1024), (64, False, 1024)])
+def test_gqa_group_of_eight(vsl, orc, hd, batched, cap):
+    """GQA with eight query heads per KV head against the oracle: a 200-token prompt through the MFMA
+    prompt pass or the per-token pass, then 24 teacher-forced greedy steps on the vector decode
+    attention (capacity 1024) or, at head_dim 128, the matrix-core one (capacity 9216): logits within
+    max-abs 2e-2 at every step, picks identical."""
+    cfg = GQA8[hd]
+    with vsl.Engine(spec=cfg, seed=0, kv_capacity=cap, batched_prefill=batched) as e:
+        m = _oracle_from_engine(orc, e, cfg)
+        _forced_parity(e, m, orc.random_ids(200, cfg["vocab_size"], 6), 24, 2e-2)
+    m.close()
+
+
 # An FFN wider than 16384 (the 70B-class 28672 needs the same path): the decode down projection stages
 # its 20480-wide input with one 16-wave block per CU.
 WIDE_FFN = dict(hidden_size=512, num_layers=2, num_heads=4, num_kv_heads=1, intermediate_size=20480,
